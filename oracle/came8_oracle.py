@@ -1,0 +1,235 @@
+"""CPU oracle for the CAME 8-bit optimizer step -- TEST INFRASTRUCTURE ONLY.
+
+This module is the checker that the HIP kernels in ``came_amd`` are compared
+against.  Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
+leg of ``bench.py`` may import it.  The product path (``came_amd``) never
+imports, calls or falls back to anything here.
+
+It restates, op for op on CPU torch tensors, the arithmetic of the reference's
+pure-PyTorch CPU path:
+
+* blockwise absmax quantisation   -- reference ``came_pytorch/blockwise_quantization.py:11-42,66-82,112-124``
+* the full8bit state layout       -- reference ``came_pytorch/CAME8bitFull.py:748-788,919-923``
+  (CPU branch; ``CAME8bitMemory.py:390-447`` uses the same shapes)
+* one full8bit parameter step     -- reference ``came_pytorch/CAME8bitFull.py:939-1075`` (CPU branch)
+* the fp32-state CAMECUDA step    -- reference ``came_pytorch/CAMECUDA.py:275-326`` (generic branch)
+
+The op sequence is kept identical to the reference because the point of the
+oracle is bit-level agreement with it: each rounding step (``mul_`` then
+``add_(alpha=)`` which torch CPU evaluates as one fused multiply-add, true
+division, ``rsqrt`` = correctly rounded ``1/sqrt``, round-half-even) is the
+same one the reference performs.  The oracle is pinned by
+``tests/golden/*.npz`` (vectors written by importing the reference's CPU path,
+see ``tests/golden/make_golden.py``) and by closed-form tests in
+``tests/test_oracle_closed_form.py``.
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict
+
+import torch
+
+SIGNED_QMAX = 127.0
+UNSIGNED_QMAX = 255.0
+
+
+# --------------------------------------------------------------------------
+# blockwise quantisation  (reference blockwise_quantization.py)
+# --------------------------------------------------------------------------
+def num_blocks(numel: int, block_size: int) -> int:
+    """Reference blockwise_quantization.py:11-14 (at least one block, even when empty)."""
+    if block_size <= 0:
+        raise ValueError(f"block_size must be > 0, got {block_size}")
+    return max(1, math.ceil(numel / block_size))
+
+
+def quantize_blockwise(x: torch.Tensor, *, signed: bool, block_size: int):
+    """Reference blockwise_quantization.py:66-82.
+
+    Flat row-major blocks of ``block_size``; the tail block is zero padded
+    (so an unsigned block's max includes 0).  ``absmax == 0 -> 1``.
+    ``q = clamp(round_half_even((x / absmax) * Q))`` with Q = 127 (int8) or 255 (uint8).
+    """
+    flat = x.detach().reshape(-1).to(torch.float32)
+    nb = num_blocks(flat.numel(), block_size)
+    buf = torch.zeros(nb * block_size, dtype=torch.float32)
+    buf[: flat.numel()] = flat
+    blocks = buf.view(nb, block_size)
+    if signed:
+        amax = blocks.abs().amax(dim=1)
+        qmax, lo, qdtype = SIGNED_QMAX, -SIGNED_QMAX, torch.int8
+    else:
+        amax = blocks.amax(dim=1)
+        qmax, lo, qdtype = UNSIGNED_QMAX, 0.0, torch.uint8
+    amax = torch.where(amax > 0, amax, torch.ones_like(amax))
+    scaled = (blocks / amax.unsqueeze(1)) * qmax
+    q = torch.round(scaled).clamp(lo, qmax).to(qdtype)
+    return q.reshape(-1)[: flat.numel()].view_as(x), amax
+
+
+def dequantize_blockwise(q: torch.Tensor, absmax: torch.Tensor, *, signed: bool, block_size: int) -> torch.Tensor:
+    """Reference blockwise_quantization.py:112-124: ``q * (absmax / Q)`` per element."""
+    qf = q.reshape(-1).to(torch.float32)
+    step = absmax.repeat_interleave(block_size)[: qf.numel()] / (SIGNED_QMAX if signed else UNSIGNED_QMAX)
+    return (qf * step).view_as(q)
+
+
+# --------------------------------------------------------------------------
+# state layout (reference CAME8bitFull._init_state, CPU branch)
+# --------------------------------------------------------------------------
+def init_full8bit_state(shape, block_size: int = 256) -> Dict[str, object]:
+    """Reference CAME8bitFull.py:748-788,919-923 (CPU branch) and blockwise_quantization.py:17-42."""
+    shape = tuple(int(s) for s in shape)
+    numel = math.prod(shape)
+    st: Dict[str, object] = {"step": 0, "_mode": "full8bit", "RMS": 0}
+    st["exp_avg_q"] = torch.zeros(shape, dtype=torch.int8)
+    st["exp_avg_absmax"] = torch.ones(num_blocks(numel, block_size), dtype=torch.float32)
+    factored = len(shape) >= 2
+    st["factored"] = factored
+    if factored:
+        row_shape = shape[:-1]
+        col_shape = shape[:-2] + shape[-1:]
+        st["factored_row_q"] = torch.zeros((2,) + row_shape, dtype=torch.uint8)
+        st["factored_row_absmax"] = torch.ones((2, num_blocks(math.prod(row_shape), block_size)), dtype=torch.float32)
+        st["factored_col_q"] = torch.zeros((2,) + col_shape, dtype=torch.uint8)
+        st["factored_col_absmax"] = torch.ones((2, num_blocks(math.prod(col_shape), block_size)), dtype=torch.float32)
+    else:
+        st["exp_avg_sq_q"] = torch.zeros(shape, dtype=torch.uint8)
+        st["exp_avg_sq_absmax"] = torch.ones(num_blocks(numel, block_size), dtype=torch.float32)
+    return st
+
+
+def _approx_sq_grad(row: torch.Tensor, col: torch.Tensor) -> torch.Tensor:
+    """Reference CAME8bitFull.py:124-128.
+
+    NB: ``col.unsqueeze(-2).clamp_min_`` clamps the caller's column state in
+    place (it is a view), so the stored/quantised column state is clamped to
+    >= 1e-30; the row state is not.
+    """
+    rmean = row.mean(dim=-1, keepdim=True).clamp_min_(1e-30)
+    r = (row / rmean).rsqrt_().unsqueeze(-1)
+    c = col.unsqueeze(-2).clamp_min_(1e-30).rsqrt()
+    return torch.mul(r, c)
+
+
+def _rms(t: torch.Tensor) -> torch.Tensor:
+    """Reference CAME8bitFull.py:121-122."""
+    return t.norm(2) / (t.numel() ** 0.5)
+
+
+@torch.no_grad()
+def full8bit_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *, beta1: float, beta2: float,
+                  beta3: float, eps0: float, eps1: float, lr: float, clip_threshold: float,
+                  weight_decay: float, block_size: int) -> None:
+    """One CPU full8bit step on parameter ``p`` (in place) and state ``st`` (in place).
+
+    Follows reference CAME8bitFull.py:962-966 (step/RMS bookkeeping) and
+    :1006-1075 (the arithmetic), in the same operation order.
+    """
+    st["step"] += 1
+    st["RMS"] = _rms(p)
+    if grad.dtype in (torch.float16, torch.bfloat16):
+        grad = grad.float()
+    bs = block_size
+    m = dequantize_blockwise(st["exp_avg_q"], st["exp_avg_absmax"], signed=True, block_size=bs)
+    upd = (grad ** 2) + eps0
+    factored = st["factored"]
+    if factored:
+        rq, ra = st["factored_row_q"], st["factored_row_absmax"]
+        cq, ca = st["factored_col_q"], st["factored_col_absmax"]
+        sq_row = dequantize_blockwise(rq[0], ra[0], signed=False, block_size=bs)
+        sq_col = dequantize_blockwise(cq[0], ca[0], signed=False, block_size=bs)
+        sq_row.mul_(beta2).add_(upd.mean(dim=-1), alpha=1.0 - beta2)
+        sq_col.mul_(beta2).add_(upd.mean(dim=-2), alpha=1.0 - beta2)
+        upd = _approx_sq_grad(sq_row, sq_col)
+        upd.mul_(grad)
+    else:
+        sq = dequantize_blockwise(st["exp_avg_sq_q"], st["exp_avg_sq_absmax"], signed=False, block_size=bs)
+        sq.mul_(beta2).add_(upd, alpha=1.0 - beta2)
+        upd = sq.clamp_min_(1e-30).rsqrt().mul_(grad)
+
+    upd.div_((_rms(upd) / clip_threshold).clamp_(min=1.0))
+    m.mul_(beta1).add_(upd, alpha=1.0 - beta1)
+    res = (upd - m) ** 2 + eps1
+    if factored:
+        res_row = dequantize_blockwise(rq[1], ra[1], signed=False, block_size=bs)
+        res_col = dequantize_blockwise(cq[1], ca[1], signed=False, block_size=bs)
+        res_row.mul_(beta3).add_(res.mean(dim=-1), alpha=1.0 - beta3)
+        res_col.mul_(beta3).add_(res.mean(dim=-2), alpha=1.0 - beta3)
+        step_dir = _approx_sq_grad(res_row, res_col).mul_(m)
+    else:
+        step_dir = m.clone()
+
+    if weight_decay != 0.0:
+        p.add_(p, alpha=-weight_decay * lr)
+    p.add_(step_dir, alpha=-lr)
+
+    q, a = quantize_blockwise(m, signed=True, block_size=bs)
+    st["exp_avg_q"].copy_(q)
+    st["exp_avg_absmax"].copy_(a)
+    if factored:
+        for k, (row, col) in enumerate(((sq_row, sq_col), (res_row, res_col))):
+            q, a = quantize_blockwise(row, signed=False, block_size=bs)
+            rq[k].copy_(q)
+            ra[k].copy_(a)
+            q, a = quantize_blockwise(col, signed=False, block_size=bs)
+            cq[k].copy_(q)
+            ca[k].copy_(a)
+    else:
+        q, a = quantize_blockwise(sq, signed=False, block_size=bs)
+        st["exp_avg_sq_q"].copy_(q)
+        st["exp_avg_sq_absmax"].copy_(a)
+
+
+# --------------------------------------------------------------------------
+# fp32-state step (reference CAMECUDA._step_param_generic)
+# --------------------------------------------------------------------------
+def init_fp32_state(shape) -> Dict[str, object]:
+    """Reference CAMECUDA.py:83-103 (state keys of the fp32-state mode)."""
+    shape = tuple(int(s) for s in shape)
+    st: Dict[str, object] = {"step": 0, "_mode": "cudafp", "factored": len(shape) >= 2}
+    st["exp_avg"] = torch.zeros(shape, dtype=torch.float32)
+    if st["factored"]:
+        st["exp_avg_sq_row"] = torch.zeros(shape[:-1], dtype=torch.float32)
+        st["exp_avg_sq_col"] = torch.zeros(shape[:-2] + shape[-1:], dtype=torch.float32)
+        st["exp_avg_res_row"] = torch.zeros(shape[:-1], dtype=torch.float32)
+        st["exp_avg_res_col"] = torch.zeros(shape[:-2] + shape[-1:], dtype=torch.float32)
+    else:
+        st["exp_avg_sq"] = torch.zeros(shape, dtype=torch.float32)
+    return st
+
+
+@torch.no_grad()
+def fp32_state_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *, beta1: float, beta2: float,
+                    beta3: float, eps0: float, eps1: float, lr: float, clip_threshold: float,
+                    weight_decay: float) -> None:
+    """Reference CAMECUDA.py:275-326 (generic fp32-state step), same op order."""
+    st["step"] += 1
+    if grad.dtype in (torch.float16, torch.bfloat16):
+        grad = grad.float()
+    m = st["exp_avg"]
+    upd = (grad ** 2) + eps0
+    if st["factored"]:
+        row, col = st["exp_avg_sq_row"], st["exp_avg_sq_col"]
+        row.mul_(beta2).add_(upd.mean(dim=-1), alpha=1.0 - beta2)
+        col.mul_(beta2).add_(upd.mean(dim=-2), alpha=1.0 - beta2)
+        upd = _approx_sq_grad(row, col)
+        upd.mul_(grad)
+    else:
+        sq = st["exp_avg_sq"]
+        sq.mul_(beta2).add_(upd, alpha=1.0 - beta2)
+        upd = sq.clamp_min_(1e-30).rsqrt().mul_(grad)
+    upd.div_((_rms(upd) / clip_threshold).clamp_(min=1.0))
+    m.mul_(beta1).add_(upd, alpha=1.0 - beta1)
+    if st["factored"]:
+        rrow, rcol = st["exp_avg_res_row"], st["exp_avg_res_col"]
+        res = (upd - m) ** 2 + eps1
+        rrow.mul_(beta3).add_(res.mean(dim=-1), alpha=1.0 - beta3)
+        rcol.mul_(beta3).add_(res.mean(dim=-2), alpha=1.0 - beta3)
+        step_dir = _approx_sq_grad(rrow, rcol).mul_(m)
+    else:
+        step_dir = m
+    if weight_decay != 0.0:
+        p.add_(p, alpha=-weight_decay * lr)
+    p.add_(step_dir, alpha=-lr)
