@@ -1,0 +1,757 @@
+// libcame8: MI355X (gfx950) CAME 8-bit optimizer step behind a C ABI (include/came8.h).
+//
+// Host side: validates the tensor list, builds a launch plan (per-tensor
+// descriptors with scratch pointers inside the caller's workspace, work lists
+// grouped by kernel variant), uploads it into the head of the workspace when
+// it changed, and enqueues the multi-tensor launch chain on the caller's
+// stream.  No host synchronisation, no allocation, no memset.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/came8.h"
+#include "came8_kernels.h"
+
+using namespace came8;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x, size_t a = kAlign) { return (x + a - 1) / a * a; }
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Rows per band: about 512K elements per workgroup work item, whole rows, at most 256 rows (so a
+// column partial sums at most 256 values before the fp64 sum across bands).
+int64_t band_rows(int64_t R, int64_t C, bool multiseg) {
+  (void)multiseg;
+  int64_t rb = std::max<int64_t>(1, (int64_t(1) << 19) / std::max<int64_t>(C, 1));
+  rb = std::min<int64_t>(rb, kMaxBandRows);
+  return std::min<int64_t>(rb, R);
+}
+
+int elem_size(int dt) { return dt == CAME8_F32 ? 4 : 2; }
+
+float round_to_bf16(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return f;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  float r;
+  std::memcpy(&r, &u, 4);
+  return r;
+}
+
+float round_to_f16(float f) { return float(_Float16(f)); }
+
+// Kernel-variant keys.
+struct BandKey {
+  int gdt, V, K;
+  bool operator<(const BandKey& o) const {
+    return std::tie(gdt, V, K) < std::tie(o.gdt, o.V, o.K);
+  }
+};
+struct TypeKey {
+  int pdt, gdt;
+  bool operator<(const TypeKey& o) const { return std::tie(pdt, gdt) < std::tie(o.pdt, o.gdt); }
+};
+
+struct WorkList {
+  std::vector<int32_t> tids;
+  std::vector<int64_t> wstart;  // prefix of work items, size tids+1
+  size_t tids_off = 0, wstart_off = 0;  // byte offsets inside the plan blob
+  int64_t total() const { return wstart.empty() ? 0 : wstart.back(); }
+};
+
+struct Plan {
+  std::vector<DevTensor> dev;
+  std::map<BandKey, WorkList> band;      // P1 / P2
+  std::map<TypeKey, WorkList> upd;       // P3 (fast block sizes)
+  std::map<TypeKey, WorkList> vecB;      // 1-D pass B (fast block sizes)
+  std::map<int, WorkList> vecA;          // 1-D pass A, by grad type
+  std::map<TypeKey, WorkList> generic;   // P3 / B for other block sizes (per quantisation block)
+  std::map<int, WorkList> refnorm;       // parity-mode clip, by grad type
+  WorkList rowmean;                      // F1a / F2a (per matrix)
+  WorkList factor;                       // F1b / F2b (per state block)
+  size_t plan_bytes = 0;
+  size_t total_bytes = 0;
+  std::vector<uint8_t> blob;
+};
+
+void add_item(WorkList& wl, int32_t tid, int64_t count) {
+  if (wl.wstart.empty()) wl.wstart.push_back(0);
+  wl.tids.push_back(tid);
+  wl.wstart.push_back(wl.wstart.back() + count);
+}
+
+bool fast_block(int B) { return B >= 8 && B <= kTile && (B & (B - 1)) == 0; }
+
+int log2_or_minus1(int B) {
+  if (B <= 0 || (B & (B - 1)) != 0) return -1;
+  int l = 0;
+  while ((1 << l) < B) ++l;
+  return l;
+}
+
+// Choose (V, K) for the band passes of a factored tensor.
+void band_variant(const came8_tensor& t, int64_t C, int& V, int& K, bool& multiseg) {
+  const int vw = t.grad_dtype == CAME8_F32 ? 4 : 8;
+  const bool aligned = (C % vw == 0) && (reinterpret_cast<uintptr_t>(t.grad) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(t.exp_avg_q) % vw == 0);
+  V = aligned ? vw : 1;
+  const int64_t chunks = ceil_div(C, V);
+  static const int kv[] = {1, 2, 4, 8};
+  static const int k1[] = {1, 2, 4, 8, 16, 32};
+  const int* ks = V > 1 ? kv : k1;
+  const int nk = V > 1 ? 4 : 6;
+  for (int i = 0; i < nk; ++i) {
+    if (int64_t(kThreads) * ks[i] >= chunks) {
+      K = ks[i];
+      multiseg = false;
+      return;
+    }
+  }
+  K = ks[nk - 1];
+  multiseg = true;
+}
+
+int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refnorm, char* ws_base, Plan& plan) {
+  (void)flags_refnorm;
+  if (n < 0) return fail(CAME8_EINVAL, "came8: n_tensors must be >= 0");
+  if (n > 0 && ts == nullptr) return fail(CAME8_EINVAL, "came8: tensors is NULL");
+  if (B <= 0) return fail(CAME8_EINVAL, "came8: block_size must be > 0, got " + std::to_string(B));
+  plan.dev.assign(n, DevTensor{});
+  // --- scratch layout (after the plan blob; offsets relative to the scratch start) ---
+  std::vector<size_t> scr_off(n, 0);
+  size_t scr = 0;
+  for (int i = 0; i < n; ++i) {
+    const came8_tensor& t = ts[i];
+    const std::string who = "came8: tensor " + std::to_string(i) + ": ";
+    if (!t.param || !t.grad || !t.exp_avg_q || !t.exp_avg_absmax || !t.row_q || !t.row_absmax)
+      return fail(CAME8_EINVAL, who + "null pointer");
+    for (int dt : {t.param_dtype, t.grad_dtype})
+      if (dt != CAME8_F32 && dt != CAME8_BF16 && dt != CAME8_F16) return fail(CAME8_EINVAL, who + "unsupported dtype");
+    if (t.prefix < 1 || t.rows < 1 || t.cols < 1) return fail(CAME8_EINVAL, who + "empty or negative shape");
+    if (!t.factored && (t.prefix != 1 || t.rows != 1)) return fail(CAME8_EINVAL, who + "1-D tensors take prefix = rows = 1");
+    if (t.factored && (!t.col_q || !t.col_absmax)) return fail(CAME8_EINVAL, who + "null column state");
+    DevTensor& d = plan.dev[i];
+    d.p = t.param;
+    d.g = t.grad;
+    d.mq = t.exp_avg_q;
+    d.ma = t.exp_avg_absmax;
+    d.rq = t.row_q;
+    d.ra = t.row_absmax;
+    d.cq = t.col_q;
+    d.ca = t.col_absmax;
+    d.P = t.prefix;
+    d.R = t.rows;
+    d.C = t.cols;
+    d.N = t.prefix * t.rows * t.cols;
+    d.nbm = std::max<int64_t>(1, ceil_div(d.N, B));
+    d.factored = t.factored ? 1 : 0;
+    const uintptr_t pp = reinterpret_cast<uintptr_t>(t.param), gp = reinterpret_cast<uintptr_t>(t.grad),
+                    mp = reinterpret_cast<uintptr_t>(t.exp_avg_q);
+    d.vec_ok = (pp % 16 == 0 && gp % 16 == 0 && mp % 8 == 0) ? 1 : 0;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+      const size_t o = off;
+      off += align_up(bytes);
+      return o;
+    };
+    struct Offs {
+      size_t Rn, rfac, RRn, rrfac, Cn, cfac, CRn, crfac, pU, pW, pR, rm, rmr, clipp, clip;
+    } o{};
+    if (t.factored) {
+      int V, K;
+      bool ms;
+      band_variant(t, d.C, V, K, ms);
+      d.rb = band_rows(d.R, d.C, ms);
+      d.nbands = ceil_div(d.R, d.rb);
+      d.nbr = std::max<int64_t>(1, ceil_div(d.P * d.R, B));
+      d.nbc = std::max<int64_t>(1, ceil_div(d.P * d.C, B));
+      d.nclip = d.nbc;
+      const size_t pr = size_t(d.P * d.R) * 4, pc = size_t(d.P * d.C) * 4;
+      const size_t part = size_t(d.P * d.nbands * d.C) * 4;
+      o.Rn = take(pr); o.rfac = take(pr); o.RRn = take(pr); o.rrfac = take(pr);
+      o.Cn = take(pc); o.cfac = take(pc); o.CRn = take(pc); o.crfac = take(pc);
+      o.pU = take(part); o.pW = take(part); o.pR = take(part);
+      o.rm = take(size_t(d.P) * 4); o.rmr = take(size_t(d.P) * 4);
+      o.clipp = take(size_t(d.nclip) * 8);
+      o.clip = take(4);
+    } else {
+      d.rb = 1;
+      d.nbands = 1;
+      d.nbr = d.nbm;
+      d.nbc = 0;
+      d.nclip = ceil_div(d.N, kTile);
+      o.clipp = take(size_t(d.nclip) * 8);
+      o.clip = take(4);
+    }
+    scr_off[i] = scr;
+    // store offsets temporarily as integers in the pointer fields (rebased below)
+    auto at = [&](size_t x) { return reinterpret_cast<float*>(scr + x); };
+    if (t.factored) {
+      d.Rn = at(o.Rn); d.rfac = at(o.rfac); d.RRn = at(o.RRn); d.rrfac = at(o.rrfac);
+      d.Cn = at(o.Cn); d.cfac = at(o.cfac); d.CRn = at(o.CRn); d.crfac = at(o.crfac);
+      d.partU = at(o.pU); d.partW = at(o.pW); d.partRes = at(o.pR);
+      d.rm = at(o.rm); d.rmr = at(o.rmr);
+    }
+    d.clip_part = reinterpret_cast<double*>(scr + o.clipp);
+    d.clip = at(o.clip);
+    scr += off;
+  }
+
+  // --- work lists ---
+  const bool fastB = fast_block(B);
+  for (int i = 0; i < n; ++i) {
+    const came8_tensor& t = ts[i];
+    const DevTensor& d = plan.dev[i];
+    const TypeKey tk{t.param_dtype, t.grad_dtype};
+    if (t.factored) {
+      int V, K;
+      bool ms;
+      band_variant(t, d.C, V, K, ms);
+      add_item(plan.band[BandKey{t.grad_dtype, V, K}], i, d.P * d.nbands);
+      add_item(plan.rowmean, i, d.P);
+      add_item(plan.factor, i, d.nbr + d.nbc);
+      if (fastB) add_item(plan.upd[tk], i, ceil_div(d.N, kTile));
+    } else {
+      add_item(plan.vecA[t.grad_dtype], i, d.nclip);
+      if (fastB) add_item(plan.vecB[tk], i, ceil_div(d.N, kTile));
+    }
+    if (!fastB) add_item(plan.generic[tk], i, d.nbm);
+    add_item(plan.refnorm[t.grad_dtype], i, 1);
+  }
+
+  // --- blob: DevTensor[n] then every work list (tids, wstart) ---
+  size_t off = align_up(sizeof(DevTensor) * size_t(n), 16);
+  auto place = [&](WorkList& wl) {
+    wl.tids_off = off;
+    off = align_up(off + wl.tids.size() * 4, 16);
+    wl.wstart_off = off;
+    off = align_up(off + wl.wstart.size() * 8, 16);
+  };
+  for (auto& kv : plan.band) place(kv.second);
+  for (auto& kv : plan.upd) place(kv.second);
+  for (auto& kv : plan.vecB) place(kv.second);
+  for (auto& kv : plan.vecA) place(kv.second);
+  for (auto& kv : plan.generic) place(kv.second);
+  for (auto& kv : plan.refnorm) place(kv.second);
+  place(plan.rowmean);
+  place(plan.factor);
+  plan.plan_bytes = align_up(off);
+  plan.total_bytes = plan.plan_bytes + scr;
+
+  if (ws_base != nullptr) {
+    char* scr_base = ws_base + plan.plan_bytes;
+    auto rebase = [&](auto*& ptr) {
+      using P = std::remove_reference_t<decltype(ptr)>;
+      ptr = reinterpret_cast<P>(scr_base + reinterpret_cast<uintptr_t>(ptr));
+    };
+    for (int i = 0; i < n; ++i) {
+      DevTensor& d = plan.dev[i];
+      if (d.factored) {
+        rebase(d.Rn); rebase(d.rfac); rebase(d.RRn); rebase(d.rrfac);
+        rebase(d.Cn); rebase(d.cfac); rebase(d.CRn); rebase(d.crfac);
+        rebase(d.partU); rebase(d.partW); rebase(d.partRes);
+        rebase(d.rm); rebase(d.rmr);
+      }
+      rebase(d.clip_part);
+      rebase(d.clip);
+    }
+    plan.blob.assign(plan.plan_bytes, 0);
+    std::memcpy(plan.blob.data(), plan.dev.data(), sizeof(DevTensor) * size_t(n));
+    auto put = [&](const WorkList& wl) {
+      std::memcpy(plan.blob.data() + wl.tids_off, wl.tids.data(), wl.tids.size() * 4);
+      std::memcpy(plan.blob.data() + wl.wstart_off, wl.wstart.data(), wl.wstart.size() * 8);
+    };
+    for (auto& kv : plan.band) put(kv.second);
+    for (auto& kv : plan.upd) put(kv.second);
+    for (auto& kv : plan.vecB) put(kv.second);
+    for (auto& kv : plan.vecA) put(kv.second);
+    for (auto& kv : plan.generic) put(kv.second);
+    for (auto& kv : plan.refnorm) put(kv.second);
+    put(plan.rowmean);
+    put(plan.factor);
+  }
+  return CAME8_OK;
+}
+
+uint64_t fnv1a(const uint8_t* p, size_t n) {
+  uint64_t h = 1469598103934665603ull;
+  for (size_t i = 0; i < n; ++i) {
+    h ^= p[i];
+    h *= 1099511628211ull;
+  }
+  return h;
+}
+
+// Plan uploads per (workspace address, caller's workspace tag).  A tag names one allocation of
+// the workspace by its owner; a freed-and-reallocated workspace at the same address gets a new
+// tag, so a stale entry can never match memory that was reused in between.  Tag 0 never reuses.
+struct CacheEntry {
+  uint64_t hash = 0;
+  size_t bytes = 0;
+  std::vector<uint8_t> keep;  // source of the last upload, alive until `done` has fired
+  hipEvent_t done = nullptr;
+};
+std::mutex g_cache_mu;
+std::map<std::pair<const void*, uint64_t>, CacheEntry> g_cache;
+
+void drop_entry(CacheEntry& ce) {
+  if (ce.done) {
+    (void)hipEventSynchronize(ce.done);
+    (void)hipEventDestroy(ce.done);
+    ce.done = nullptr;
+  }
+  ce.keep.clear();
+  ce.keep.shrink_to_fit();
+}
+
+Hp make_hp(const came8_hparams& h) {
+  Hp hp{};
+  hp.b1 = float(h.beta1);
+  hp.a1 = float(1.0 - h.beta1);
+  hp.b2 = float(h.beta2);
+  hp.a2 = float(1.0 - h.beta2);
+  hp.b3 = float(h.beta3);
+  hp.a3 = float(1.0 - h.beta3);
+  hp.eps0 = float(h.eps0);
+  hp.eps1 = float(h.eps1);
+  hp.awd = float(-h.weight_decay * h.lr);
+  hp.awd_bf16 = round_to_bf16(hp.awd);
+  hp.awd_f16 = round_to_f16(hp.awd);
+  hp.alr = float(-h.lr);
+  hp.thr = float(h.clip_threshold);
+  hp.wd = h.weight_decay != 0.0 ? 1 : 0;
+  hp.B = h.block_size;
+  hp.log2B = log2_or_minus1(h.block_size);
+  return hp;
+}
+
+// ---------------------------------------------------------------------------
+// kernel-variant dispatch
+// ---------------------------------------------------------------------------
+template <typename TG>
+using BandFn = void (*)(const DevTensor*, const int32_t*, const int64_t*, int, Hp);
+
+template <typename TG, int V>
+BandFn<TG> band_fn_k(bool pass2, int K) {
+  switch (K) {
+    case 1: return pass2 ? k_fact_pass2<TG, V, 1> : k_fact_pass1<TG, V, 1>;
+    case 2: return pass2 ? k_fact_pass2<TG, V, 2> : k_fact_pass1<TG, V, 2>;
+    case 4: return pass2 ? k_fact_pass2<TG, V, 4> : k_fact_pass1<TG, V, 4>;
+    case 8: return pass2 ? k_fact_pass2<TG, V, 8> : k_fact_pass1<TG, V, 8>;
+    default: break;
+  }
+  if constexpr (V == 1) {
+    if (K == 16) return pass2 ? k_fact_pass2<TG, 1, 16> : k_fact_pass1<TG, 1, 16>;
+    if (K == 32) return pass2 ? k_fact_pass2<TG, 1, 32> : k_fact_pass1<TG, 1, 32>;
+  }
+  return nullptr;
+}
+
+template <typename TG, int VW>
+BandFn<TG> band_fn(bool pass2, int V, int K) {
+  return V == 1 ? band_fn_k<TG, 1>(pass2, K) : band_fn_k<TG, VW>(pass2, K);
+}
+
+using GenFn = void (*)(const DevTensor*, const int32_t*, const int64_t*, int, Hp);
+
+#define CAME8_TYPE_SWITCH2(KERNEL, pdt, gdt, out)                                       \
+  do {                                                                                  \
+    out = nullptr;                                                                      \
+    if (pdt == CAME8_F32 && gdt == CAME8_F32) out = KERNEL<F32, F32>;                   \
+    if (pdt == CAME8_F32 && gdt == CAME8_BF16) out = KERNEL<F32, BF16>;                 \
+    if (pdt == CAME8_F32 && gdt == CAME8_F16) out = KERNEL<F32, F16>;                   \
+    if (pdt == CAME8_BF16 && gdt == CAME8_F32) out = KERNEL<BF16, F32>;                 \
+    if (pdt == CAME8_BF16 && gdt == CAME8_BF16) out = KERNEL<BF16, BF16>;               \
+    if (pdt == CAME8_BF16 && gdt == CAME8_F16) out = KERNEL<BF16, F16>;                 \
+    if (pdt == CAME8_F16 && gdt == CAME8_F32) out = KERNEL<F16, F32>;                   \
+    if (pdt == CAME8_F16 && gdt == CAME8_BF16) out = KERNEL<F16, BF16>;                 \
+    if (pdt == CAME8_F16 && gdt == CAME8_F16) out = KERNEL<F16, F16>;                   \
+  } while (0)
+
+#define CAME8_TYPE_SWITCH1(KERNEL, gdt, out)           \
+  do {                                                 \
+    out = nullptr;                                     \
+    if (gdt == CAME8_F32) out = KERNEL<F32>;           \
+    if (gdt == CAME8_BF16) out = KERNEL<BF16>;         \
+    if (gdt == CAME8_F16) out = KERNEL<F16>;           \
+  } while (0)
+
+constexpr int64_t kMaxGrid = 16384;
+
+unsigned grid_for(int64_t work, int64_t per_block = 1) {
+  const int64_t blocks = ceil_div(std::max<int64_t>(work, 1), per_block);
+  return unsigned(std::min<int64_t>(blocks, kMaxGrid));
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(CAME8_EHIP, std::string("came8: launch of ") + what + " failed: " + hipGetErrorString(e));
+  return CAME8_OK;
+}
+
+// ---------------------------------------------------------------------------
+// optional per-launch device timing (HIP events on the launch stream)
+// ---------------------------------------------------------------------------
+const char* const kPhaseNames[] = {"pass1", "vec_passA", "row_mean", "factor_blocks", "clip", "clip_refnorm",
+                                   "pass2", "row_mean_res", "factor_blocks_res", "pass3", "vec_passB",
+                                   "generic_update"};
+constexpr int kNumPhases = sizeof(kPhaseNames) / sizeof(kPhaseNames[0]);
+enum Phase { PH_PASS1, PH_VECA, PH_ROWMEAN, PH_FACTOR, PH_CLIP, PH_CLIP_REF, PH_PASS2, PH_ROWMEAN_RES,
+             PH_FACTOR_RES, PH_PASS3, PH_VECB, PH_GENERIC };
+
+struct Pending {
+  int phase;
+  hipEvent_t a, b;
+  double bytes;
+};
+struct Profiler {
+  std::mutex mu;
+  bool on = false;
+  std::vector<Pending> pending;
+  std::vector<hipEvent_t> pool;
+  int64_t launches[kNumPhases] = {};
+  double total_ms[kNumPhases] = {};
+  double bytes[kNumPhases] = {};
+};
+Profiler& prof() {
+  static Profiler p;
+  return p;
+}
+
+hipEvent_t take_event(Profiler& p) {
+  if (!p.pool.empty()) {
+    hipEvent_t e = p.pool.back();
+    p.pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Records an event before the launch and, in the destructor, after it.
+struct PhaseTimer {
+  hipEvent_t a = nullptr, b = nullptr;
+  int phase;
+  double bytes;
+  hipStream_t stream;
+  bool active = false;
+  PhaseTimer(int ph, double alg_bytes, hipStream_t s) : phase(ph), bytes(alg_bytes), stream(s) {
+    Profiler& p = prof();
+    std::lock_guard<std::mutex> lk(p.mu);
+    if (!p.on) return;
+    a = take_event(p);
+    b = take_event(p);
+    if (a && b && hipEventRecord(a, stream) == hipSuccess) active = true;
+  }
+  ~PhaseTimer() {
+    if (!active) return;
+    Profiler& p = prof();
+    std::lock_guard<std::mutex> lk(p.mu);
+    if (hipEventRecord(b, stream) == hipSuccess) p.pending.push_back(Pending{phase, a, b, bytes});
+  }
+};
+
+double elem_bytes(int dt) { return dt == CAME8_F32 ? 4.0 : 2.0; }
+
+// Algorithmic bytes of one launch: every operand the kernel must touch, counted once.
+double alg_bytes(const Plan& plan, const WorkList& wl, const came8_tensor* ts, int phase) {
+  double tot = 0.0;
+  for (int32_t i : wl.tids) {
+    const DevTensor& d = plan.dev[i];
+    const double N = double(d.N), sg = elem_bytes(ts[i].grad_dtype), sp = elem_bytes(ts[i].param_dtype);
+    const double nbm = double(d.nbm);
+    switch (phase) {
+      case PH_PASS1: tot += N * sg + double(d.P * d.R) + 4.0 * double(d.nbr); break;              // g, old row codes
+      case PH_PASS2: tot += N * (sg + 1.0) + 4.0 * nbm; break;                                     // g, m codes
+      case PH_PASS3: tot += N * (sg + 2.0 * sp + 2.0) + 8.0 * nbm; break;                          // g, p rw, m rw
+      case PH_VECA: tot += N * (sg + 1.0) + 4.0 * nbm; break;                                      // g, v codes
+      case PH_VECB: tot += N * (sg + 2.0 * sp + 4.0) + 16.0 * nbm; break;                          // g, p, m, v
+      case PH_GENERIC:
+        tot += d.factored ? N * (sg + 2.0 * sp + 2.0) + 8.0 * nbm : N * (sg + 2.0 * sp + 4.0) + 16.0 * nbm;
+        break;
+      case PH_FACTOR: case PH_FACTOR_RES:  // one row + one column state: codes rw, scales rw
+        tot += 2.0 * double(d.P * d.R + d.P * d.C) + 8.0 * double(d.nbr + d.nbc);
+        break;
+      default: break;
+    }
+  }
+  return tot;
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+const char* came8_version(void) { return "came8-mi355x 0.1 (gfx950)"; }
+int came8_abi_version(void) { return CAME8_ABI_VERSION; }
+const char* came8_last_error(void) { return g_last_error.c_str(); }
+
+int came8_workspace_size(const came8_tensor* tensors, int32_t n_tensors, int32_t block_size, size_t* bytes) {
+  if (!bytes) return fail(CAME8_EINVAL, "came8_workspace_size: bytes is NULL");
+  Plan plan;
+  const int rc = build_plan(tensors, n_tensors, block_size, 0, nullptr, plan);
+  if (rc != CAME8_OK) return rc;
+  *bytes = plan.total_bytes;
+  return CAME8_OK;
+}
+
+int came8_release_workspace(const void* workspace) {
+  std::lock_guard<std::mutex> lk(g_cache_mu);
+  for (auto it = g_cache.begin(); it != g_cache.end();) {
+    if (it->first.first == workspace) {
+      drop_entry(it->second);
+      it = g_cache.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  return CAME8_OK;
+}
+
+int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hparams* hp_in, void* workspace,
+               size_t workspace_bytes, uint64_t workspace_tag, void* stream_ptr) {
+  if (!hp_in) return fail(CAME8_EINVAL, "came8_step: hparams is NULL");
+  if (n_tensors == 0) return CAME8_OK;
+  const came8_hparams& h = *hp_in;
+  if (!(h.lr > 0.0)) return fail(CAME8_EINVAL, "came8_step: lr must be > 0");
+  if (!(h.clip_threshold > 0.0)) return fail(CAME8_EINVAL, "came8_step: clip_threshold must be > 0");
+  if (!workspace) return fail(CAME8_EINVAL, "came8_step: workspace is NULL");
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  Plan plan;
+  int rc = build_plan(tensors, n_tensors, h.block_size, 0, static_cast<char*>(workspace), plan);
+  if (rc != CAME8_OK) return rc;
+  if (workspace_bytes < plan.total_bytes)
+    return fail(CAME8_ESPACE, "came8_step: workspace has " + std::to_string(workspace_bytes) + " bytes, needs " +
+                                  std::to_string(plan.total_bytes));
+  {
+    const uint64_t hsh = fnv1a(plan.blob.data(), plan.blob.size());
+    std::lock_guard<std::mutex> lk(g_cache_mu);
+    const auto key = std::make_pair(static_cast<const void*>(workspace), workspace_tag);
+    CacheEntry& ce = g_cache[key];
+    if (workspace_tag == 0 || ce.hash != hsh || ce.bytes != plan.blob.size()) {
+      drop_entry(ce);  // the previous upload from this entry has completed before its source is replaced
+      ce.keep = std::move(plan.blob);
+      hipError_t e = hipMemcpyAsync(workspace, ce.keep.data(), ce.keep.size(), hipMemcpyHostToDevice, stream);
+      if (e == hipSuccess) e = hipEventCreateWithFlags(&ce.done, hipEventDisableTiming);
+      if (e == hipSuccess) e = hipEventRecord(ce.done, stream);
+      if (e != hipSuccess) {
+        drop_entry(ce);
+        g_cache.erase(key);
+        return fail(CAME8_EHIP, std::string("came8_step: plan upload failed: ") + hipGetErrorString(e));
+      }
+      ce.hash = hsh;
+      ce.bytes = ce.keep.size();
+    }
+  }
+  const Hp hp = make_hp(h);
+  const char* base = static_cast<const char*>(workspace);
+  const DevTensor* dT = reinterpret_cast<const DevTensor*>(base);
+  auto tids = [&](const WorkList& wl) { return reinterpret_cast<const int32_t*>(base + wl.tids_off); };
+  auto wst = [&](const WorkList& wl) { return reinterpret_cast<const int64_t*>(base + wl.wstart_off); };
+  const dim3 blk(kThreads);
+  const bool refnorm = (h.flags & CAME8_FLAG_REFERENCE_NORM) != 0;
+  const bool fastB = fast_block(h.block_size);
+
+  // ---- P1 and 1-D pass A ----
+  for (auto& kv : plan.band) {
+    const BandKey& k = kv.first;
+    const WorkList& wl = kv.second;
+    void (*fn)(const DevTensor*, const int32_t*, const int64_t*, int, Hp) = nullptr;
+    if (k.gdt == CAME8_F32) fn = band_fn<F32, 4>(false, k.V, k.K);
+    if (k.gdt == CAME8_BF16) fn = band_fn<BF16, 8>(false, k.V, k.K);
+    if (k.gdt == CAME8_F16) fn = band_fn<F16, 8>(false, k.V, k.K);
+    if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
+    { PhaseTimer pt(PH_PASS1, alg_bytes(plan, wl, tensors, PH_PASS1), stream);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+    if ((rc = check_launch("pass1")) != CAME8_OK) return rc; }
+  }
+  for (auto& kv : plan.vecA) {
+    const WorkList& wl = kv.second;
+    GenFn fn;
+    CAME8_TYPE_SWITCH1(k_vec_passA, kv.first, fn);
+    { PhaseTimer pt(PH_VECA, alg_bytes(plan, wl, tensors, PH_VECA), stream);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+    if ((rc = check_launch("vec_passA")) != CAME8_OK) return rc; }
+  }
+  const bool any_fact = !plan.rowmean.tids.empty();
+  if (any_fact) {
+    const WorkList& rm = plan.rowmean;
+    { PhaseTimer pt(PH_ROWMEAN, alg_bytes(plan, rm, tensors, PH_ROWMEAN), stream);
+    hipLaunchKernelGGL(k_row_mean<false>, dim3(grid_for(rm.total(), 4)), blk, 0, stream, dT, tids(rm), wst(rm),
+                       int(rm.tids.size()));
+    if ((rc = check_launch("row_mean")) != CAME8_OK) return rc; }
+    const WorkList& fb = plan.factor;
+    { PhaseTimer pt(PH_FACTOR, alg_bytes(plan, fb, tensors, PH_FACTOR), stream);
+    hipLaunchKernelGGL(k_factor_blocks<false>, dim3(grid_for(fb.total())), blk, 0, stream, dT, tids(fb), wst(fb),
+                       int(fb.tids.size()), hp);
+    if ((rc = check_launch("factor_blocks")) != CAME8_OK) return rc; }
+  }
+  // ---- clip divisor ----
+  if (refnorm) {
+    for (auto& kv : plan.refnorm) {
+      const WorkList& wl = kv.second;
+      void (*fn)(const DevTensor*, const int32_t*, int, Hp) = nullptr;
+      CAME8_TYPE_SWITCH1(k_clip_refnorm, kv.first, fn);
+      { PhaseTimer pt(PH_CLIP_REF, alg_bytes(plan, wl, tensors, PH_CLIP_REF), stream);
+    hipLaunchKernelGGL(fn, dim3(grid_for(int64_t(wl.tids.size()))), blk, 0, stream, dT, tids(wl), int(wl.tids.size()), hp);
+      if ((rc = check_launch("clip_refnorm")) != CAME8_OK) return rc; }
+    }
+  } else {
+    PhaseTimer pt(PH_CLIP, 0.0, stream);
+    hipLaunchKernelGGL(k_clip, dim3(grid_for(n_tensors)), blk, 0, stream, dT, int(n_tensors), hp);
+    if ((rc = check_launch("clip")) != CAME8_OK) return rc;
+  }
+  // ---- P2, residual factors ----
+  if (any_fact) {
+    for (auto& kv : plan.band) {
+      const BandKey& k = kv.first;
+      const WorkList& wl = kv.second;
+      void (*fn)(const DevTensor*, const int32_t*, const int64_t*, int, Hp) = nullptr;
+      if (k.gdt == CAME8_F32) fn = band_fn<F32, 4>(true, k.V, k.K);
+      if (k.gdt == CAME8_BF16) fn = band_fn<BF16, 8>(true, k.V, k.K);
+      if (k.gdt == CAME8_F16) fn = band_fn<F16, 8>(true, k.V, k.K);
+      { PhaseTimer pt(PH_PASS2, alg_bytes(plan, wl, tensors, PH_PASS2), stream);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      if ((rc = check_launch("pass2")) != CAME8_OK) return rc; }
+    }
+    const WorkList& rm = plan.rowmean;
+    { PhaseTimer pt(PH_ROWMEAN_RES, alg_bytes(plan, rm, tensors, PH_ROWMEAN_RES), stream);
+    hipLaunchKernelGGL(k_row_mean<true>, dim3(grid_for(rm.total(), 4)), blk, 0, stream, dT, tids(rm), wst(rm),
+                       int(rm.tids.size()));
+    if ((rc = check_launch("row_mean_res")) != CAME8_OK) return rc; }
+    const WorkList& fb = plan.factor;
+    { PhaseTimer pt(PH_FACTOR_RES, alg_bytes(plan, fb, tensors, PH_FACTOR_RES), stream);
+    hipLaunchKernelGGL(k_factor_blocks<true>, dim3(grid_for(fb.total())), blk, 0, stream, dT, tids(fb), wst(fb),
+                       int(fb.tids.size()), hp);
+    if ((rc = check_launch("factor_blocks_res")) != CAME8_OK) return rc; }
+  }
+  // ---- P3 and 1-D pass B ----
+  if (fastB) {
+    for (auto& kv : plan.upd) {
+      const WorkList& wl = kv.second;
+      GenFn fn;
+      CAME8_TYPE_SWITCH2(k_fact_pass3, kv.first.pdt, kv.first.gdt, fn);
+      { PhaseTimer pt(PH_PASS3, alg_bytes(plan, wl, tensors, PH_PASS3), stream);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      if ((rc = check_launch("pass3")) != CAME8_OK) return rc; }
+    }
+    for (auto& kv : plan.vecB) {
+      const WorkList& wl = kv.second;
+      GenFn fn;
+      CAME8_TYPE_SWITCH2(k_vec_passB, kv.first.pdt, kv.first.gdt, fn);
+      { PhaseTimer pt(PH_VECB, alg_bytes(plan, wl, tensors, PH_VECB), stream);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      if ((rc = check_launch("vec_passB")) != CAME8_OK) return rc; }
+    }
+  } else {
+    for (auto& kv : plan.generic) {
+      const WorkList& wl = kv.second;
+      GenFn fn;
+      CAME8_TYPE_SWITCH2(k_generic_update, kv.first.pdt, kv.first.gdt, fn);
+      { PhaseTimer pt(PH_GENERIC, alg_bytes(plan, wl, tensors, PH_GENERIC), stream);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      if ((rc = check_launch("generic_update")) != CAME8_OK) return rc; }
+    }
+  }
+  return CAME8_OK;
+}
+
+int came8_profile_enable(int32_t on) {
+  Profiler& p = prof();
+  std::lock_guard<std::mutex> lk(p.mu);
+  p.on = on != 0;
+  return CAME8_OK;
+}
+
+int came8_profile_read(came8_phase_stat* out, int32_t max_phases, int32_t* n_phases, int32_t reset) {
+  if (!n_phases) return fail(CAME8_EINVAL, "came8_profile_read: n_phases is NULL");
+  Profiler& p = prof();
+  std::lock_guard<std::mutex> lk(p.mu);
+  for (const Pending& q : p.pending) {
+    float ms = 0.0f;
+    if (hipEventSynchronize(q.b) != hipSuccess || hipEventElapsedTime(&ms, q.a, q.b) != hipSuccess)
+      return fail(CAME8_EHIP, "came8_profile_read: event query failed");
+    p.launches[q.phase] += 1;
+    p.total_ms[q.phase] += double(ms);
+    p.bytes[q.phase] += q.bytes;
+    p.pool.push_back(q.a);
+    p.pool.push_back(q.b);
+  }
+  p.pending.clear();
+  int32_t k = 0;
+  for (int ph = 0; ph < kNumPhases; ++ph) {
+    if (p.launches[ph] == 0) continue;
+    if (out && k < max_phases) {
+      came8_phase_stat& o = out[k];
+      std::memset(&o, 0, sizeof(o));
+      std::snprintf(o.name, sizeof(o.name), "%s", kPhaseNames[ph]);
+      o.launches = p.launches[ph];
+      o.total_ms = p.total_ms[ph];
+      o.alg_bytes = p.bytes[ph];
+    }
+    ++k;
+  }
+  *n_phases = k;
+  if (reset) {
+    for (int ph = 0; ph < kNumPhases; ++ph) {
+      p.launches[ph] = 0;
+      p.total_ms[ph] = 0.0;
+      p.bytes[ph] = 0.0;
+    }
+  }
+  return CAME8_OK;
+}
+
+int came8_quantize_blockwise(const float* x, int64_t n, int32_t is_signed, int32_t block_size, void* q, float* absmax,
+                             void* stream_ptr) {
+  if (block_size <= 0) return fail(CAME8_EINVAL, "came8_quantize_blockwise: block_size must be > 0");
+  if (n < 0) return fail(CAME8_EINVAL, "came8_quantize_blockwise: n must be >= 0");
+  if (!absmax || (n > 0 && (!x || !q))) return fail(CAME8_EINVAL, "came8_quantize_blockwise: null pointer");
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const int64_t nb = std::max<int64_t>(1, ceil_div(n, block_size));
+  if (is_signed)
+    hipLaunchKernelGGL(k_quantize<true>, dim3(grid_for(nb)), dim3(kThreads), 0, stream, x, n, block_size, nb, q, absmax);
+  else
+    hipLaunchKernelGGL(k_quantize<false>, dim3(grid_for(nb)), dim3(kThreads), 0, stream, x, n, block_size, nb, q, absmax);
+  return check_launch("quantize");
+}
+
+int came8_dequantize_blockwise(const void* q, const float* absmax, int64_t n, int32_t is_signed, int32_t block_size,
+                               float* out, void* stream_ptr) {
+  if (block_size <= 0) return fail(CAME8_EINVAL, "came8_dequantize_blockwise: block_size must be > 0");
+  if (n < 0) return fail(CAME8_EINVAL, "came8_dequantize_blockwise: n must be >= 0");
+  if (n == 0) return CAME8_OK;
+  if (!q || !absmax || !out) return fail(CAME8_EINVAL, "came8_dequantize_blockwise: null pointer");
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  if (is_signed)
+    hipLaunchKernelGGL(k_dequantize<true>, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, stream, q, absmax, n,
+                       block_size, out);
+  else
+    hipLaunchKernelGGL(k_dequantize<false>, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, stream, q, absmax, n,
+                       block_size, out);
+  return check_launch("dequantize");
+}
+
+}  // extern "C"

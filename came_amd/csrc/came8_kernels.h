@@ -1,0 +1,1010 @@
+// Kernels of the CAME 8-bit step (gfx950).  Included once, by came8.hip.
+//
+// One optimizer step over a list of tensors runs as a short chain of
+// multi-tensor launches on one stream (every launch covers all tensors of its
+// kind):
+//
+//   P1  band pass over G of every factored tensor: row sums of g^2+eps0 (whole
+//       rows per workgroup, so the new row state R_i is known locally), column
+//       partial sums of g^2+eps0 and of g^2/R_i per row band.
+//   A   1-D tensors: sum of u^2 per 2048-element tile.
+//   F1a per matrix: mean of the new row state (rm).
+//   F1b row-state blocks: r_i = rsqrt(R_i/rm), uint8 requantisation of R;
+//       column-state blocks: C_j = EMA(mean_i), clamp 1e-30, c_j = rsqrt(C_j),
+//       uint8 requantisation, and the clip numerator  rm * c_j^2 * sum_i g^2/R_i.
+//   CLIP per tensor: update-RMS clip divisor.
+//   P2  band pass over G and the int8 momentum: u, m_new, residual
+//       (u-m)^2+eps1; row sums -> residual row state, column partials.
+//   F2a/F2b residual factors rr_i, cr_j and their uint8 requantisation.
+//   P3  flat pass over whole quantisation blocks: u, m_new, step, weight decay,
+//       parameter write, int8 requantisation of m.
+//   B   1-D tensors: v, u/clip, m, parameter write, int8 + uint8 requantisation.
+//
+// The arithmetic of every element follows the reference's CPU path
+// (came_pytorch/CAME8bitFull.py:1006-1075) operation for operation, with the
+// same roundings (fused multiply-add where torch's CPU kernels fuse, IEEE
+// division and square root, round-half-even).  Reductions use fixed
+// combination orders, so results are identical from run to run.
+#pragma once
+
+#include <type_traits>
+
+#include "came8_device.h"
+
+namespace came8 {
+
+// Per-tensor descriptor in device memory (built by the host plan).
+struct DevTensor {
+  void* p;
+  const void* g;
+  int8_t* mq;     // exp_avg codes [N]
+  float* ma;      // exp_avg absmax [nbm]
+  uint8_t* rq;    // factored: [2][P*R]; 1-D: exp_avg_sq codes [N]
+  float* ra;      // factored: [2][nbr]; 1-D: [nbm]
+  uint8_t* cq;    // [2][P*C]
+  float* ca;      // [2][nbc]
+  int64_t P, R, C, N;
+  int64_t nbr, nbc, nbm;  // absmax blocks of one row state, one col state, exp_avg
+  int64_t nbands;         // row bands per matrix
+  int64_t rb;             // rows per band
+  // scratch (workspace)
+  float* Rn;      // new row state (fp32)           [P*R]
+  float* rfac;    // rsqrt(R/rm)                     [P*R]
+  float* RRn;     // new residual row state          [P*R]
+  float* rrfac;   //                                 [P*R]
+  float* Cn;      // new column state (clamped)      [P*C]
+  float* cfac;    //                                 [P*C]
+  float* CRn;     //                                 [P*C]
+  float* crfac;   //                                 [P*C]
+  float* partU;   // column partials of g^2+eps0     [P*nbands*C]
+  float* partW;   // column partials of g^2/R_i      [P*nbands*C]
+  float* partRes; // column partials of residual     [P*nbands*C]
+  float* rm;      // mean row state per matrix       [P]
+  float* rmr;     // mean residual row state         [P]
+  double* clip_part;  // clip numerator partials     [nclip]
+  float* clip;        // clip divisor                [1]
+  int64_t nclip;
+  int32_t vec_ok;     // p, g, codes 16-byte aligned (flat passes may use vector access)
+  int32_t factored;
+};
+
+// Hyper-parameters as the fp32 constants the reference's CPU ops use.
+struct Hp {
+  float b1, a1, b2, a2, b3, a3;  // beta, (1 - beta) computed in double then rounded
+  float eps0, eps1;
+  float awd;       // -wd*lr rounded to fp32 (fp32 params)
+  float awd_bf16;  // the same rounded to bf16 (torch's reduced-precision add_ alpha)
+  float awd_f16;
+  float alr;       // -lr
+  float thr;       // clip_threshold
+  int32_t wd;      // weight_decay != 0
+  int32_t B;       // quantisation block size
+  int32_t log2B;   // log2(B) if B is a power of two, else -1
+};
+
+__device__ __forceinline__ int64_t blk_of(int64_t e, const Hp& hp) {
+  return hp.log2B >= 0 ? (e >> hp.log2B) : (e / hp.B);
+}
+
+// wstart has n+1 entries, wstart[0] = 0; returns k with wstart[k] <= w < wstart[k+1]
+__device__ __forceinline__ int find_slot(const int64_t* __restrict__ wstart, int n, int64_t w) {
+  int lo = 0, hi = n;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (wstart[mid] <= w) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+template <typename TP>
+__device__ __forceinline__ float wd_alpha(const Hp& hp);
+template <> __device__ __forceinline__ float wd_alpha<F32>(const Hp& hp) { return hp.awd; }
+template <> __device__ __forceinline__ float wd_alpha<BF16>(const Hp& hp) { return hp.awd_bf16; }
+template <> __device__ __forceinline__ float wd_alpha<F16>(const Hp& hp) { return hp.awd_f16; }
+
+// p <- p + (-wd*lr)*p (if wd != 0), rounded to the param type; then p + (-lr)*step, rounded again
+// (reference CAME8bitFull.py:1053-1056).
+template <typename TP>
+__device__ __forceinline__ float param_update(float p, float step, const Hp& hp) {
+  if (hp.wd) p = TP::load(TP::store(fmaf(p, wd_alpha<TP>(hp), p)));
+  return fmaf(step, hp.alr, p);
+}
+
+constexpr int kTile = 2048;  // elements per workgroup tile in the flat passes (8 per thread)
+constexpr int kMaxBandRows = 256;
+
+// ===========================================================================
+// P1 / P2: band passes over whole rows
+// ===========================================================================
+// Thread t owns column chunks t, t+256, ..., t+256*(K-1) of V elements each.
+// When C <= 256*V*K each row is read once and kept in registers between the
+// row reduction and the column accumulation; wider rows are handled in
+// column segments after a first sweep that forms the row sums.
+
+template <int V, int K>
+struct BandShape {
+  static constexpr int kElems = V * K;
+  static constexpr int S = (64 / kElems) < 1 ? 1 : ((64 / kElems) > 16 ? 16 : (64 / kElems));
+};
+
+// Column accumulators: fp64 when a thread owns few columns (short rows, so bands span many rows),
+// fp32 otherwise (bands are at most 256 rows long).
+template <int V, int K>
+using ColAcc = typename std::conditional<(V * K <= 8), double, float>::type;
+
+// Reduce S row partials across the workgroup; red is a [2][16][4] LDS buffer, parity alternates per call.
+template <int S>
+__device__ __forceinline__ void block_row_sums(float (&ps)[S], float (*red)[16][4], int par, float (&tot)[S]) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const float w = wave_sum(ps[s]);
+    if (lane == 0) red[par][s][wid] = w;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < S; ++s) tot[s] = ((red[par][s][0] + red[par][s][1]) + red[par][s][2]) + red[par][s][3];
+}
+
+// ---------------- P1 ----------------
+template <typename TG, int V, int K>
+__global__ __launch_bounds__(kThreads) void k_fact_pass1(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                         const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using GS = typename TG::storage;
+  constexpr int S = BandShape<V, K>::S;
+  __shared__ float red[2][16][4];
+  __shared__ float rowR[kMaxBandRows];
+  const int tid = threadIdx.x;
+  int par = 0;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t local = w - wstart[slot];
+    const int64_t b = local / t.nbands;
+    const int64_t band = local - b * t.nbands;
+    const int64_t R = t.R, C = t.C;
+    const int64_t r0 = band * t.rb;
+    const int64_t r1 = (r0 + t.rb < R) ? (r0 + t.rb) : R;
+    const GS* __restrict__ g = static_cast<const GS*>(t.g) + (b * R) * C;
+    const float fC = float(C);
+    constexpr int64_t segw = int64_t(kThreads) * V * K;
+    const int64_t nseg = (C + segw - 1) / segw;
+    float* __restrict__ pU = t.partU + (b * t.nbands + band) * C;
+    float* __restrict__ pW = t.partW + (b * t.nbands + band) * C;
+
+    if (nseg == 1) {
+      ColAcc<V, K> colU[K][V], colW[K][V];
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int v = 0; v < V; ++v) colU[k][v] = colW[k][v] = 0;
+      for (int64_t r = r0; r < r1; r += S) {
+        float x[S][K][V];
+        float ps[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          ps[s] = 0.0f;
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            const int64_t c0 = (int64_t(tid) + int64_t(k) * kThreads) * V;
+            if (r + s < r1 && c0 < C) {
+              load_vec<TG, V>(g + (r + s) * C + c0, x[s][k]);
+#pragma unroll
+              for (int v = 0; v < V; ++v) ps[s] += x[s][k][v] * x[s][k][v] + hp.eps0;
+            } else {
+#pragma unroll
+              for (int v = 0; v < V; ++v) x[s][k][v] = 0.0f;
+            }
+          }
+        }
+        float tot[S];
+        block_row_sums<S>(ps, red, par, tot);
+        par ^= 1;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          if (r + s < r1) {
+            const int64_t row = b * R + r + s;
+            const float Rold = deq_u8(t.rq[row], t.ra[blk_of(row, hp)]);
+            const float Rnew = fmaf(tot[s] / fC, hp.a2, Rold * hp.b2);
+            if (tid == 0) t.Rn[row] = Rnew;
+            const float invR = 1.0f / Rnew;
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+              const int64_t c0 = (int64_t(tid) + int64_t(k) * kThreads) * V;
+              if (c0 < C) {
+#pragma unroll
+                for (int v = 0; v < V; ++v) {
+                  const float gg = x[s][k][v] * x[s][k][v];
+                  colU[k][v] += ColAcc<V, K>(gg + hp.eps0);
+                  colW[k][v] += ColAcc<V, K>(gg * invR);
+                }
+              }
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int64_t c0 = (int64_t(tid) + int64_t(k) * kThreads) * V;
+        if (c0 < C) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            pU[c0 + v] = float(colU[k][v]);
+            pW[c0 + v] = float(colW[k][v]);
+          }
+        }
+      }
+    } else {
+      // phase A: row sums over all segments
+      for (int64_t r = r0; r < r1; r += S) {
+        float ps[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) ps[s] = 0.0f;
+        for (int64_t seg = 0; seg < nseg; ++seg) {
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+              const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * kThreads) * V;
+              if (r + s < r1 && c0 < C) {
+                float x[V];
+                load_vec<TG, V>(g + (r + s) * C + c0, x);
+#pragma unroll
+                for (int v = 0; v < V; ++v) ps[s] += x[v] * x[v] + hp.eps0;
+              }
+            }
+          }
+        }
+        float tot[S];
+        block_row_sums<S>(ps, red, par, tot);
+        par ^= 1;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          if (r + s < r1) {
+            const int64_t row = b * R + r + s;
+            const float Rold = deq_u8(t.rq[row], t.ra[blk_of(row, hp)]);
+            const float Rnew = fmaf(tot[s] / fC, hp.a2, Rold * hp.b2);
+            if (tid == 0) {
+              t.Rn[row] = Rnew;
+              rowR[r + s - r0] = Rnew;
+            }
+          }
+        }
+      }
+      __syncthreads();
+      // phase B: column partials segment by segment
+      for (int64_t seg = 0; seg < nseg; ++seg) {
+        float colU[K][V], colW[K][V];
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+#pragma unroll
+          for (int v = 0; v < V; ++v) colU[k][v] = colW[k][v] = 0.0f;
+        for (int64_t r = r0; r < r1; ++r) {
+          const float invR = 1.0f / rowR[r - r0];
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * kThreads) * V;
+            if (c0 < C) {
+              float x[V];
+              load_vec<TG, V>(g + r * C + c0, x);
+#pragma unroll
+              for (int v = 0; v < V; ++v) {
+                const float gg = x[v] * x[v];
+                colU[k][v] += gg + hp.eps0;
+                colW[k][v] += gg * invR;
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * kThreads) * V;
+          if (c0 < C) {
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              pU[c0 + v] = colU[k][v];
+              pW[c0 + v] = colW[k][v];
+            }
+          }
+        }
+      }
+      __syncthreads();  // rowR is reused by the next work item
+    }
+  }
+}
+
+// ---------------- P2 ----------------
+// Per element: u = (r_i*c_j)*g / clip; m = fma(u, 1-b1, m_old*b1); res = (u-m)^2 + eps1.
+template <int V>
+__device__ __forceinline__ void load_codes(const int8_t* __restrict__ q, float (&out)[V]) {
+  if constexpr (V == 8) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(q);
+    const int8_t* s = reinterpret_cast<const int8_t*>(&raw);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) out[v] = float(s[v]);
+  } else if constexpr (V == 4) {
+    const uint32_t raw = *reinterpret_cast<const uint32_t*>(q);
+    const int8_t* s = reinterpret_cast<const int8_t*>(&raw);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) out[v] = float(s[v]);
+  } else {
+#pragma unroll
+    for (int v = 0; v < V; ++v) out[v] = float(q[v]);
+  }
+}
+
+template <typename TG, int V, int K>
+__global__ __launch_bounds__(kThreads) void k_fact_pass2(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                         const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using GS = typename TG::storage;
+  constexpr int S = BandShape<V, K>::S;
+  __shared__ float red[2][16][4];
+  const int tid = threadIdx.x;
+  int par = 0;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t local = w - wstart[slot];
+    const int64_t b = local / t.nbands;
+    const int64_t band = local - b * t.nbands;
+    const int64_t R = t.R, C = t.C;
+    const int64_t r0 = band * t.rb;
+    const int64_t r1 = (r0 + t.rb < R) ? (r0 + t.rb) : R;
+    const int64_t ebase = (b * R) * C;
+    const GS* __restrict__ g = static_cast<const GS*>(t.g) + ebase;
+    const int8_t* __restrict__ mq = t.mq + ebase;
+    const float* __restrict__ cf = t.cfac + b * C;
+    const float clip = t.clip[0];
+    const float fC = float(C);
+    constexpr int64_t segw = int64_t(kThreads) * V * K;
+    const int64_t nseg = (C + segw - 1) / segw;
+    float* __restrict__ pR = t.partRes + (b * t.nbands + band) * C;
+    const int64_t PR = t.P * R;
+
+    for (int64_t seg = 0; seg < nseg; ++seg) {
+      // column factors for this thread's columns
+      float cj[K][V];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * kThreads) * V;
+#pragma unroll
+        for (int v = 0; v < V; ++v) cj[k][v] = (c0 + v < C) ? cf[c0 + v] : 0.0f;
+      }
+      ColAcc<V, K> colR[K][V];
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int v = 0; v < V; ++v) colR[k][v] = 0;
+      for (int64_t r = r0; r < r1; r += S) {
+        float ps[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          ps[s] = 0.0f;
+          if (r + s < r1) {
+            const int64_t row = b * R + r + s;
+            const float ri = t.rfac[row];
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+              const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * kThreads) * V;
+              if (c0 < C) {
+                const int64_t e = (r + s) * C + c0;
+                float x[V], q[V];
+                load_vec<TG, V>(g + e, x);
+                load_codes<V>(mq + e, q);
+#pragma unroll
+                for (int v = 0; v < V; ++v) {
+                  const float scale = t.ma[blk_of(ebase + e + v, hp)] / kSignedQ;
+                  const float u = ((ri * cj[k][v]) * x[v]) / clip;
+                  const float m = fmaf(u, hp.a1, (q[v] * scale) * hp.b1);
+                  const float d = u - m;
+                  const float res = d * d + hp.eps1;
+                  ps[s] += res;
+                  colR[k][v] += ColAcc<V, K>(res);
+                }
+              }
+            }
+          }
+        }
+        if (nseg == 1) {
+          float tot[S];
+          block_row_sums<S>(ps, red, par, tot);
+          par ^= 1;
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            if (r + s < r1 && tid == 0) {
+              const int64_t row = b * R + r + s;
+              const float RRold = deq_u8(t.rq[PR + row], t.ra[t.nbr + blk_of(row, hp)]);
+              t.RRn[row] = fmaf(tot[s] / fC, hp.a3, RRold * hp.b3);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * kThreads) * V;
+        if (c0 < C) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) pR[c0 + v] = float(colR[k][v]);
+        }
+      }
+    }
+    if (nseg > 1) {
+      // row sums of the residual over the whole row (second sweep for wide rows)
+      for (int64_t r = r0; r < r1; r += S) {
+        float ps[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          ps[s] = 0.0f;
+          if (r + s < r1) {
+            const int64_t row = b * R + r + s;
+            const float ri = t.rfac[row];
+            for (int64_t seg = 0; seg < nseg; ++seg) {
+#pragma unroll
+              for (int k = 0; k < K; ++k) {
+                const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * kThreads) * V;
+                if (c0 < C) {
+                  const int64_t e = (r + s) * C + c0;
+                  float x[V], q[V];
+                  load_vec<TG, V>(g + e, x);
+                  load_codes<V>(mq + e, q);
+#pragma unroll
+                  for (int v = 0; v < V; ++v) {
+                    const float scale = t.ma[blk_of(ebase + e + v, hp)] / kSignedQ;
+                    const float u = ((ri * cf[c0 + v]) * x[v]) / clip;
+                    const float m = fmaf(u, hp.a1, (q[v] * scale) * hp.b1);
+                    const float d = u - m;
+                    ps[s] += d * d + hp.eps1;
+                  }
+                }
+              }
+            }
+          }
+        }
+        float tot[S];
+        block_row_sums<S>(ps, red, par, tot);
+        par ^= 1;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          if (r + s < r1 && tid == 0) {
+            const int64_t row = b * R + r + s;
+            const float RRold = deq_u8(t.rq[PR + row], t.ra[t.nbr + blk_of(row, hp)]);
+            t.RRn[row] = fmaf(tot[s] / fC, hp.a3, RRold * hp.b3);
+          }
+        }
+      }
+    }
+  }
+}
+
+// ===========================================================================
+// F1a / F2a: mean of the new row state per matrix (one wavefront per matrix)
+// ===========================================================================
+template <bool RES>
+__global__ __launch_bounds__(kThreads) void k_row_mean(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                       const int64_t* __restrict__ wstart, int ntens) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = int64_t(blockIdx.x) * 4 + wid; w < total; w += int64_t(gridDim.x) * 4) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t b = w - wstart[slot];
+    const float* __restrict__ src = (RES ? t.RRn : t.Rn) + b * t.R;
+    float s = 0.0f;
+    for (int64_t i = lane; i < t.R; i += kWave) s += src[i];
+    s = wave_sum(s);
+    if (lane == 0) (RES ? t.rmr : t.rm)[b] = clamp_min_tiny(s / float(t.R));
+  }
+}
+
+// ===========================================================================
+// F1b / F2b: factors and uint8 requantisation of the row / column states
+// ===========================================================================
+// Work item = one quantisation block of the row state (first nbr items of a
+// tensor) or of the column state (next nbc items).
+template <bool RES>
+__global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                            const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  __shared__ float smax[4];
+  __shared__ double ssum[4];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t local = w - wstart[slot];
+    const bool is_row = local < t.nbr;
+    const int64_t blk = is_row ? local : local - t.nbr;
+    const int64_t len = is_row ? t.P * t.R : t.P * t.C;
+    const int64_t i0 = blk * hp.B;
+    const int64_t i1 = (i0 + hp.B < len) ? (i0 + hp.B) : len;
+    const bool partial = (i1 - i0) < hp.B;  // zero padding joins the max
+    float vmax = partial ? 0.0f : -__builtin_inff();
+    double csum = 0.0;
+    const float beta = RES ? hp.b3 : hp.b2;
+    const float alpha = RES ? hp.a3 : hp.a2;
+    if (is_row) {
+      const float* __restrict__ Rsrc = RES ? t.RRn : t.Rn;
+      float* __restrict__ fac = RES ? t.rrfac : t.rfac;
+      const float* __restrict__ mean = RES ? t.rmr : t.rm;
+      for (int64_t i = i0 + tid; i < i1; i += kThreads) {
+        const float v = Rsrc[i];
+        fac[i] = rsqrt_ref(v / mean[i / t.R]);
+        vmax = nan_max(vmax, v);
+      }
+    } else {
+      const int64_t off = RES ? t.P * t.C : 0;
+      const int64_t aoff = RES ? t.nbc : 0;
+      const float* __restrict__ part = RES ? t.partRes : t.partU;
+      float* __restrict__ Cdst = RES ? t.CRn : t.Cn;
+      float* __restrict__ fac = RES ? t.crfac : t.cfac;
+      const float fR = float(t.R);
+      for (int64_t i = i0 + tid; i < i1; i += kThreads) {
+        const int64_t b = i / t.C;
+        const int64_t j = i - b * t.C;
+        const float* __restrict__ pp = part + (b * t.nbands) * t.C + j;
+        double s = 0.0;
+        for (int64_t band = 0; band < t.nbands; ++band) s += double(pp[band * t.C]);
+        const float Cold = deq_u8(t.cq[off + i], t.ca[aoff + blk_of(i, hp)]);
+        const float Cv = clamp_min_tiny(fmaf(float(s) / fR, alpha, Cold * beta));
+        const float c = rsqrt_ref(Cv);
+        Cdst[i] = Cv;
+        fac[i] = c;
+        vmax = nan_max(vmax, Cv);
+        if (!RES) {
+          const float* __restrict__ pw = t.partW + (b * t.nbands) * t.C + j;
+          double W = 0.0;
+          for (int64_t band = 0; band < t.nbands; ++band) W += double(pw[band * t.C]);
+          csum += double(t.rm[b]) * double(c) * double(c) * W;
+        }
+      }
+    }
+    // block max and clip partial (fixed order)
+    vmax = group_max<64>(vmax);
+    if (!RES) csum = wave_sum(csum);
+    if (lane == 0) {
+      smax[wid] = vmax;
+      ssum[wid] = csum;
+    }
+    __syncthreads();
+    const float amax = fix_absmax(nan_max(nan_max(smax[0], smax[1]), nan_max(smax[2], smax[3])));
+    if (tid == 0) {
+      if (is_row) {
+        t.ra[(RES ? t.nbr : 0) + blk] = amax;
+      } else {
+        t.ca[(RES ? t.nbc : 0) + blk] = amax;
+        if (!RES) t.clip_part[blk] = ((ssum[0] + ssum[1]) + ssum[2]) + ssum[3];
+      }
+    }
+    if (is_row) {
+      const float* __restrict__ Rsrc = RES ? t.RRn : t.Rn;
+      uint8_t* __restrict__ q = t.rq + (RES ? t.P * t.R : 0);
+      for (int64_t i = i0 + tid; i < i1; i += kThreads) q[i] = quant_u8(Rsrc[i], amax);
+    } else {
+      const float* __restrict__ Csrc = RES ? t.CRn : t.Cn;
+      uint8_t* __restrict__ q = t.cq + (RES ? t.P * t.C : 0);
+      for (int64_t i = i0 + tid; i < i1; i += kThreads) q[i] = quant_u8(Csrc[i], amax);
+    }
+    __syncthreads();  // smax / ssum reused by the next item
+  }
+}
+
+// ===========================================================================
+// 1-D tensors, pass A: sum of u^2 per tile, u = rsqrt(clamp(v)) * g
+// ===========================================================================
+template <typename TG>
+__device__ __forceinline__ float vec_v_new(const DevTensor& t, int64_t e, float gv, const Hp& hp) {
+  const float vold = deq_u8(t.rq[e], t.ra[blk_of(e, hp)]);
+  return clamp_min_tiny(fmaf(gv * gv + hp.eps0, hp.a2, vold * hp.b2));
+}
+
+template <typename TG>
+__global__ __launch_bounds__(kThreads) void k_vec_passA(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                        const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using GS = typename TG::storage;
+  __shared__ double ssum[4];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t tile = w - wstart[slot];
+    const int64_t e0 = tile * kTile + int64_t(tid) * 8;
+    const GS* __restrict__ g = static_cast<const GS*>(t.g);
+    double s = 0.0;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int64_t e = e0 + v;
+      if (e < t.N) {
+        const float gv = TG::load(g[e]);
+        const float u = rsqrt_ref(vec_v_new<TG>(t, e, gv, hp)) * gv;
+        s += double(u) * double(u);
+      }
+    }
+    s = wave_sum(s);
+    if (lane == 0) ssum[wid] = s;
+    __syncthreads();
+    if (tid == 0) t.clip_part[tile] = ((ssum[0] + ssum[1]) + ssum[2]) + ssum[3];
+    __syncthreads();
+  }
+}
+
+// ===========================================================================
+// CLIP: per-tensor divisor  max(||u|| / sqrt(N) / clip_threshold, 1)
+// ===========================================================================
+__device__ __forceinline__ float clip_from_norm(float norm, int64_t N, const Hp& hp) {
+  const float rms = norm / float(sqrt(double(N)));
+  const float q = rms / hp.thr;
+  return q < 1.0f ? 1.0f : q;
+}
+
+__global__ __launch_bounds__(kThreads) void k_clip(const DevTensor* __restrict__ T, int ntens, Hp hp) {
+  __shared__ double ssum[4];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  for (int k = blockIdx.x; k < ntens; k += gridDim.x) {
+    const DevTensor& t = T[k];
+    double s = 0.0;
+    for (int64_t i = tid; i < t.nclip; i += kThreads) s += t.clip_part[i];
+    s = wave_sum(s);
+    if (lane == 0) ssum[wid] = s;
+    __syncthreads();
+    if (tid == 0) {
+      const double tot = ((ssum[0] + ssum[1]) + ssum[2]) + ssum[3];
+      t.clip[0] = clip_from_norm(float(sqrt(tot)), t.N, hp);
+    }
+    __syncthreads();
+  }
+}
+
+// Unclipped update u at flat index e, computed exactly as the reference does.
+template <typename TG>
+__device__ __forceinline__ float u_at(const DevTensor& t, int64_t e, const Hp& hp) {
+  const float gv = TG::load(static_cast<const typename TG::storage*>(t.g)[e]);
+  if (t.factored) {
+    const int64_t row = e / t.C;
+    const int64_t j = e - row * t.C;
+    const int64_t b = row / t.R;
+    return (t.rfac[row] * t.cfac[b * t.C + j]) * gv;
+  }
+  return rsqrt_ref(vec_v_new<TG>(t, e, gv, hp)) * gv;
+}
+
+// Parity mode: the norm summed in the order of the reference CPU kernel for
+// tensor.norm(2) on fp32 (8 interleaved fused-multiply-add accumulators over
+// the first N - N%8 elements, a left-to-right sum of the 8 accumulators, then
+// the remaining elements as separately rounded square-and-add), so the clip
+// divisor equals the reference's bit for bit.  One workgroup per tensor;
+// slow by design (serial in N/8).
+template <typename TG>
+__global__ __launch_bounds__(kThreads) void k_clip_refnorm(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                           int ntens, Hp hp) {
+  __shared__ float ubuf[kTile];
+  __shared__ float accs[8];
+  const int tid = threadIdx.x;
+  for (int k = blockIdx.x; k < ntens; k += gridDim.x) {
+    const DevTensor& t = T[tids[k]];
+    const int64_t N = t.N;
+    const int64_t main = N - (N % 8);
+    float acc = 0.0f;
+    for (int64_t base = 0; base < main; base += kTile) {
+      const int64_t cnt = (main - base < kTile) ? (main - base) : kTile;
+      for (int i = tid; i < cnt; i += kThreads) ubuf[i] = u_at<TG>(t, base + i, hp);
+      __syncthreads();
+      if (tid < 8)
+        for (int i = tid; i < cnt; i += 8) acc = fmaf(ubuf[i], ubuf[i], acc);
+      __syncthreads();
+    }
+    if (tid < 8) accs[tid] = acc;
+    __syncthreads();
+    if (tid == 0) {
+      float bsum = accs[0];
+      for (int j = 1; j < 8; ++j) bsum = bsum + accs[j];
+      for (int64_t d = main; d < N; ++d) {
+        const float u = u_at<TG>(t, d, hp);
+        const float uu = u * u;
+        bsum = bsum + uu;
+      }
+      t.clip[0] = clip_from_norm(sqrtf(bsum), N, hp);
+    }
+    __syncthreads();
+  }
+}
+
+// ===========================================================================
+// P3: flat pass over whole quantisation blocks (factored tensors)
+// ===========================================================================
+// 2048-element tiles, 8 consecutive elements per thread, L = B/8 lanes per
+// quantisation block (B a power of two in [8, 2048]).
+template <typename TP, typename TG>
+__global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                         const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using PS = typename TP::storage;
+  using GS = typename TG::storage;
+  __shared__ float wmax[2][4];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int L = hp.B >> 3;  // lanes per block
+  int par = 0;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t tile = w - wstart[slot];
+    const int64_t e0 = tile * kTile + int64_t(tid) * 8;
+    const int64_t N = t.N, C = t.C, R = t.R;
+    PS* __restrict__ p = static_cast<PS*>(t.p);
+    const GS* __restrict__ g = static_cast<const GS*>(t.g);
+    const float clip = t.clip[0];
+    float m[8], pv[8];
+    const bool full = t.vec_ok && (e0 + 8 <= N);
+    if (e0 < N) {
+      float gv[8], q[8];
+      if (full) {
+        load8<TG>(g + e0, gv);
+        load8<TP>(p + e0, pv);
+        load_codes<8>(t.mq + e0, q);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const bool ok = e0 + v < N;
+          gv[v] = ok ? TG::load(g[e0 + v]) : 0.0f;
+          pv[v] = ok ? TP::load(p[e0 + v]) : 0.0f;
+          q[v] = ok ? float(t.mq[e0 + v]) : 0.0f;
+        }
+      }
+      const float scale = t.ma[blk_of(e0, hp)] / kSignedQ;  // 8 elements share a block (B >= 8)
+      int64_t row = e0 / C;
+      int64_t j = e0 - row * C;
+      int64_t bb = row / R;
+      int64_t i = row - bb * R;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        if (e0 + v < N) {
+          const float ri = t.rfac[row], rri = t.rrfac[row];
+          const float cj = t.cfac[bb * C + j], crj = t.crfac[bb * C + j];
+          const float u = ((ri * cj) * gv[v]) / clip;
+          m[v] = fmaf(u, hp.a1, (q[v] * scale) * hp.b1);
+          const float step = (rri * crj) * m[v];
+          pv[v] = param_update<TP>(pv[v], step, hp);
+        } else {
+          m[v] = 0.0f;
+        }
+        if (++j == C) {
+          j = 0;
+          ++row;
+          if (++i == R) {
+            i = 0;
+            ++bb;
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) m[v] = 0.0f;
+    }
+    // block absmax of |m|
+    float amax = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) amax = nan_max(amax, fabsf(m[v]));
+    if (L <= 64) {
+      amax = group_max_rt(amax, L);
+    } else {
+      amax = group_max<64>(amax);
+      if (lane == 0) wmax[par][wid] = amax;
+      __syncthreads();
+      const int wpb = L >> 6;  // waves per block
+      const int w0 = (wid / wpb) * wpb;
+      amax = wmax[par][w0];
+      for (int k = 1; k < wpb; ++k) amax = nan_max(amax, wmax[par][w0 + k]);
+      par ^= 1;
+    }
+    amax = fix_absmax(amax);
+    if (e0 < N) {
+      if (((e0 & (hp.B - 1)) == 0)) t.ma[blk_of(e0, hp)] = amax;
+      if (full) {
+        uint2 raw;
+        int8_t* s = reinterpret_cast<int8_t*>(&raw);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) s[v] = quant_s8(m[v], amax);
+        *reinterpret_cast<uint2*>(t.mq + e0) = raw;
+        store8<TP>(p + e0, pv);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          if (e0 + v < N) {
+            t.mq[e0 + v] = quant_s8(m[v], amax);
+            p[e0 + v] = TP::store(pv[v]);
+          }
+        }
+      }
+    }
+  }
+}
+
+// ===========================================================================
+// 1-D tensors, pass B: v, u/clip, m, parameter write, requantisation
+// ===========================================================================
+template <typename TP, typename TG>
+__global__ __launch_bounds__(kThreads) void k_vec_passB(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                        const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using PS = typename TP::storage;
+  using GS = typename TG::storage;
+  __shared__ float wmax[2][2][4];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int L = hp.B >> 3;
+  int par = 0;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t tile = w - wstart[slot];
+    const int64_t e0 = tile * kTile + int64_t(tid) * 8;
+    const int64_t N = t.N;
+    PS* __restrict__ p = static_cast<PS*>(t.p);
+    const GS* __restrict__ g = static_cast<const GS*>(t.g);
+    const float clip = t.clip[0];
+    float m[8], vv[8], pv[8];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int64_t e = e0 + v;
+      if (e < N) {
+        const float gv = TG::load(g[e]);
+        vv[v] = vec_v_new<TG>(t, e, gv, hp);
+        const float u = (rsqrt_ref(vv[v]) * gv) / clip;
+        const float mold = deq_s8(t.mq[e], t.ma[blk_of(e, hp)]);
+        m[v] = fmaf(u, hp.a1, mold * hp.b1);
+        pv[v] = param_update<TP>(TP::load(p[e]), m[v], hp);
+      } else {
+        m[v] = 0.0f;
+        vv[v] = 0.0f;
+      }
+    }
+    float am = 0.0f, av = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      am = nan_max(am, fabsf(m[v]));
+      av = nan_max(av, vv[v]);
+    }
+    if (L <= 64) {
+      am = group_max_rt(am, L);
+      av = group_max_rt(av, L);
+    } else {
+      am = group_max<64>(am);
+      av = group_max<64>(av);
+      if (lane == 0) {
+        wmax[par][0][wid] = am;
+        wmax[par][1][wid] = av;
+      }
+      __syncthreads();
+      const int wpb = L >> 6;
+      const int w0 = (wid / wpb) * wpb;
+      am = wmax[par][0][w0];
+      av = wmax[par][1][w0];
+      for (int k = 1; k < wpb; ++k) {
+        am = nan_max(am, wmax[par][0][w0 + k]);
+        av = nan_max(av, wmax[par][1][w0 + k]);
+      }
+      par ^= 1;
+    }
+    am = fix_absmax(am);
+    av = fix_absmax(av);
+    if (e0 < N && ((e0 & (hp.B - 1)) == 0)) {
+      t.ma[blk_of(e0, hp)] = am;
+      t.ra[blk_of(e0, hp)] = av;
+    }
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int64_t e = e0 + v;
+      if (e < N) {
+        t.mq[e] = quant_s8(m[v], am);
+        t.rq[e] = quant_u8(vv[v], av);
+        p[e] = TP::store(pv[v]);
+      }
+    }
+  }
+}
+
+// ===========================================================================
+// Generic block-size fallback for P3 / B: one workgroup per quantisation
+// block, any block size.  Values are recomputed in a second sweep after the
+// block absmax is known.
+// ===========================================================================
+template <typename TG>
+__device__ __forceinline__ float m_new_fact(const DevTensor& t, int64_t e, float clip, const Hp& hp) {
+  const float u = u_at<TG>(t, e, hp) / clip;
+  return fmaf(u, hp.a1, deq_s8(t.mq[e], t.ma[blk_of(e, hp)]) * hp.b1);
+}
+
+template <typename TP, typename TG>
+__global__ __launch_bounds__(kThreads) void k_generic_update(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                             const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using PS = typename TP::storage;
+  __shared__ float wm[2][4];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t blk = w - wstart[slot];
+    const int64_t i0 = blk * hp.B;
+    const int64_t i1 = (i0 + hp.B < t.N) ? (i0 + hp.B) : t.N;
+    const float clip = t.clip[0];
+    const typename TG::storage* __restrict__ g = static_cast<const typename TG::storage*>(t.g);
+    PS* __restrict__ p = static_cast<PS*>(t.p);
+    // sweep 1: block absmax of the new momentum (and of the new 1-D second moment)
+    float am = 0.0f, av = 0.0f;
+    for (int64_t e = i0 + tid; e < i1; e += kThreads) {
+      am = nan_max(am, fabsf(m_new_fact<TG>(t, e, clip, hp)));
+      if (!t.factored) av = nan_max(av, vec_v_new<TG>(t, e, TG::load(g[e]), hp));
+    }
+    am = group_max<64>(am);
+    av = group_max<64>(av);
+    if (lane == 0) {
+      wm[0][wid] = am;
+      wm[1][wid] = av;
+    }
+    __syncthreads();
+    am = fix_absmax(nan_max(nan_max(wm[0][0], wm[0][1]), nan_max(wm[0][2], wm[0][3])));
+    av = fix_absmax(nan_max(nan_max(wm[1][0], wm[1][1]), nan_max(wm[1][2], wm[1][3])));
+    // sweep 2: each element is recomputed from its old codes and rewritten by the same
+    // thread; the old block scales are overwritten only after the barrier below
+    for (int64_t e = i0 + tid; e < i1; e += kThreads) {
+      const float m = m_new_fact<TG>(t, e, clip, hp);
+      float step;
+      if (t.factored) {
+        const int64_t row = e / t.C;
+        const int64_t j = e - row * t.C;
+        const int64_t b = row / t.R;
+        step = (t.rrfac[row] * t.crfac[b * t.C + j]) * m;
+      } else {
+        step = m;
+        t.rq[e] = quant_u8(vec_v_new<TG>(t, e, TG::load(g[e]), hp), av);
+      }
+      p[e] = TP::store(param_update<TP>(TP::load(p[e]), step, hp));
+      t.mq[e] = quant_s8(m, am);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      t.ma[blk] = am;
+      if (!t.factored) t.ra[blk] = av;
+    }
+    __syncthreads();
+  }
+}
+
+// ===========================================================================
+// standalone blockwise quantisation (fp32 -> int8/uint8 + absmax) and dequantisation
+// ===========================================================================
+template <bool SIGNED>
+__global__ __launch_bounds__(kThreads) void k_quantize(const float* __restrict__ x, int64_t n, int32_t B, int64_t nblocks,
+                                                       void* __restrict__ q, float* __restrict__ absmax) {
+  __shared__ float wm[4];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  for (int64_t blk = blockIdx.x; blk < nblocks; blk += gridDim.x) {
+    const int64_t i0 = blk * B;
+    const int64_t i1 = (i0 + B < n) ? (i0 + B) : n;
+    float a = (SIGNED || (i1 - i0) < B) ? 0.0f : -__builtin_inff();
+    for (int64_t i = i0 + tid; i < i1; i += kThreads) a = nan_max(a, SIGNED ? fabsf(x[i]) : x[i]);
+    a = group_max<64>(a);
+    if (lane == 0) wm[wid] = a;
+    __syncthreads();
+    a = fix_absmax(nan_max(nan_max(wm[0], wm[1]), nan_max(wm[2], wm[3])));
+    for (int64_t i = i0 + tid; i < i1; i += kThreads) {
+      if (SIGNED) static_cast<int8_t*>(q)[i] = quant_s8(x[i], a);
+      else static_cast<uint8_t*>(q)[i] = quant_u8(x[i], a);
+    }
+    if (tid == 0) absmax[blk] = a;
+    __syncthreads();
+  }
+}
+
+template <bool SIGNED>
+__global__ __launch_bounds__(kThreads) void k_dequantize(const void* __restrict__ q, const float* __restrict__ absmax, int64_t n,
+                                                         int32_t B, float* __restrict__ out) {
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += int64_t(gridDim.x) * kThreads) {
+    const float a = absmax[i / B];
+    out[i] = SIGNED ? deq_s8(static_cast<const int8_t*>(q)[i], a) : deq_u8(static_cast<const uint8_t*>(q)[i], a);
+  }
+}
+
+}  // namespace came8

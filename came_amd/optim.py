@@ -1,0 +1,509 @@
+"""CAME 8-bit optimizers whose step runs in libcame8 (hand-written HIP kernels for MI355X).
+
+Drop-in replacements for the reference classes of the same names:
+
+  * ``CAME8bitFull``   -- came_pytorch/CAME8bitFull.py:39-120 (constructor), :748-937 (state),
+                          :939-1118 (step)
+  * ``CAME8bit``       -- came_pytorch/CAME8bit.py:24-206 (constructor and kwarg validation),
+                          :672-693 (prime_for_cuda_graph), :712-912 (step)
+  * ``CAME8bitMemory`` -- came_pytorch/CAME8bitMemory.py:17-52 (constructor), :390-447 (state),
+                          :559-635 (step)
+
+Same constructor arguments, defaults and ``ValueError`` texts, same param-group
+keys, same per-parameter state keys, dtypes and shapes as the reference's
+full8bit layout (flat row-major 256-element blocks, ``CAME8bitFull.py:748-788``).
+Each ``step()`` hands every parameter of a param group to ONE ``came8_step``
+call (include/came8.h), which runs the whole update as a few multi-tensor
+launches on the current stream: no per-parameter launches, no host sync.
+
+Parameters must live on the GPU; there is no CPU path (the reference's CPU
+arithmetic is the test oracle, not part of this package).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import time
+import warnings
+import weakref
+from collections import defaultdict
+from itertools import chain
+
+import torch
+import torch.optim
+
+from . import _lib
+from .blockwise_quantization import init_batched_qstate, init_qstate, num_blocks
+
+_DTYPE_CODE = {torch.float32: _lib.CAME8_F32, torch.bfloat16: _lib.CAME8_BF16, torch.float16: _lib.CAME8_F16}
+
+# state keys whose dtype is not the parameter's (torch's load_state_dict would cast them)
+_STATE_DTYPES = {
+    "exp_avg_q": torch.int8,
+    "exp_avg_absmax": torch.float32,
+    "factored_row_q": torch.uint8,
+    "factored_row_absmax": torch.float32,
+    "factored_col_q": torch.uint8,
+    "factored_col_absmax": torch.float32,
+    "exp_avg_sq_q": torch.uint8,
+    "exp_avg_sq_absmax": torch.float32,
+}
+_VIEW_KEYS = (
+    "exp_avg_sq_row_q", "exp_avg_res_row_q", "exp_avg_sq_col_q", "exp_avg_res_col_q",
+    "exp_avg_sq_row_absmax", "exp_avg_res_row_absmax", "exp_avg_sq_col_absmax", "exp_avg_res_col_absmax",
+)
+
+
+def _release_workspace(ptr: int) -> None:
+    try:
+        _lib.load().came8_release_workspace(ptr)
+    except Exception:  # interpreter shutdown
+        pass
+
+
+class _Came8Base(torch.optim.Optimizer):
+    """Shared step machinery: state layout, descriptor table, workspace, one library call per group."""
+
+    def _validate_and_defaults(self, lr, eps, clip_threshold, betas, weight_decay, block_size):
+        # came_pytorch/CAME8bitFull.py:73-91
+        if lr is None or lr <= 0.0:
+            raise ValueError(f"lr must be > 0, got {lr}")
+        if clip_threshold <= 0.0:
+            raise ValueError(f"clip_threshold must be > 0, got {clip_threshold}")
+        if len(eps) != 2:
+            raise ValueError(f"eps must be a tuple of length 2, got eps={eps}")
+        if len(betas) != 3:
+            raise ValueError(f"betas must be a tuple of length 3, got betas={betas}")
+        if block_size <= 0:
+            raise ValueError(f"block_size must be > 0, got {block_size}")
+        return dict(
+            lr=float(lr),
+            eps=(float(eps[0]), float(eps[1])),
+            clip_threshold=float(clip_threshold),
+            betas=(float(betas[0]), float(betas[1]), float(betas[2])),
+            weight_decay=float(weight_decay),
+            block_size=int(block_size),
+        )
+
+    # ------------------------------------------------------------------ state
+    @staticmethod
+    def _bind_factored_views(state: dict) -> None:
+        """Views of the stacked row/col states (CAME8bitFull.py:214-223)."""
+        state["exp_avg_sq_row_q"] = state["factored_row_q"][0]
+        state["exp_avg_res_row_q"] = state["factored_row_q"][1]
+        state["exp_avg_sq_col_q"] = state["factored_col_q"][0]
+        state["exp_avg_res_col_q"] = state["factored_col_q"][1]
+        state["exp_avg_sq_row_absmax"] = state["factored_row_absmax"][0]
+        state["exp_avg_res_row_absmax"] = state["factored_row_absmax"][1]
+        state["exp_avg_sq_col_absmax"] = state["factored_col_absmax"][0]
+        state["exp_avg_res_col_absmax"] = state["factored_col_absmax"][1]
+
+    def _init_state(self, state: dict, grad: torch.Tensor, block_size: int) -> None:
+        """The reference's full8bit layout (CAME8bitFull.py:748-788, 919-923)."""
+        state["step"] = 0
+        state["_mode"] = "full8bit"
+        state["RMS"] = 0
+        state["exp_avg_q"], state["exp_avg_absmax"] = init_qstate(
+            grad.shape, device=grad.device, signed=True, block_size=block_size)
+        factored = len(grad.shape) >= 2
+        state["factored"] = factored
+        if factored:
+            row_shape = grad.shape[:-1]
+            col_shape = grad.shape[:-2] + grad.shape[-1:]
+            state["factored_row_q"], state["factored_row_absmax"] = init_batched_qstate(
+                row_shape, batch_size=2, device=grad.device, signed=False, block_size=block_size)
+            state["factored_col_q"], state["factored_col_absmax"] = init_batched_qstate(
+                col_shape, batch_size=2, device=grad.device, signed=False, block_size=block_size)
+            self._bind_factored_views(state)
+        else:
+            state["exp_avg_sq_q"], state["exp_avg_sq_absmax"] = init_qstate(
+                grad.shape, device=grad.device, signed=False, block_size=block_size)
+
+    def _check_state(self, p: torch.Tensor, state: dict, block_size: int) -> None:
+        if tuple(state["exp_avg_q"].shape) != tuple(p.shape):
+            raise RuntimeError("Parameter shape changed; this optimizer does not support resizing 8-bit state.")
+        if state["exp_avg_absmax"].numel() != num_blocks(p.numel(), block_size):
+            raise RuntimeError("block_size changed after the 8-bit state was created; the state layout is fixed.")
+        if state["exp_avg_q"].device != p.device:
+            raise RuntimeError("optimizer state lives on a different device than its parameter")
+
+    # -------------------------------------------------------------- checkpoint
+    def load_state_dict(self, state_dict: dict) -> None:
+        """torch's loader casts every floating state tensor to the parameter dtype; the 8-bit codes and
+        the fp32 block scales must keep their own dtypes, so the originals are put back afterwards."""
+        saved_groups = state_dict["param_groups"]
+        saved_state = state_dict["state"]
+        super().load_state_dict(state_dict)
+        id_map = dict(zip(chain.from_iterable(g["params"] for g in saved_groups),
+                          chain.from_iterable(g["params"] for g in self.param_groups)))
+        for k, st in saved_state.items():
+            p = id_map.get(k)
+            if p is None or p not in self.state:
+                continue
+            live = self.state[p]
+            for key, dt in _STATE_DTYPES.items():
+                v = st.get(key)
+                if isinstance(v, torch.Tensor):
+                    live[key] = v.detach().to(device=p.device, dtype=dt).clone()
+            # torch's loader rebuilds iterables element-wise, which turns the string "_mode" into a
+            # generator (and a mode mismatch would reset the state on the next step): plain values
+            # are restored as saved
+            for key, v in st.items():
+                if isinstance(v, (str, bool, int, float)):
+                    live[key] = v
+            if live.get("factored") and "factored_row_q" in live:
+                self._bind_factored_views(live)
+
+    # ------------------------------------------------------------------- step
+    def _group_hparams(self, group: dict) -> _lib.Came8HParams:
+        b1, b2, b3 = group["betas"]
+        e0, e1 = group["eps"]
+        flags = _lib.CAME8_FLAG_REFERENCE_NORM if getattr(self, "reference_norm", False) else 0
+        return _lib.Came8HParams(float(group["lr"]), float(b1), float(b2), float(b3), float(e0), float(e1),
+                                 float(group["clip_threshold"]), float(group["weight_decay"]),
+                                 int(group["block_size"]), flags)
+
+    def _workspace(self, device: torch.device, descs, n: int, block_size: int):
+        """(workspace tensor, tag) for `device`, grown when the tensor list needs more.
+
+        The workspace holds the launch plan between steps and nothing else writes to it; each
+        allocation gets a fresh tag, so the library never trusts a plan left in reused memory.
+        """
+        lib = _lib.load()
+        need = ctypes.c_size_t(0)
+        _lib.check(lib.came8_workspace_size(descs, n, block_size, ctypes.byref(need)), "came8_workspace_size")
+        cache = self.__dict__.setdefault("_came8_workspaces", {})
+        ent = cache.get(device)
+        if ent is None or ent[0].numel() < need.value:
+            if ent is not None:
+                lib.came8_release_workspace(ent[0].data_ptr())
+            ws = torch.empty(max(int(need.value), 256), dtype=torch.uint8, device=device)
+            weakref.finalize(ws, _release_workspace, ws.data_ptr())
+            ent = (ws, _lib.new_workspace_tag())
+            cache[device] = ent
+        return ent
+
+    def _prepare_param(self, p: torch.Tensor, block_size: int):
+        grad = p.grad
+        if grad.is_sparse:
+            raise RuntimeError("CAME does not support sparse gradients.")
+        if not p.is_cuda:
+            raise RuntimeError(
+                f"{type(self).__name__} (came_amd) runs the step on the GPU; got a parameter on {p.device}")
+        if p.dtype not in _DTYPE_CODE or grad.dtype not in _DTYPE_CODE:
+            raise RuntimeError(f"unsupported dtype: param {p.dtype}, grad {grad.dtype} "
+                               "(float32, bfloat16 and float16 are supported)")
+        if grad.shape != p.shape:
+            raise RuntimeError(f"grad shape {tuple(grad.shape)} does not match param shape {tuple(p.shape)}")
+        state = self.state[p]
+        if len(state) == 0 or state.get("_mode") != "full8bit":
+            state.clear()
+            self._init_state(state, grad, block_size)
+        self._check_state(p, state, block_size)
+        return state, grad
+
+    @torch.no_grad()
+    def _step_group(self, group: dict, params: list) -> None:
+        block_size = int(group["block_size"])
+        hp = self._group_hparams(group)
+        by_device: dict = defaultdict(list)
+        for p in params:
+            by_device[p.device].append(p)
+        lib = _lib.load()
+        for device, plist in by_device.items():
+            items = []
+            for p in plist:
+                state, grad = self._prepare_param(p, block_size)
+                state["step"] += 1
+                if p.numel() == 0:
+                    continue
+                items.append((p, state, grad))
+            if not items:
+                continue
+            n = len(items)
+            descs = (_lib.Came8Tensor * n)()
+            keep, copyback = [], []
+            for i, (p, state, grad) in enumerate(items):
+                pd = p.data
+                if not pd.is_contiguous():
+                    pd = pd.contiguous()
+                    copyback.append((p, pd))
+                g = grad if grad.is_contiguous() else grad.contiguous()
+                keep.append(g)
+                d = descs[i]
+                d.param = pd.data_ptr()
+                d.grad = g.data_ptr()
+                d.exp_avg_q = state["exp_avg_q"].data_ptr()
+                d.exp_avg_absmax = state["exp_avg_absmax"].data_ptr()
+                d.param_dtype = _DTYPE_CODE[p.dtype]
+                d.grad_dtype = _DTYPE_CODE[g.dtype]
+                if state["factored"]:
+                    shape = tuple(p.shape)
+                    d.prefix = math.prod(shape[:-2])
+                    d.rows, d.cols = shape[-2], shape[-1]
+                    d.factored = 1
+                    d.row_q = state["factored_row_q"].data_ptr()
+                    d.row_absmax = state["factored_row_absmax"].data_ptr()
+                    d.col_q = state["factored_col_q"].data_ptr()
+                    d.col_absmax = state["factored_col_absmax"].data_ptr()
+                else:
+                    d.prefix, d.rows, d.cols = 1, 1, p.numel()
+                    d.factored = 0
+                    d.row_q = state["exp_avg_sq_q"].data_ptr()
+                    d.row_absmax = state["exp_avg_sq_absmax"].data_ptr()
+            ws, tag = self._workspace(device, descs, n, block_size)
+            with torch.cuda.device(device):
+                stream = torch.cuda.current_stream(device).cuda_stream
+                _lib.check(lib.came8_step(descs, n, ctypes.byref(hp), ws.data_ptr(), ws.numel(), tag, stream),
+                           "came8_step")
+            for p, pd in copyback:
+                p.data.copy_(pd)
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        timing = self._dispatch_timing_is_enabled()
+        t0 = time.perf_counter()
+        count = 0
+        for group in self.param_groups:
+            params = []
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                if p.grad.is_sparse:
+                    raise RuntimeError("CAME does not support sparse gradients.")
+                params.append(p)
+            if params:
+                self._step_group(group, params)
+                count += len(params)
+        if timing:
+            self._benchmark_dispatch_timing_last = {
+                "came8_step_host_time_ms": (time.perf_counter() - t0) * 1000.0,
+                "came8_step_param_count": count,
+            }
+        return loss
+
+    def _dispatch_timing_is_enabled(self) -> bool:
+        return bool(getattr(self, "_benchmark_dispatch_timing", False))
+
+
+class CAME8bitFull(_Came8Base):
+    """All-state blockwise 8-bit CAME (reference came_pytorch/CAME8bitFull.py:39)."""
+
+    def __init__(
+        self,
+        params,
+        lr: float,
+        eps: tuple[float, float] = (1e-30, 1e-16),
+        clip_threshold: float = 1.0,
+        betas: tuple[float, float, float] = (0.9, 0.999, 0.9999),
+        weight_decay: float = 0.0,
+        block_size: int = 256,
+        prefer_factored_cuda_ext_path: bool = True,
+        cuda_factored_nd_chunk_size_override: int | None = None,
+        cuda_factored_nd_chunked_direct_row_sum_min_matrix_numel: int | None = None,
+        cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel: int | None = None,
+        cuda_nonfactored_use_fp16_update: bool = False,
+    ):
+        defaults = self._validate_and_defaults(lr, eps, clip_threshold, betas, weight_decay, block_size)
+        super().__init__(params, defaults)
+        # Accepted for signature compatibility (CAME8bitFull.py:92-120); they tuned the reference's
+        # per-parameter CUDA chains and select nothing here, but their validation is kept.
+        self.prefer_factored_cuda_ext_path = bool(prefer_factored_cuda_ext_path)
+        self.cuda_factored_nd_chunk_size_override = (
+            None if cuda_factored_nd_chunk_size_override is None else int(cuda_factored_nd_chunk_size_override))
+        self.cuda_factored_nd_chunked_direct_row_sum_min_matrix_numel = (
+            None if cuda_factored_nd_chunked_direct_row_sum_min_matrix_numel is None
+            else int(cuda_factored_nd_chunked_direct_row_sum_min_matrix_numel))
+        self.cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel = (
+            None if cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel is None
+            else int(cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel))
+        self.cuda_nonfactored_use_fp16_update = bool(cuda_nonfactored_use_fp16_update)
+        if self.cuda_factored_nd_chunk_size_override is not None and self.cuda_factored_nd_chunk_size_override <= 0:
+            raise ValueError("cuda_factored_nd_chunk_size_override must be positive when set")
+        self.cuda_factored_nd_chunked_direct_row_sum = not (
+            self.cuda_factored_nd_chunked_direct_row_sum_min_matrix_numel is None
+            and self.cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel is None)
+        self.track_cuda_rms_state = False
+        self.reference_norm = False
+
+
+class CAME8bitMemory(CAME8bitFull):
+    """8-bit CAME with compact state (reference came_pytorch/CAME8bitMemory.py:17).
+
+    The reference shares scratch buffers per device between parameters; here every param group's
+    step uses one workspace per optimizer and device, so the same holds by construction.
+    """
+
+    def __init__(
+        self,
+        params,
+        lr: float,
+        eps: tuple[float, float] = (1e-30, 1e-16),
+        clip_threshold: float = 1.0,
+        betas: tuple[float, float, float] = (0.9, 0.999, 0.9999),
+        weight_decay: float = 0.0,
+        block_size: int = 256,
+    ):
+        super().__init__(params, lr=lr, eps=eps, clip_threshold=clip_threshold, betas=betas,
+                         weight_decay=weight_decay, block_size=block_size,
+                         prefer_factored_cuda_ext_path=False, cuda_nonfactored_use_fp16_update=False)
+
+
+class CAME8bit(CAME8bitFull):
+    """Single-entry 8-bit CAME (reference came_pytorch/CAME8bit.py:24).
+
+    Every parameter, whatever its rank, takes the full8bit state layout and the one multi-tensor
+    step; the reference's per-rank dispatch knobs are validated and recorded but select nothing.
+    """
+
+    CUDA_1D_RUNTIME_MODE_DEFAULT = "default"
+    CUDA_1D_RUNTIME_MODE_REPEATED_FP16_PAIRMIN = "repeated_fp16_pairmin"
+    CUDA_ND_RUNTIME_MODE_DEFAULT = "default"
+    CUDA_ND_RUNTIME_MODE_CHUNK32_LARGE_DIRECT_ROW_SUM = "chunk32_large_direct_row_sum"
+    EXPLICIT_USER_FACING_KWARGS = frozenset({
+        "prefer_cuda_fast_path", "prefer_cuda_2d_fast_path", "prefer_factored_cuda_ext_path",
+        "cuda_1d_runtime_mode", "cuda_nd_runtime_mode", "cuda_graph_compatible",
+    })
+    EXPERIMENTAL_CUDA_TUNING_DEFAULTS = {
+        "prefer_cuda_1d_batched_fast_path": False,
+        "prefer_cuda_1d_multitensor_fast_path": False,
+        "cuda_1d_batched_use_fp16_update": False,
+        "cuda_1d_batched_chunk_size": 8,
+        "cuda_1d_batched_min_bucket_size": 4,
+        "cuda_1d_batched_min_numel": 1024,
+        "cuda_1d_batched_max_numel": 65536,
+        "cuda_factored_nd_chunk_size_override": None,
+        "cuda_factored_nd_chunked_direct_row_sum_min_matrix_numel": None,
+        "cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel": None,
+        "cuda_nonfactored_use_fp16_update": False,
+    }
+
+    def __init__(
+        self,
+        params,
+        lr: float,
+        eps: tuple[float, float] = (1e-30, 1e-16),
+        clip_threshold: float = 1.0,
+        betas: tuple[float, float, float] = (0.9, 0.999, 0.9999),
+        weight_decay: float = 0.0,
+        block_size: int = 256,
+        prefer_cuda_fast_path: bool = True,
+        prefer_cuda_2d_fast_path: bool | None = None,
+        prefer_cuda_1d_fast_path: bool | None = None,
+        prefer_cuda_1d_batched_fast_path: bool = False,
+        prefer_cuda_1d_multitensor_fast_path: bool = False,
+        cuda_1d_batched_use_fp16_update: bool = False,
+        cuda_1d_batched_chunk_size: int = 8,
+        cuda_1d_batched_min_bucket_size: int = 4,
+        cuda_1d_batched_min_numel: int = 1024,
+        cuda_1d_batched_max_numel: int = 65536,
+        cuda_1d_runtime_mode: str = CUDA_1D_RUNTIME_MODE_DEFAULT,
+        prefer_factored_cuda_ext_path: bool = True,
+        cuda_factored_nd_chunk_size_override: int | None = None,
+        cuda_factored_nd_chunked_direct_row_sum_min_matrix_numel: int | None = None,
+        cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel: int | None = None,
+        cuda_nd_runtime_mode: str = CUDA_ND_RUNTIME_MODE_DEFAULT,
+        cuda_nonfactored_use_fp16_update: bool = False,
+        cuda_graph_compatible: bool = False,
+    ):
+        # validation order and messages follow CAME8bit.py:94-206
+        if cuda_1d_runtime_mode not in {self.CUDA_1D_RUNTIME_MODE_DEFAULT,
+                                        self.CUDA_1D_RUNTIME_MODE_REPEATED_FP16_PAIRMIN}:
+            raise ValueError(
+                "cuda_1d_runtime_mode must be one of "
+                f"{self.CUDA_1D_RUNTIME_MODE_DEFAULT!r}, {self.CUDA_1D_RUNTIME_MODE_REPEATED_FP16_PAIRMIN!r}; "
+                f"got {cuda_1d_runtime_mode!r}")
+        if cuda_nd_runtime_mode not in {self.CUDA_ND_RUNTIME_MODE_DEFAULT,
+                                        self.CUDA_ND_RUNTIME_MODE_CHUNK32_LARGE_DIRECT_ROW_SUM}:
+            raise ValueError(
+                "cuda_nd_runtime_mode must be one of "
+                f"{self.CUDA_ND_RUNTIME_MODE_DEFAULT!r}, {self.CUDA_ND_RUNTIME_MODE_CHUNK32_LARGE_DIRECT_ROW_SUM!r}; "
+                f"got {cuda_nd_runtime_mode!r}")
+        overrides = self._experimental_cuda_tuning_overrides(
+            prefer_cuda_1d_batched_fast_path=prefer_cuda_1d_batched_fast_path,
+            prefer_cuda_1d_multitensor_fast_path=prefer_cuda_1d_multitensor_fast_path,
+            cuda_1d_batched_use_fp16_update=cuda_1d_batched_use_fp16_update,
+            cuda_1d_batched_chunk_size=cuda_1d_batched_chunk_size,
+            cuda_1d_batched_min_bucket_size=cuda_1d_batched_min_bucket_size,
+            cuda_1d_batched_min_numel=cuda_1d_batched_min_numel,
+            cuda_1d_batched_max_numel=cuda_1d_batched_max_numel,
+            cuda_factored_nd_chunk_size_override=cuda_factored_nd_chunk_size_override,
+            cuda_factored_nd_chunked_direct_row_sum_min_matrix_numel=(
+                cuda_factored_nd_chunked_direct_row_sum_min_matrix_numel),
+            cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel=(
+                cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel),
+            cuda_nonfactored_use_fp16_update=cuda_nonfactored_use_fp16_update,
+        )
+        if overrides:
+            warnings.warn(
+                "CAME8bit low-level CUDA tuning kwargs are experimental and intended for "
+                "benchmark/diagnostic use: " + ", ".join(overrides)
+                + ". Prefer cuda_1d_runtime_mode/cuda_nd_runtime_mode for tracked user-facing opt-ins.",
+                RuntimeWarning, stacklevel=2)
+        eff_1d_fast = prefer_cuda_1d_fast_path
+        eff_1d_batched = prefer_cuda_1d_batched_fast_path
+        eff_1d_mt = prefer_cuda_1d_multitensor_fast_path
+        eff_1d_fp16 = cuda_1d_batched_use_fp16_update
+        eff_min_bucket = cuda_1d_batched_min_bucket_size
+        eff_nd_chunk = cuda_factored_nd_chunk_size_override
+        eff_nd_min = cuda_factored_nd_chunked_direct_row_sum_min_matrix_numel
+        eff_nf_fp16 = cuda_nonfactored_use_fp16_update
+        if cuda_1d_runtime_mode == self.CUDA_1D_RUNTIME_MODE_REPEATED_FP16_PAIRMIN:
+            eff_1d_fast = eff_1d_batched = eff_1d_mt = eff_1d_fp16 = True
+            eff_min_bucket = 2
+            eff_nf_fp16 = True
+        if cuda_nd_runtime_mode == self.CUDA_ND_RUNTIME_MODE_CHUNK32_LARGE_DIRECT_ROW_SUM:
+            eff_nd_chunk = 32
+            eff_nd_min = 256 * 256
+        super().__init__(
+            params, lr=lr, eps=eps, clip_threshold=clip_threshold, betas=betas, weight_decay=weight_decay,
+            block_size=block_size, prefer_factored_cuda_ext_path=prefer_factored_cuda_ext_path,
+            cuda_factored_nd_chunk_size_override=eff_nd_chunk,
+            cuda_factored_nd_chunked_direct_row_sum_min_matrix_numel=eff_nd_min,
+            cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel=cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel,
+            cuda_nonfactored_use_fp16_update=eff_nf_fp16,
+        )
+        self.cuda_1d_runtime_mode = cuda_1d_runtime_mode
+        self.cuda_nd_runtime_mode = cuda_nd_runtime_mode
+        self.prefer_cuda_fast_path = bool(prefer_cuda_fast_path)
+        self.prefer_cuda_2d_fast_path = (
+            self.prefer_cuda_fast_path if prefer_cuda_2d_fast_path is None else bool(prefer_cuda_2d_fast_path))
+        self.prefer_cuda_1d_batched_fast_path = bool(eff_1d_batched)
+        self.prefer_cuda_1d_multitensor_fast_path = bool(eff_1d_mt)
+        self.cuda_1d_batched_use_fp16_update = bool(eff_1d_fp16)
+        self.prefer_cuda_1d_fast_path = (
+            self.prefer_cuda_1d_batched_fast_path if eff_1d_fast is None else bool(eff_1d_fast))
+        self.cuda_1d_batched_chunk_size = int(cuda_1d_batched_chunk_size)
+        self.cuda_1d_batched_min_bucket_size = int(eff_min_bucket)
+        self.cuda_1d_batched_min_numel = int(cuda_1d_batched_min_numel)
+        self.cuda_1d_batched_max_numel = int(cuda_1d_batched_max_numel)
+        if self.cuda_1d_batched_chunk_size <= 0:
+            raise ValueError("cuda_1d_batched_chunk_size must be positive")
+        if self.cuda_1d_batched_min_bucket_size <= 0:
+            raise ValueError("cuda_1d_batched_min_bucket_size must be positive")
+        if self.cuda_1d_batched_min_numel <= 0 or self.cuda_1d_batched_max_numel < self.cuda_1d_batched_min_numel:
+            raise ValueError("cuda_1d_batched_min_numel/max_numel must define a positive range")
+        self.cuda_graph_compatible = bool(cuda_graph_compatible)
+        self.experimental_cuda_tuning_overrides = overrides
+
+    @classmethod
+    def _experimental_cuda_tuning_overrides(cls, **kwargs) -> tuple[str, ...]:
+        return tuple(k for k, default in cls.EXPERIMENTAL_CUDA_TUNING_DEFAULTS.items() if kwargs[k] != default)
+
+    @torch.no_grad()
+    def prime_for_cuda_graph(self) -> None:
+        """Create every state and the workspace before capture (CAME8bit.py:672-693)."""
+        for group in self.param_groups:
+            block_size = group["block_size"]
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                if p.grad.is_sparse:
+                    raise RuntimeError("CAME does not support sparse gradients.")
+                if not (p.data.is_contiguous() and p.grad.is_contiguous()):
+                    raise RuntimeError("CUDA graph capture requires contiguous parameter and gradient tensors.")
+                self._prepare_param(p, block_size)

@@ -1,0 +1,178 @@
+/*
+ * came8.h -- C ABI of the MI355X CAME 8-bit optimizer step (libcame8.so).
+ *
+ * Plain pointers, sizes and a hipStream_t; no torch types.  The caller owns
+ * every buffer: parameters, gradients, the quantised optimizer state and a
+ * workspace sized by came8_workspace_size().  All launches are asynchronous
+ * on the given stream; no call synchronises the host with the device.
+ *
+ * Reference interfaces replaced (paths relative to the reference tree):
+ *   came8_step           -- the per-parameter CUDA chains that the full8bit
+ *                           optimizers run for one step:
+ *                           came_full_factored_sq_step          came_pytorch/came_cuda/csrc/came_bindings.cpp:1406-1453
+ *                           came_full_factored_expavg_res_prepare              came_bindings.cpp:1589-1633
+ *                           came_full_factored_res_step                        came_bindings.cpp:1507-1549
+ *                           came_full_factored_param_update                    came_bindings.cpp:1675-1691
+ *                           came_full_nonfactored_step                         came_bindings.cpp:856-915
+ *                           came_full_factored_step_multitensor_same_shape_ptrs came_bindings.cpp:1795-1907
+ *                           came_full_nonfactored_step_multitensor_ptrs        came_bindings.cpp:1170-1222
+ *                         (Python wrappers: came_pytorch/came_cuda/__init__.py:253-963;
+ *                          arithmetic: came_pytorch/CAME8bitFull.py:1006-1075).
+ *   came8_quantize_blockwise / came8_dequantize_blockwise
+ *                        -- blockwise_quant / blockwise_dequant
+ *                           came_bindings.cpp:756-801 (Python: came_cuda/__init__.py:205-228;
+ *                           arithmetic: came_pytorch/blockwise_quantization.py:66-82,112-124).
+ *
+ * Errors: every entry point returns CAME8_OK (0) or a negative CAME8_E* code;
+ * came8_last_error() returns the message of the last failure on the calling
+ * thread (the reference raised RuntimeError from TORCH_CHECK with that text).
+ */
+#ifndef CAME8_H
+#define CAME8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CAME8_ABI_VERSION 1
+
+/* element types of parameters and gradients */
+#define CAME8_F32 0
+#define CAME8_BF16 1
+#define CAME8_F16 2
+
+/* status codes */
+#define CAME8_OK 0
+#define CAME8_EINVAL (-1)   /* bad argument: shape, dtype, block size, null pointer */
+#define CAME8_ESPACE (-2)   /* workspace smaller than came8_workspace_size() */
+#define CAME8_EHIP (-3)     /* a HIP runtime call failed */
+
+/* flags for came8_hparams.flags */
+#define CAME8_FLAG_REFERENCE_NORM 1u /* clip RMS summed in the reference CPU order (slow; parity runs) */
+
+/*
+ * One parameter tensor and its full8bit state, laid out exactly as the
+ * reference's CPU branch of CAME8bitFull._init_state keeps it
+ * (came_pytorch/CAME8bitFull.py:748-788, 919-923):
+ *
+ *   shape S = (..., R, C), numel N = P*R*C with P = prod(S[:-2]) (P = 1 for 2-D).
+ *   exp_avg_q        int8   [N]                 (row-major, flat 256-element blocks)
+ *   exp_avg_absmax   f32    [ceil(N/B)]
+ *   factored (ndim >= 2):
+ *     row_q          uint8  [2][P*R]  ([0] = exp_avg_sq_row, [1] = exp_avg_res_row)
+ *     row_absmax     f32    [2][ceil(P*R/B)]
+ *     col_q          uint8  [2][P*C]  ([0] = exp_avg_sq_col, [1] = exp_avg_res_col)
+ *     col_absmax     f32    [2][ceil(P*C/B)]
+ *   non-factored (ndim == 1; R = 1, C = N, P = 1):
+ *     row_q          uint8  [N]       (exp_avg_sq_q)
+ *     row_absmax     f32    [ceil(N/B)] (exp_avg_sq_absmax)
+ *     col_q, col_absmax unused (NULL)
+ *
+ * param and grad are contiguous; param is updated in place.
+ */
+typedef struct came8_tensor {
+  void* param;
+  const void* grad;
+  int8_t* exp_avg_q;
+  float* exp_avg_absmax;
+  uint8_t* row_q;
+  float* row_absmax;
+  uint8_t* col_q;
+  float* col_absmax;
+  int64_t prefix; /* P */
+  int64_t rows;   /* R */
+  int64_t cols;   /* C */
+  int32_t param_dtype; /* CAME8_F32 / CAME8_BF16 / CAME8_F16 */
+  int32_t grad_dtype;
+  int32_t factored;    /* 1 for ndim >= 2, 0 for 1-D */
+  int32_t reserved;
+} came8_tensor;
+
+/* Hyper-parameters of one param group (the reference's group keys, as Python floats). */
+typedef struct came8_hparams {
+  double lr;
+  double beta1, beta2, beta3;
+  double eps0, eps1;
+  double clip_threshold;
+  double weight_decay;
+  int32_t block_size;
+  uint32_t flags;
+} came8_hparams;
+
+/* Library identification. */
+const char* came8_version(void);
+int came8_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* came8_last_error(void);
+
+/*
+ * Bytes of device workspace came8_step needs for this tensor list and block
+ * size.  Depends only on shapes, dtypes and block size.
+ */
+int came8_workspace_size(const came8_tensor* tensors, int32_t n_tensors, int32_t block_size, size_t* bytes);
+
+/*
+ * Forget every cached launch plan for `workspace` (call when freeing it; frees
+ * the host copies the library keeps of its uploads).  No reference
+ * counterpart: the reference rebuilt pointer tables on every call
+ * (came_pytorch/came_cuda/csrc/came_bindings.cpp:461-478).
+ */
+int came8_release_workspace(const void* workspace);
+
+/*
+ * One CAME 8-bit step over all tensors of a param group: the factored update
+ * (row/column second moments, update-RMS clip, beta1 momentum, confidence
+ * residual, weight decay, parameter write) for ndim >= 2 tensors, the
+ * unfactored update for 1-D tensors, and blockwise int8/uint8 requantisation
+ * of every state.  Arithmetic follows came_pytorch/CAME8bitFull.py:1006-1075.
+ * Enqueued on `stream`; returns before the device finishes.
+ *
+ * The head of the workspace holds the launch plan.  `workspace_tag` names the
+ * caller's current allocation of `workspace` (a value it never reuses for
+ * another allocation, e.g. a process-wide counter): with a nonzero tag the
+ * plan is re-uploaded only when the tensor list (pointers, shapes, dtypes) or
+ * the block size changes, and the caller must not write to the workspace
+ * between calls; tag 0 uploads on every call.
+ */
+int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hparams* hp,
+               void* workspace, size_t workspace_bytes, uint64_t workspace_tag, void* stream);
+
+/*
+ * Per-kernel device timing.  While enabled, every launch of came8_step is
+ * bracketed by HIP events recorded on the launch stream; came8_profile_read
+ * waits for the recorded events and returns, per kernel phase, the number of
+ * launches, their summed device time and their summed algorithmic bytes (each
+ * operand the kernel must touch counted once).  No reference counterpart
+ * beyond its host-side dispatch timing (came_pytorch/CAME8bit.py:695-710).
+ */
+typedef struct came8_phase_stat {
+  char name[32];
+  int64_t launches;
+  double total_ms;
+  double alg_bytes;
+} came8_phase_stat;
+
+int came8_profile_enable(int32_t on);
+int came8_profile_read(came8_phase_stat* out, int32_t max_phases, int32_t* n_phases, int32_t reset);
+
+/*
+ * Blockwise absmax quantisation of n fp32 values into int8 (is_signed, Q = 127)
+ * or uint8 (Q = 255) codes with one fp32 absmax per block of block_size
+ * (came_pytorch/blockwise_quantization.py:66-82).
+ */
+int came8_quantize_blockwise(const float* x, int64_t n, int32_t is_signed, int32_t block_size,
+                             void* q, float* absmax, void* stream);
+
+/* Inverse: out[i] = q[i] * (absmax[i / block_size] / Q)  (blockwise_quantization.py:112-124). */
+int came8_dequantize_blockwise(const void* q, const float* absmax, int64_t n, int32_t is_signed,
+                               int32_t block_size, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CAME8_H */

@@ -121,11 +121,21 @@ def _rms(t: torch.Tensor) -> torch.Tensor:
 @torch.no_grad()
 def full8bit_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *, beta1: float, beta2: float,
                   beta3: float, eps0: float, eps1: float, lr: float, clip_threshold: float,
-                  weight_decay: float, block_size: int) -> None:
+                  weight_decay: float, block_size: int, capture: Dict[str, torch.Tensor] | None = None,
+                  exact_norm: bool = False) -> None:
     """One CPU full8bit step on parameter ``p`` (in place) and state ``st`` (in place).
 
     Follows reference CAME8bitFull.py:962-966 (step/RMS bookkeeping) and
-    :1006-1075 (the arithmetic), in the same operation order.
+    :1006-1075 (the arithmetic), in the same operation order.  If ``capture``
+    is a dict it receives the fp32 states just before they are requantised
+    (keys ``exp_avg``, ``sq_row``/``sq_col``/``res_row``/``res_col`` or ``sq``)
+    and the clip divisor; capturing does not change any result.
+
+    ``exact_norm=True`` replaces the reference's float32 ``norm(2)`` (whose
+    accumulation error reaches ~1e-4 relative on multi-million-element
+    tensors) by sqrt of the fp64 sum of squares rounded to float32: the
+    definition the GPU's default mode implements.  Every other operation is
+    unchanged.
     """
     st["step"] += 1
     st["RMS"] = _rms(p)
@@ -149,7 +159,13 @@ def full8bit_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *,
         sq.mul_(beta2).add_(upd, alpha=1.0 - beta2)
         upd = sq.clamp_min_(1e-30).rsqrt().mul_(grad)
 
-    upd.div_((_rms(upd) / clip_threshold).clamp_(min=1.0))
+    if exact_norm:
+        norm = torch.tensor(math.sqrt(float((upd.double() ** 2).sum())), dtype=torch.float32)
+        rms = norm / (upd.numel() ** 0.5)
+    else:
+        rms = _rms(upd)
+    clipv = (rms / clip_threshold).clamp_(min=1.0)
+    upd.div_(clipv)
     m.mul_(beta1).add_(upd, alpha=1.0 - beta1)
     res = (upd - m) ** 2 + eps1
     if factored:
@@ -165,6 +181,14 @@ def full8bit_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *,
         p.add_(p, alpha=-weight_decay * lr)
     p.add_(step_dir, alpha=-lr)
 
+    if capture is not None:
+        capture["clip"] = clipv.clone()
+        capture["exp_avg"] = m.clone()
+        if factored:
+            capture.update(sq_row=sq_row.clone(), sq_col=sq_col.clone(), res_row=res_row.clone(),
+                           res_col=res_col.clone())
+        else:
+            capture["sq"] = sq.clone()
     q, a = quantize_blockwise(m, signed=True, block_size=bs)
     st["exp_avg_q"].copy_(q)
     st["exp_avg_absmax"].copy_(a)

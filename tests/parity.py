@@ -1,0 +1,314 @@
+"""Shared helpers for the parity tests: run the GPU optimizer and the CPU oracle on the same inputs
+and compare state and parameters under the tolerances the tests state."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from collections import namedtuple
+
+from oracle import came8_oracle as orc
+
+Lockstep = namedtuple("Lockstep", "gpu_param ref_param gpu_state ref_state tainted flips movement")
+
+HP_DEFAULTS = dict(lr=None, eps=(1e-30, 1e-16), clip_threshold=1.0, betas=(0.9, 0.999, 0.9999),
+                   weight_decay=0.0, block_size=256)
+
+
+def oracle_hp(hp: dict) -> dict:
+    h = dict(HP_DEFAULTS)
+    h.update(hp)
+    b1, b2, b3 = h["betas"]
+    return dict(beta1=b1, beta2=b2, beta3=b3, eps0=h["eps"][0], eps1=h["eps"][1], lr=h["lr"],
+                clip_threshold=h["clip_threshold"], weight_decay=h["weight_decay"], block_size=h["block_size"])
+
+
+STATE_KEYS = ("exp_avg_q", "exp_avg_absmax", "factored_row_q", "factored_row_absmax", "factored_col_q",
+              "factored_col_absmax", "exp_avg_sq_q", "exp_avg_sq_absmax")
+
+
+def code_mismatch(a: torch.Tensor, b: torch.Tensor):
+    """(fraction of codes that differ, max |difference|)."""
+    a = a.detach().cpu().to(torch.int32).reshape(-1)
+    b = b.detach().cpu().to(torch.int32).reshape(-1)
+    if a.numel() == 0:
+        return 0.0, 0
+    d = (a - b).abs()
+    return float((d != 0).float().mean()), int(d.max())
+
+
+def rel_err(a: torch.Tensor, b: torch.Tensor):
+    """(max elementwise |a-b|/|b| over |b| > tiny, ||a-b|| / ||b||)."""
+    a = a.detach().cpu().double().reshape(-1)
+    b = b.detach().cpu().double().reshape(-1)
+    if a.numel() == 0:
+        return 0.0, 0.0
+    nb = b.norm().item()
+    normrel = (a - b).norm().item() / nb if nb > 0 else (a - b).norm().item()
+    mask = b.abs() > 1e-30
+    if mask.any():
+        m = ((a - b).abs()[mask] / b.abs()[mask]).max().item()
+    else:
+        m = 0.0
+    m = max(m, (a - b).abs()[~mask].max().item() if (~mask).any() else 0.0)
+    return m, normrel
+
+
+def param_err(a: torch.Tensor, b: torch.Tensor) -> float:
+    """max_i |a_i - b_i| / (|b_i| + 1e-2 * rms(b)) for fp32 parameters.
+
+    A bound of 1e-5 on this reads "within 1e-5 relative, or within ~1e-7 of the tensor's RMS"
+    (about one fp32 ulp at the parameter scale).  The floor matters where p - lr*step cancels to
+    a value near zero: there a one-ulp difference in the step direction is a large relative
+    difference of the (tiny) result while being an ulp-level difference of the update.
+    """
+    a = a.detach().cpu().double().reshape(-1)
+    b = b.detach().cpu().double().reshape(-1)
+    if a.numel() == 0:
+        return 0.0
+    rms = b.pow(2).mean().sqrt().item()
+    return ((a - b).abs() / (b.abs() + 1e-2 * rms + 1e-38)).max().item()
+
+
+def lowp_close(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """bf16/fp16 parameters: every element within 1 ulp, or (cancellation to near zero) within 1e-7 of the RMS."""
+    ai = a.detach().cpu().contiguous().view(torch.int16).to(torch.int32).reshape(-1)
+    bi = b.detach().cpu().contiguous().view(torch.int16).to(torch.int32).reshape(-1)
+    if ai.numel() == 0:
+        return True
+
+    def ordered(x):
+        return torch.where(x < 0, -(x & 0x7FFF), x)
+
+    ulps = (ordered(ai) - ordered(bi)).abs()
+    af, bf = a.detach().cpu().double().reshape(-1), b.detach().cpu().double().reshape(-1)
+    rms = bf.pow(2).mean().sqrt().item()
+    ok = (ulps <= 1) | ((af - bf).abs() <= 1e-7 * rms)
+    return bool(ok.all())
+
+
+def ulp_diff_lowp(a: torch.Tensor, b: torch.Tensor) -> int:
+    """Max distance in units in the last place between two bf16/fp16 tensors of the same dtype."""
+    ai = a.detach().cpu().contiguous().view(torch.int16).to(torch.int32).reshape(-1)
+    bi = b.detach().cpu().contiguous().view(torch.int16).to(torch.int32).reshape(-1)
+
+    def ordered(x):  # sign-magnitude -> two's complement ordering
+        return torch.where(x < 0, -(x & 0x7FFF), x)
+
+    if ai.numel() == 0:
+        return 0
+    return int((ordered(ai) - ordered(bi)).abs().max())
+
+
+def _ref_values(k: str, ref_fp32: dict):
+    """fp32 values the reference quantised into code array `k` (stacked like the codes)."""
+    if k == "exp_avg_q":
+        return ref_fp32["exp_avg"], True
+    if k == "exp_avg_sq_q":
+        return ref_fp32["sq"], False
+    if k == "factored_row_q":
+        return torch.stack([ref_fp32["sq_row"], ref_fp32["res_row"]]), False
+    if k == "factored_col_q":
+        return torch.stack([ref_fp32["sq_col"], ref_fp32["res_col"]]), False
+    raise KeyError(k)
+
+
+def tie_distance(k: str, ref_state: dict, ref_fp32: dict, block: int) -> torch.Tensor:
+    """|frac(scaled) - 0.5| of the reference's scaled value (x / absmax) * Q for every code of `k`."""
+    vals, signed = _ref_values(k, ref_fp32)
+    ak = k.replace("_q", "_absmax")
+    absmax = ref_state[ak]
+    rows = vals.reshape(absmax.shape[0], -1) if absmax.dim() == 2 else vals.reshape(1, -1)
+    am = absmax.reshape(rows.shape[0], -1)
+    out = []
+    for rv, a in zip(rows, am):
+        scale = a.repeat_interleave(block)[: rv.numel()]
+        scaled = (rv.float() / scale) * (127.0 if signed else 255.0)
+        out.append((scaled - scaled.floor() - 0.5).abs())
+    return torch.stack(out).reshape(ref_state[k].shape)
+
+
+def compare_states(gpu_state: dict, ref_state: dict, *, code_frac: float, abs_rel: float, where: str,
+                   ref_fp32: dict | None = None, tie_tol: float | None = None, block: int = 256,
+                   max_code_diff: int = 1):
+    """Codes: never more than 1 apart, at most max(2, code_frac * n) differ, and (given the oracle's
+    pre-quantisation values) every differing code sits within `tie_tol` of a rounding tie of the
+    reference's scaled value; block scales within `abs_rel` relative."""
+    report = {}
+    for k in STATE_KEYS:
+        if k not in ref_state:
+            continue
+        g, r = gpu_state[k].detach().cpu(), ref_state[k]
+        assert g.dtype == r.dtype and tuple(g.shape) == tuple(r.shape), f"{where}/{k}: {g.dtype}{tuple(g.shape)} vs {r.dtype}{tuple(r.shape)}"
+        if k.endswith("_q"):
+            frac, mx = code_mismatch(g, r)
+            report[k] = (frac, mx)
+            assert mx <= max_code_diff, f"{where}/{k}: a code differs by {mx}"
+            n = max(1, g.numel())
+            assert frac * n <= max(2.0, code_frac * n), f"{where}/{k}: {frac:.3e} of codes differ (bound {code_frac})"
+            if ref_fp32 is not None and tie_tol is not None and mx > 0:
+                dist = tie_distance(k, ref_state, ref_fp32, block)
+                diff = g.to(torch.int32) != r.to(torch.int32)
+                worst = dist[diff].max().item()
+                assert worst <= tie_tol, f"{where}/{k}: a differing code is {worst:.2e} from a rounding tie (> {tie_tol})"
+        else:
+            m, _ = rel_err(g, r)
+            report[k] = m
+            assert m <= abs_rel, f"{where}/{k}: block scale rel err {m:.3e} > {abs_rel}"
+    return report
+
+
+def make_params(shapes, dtype, seed, device="cpu"):
+    gen = torch.Generator().manual_seed(seed)
+    return [(torch.randn(s, generator=gen) * 0.02).to(dtype) for s in shapes]
+
+
+def heavy_grad(gen, shape, dtype):
+    """Student-t(2) * 1e-3 with 10% exact zeros and ~1 outlier of +-1e3 per 256 elements."""
+    z = torch.randn(shape, generator=gen)
+    chi = torch.randn((2,) + tuple(shape), generator=gen)
+    g = z / torch.sqrt((chi ** 2).mean(dim=0)) * 1e-3
+    g = torch.where(torch.rand(shape, generator=gen) < 0.1, torch.zeros_like(g), g)
+    flat = g.reshape(-1)
+    n = flat.numel()
+    if n >= 16:
+        pick = torch.randint(0, n, (max(1, n // 256),), generator=gen)
+        flat[pick] = torch.where(torch.rand(pick.shape, generator=gen) < 0.5, -1e3, 1e3)
+    return g.to(dtype)
+
+
+def run_oracle(params, grads_per_step, hp: dict, steps: int):
+    """CPU oracle over `steps` steps; returns (params, states)."""
+    ohp = oracle_hp(hp)
+    ps = [p.clone() for p in params]
+    sts = [orc.init_full8bit_state(p.shape, ohp["block_size"]) for p in ps]
+    for s in range(steps):
+        for p, g, st in zip(ps, grads_per_step[s], sts):
+            orc.full8bit_step(p, g, st, **ohp)
+    return ps, sts
+
+
+def run_gpu(cls, params, grads_per_step, hp: dict, steps: int, reference_norm=False, device="cuda"):
+    ps = [torch.nn.Parameter(p.clone().to(device)) for p in params]
+    kw = {k: v for k, v in hp.items()}
+    opt = cls(ps, **kw)
+    opt.reference_norm = reference_norm
+    for s in range(steps):
+        for p, g in zip(ps, grads_per_step[s]):
+            p.grad = g.to(device)
+        opt.step()
+    torch.cuda.synchronize()
+    return ps, opt
+
+
+def run_lockstep(cls, params, grads_per_step, hp: dict, steps: int, reference_norm=False, device="cuda",
+                 exact_norm=False):
+    """GPU optimizer and CPU oracle side by side on the same inputs.
+
+    Returns, per tensor: (gpu_param, ref_param, gpu_state, ref_state, tainted, flips) where
+    `tainted` marks elements whose inputs to a later step differed because an 8-bit code of
+    theirs (momentum, or the row/column second-moment or residual state of their row/column)
+    came out one apart at an earlier step, and `flips` is the per-step fraction of differing
+    momentum codes.  A code flip moves the element's later updates by up to absmax/127 of the
+    momentum times the residual factor, so untainted elements are held to the tight bound and
+    tainted ones are only counted.
+    """
+    ohp = oracle_hp(hp)
+    ps = [torch.nn.Parameter(p.clone().to(device)) for p in params]
+    opt = cls(ps, **hp)
+    opt.reference_norm = reference_norm
+    refs = [p.clone() for p in params]
+    sts = [orc.init_full8bit_state(p.shape, ohp["block_size"]) for p in refs]
+    tainted = [torch.zeros(p.shape, dtype=torch.bool) for p in params]
+    movement = [torch.zeros(p.shape, dtype=torch.float64) for p in params]
+    flips = [[] for _ in params]
+    for s in range(steps):
+        for p, g in zip(ps, grads_per_step[s]):
+            p.grad = g.to(device)
+        opt.step()
+        torch.cuda.synchronize()
+        for i, (r, g, st) in enumerate(zip(refs, grads_per_step[s], sts)):
+            before = r.double()
+            orc.full8bit_step(r, g, st, exact_norm=exact_norm, **ohp)
+            movement[i] += (r.double() - before).abs()
+            gs = opt.state[ps[i]]
+            dq = gs["exp_avg_q"].cpu() != st["exp_avg_q"]
+            flips[i].append(float(dq.float().mean()))
+            t = dq.clone()
+            if st["factored"]:
+                shape = tuple(r.shape)
+                rowd = (gs["factored_row_q"].cpu() != st["factored_row_q"]).any(dim=0)  # shape[:-1]
+                cold = (gs["factored_col_q"].cpu() != st["factored_col_q"]).any(dim=0)  # shape[:-2]+(C,)
+                t |= rowd.unsqueeze(-1).expand(shape)
+                t |= cold.unsqueeze(-2).expand(shape)
+            else:
+                t |= gs["exp_avg_sq_q"].cpu() != st["exp_avg_sq_q"]
+            tainted[i] |= t
+    return [Lockstep(ps[i].data, refs[i], opt.state[ps[i]], sts[i], tainted[i], flips[i], movement[i])
+            for i in range(len(ps))]
+
+
+def check_untainted_params(gp: torch.Tensor, rp: torch.Tensor, tainted: torch.Tensor, where: str,
+                           movement: torch.Tensor | None = None, tol: float = 1e-5) -> float:
+    """Untainted elements, fp32: |dp| <= 1e-5 * (|p_ref| + sum_steps |p_ref step change|) + 1e-7 * rms(p_ref);
+    bf16/fp16: within 1 ulp, or within that bound.  Returns the tainted fraction.
+
+    Relative to the movement as well as to the value: where lr*|step| is comparable to or larger
+    than |p| (small matrices, whose residual factors are large), an ulp-level relative difference
+    of the update is that large relative to the parameter scale."""
+    keep = ~tainted.reshape(-1)
+    g = gp.detach().cpu().reshape(-1)
+    r = rp.detach().cpu().reshape(-1)
+    mv = torch.zeros(r.shape, dtype=torch.float64) if movement is None else movement.reshape(-1)
+    if keep.any():
+        rd, gd = r.double(), g.double()
+        rms = rd.pow(2).mean().sqrt().item()
+        err = ((gd - rd).abs() / (rd.abs() + mv + 1e-2 * rms + 1e-38))
+        if r.dtype == torch.float32:
+            worst = err[keep].max().item()
+            assert worst <= tol, f"{where}: untainted param err {worst:.3e} > {tol}"
+        else:
+            ai = g.contiguous().view(torch.int16).to(torch.int32)
+            bi = r.contiguous().view(torch.int16).to(torch.int32)
+            ordered = lambda x: torch.where(x < 0, -(x & 0x7FFF), x)  # noqa: E731
+            ulps = (ordered(ai) - ordered(bi)).abs()
+            ok = (ulps <= 1) | (err <= tol)
+            assert bool(ok[keep].all()), f"{where}: untainted low-precision params beyond 1 ulp (max {int(ulps[keep].max())})"
+    return float(tainted.float().mean())
+
+
+def run_teacher_forced(cls, params, grads_per_step, hp: dict, steps: int, reference_norm=False, device="cuda",
+                       check=None):
+    """Every step starts the GPU from the oracle's state and parameters of the previous step, so each
+    step's arithmetic is compared on identical inputs (no divergence carried from earlier code flips).
+    The oracle uses the reference's float32 norm in parity mode and the exactly rounded norm otherwise.
+    `check(step, i, gpu_param, ref_param, gpu_state, ref_state, movement)` is called per tensor."""
+    ohp = oracle_hp(hp)
+    ps = [torch.nn.Parameter(p.clone().to(device)) for p in params]
+    opt = cls(ps, **hp)
+    opt.reference_norm = reference_norm
+    refs = [p.clone() for p in params]
+    sts = [orc.init_full8bit_state(p.shape, ohp["block_size"]) for p in refs]
+    for s in range(steps):
+        with torch.no_grad():
+            for p, r, st in zip(ps, refs, sts):
+                p.data.copy_(r.to(device))
+                gst = opt.state[p]
+                if len(gst):
+                    for k in STATE_KEYS:
+                        if k in st:
+                            gst[k].copy_(st[k].to(device))
+        for p, g in zip(ps, grads_per_step[s]):
+            p.grad = g.to(device)
+        opt.step()
+        torch.cuda.synchronize()
+        for i, (r, g, st) in enumerate(zip(refs, grads_per_step[s], sts)):
+            before = r.double()
+            cap = {}
+            orc.full8bit_step(r, g, st, capture=cap, exact_norm=not reference_norm, **ohp)
+            mv = (r.double() - before).abs()
+            if check is not None:
+                check(s + 1, i, ps[i].data, r, opt.state[ps[i]], st, mv, cap)
+    return ps, opt, refs, sts

@@ -1,0 +1,177 @@
+"""CPU-side checks of the product package: the C-ABI library loads and exports every symbol
+include/came8.h declares, argument validation returns the documented error codes before any device
+work, and the optimizer classes keep the reference's constructor validation and state layout."""
+import ctypes
+import os
+import re
+import warnings
+
+import pytest
+import torch
+
+import came_amd
+from came_amd import _lib as L
+from oracle import came8_oracle as orc
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    src = open(os.path.join(ROOT, "include", "came8.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(came8_\w+)\s*\(", src, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.load()
+    declared = _header_functions()
+    assert set(declared) == set(L.EXPORTED_SYMBOLS), declared
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.came8_abi_version() == 1
+    assert b"gfx950" in lib.came8_version()
+
+
+def _desc(shape, dtype=L.CAME8_F32, fake=0x100000):
+    d = L.Came8Tensor()
+    d.param, d.grad = fake, fake + 0x10000000
+    d.exp_avg_q, d.exp_avg_absmax = fake + 0x20000000, fake + 0x30000000
+    d.row_q, d.row_absmax = fake + 0x40000000, fake + 0x50000000
+    if len(shape) >= 2:
+        d.col_q, d.col_absmax = fake + 0x60000000, fake + 0x70000000
+        d.prefix = int(torch.tensor(shape[:-2]).prod().item()) if len(shape) > 2 else 1
+        d.rows, d.cols, d.factored = shape[-2], shape[-1], 1
+    else:
+        d.prefix, d.rows, d.cols, d.factored = 1, 1, shape[0], 0
+    d.param_dtype = d.grad_dtype = dtype
+    return d
+
+
+def test_workspace_size_host_only():
+    lib = L.load()
+    arr = (L.Came8Tensor * 3)(_desc((4096, 4096), L.CAME8_BF16), _desc((4096,)), _desc((2, 3, 5, 7)))
+    out = ctypes.c_size_t(0)
+    assert lib.came8_workspace_size(arr, 3, 256, ctypes.byref(out)) == L.CAME8_OK
+    # column partials dominate: 3 arrays of (4096/128 bands) x 4096 fp32 for the matrix
+    assert 3 * 32 * 4096 * 4 < out.value < 64 << 20
+    assert lib.came8_workspace_size(arr, 0, 256, ctypes.byref(out)) == L.CAME8_OK
+
+
+@pytest.mark.parametrize("bad", ["block", "shape", "dtype", "null"])
+def test_invalid_arguments_are_rejected(bad):
+    lib = L.load()
+    d = _desc((8, 8))
+    block = 256
+    if bad == "block":
+        block = 0
+    elif bad == "shape":
+        d.rows = 0
+    elif bad == "dtype":
+        d.grad_dtype = 7
+    else:
+        d.exp_avg_q = 0
+    arr = (L.Came8Tensor * 1)(d)
+    out = ctypes.c_size_t(0)
+    assert lib.came8_workspace_size(arr, 1, block, ctypes.byref(out)) == L.CAME8_EINVAL
+    assert lib.came8_last_error()
+    hp = L.Came8HParams(1e-3, 0.9, 0.999, 0.9999, 1e-30, 1e-16, 1.0, 0.0, block, 0)
+    assert lib.came8_step(arr, 1, ctypes.byref(hp), 0x1000, 1 << 30, 0, None) == L.CAME8_EINVAL
+
+
+def test_step_rejects_small_workspace_and_bad_hparams():
+    lib = L.load()
+    arr = (L.Came8Tensor * 1)(_desc((64, 64)))
+    hp = L.Came8HParams(1e-3, 0.9, 0.999, 0.9999, 1e-30, 1e-16, 1.0, 0.0, 256, 0)
+    assert lib.came8_step(arr, 1, ctypes.byref(hp), 0x1000, 16, 0, None) == L.CAME8_ESPACE
+    hp.lr = 0.0
+    assert lib.came8_step(arr, 1, ctypes.byref(hp), 0x1000, 1 << 30, 0, None) == L.CAME8_EINVAL
+    hp.lr, hp.clip_threshold = 1e-3, -1.0
+    assert lib.came8_step(arr, 1, ctypes.byref(hp), 0x1000, 1 << 30, 0, None) == L.CAME8_EINVAL
+
+
+# --- constructor validation: messages of came_pytorch/CAME8bitFull.py:73-82, CAME8bit.py:94-206 ---
+P0 = [torch.nn.Parameter(torch.zeros(2, 2))]
+
+
+@pytest.mark.parametrize("cls", ["CAME8bit", "CAME8bitFull", "CAME8bitMemory"])
+@pytest.mark.parametrize("kw,msg", [
+    (dict(lr=0.0), "lr must be > 0"),
+    (dict(lr=1e-3, clip_threshold=0.0), "clip_threshold must be > 0"),
+    (dict(lr=1e-3, eps=(1e-30,)), "eps must be a tuple of length 2"),
+    (dict(lr=1e-3, betas=(0.9, 0.99)), "betas must be a tuple of length 3"),
+    (dict(lr=1e-3, block_size=0), "block_size must be > 0"),
+])
+def test_constructor_validation(cls, kw, msg):
+    with pytest.raises(ValueError, match=msg):
+        getattr(came_amd, cls)(P0, **kw)
+
+
+def test_came8bit_mode_validation_and_warning():
+    with pytest.raises(ValueError, match="cuda_1d_runtime_mode must be one of"):
+        came_amd.CAME8bit(P0, lr=1e-3, cuda_1d_runtime_mode="nope")
+    with pytest.raises(ValueError, match="cuda_nd_runtime_mode must be one of"):
+        came_amd.CAME8bit(P0, lr=1e-3, cuda_nd_runtime_mode="nope")
+    with pytest.raises(ValueError, match="cuda_1d_batched_chunk_size must be positive"):
+        came_amd.CAME8bit(P0, lr=1e-3, cuda_1d_batched_chunk_size=0)
+    with pytest.warns(RuntimeWarning, match="experimental"):
+        opt = came_amd.CAME8bit(P0, lr=1e-3, cuda_1d_batched_chunk_size=4)
+    assert opt.experimental_cuda_tuning_overrides == ("cuda_1d_batched_chunk_size",)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        opt = came_amd.CAME8bit(P0, lr=1e-3, cuda_1d_runtime_mode="repeated_fp16_pairmin")
+    assert opt.cuda_1d_batched_min_bucket_size == 2 and opt.prefer_cuda_1d_fast_path
+    opt = came_amd.CAME8bit(P0, lr=1e-3, cuda_nd_runtime_mode="chunk32_large_direct_row_sum")
+    assert opt.cuda_factored_nd_chunk_size_override == 32
+    assert opt.param_groups[0]["block_size"] == 256
+    assert set(opt.param_groups[0]) >= {"lr", "eps", "clip_threshold", "betas", "weight_decay", "block_size"}
+
+
+def test_cpu_parameters_are_refused():
+    p = torch.nn.Parameter(torch.zeros(4, 4))
+    opt = came_amd.CAME8bitFull([p], lr=1e-3)
+    p.grad = torch.zeros(4, 4)
+    with pytest.raises(RuntimeError, match="GPU"):
+        opt.step()
+
+
+@pytest.mark.parametrize("shape", [(7,), (5, 9), (2, 3, 5, 7), (300, 1000)])
+@pytest.mark.parametrize("block", [256, 64])
+def test_state_layout_matches_reference(shape, block):
+    opt = came_amd.CAME8bitFull([torch.nn.Parameter(torch.zeros(shape))], lr=1e-3, block_size=block)
+    st = {}
+    opt._init_state(st, torch.zeros(shape), block)
+    ref = orc.init_full8bit_state(shape, block)
+    for k, v in ref.items():
+        assert k in st, k
+        if isinstance(v, torch.Tensor):
+            assert st[k].dtype == v.dtype and tuple(st[k].shape) == tuple(v.shape), k
+            assert torch.equal(st[k], v), k
+        else:
+            assert st[k] == v, k
+    if len(shape) >= 2:
+        assert st["exp_avg_res_col_q"].data_ptr() == st["factored_col_q"][1].data_ptr()
+
+
+def test_load_state_dict_keeps_dtypes_mode_and_copies():
+    """torch's loader would cast codes and fp32 block scales to the parameter dtype and turn the
+    "_mode" string into a generator; the loaded state must equal the saved one, in its own memory."""
+    ps = [torch.nn.Parameter(torch.randn(130, 260).bfloat16()), torch.nn.Parameter(torch.randn(260).bfloat16())]
+    opt = came_amd.CAME8bitFull(ps, lr=2e-4)
+    for p in ps:
+        opt._init_state(opt.state[p], p, 256)
+        opt.state[p]["exp_avg_absmax"].uniform_(0.1, 1.0)
+        opt.state[p]["exp_avg_q"].random_(-127, 128)
+        opt.state[p]["step"] = 7
+    sd = opt.state_dict()
+    ps2 = [torch.nn.Parameter(p.data.clone()) for p in ps]
+    opt2 = came_amd.CAME8bitFull(ps2, lr=2e-4)
+    opt2.load_state_dict(sd)
+    for p, p2 in zip(ps, ps2):
+        a, b = opt.state[p], opt2.state[p2]
+        assert b["_mode"] == "full8bit" and b["step"] == 7 and b["factored"] == a["factored"]
+        for k, v in a.items():
+            if isinstance(v, torch.Tensor):
+                assert b[k].dtype == v.dtype and torch.equal(b[k], v), k
+                if k in ("exp_avg_q", "exp_avg_absmax"):
+                    assert b[k].data_ptr() != v.data_ptr(), k
+        if a["factored"]:
+            assert b["exp_avg_res_row_q"].data_ptr() == b["factored_row_q"][1].data_ptr()
