@@ -60,9 +60,9 @@ float round_to_f16(float f) { return float(_Float16(f)); }
 
 // Kernel-variant keys.
 struct BandKey {
-  int gdt, V, K;
+  int gdt, V, K, TPB;
   bool operator<(const BandKey& o) const {
-    return std::tie(gdt, V, K) < std::tie(o.gdt, o.V, o.K);
+    return std::tie(gdt, V, K, TPB) < std::tie(o.gdt, o.V, o.K, o.TPB);
   }
 };
 struct TypeKey {
@@ -107,26 +107,44 @@ int log2_or_minus1(int B) {
   return l;
 }
 
-// Choose (V, K) for the band passes of a factored tensor.
-void band_variant(const came8_tensor& t, int64_t C, int& V, int& K, bool& multiseg) {
+// Kernel shape of the band passes of a factored tensor: V elements per chunk (16 bytes of the
+// gradient type when rows are 16-byte aligned and a chunk never straddles a quantisation block,
+// else 1), K chunks per thread, TPB threads per workgroup.  `multiseg` when a row is wider than
+// one sweep of the workgroup.
+struct BandShapeSel {
+  int V, K, TPB;
+  bool multiseg;
+};
+
+BandShapeSel band_variant(const came8_tensor& t, int64_t C, int32_t B) {
   const int vw = t.grad_dtype == CAME8_F32 ? 4 : 8;
-  const bool aligned = (C % vw == 0) && (reinterpret_cast<uintptr_t>(t.grad) % 16 == 0) &&
+  const bool aligned = (C % vw == 0) && (B % vw == 0) && (reinterpret_cast<uintptr_t>(t.grad) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(t.exp_avg_q) % vw == 0);
-  V = aligned ? vw : 1;
-  const int64_t chunks = ceil_div(C, V);
-  static const int kv[] = {1, 2, 4, 8};
-  static const int k1[] = {1, 2, 4, 8, 16, 32};
-  const int* ks = V > 1 ? kv : k1;
-  const int nk = V > 1 ? 4 : 6;
-  for (int i = 0; i < nk; ++i) {
-    if (int64_t(kThreads) * ks[i] >= chunks) {
-      K = ks[i];
-      multiseg = false;
-      return;
+  BandShapeSel sel{aligned ? vw : 1, 0, 256, false};
+  const int64_t chunks = ceil_div(C, sel.V);
+  static const int vec_k[][2] = {{1, 256}, {2, 256}, {2, 512}, {3, 512}, {4, 512}};
+  static const int one_k[][2] = {{1, 256}, {2, 256}, {4, 256}, {8, 256}, {16, 256}, {32, 256}};
+  const int (*cand)[2] = sel.V > 1 ? vec_k : one_k;
+  const int nc = sel.V > 1 ? 5 : 6;
+  for (int i = 0; i < nc; ++i) {
+    if (int64_t(cand[i][0]) * cand[i][1] >= chunks) {
+      sel.K = cand[i][0];
+      sel.TPB = cand[i][1];
+      return sel;
     }
   }
-  K = ks[nk - 1];
-  multiseg = true;
+  sel.K = cand[nc - 1][0];
+  sel.TPB = cand[nc - 1][1];
+  sel.multiseg = true;
+  return sel;
+}
+
+// magic multiplier and shift for n / d with n < 2^31 (floor(2^s / d) + 1, s = 32 + ceil(log2 d))
+void magic_div(int64_t d, uint64_t& m, uint32_t& s) {
+  uint32_t l = 0;
+  while ((int64_t(1) << l) < d) ++l;
+  s = 32 + l;
+  m = uint64_t(((__uint128_t(1) << s) / uint64_t(d)) + 1);
 }
 
 int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refnorm, char* ws_base, Plan& plan) {
@@ -175,11 +193,13 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     struct Offs {
       size_t Rn, rfac, RRn, rrfac, Cn, cfac, CRn, crfac, pU, pW, pR, rm, rmr, clipp, clip;
     } o{};
+    d.idx32 = d.N < (int64_t(1) << 31) ? 1 : 0;
+    d.c8 = (d.C % 8 == 0) ? 1 : 0;
+    magic_div(d.C, d.mC, d.sC);
+    magic_div(d.R, d.mR, d.sR);
     if (t.factored) {
-      int V, K;
-      bool ms;
-      band_variant(t, d.C, V, K, ms);
-      d.rb = band_rows(d.R, d.C, ms);
+      const BandShapeSel sel = band_variant(t, d.C, B);
+      d.rb = band_rows(d.R, d.C, sel.multiseg);
       d.nbands = ceil_div(d.R, d.rb);
       d.nbr = std::max<int64_t>(1, ceil_div(d.P * d.R, B));
       d.nbc = std::max<int64_t>(1, ceil_div(d.P * d.C, B));
@@ -191,7 +211,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       o.pU = take(part); o.pW = take(part); o.pR = take(part);
       o.rm = take(size_t(d.P) * 4); o.rmr = take(size_t(d.P) * 4);
       o.clipp = take(size_t(d.nclip) * 8);
-      o.clip = take(4);
+      o.clip = take(8);
     } else {
       d.rb = 1;
       d.nbands = 1;
@@ -199,7 +219,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       d.nbc = 0;
       d.nclip = ceil_div(d.N, kTile);
       o.clipp = take(size_t(d.nclip) * 8);
-      o.clip = take(4);
+      o.clip = take(8);
     }
     scr_off[i] = scr;
     // store offsets temporarily as integers in the pointer fields (rebased below)
@@ -222,10 +242,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     const DevTensor& d = plan.dev[i];
     const TypeKey tk{t.param_dtype, t.grad_dtype};
     if (t.factored) {
-      int V, K;
-      bool ms;
-      band_variant(t, d.C, V, K, ms);
-      add_item(plan.band[BandKey{t.grad_dtype, V, K}], i, d.P * d.nbands);
+      const BandShapeSel sel = band_variant(t, d.C, B);
+      add_item(plan.band[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB}], i, d.P * d.nbands);
       add_item(plan.rowmean, i, d.P);
       add_item(plan.factor, i, d.nbr + d.nbc);
       if (fastB) add_item(plan.upd[tk], i, ceil_div(d.N, kTile));
@@ -346,28 +364,35 @@ Hp make_hp(const came8_hparams& h) {
 // ---------------------------------------------------------------------------
 // kernel-variant dispatch
 // ---------------------------------------------------------------------------
-template <typename TG>
 using BandFn = void (*)(const DevTensor*, const int32_t*, const int64_t*, int, Hp);
 
-template <typename TG, int V>
-BandFn<TG> band_fn_k(bool pass2, int K) {
-  switch (K) {
-    case 1: return pass2 ? k_fact_pass2<TG, V, 1> : k_fact_pass1<TG, V, 1>;
-    case 2: return pass2 ? k_fact_pass2<TG, V, 2> : k_fact_pass1<TG, V, 2>;
-    case 4: return pass2 ? k_fact_pass2<TG, V, 4> : k_fact_pass1<TG, V, 4>;
-    case 8: return pass2 ? k_fact_pass2<TG, V, 8> : k_fact_pass1<TG, V, 8>;
-    default: break;
-  }
-  if constexpr (V == 1) {
-    if (K == 16) return pass2 ? k_fact_pass2<TG, 1, 16> : k_fact_pass1<TG, 1, 16>;
-    if (K == 32) return pass2 ? k_fact_pass2<TG, 1, 32> : k_fact_pass1<TG, 1, 32>;
-  }
-  return nullptr;
+template <typename TG, int V, int K, int TPB>
+BandFn band_pick(bool pass2) {
+  return pass2 ? k_fact_pass2<TG, V, K, TPB> : k_fact_pass1<TG, V, K, TPB>;
 }
 
+// the (V, K, TPB) variants band_variant() can choose
 template <typename TG, int VW>
-BandFn<TG> band_fn(bool pass2, int V, int K) {
-  return V == 1 ? band_fn_k<TG, 1>(pass2, K) : band_fn_k<TG, VW>(pass2, K);
+BandFn band_fn(bool pass2, int V, int K, int TPB) {
+  if (V == 1 && TPB == 256) {
+    switch (K) {
+      case 1: return band_pick<TG, 1, 1, 256>(pass2);
+      case 2: return band_pick<TG, 1, 2, 256>(pass2);
+      case 4: return band_pick<TG, 1, 4, 256>(pass2);
+      case 8: return band_pick<TG, 1, 8, 256>(pass2);
+      case 16: return band_pick<TG, 1, 16, 256>(pass2);
+      case 32: return band_pick<TG, 1, 32, 256>(pass2);
+      default: return nullptr;
+    }
+  }
+  if (V == VW) {
+    if (TPB == 256 && K == 1) return band_pick<TG, VW, 1, 256>(pass2);
+    if (TPB == 256 && K == 2) return band_pick<TG, VW, 2, 256>(pass2);
+    if (TPB == 512 && K == 2) return band_pick<TG, VW, 2, 512>(pass2);
+    if (TPB == 512 && K == 3) return band_pick<TG, VW, 3, 512>(pass2);
+    if (TPB == 512 && K == 4) return band_pick<TG, VW, 4, 512>(pass2);
+  }
+  return nullptr;
 }
 
 using GenFn = void (*)(const DevTensor*, const int32_t*, const int64_t*, int, Hp);
@@ -578,13 +603,13 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
   for (auto& kv : plan.band) {
     const BandKey& k = kv.first;
     const WorkList& wl = kv.second;
-    void (*fn)(const DevTensor*, const int32_t*, const int64_t*, int, Hp) = nullptr;
-    if (k.gdt == CAME8_F32) fn = band_fn<F32, 4>(false, k.V, k.K);
-    if (k.gdt == CAME8_BF16) fn = band_fn<BF16, 8>(false, k.V, k.K);
-    if (k.gdt == CAME8_F16) fn = band_fn<F16, 8>(false, k.V, k.K);
+    BandFn fn = nullptr;
+    if (k.gdt == CAME8_F32) fn = band_fn<F32, 4>(false, k.V, k.K, k.TPB);
+    if (k.gdt == CAME8_BF16) fn = band_fn<BF16, 8>(false, k.V, k.K, k.TPB);
+    if (k.gdt == CAME8_F16) fn = band_fn<F16, 8>(false, k.V, k.K, k.TPB);
     if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
     { PhaseTimer pt(PH_PASS1, alg_bytes(plan, wl, tensors, PH_PASS1), stream);
-    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
     if ((rc = check_launch("pass1")) != CAME8_OK) return rc; }
   }
   for (auto& kv : plan.vecA) {
@@ -628,12 +653,13 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     for (auto& kv : plan.band) {
       const BandKey& k = kv.first;
       const WorkList& wl = kv.second;
-      void (*fn)(const DevTensor*, const int32_t*, const int64_t*, int, Hp) = nullptr;
-      if (k.gdt == CAME8_F32) fn = band_fn<F32, 4>(true, k.V, k.K);
-      if (k.gdt == CAME8_BF16) fn = band_fn<BF16, 8>(true, k.V, k.K);
-      if (k.gdt == CAME8_F16) fn = band_fn<F16, 8>(true, k.V, k.K);
+      BandFn fn = nullptr;
+      if (k.gdt == CAME8_F32) fn = band_fn<F32, 4>(true, k.V, k.K, k.TPB);
+      if (k.gdt == CAME8_BF16) fn = band_fn<BF16, 8>(true, k.V, k.K, k.TPB);
+      if (k.gdt == CAME8_F16) fn = band_fn<F16, 8>(true, k.V, k.K, k.TPB);
+      if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
       { PhaseTimer pt(PH_PASS2, alg_bytes(plan, wl, tensors, PH_PASS2), stream);
-    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("pass2")) != CAME8_OK) return rc; }
     }
     const WorkList& rm = plan.rowmean;

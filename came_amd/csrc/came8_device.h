@@ -23,16 +23,12 @@ struct F32 {
   static __device__ __forceinline__ storage store(float f) { return f; }
 };
 
-// bfloat16 with round-to-nearest-even and NaN -> 0x7FC0, the rounding c10::BFloat16 applies.
+// bfloat16: the conversion from fp32 rounds to nearest even (gfx950's v_cvt_pk_bf16_f32), the
+// rounding c10::BFloat16 applies to every non-NaN value.
 struct BF16 {
   using storage = uint16_t;
   static __device__ __forceinline__ float load(storage v) { return __uint_as_float(uint32_t(v) << 16); }
-  static __device__ __forceinline__ storage store(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t(0x7FC0);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return uint16_t(u >> 16);
-  }
+  static __device__ __forceinline__ storage store(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 };
 
 // IEEE half, round-to-nearest-even conversion.
@@ -135,6 +131,46 @@ __device__ __forceinline__ uint8_t quant_u8(float x, float absmax) {
 // dequant: q * (absmax / Q), the scale rounded to fp32 first
 __device__ __forceinline__ float deq_s8(int8_t q, float absmax) { return float(q) * (absmax / kSignedQ); }
 __device__ __forceinline__ float deq_u8(uint8_t q, float absmax) { return float(q) * (absmax / kUnsignedQ); }
+
+// a / b for b > 0 given y = rcp_for_div(b): q0 = a*y, r = a - q0*b (exact, fused), q1 = q0 + r*y
+// (fused) is the correctly rounded quotient when a, b and q1 are normal numbers in [2^-100, 2^100]
+// (checked exhaustively over every significand of a for hundreds of divisors, _work-free test in
+// tests/test_div_rcp.py); zeros pass through with their sign, every other case takes the IEEE division.
+__device__ __forceinline__ float div_rcp(float a, float b, float y) {
+  const float q0 = a * y;
+  const float r = fmaf(-q0, b, a);
+  float q = fmaf(r, y, q0);
+  const float aa = fabsf(a), aq = fabsf(q);
+  const bool fast = aa >= 0x1p-100f && aa <= 0x1p100f && aq >= 0x1p-100f && aq <= 0x1p100f;
+  if (a == 0.0f) {
+    q = a;
+  } else if (__builtin_expect(!fast, 0)) {
+    q = a / b;
+  }
+  return q;
+}
+
+// the reciprocal div_rcp expects; NaN (forcing the IEEE division) for divisors outside [2^-100, 2^100]
+__device__ __forceinline__ float rcp_for_div(float b) {
+  return (b >= 0x1p-100f && b <= 0x1p100f) ? 1.0f / b : __builtin_nanf("");
+}
+
+// quantisation with the block's reciprocal absmax precomputed (same results as quant_s8/quant_u8)
+__device__ __forceinline__ int8_t quant_s8_r(float x, float absmax, float rcp) {
+  float q = rintf(div_rcp(x, absmax, rcp) * kSignedQ);
+  q = q < -kSignedQ ? -kSignedQ : (q > kSignedQ ? kSignedQ : q);
+  return int8_t(int(q));
+}
+__device__ __forceinline__ uint8_t quant_u8_r(float x, float absmax, float rcp) {
+  float q = rintf(div_rcp(x, absmax, rcp) * kUnsignedQ);
+  q = q < 0.0f ? 0.0f : (q > kUnsignedQ ? kUnsignedQ : q);
+  return uint8_t(int(q));
+}
+
+// n / d for n < 2^31 with the host-precomputed magic m = floor(2^s / d) + 1, s = 32 + ceil(log2 d)
+__device__ __forceinline__ uint32_t udiv_magic(uint32_t n, uint64_t m, uint32_t s) {
+  return uint32_t((uint64_t(n) * m) >> s);
+}
 
 // 1/sqrt(x) as the reference computes rsqrt on CPU: correctly rounded sqrt, then a correctly rounded divide.
 __device__ __forceinline__ float rsqrt_ref(float x) { return 1.0f / sqrtf(x); }

@@ -62,8 +62,12 @@ struct DevTensor {
   float* rm;      // mean row state per matrix       [P]
   float* rmr;     // mean residual row state         [P]
   double* clip_part;  // clip numerator partials     [nclip]
-  float* clip;        // clip divisor                [1]
+  float* clip;        // clip divisor and rcp_for_div of it [2]
   int64_t nclip;
+  uint64_t mC, mR;    // magic multipliers for n / C and n / R (n < 2^31)
+  uint32_t sC, sR;    // and their shifts
+  int32_t idx32;      // N < 2^31: flat indices fit the magic division
+  int32_t c8;         // C % 8 == 0: 8 consecutive elements never cross a row
   int32_t vec_ok;     // p, g, codes 16-byte aligned (flat passes may use vector access)
   int32_t factored;
 };
@@ -116,25 +120,69 @@ constexpr int kMaxBandRows = 256;
 // ===========================================================================
 // P1 / P2: band passes over whole rows
 // ===========================================================================
-// Thread t owns column chunks t, t+256, ..., t+256*(K-1) of V elements each.
-// When C <= 256*V*K each row is read once and kept in registers between the
-// row reduction and the column accumulation; wider rows are handled in
-// column segments after a first sweep that forms the row sums.
+// A workgroup of TPB threads owns a band of consecutive rows of one matrix.
+// Thread t owns column chunks t, t+TPB, ..., t+TPB*(K-1) of V elements each
+// (V = 16 bytes of the gradient type when rows are 16-byte aligned, else 1).
+// When C <= TPB*V*K a row is read once: it stays in registers, in its storage
+// type, between the row reduction and the column accumulation, and the next
+// stage of rows is already loading while the current one is reduced (two
+// register buffers).  Wider rows are handled in column segments after a first
+// sweep that forms the row sums.
 
-template <int V, int K>
-struct BandShape {
-  static constexpr int kElems = V * K;
-  static constexpr int S = (64 / kElems) < 1 ? 1 : ((64 / kElems) > 16 ? 16 : (64 / kElems));
+template <typename TG, int V>
+struct Chunk {
+  typename TG::storage s[V];
+  __device__ __forceinline__ void load(const typename TG::storage* __restrict__ p) {
+    if constexpr (V == 1) {
+      s[0] = p[0];
+    } else {
+      static_assert(V * sizeof(typename TG::storage) == 16, "vector chunk must be 16 bytes");
+      *reinterpret_cast<uint4*>(s) = *reinterpret_cast<const uint4*>(p);
+    }
+  }
+  __device__ __forceinline__ float operator[](int v) const { return TG::load(s[v]); }
 };
 
-// Column accumulators: fp64 when a thread owns few columns (short rows, so bands span many rows),
-// fp32 otherwise (bands are at most 256 rows long).
+template <int V>
+struct CodeChunk {
+  int8_t s[V];
+  __device__ __forceinline__ void load(const int8_t* __restrict__ p) {
+    if constexpr (V == 8) {
+      *reinterpret_cast<uint2*>(s) = *reinterpret_cast<const uint2*>(p);
+    } else if constexpr (V == 4) {
+      *reinterpret_cast<uint32_t*>(s) = *reinterpret_cast<const uint32_t*>(p);
+    } else {
+#pragma unroll
+      for (int v = 0; v < V; ++v) s[v] = p[v];
+    }
+  }
+};
+
+// V int8 codes as floats (V consecutive, V-byte aligned)
+template <int V>
+__device__ __forceinline__ void load_codes(const int8_t* __restrict__ q, float (&out)[V]) {
+  CodeChunk<V> c;
+  c.load(q);
+#pragma unroll
+  for (int v = 0; v < V; ++v) out[v] = float(c.s[v]);
+}
+
+// Rows per register stage: about 64 bytes of gradient per thread, 1..16 rows.
+template <typename TG, int V, int K>
+struct Stage {
+  static constexpr int bytes = int(sizeof(typename TG::storage)) * V * K;
+  static constexpr int S = (64 / bytes) < 1 ? 1 : ((64 / bytes) > 16 ? 16 : (64 / bytes));
+};
+
+// Column accumulators: fp64 when a thread owns few columns (short rows, so a band spans many rows),
+// fp32 otherwise (a band is at most 256 rows).
 template <int V, int K>
 using ColAcc = typename std::conditional<(V * K <= 8), double, float>::type;
 
-// Reduce S row partials across the workgroup; red is a [2][16][4] LDS buffer, parity alternates per call.
-template <int S>
-__device__ __forceinline__ void block_row_sums(float (&ps)[S], float (*red)[16][4], int par, float (&tot)[S]) {
+// Sum S per-thread row partials over the workgroup (NW wavefronts) in a fixed order;
+// red is a [2][16][NW] LDS buffer whose half alternates between calls.
+template <int S, int NW>
+__device__ __forceinline__ void block_row_sums(const float (&ps)[S], float (*red)[16][NW], int par, float (&tot)[S]) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
 #pragma unroll
   for (int s = 0; s < S; ++s) {
@@ -143,63 +191,92 @@ __device__ __forceinline__ void block_row_sums(float (&ps)[S], float (*red)[16][
   }
   __syncthreads();
 #pragma unroll
-  for (int s = 0; s < S; ++s) tot[s] = ((red[par][s][0] + red[par][s][1]) + red[par][s][2]) + red[par][s][3];
+  for (int s = 0; s < S; ++s) {
+    float t = red[par][s][0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) t += red[par][s][w];
+    tot[s] = t;
+  }
+}
+
+// Work item -> (tensor, matrix, band) of a band launch.
+struct BandItem {
+  const DevTensor* t;
+  int64_t b, band, r0, r1;
+};
+__device__ __forceinline__ BandItem band_item(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                              const int64_t* __restrict__ wstart, int ntens, int64_t w) {
+  const int slot = find_slot(wstart, ntens, w);
+  const DevTensor& t = T[tids[slot]];
+  const int64_t local = w - wstart[slot];
+  BandItem it;
+  it.t = &t;
+  it.b = local / t.nbands;
+  it.band = local - it.b * t.nbands;
+  it.r0 = it.band * t.rb;
+  it.r1 = (it.r0 + t.rb < t.R) ? (it.r0 + t.rb) : t.R;
+  return it;
 }
 
 // ---------------- P1 ----------------
-template <typename TG, int V, int K>
-__global__ __launch_bounds__(kThreads) void k_fact_pass1(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
-                                                         const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+template <typename TG, int V, int K, int TPB>
+__global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                    const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using GS = typename TG::storage;
-  constexpr int S = BandShape<V, K>::S;
-  __shared__ float red[2][16][4];
+  using Acc = ColAcc<V, K>;
+  constexpr int NW = TPB / kWave;
+  constexpr int S = Stage<TG, V, K>::S;
+  constexpr int64_t segw = int64_t(TPB) * V * K;
+  __shared__ float red[2][16][NW];
   __shared__ float rowR[kMaxBandRows];
   const int tid = threadIdx.x;
   int par = 0;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
-    const int slot = find_slot(wstart, ntens, w);
-    const DevTensor& t = T[tids[slot]];
-    const int64_t local = w - wstart[slot];
-    const int64_t b = local / t.nbands;
-    const int64_t band = local - b * t.nbands;
-    const int64_t R = t.R, C = t.C;
-    const int64_t r0 = band * t.rb;
-    const int64_t r1 = (r0 + t.rb < R) ? (r0 + t.rb) : R;
+    const BandItem it = band_item(T, tids, wstart, ntens, w);
+    const DevTensor& t = *it.t;
+    const int64_t R = t.R, C = t.C, b = it.b, r0 = it.r0, r1 = it.r1;
     const GS* __restrict__ g = static_cast<const GS*>(t.g) + (b * R) * C;
     const float fC = float(C);
-    constexpr int64_t segw = int64_t(kThreads) * V * K;
     const int64_t nseg = (C + segw - 1) / segw;
-    float* __restrict__ pU = t.partU + (b * t.nbands + band) * C;
-    float* __restrict__ pW = t.partW + (b * t.nbands + band) * C;
+    float* __restrict__ pU = t.partU + (b * t.nbands + it.band) * C;
+    float* __restrict__ pW = t.partW + (b * t.nbands + it.band) * C;
 
     if (nseg == 1) {
-      ColAcc<V, K> colU[K][V], colW[K][V];
+      Acc colU[K][V], colW[K][V];
 #pragma unroll
       for (int k = 0; k < K; ++k)
 #pragma unroll
-        for (int v = 0; v < V; ++v) colU[k][v] = colW[k][v] = 0;
-      for (int64_t r = r0; r < r1; r += S) {
-        float x[S][K][V];
+        for (int v = 0; v < V; ++v) colU[k][v] = colW[k][v] = Acc(0);
+      Chunk<TG, V> A[S][K], Bf[S][K];
+      auto load_stage = [&](Chunk<TG, V> (&buf)[S][K], int64_t r) {
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
+            if (r + s < r1 && c0 < C) buf[s][k].load(g + (r + s) * C + c0);
+          }
+      };
+      auto process = [&](const Chunk<TG, V> (&buf)[S][K], int64_t r) {
         float ps[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           ps[s] = 0.0f;
 #pragma unroll
           for (int k = 0; k < K; ++k) {
-            const int64_t c0 = (int64_t(tid) + int64_t(k) * kThreads) * V;
+            const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
             if (r + s < r1 && c0 < C) {
-              load_vec<TG, V>(g + (r + s) * C + c0, x[s][k]);
 #pragma unroll
-              for (int v = 0; v < V; ++v) ps[s] += x[s][k][v] * x[s][k][v] + hp.eps0;
-            } else {
-#pragma unroll
-              for (int v = 0; v < V; ++v) x[s][k][v] = 0.0f;
+              for (int v = 0; v < V; ++v) {
+                const float x = buf[s][k][v];
+                ps[s] += x * x + hp.eps0;
+              }
             }
           }
         }
         float tot[S];
-        block_row_sums<S>(ps, red, par, tot);
+        block_row_sums<S, NW>(ps, red, par, tot);
         par ^= 1;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
@@ -211,22 +288,32 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass1(const DevTensor* __rest
             const float invR = 1.0f / Rnew;
 #pragma unroll
             for (int k = 0; k < K; ++k) {
-              const int64_t c0 = (int64_t(tid) + int64_t(k) * kThreads) * V;
+              const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
               if (c0 < C) {
 #pragma unroll
                 for (int v = 0; v < V; ++v) {
-                  const float gg = x[s][k][v] * x[s][k][v];
-                  colU[k][v] += ColAcc<V, K>(gg + hp.eps0);
-                  colW[k][v] += ColAcc<V, K>(gg * invR);
+                  const float x = buf[s][k][v];
+                  const float gg = x * x;
+                  colU[k][v] += Acc(gg + hp.eps0);
+                  colW[k][v] += Acc(gg * invR);
                 }
               }
             }
           }
         }
+      };
+      load_stage(A, r0);
+      for (int64_t r = r0; r < r1; r += 2 * S) {
+        if (r + S < r1) load_stage(Bf, r + S);
+        process(A, r);
+        if (r + S < r1) {
+          if (r + 2 * S < r1) load_stage(A, r + 2 * S);
+          process(Bf, r + S);
+        }
       }
 #pragma unroll
       for (int k = 0; k < K; ++k) {
-        const int64_t c0 = (int64_t(tid) + int64_t(k) * kThreads) * V;
+        const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
         if (c0 < C) {
 #pragma unroll
           for (int v = 0; v < V; ++v) {
@@ -246,10 +333,10 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass1(const DevTensor* __rest
           for (int s = 0; s < S; ++s) {
 #pragma unroll
             for (int k = 0; k < K; ++k) {
-              const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * kThreads) * V;
+              const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
               if (r + s < r1 && c0 < C) {
-                float x[V];
-                load_vec<TG, V>(g + (r + s) * C + c0, x);
+                Chunk<TG, V> x;
+                x.load(g + (r + s) * C + c0);
 #pragma unroll
                 for (int v = 0; v < V; ++v) ps[s] += x[v] * x[v] + hp.eps0;
               }
@@ -257,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass1(const DevTensor* __rest
           }
         }
         float tot[S];
-        block_row_sums<S>(ps, red, par, tot);
+        block_row_sums<S, NW>(ps, red, par, tot);
         par ^= 1;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
@@ -275,36 +362,36 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass1(const DevTensor* __rest
       __syncthreads();
       // phase B: column partials segment by segment
       for (int64_t seg = 0; seg < nseg; ++seg) {
-        float colU[K][V], colW[K][V];
+        Acc colU[K][V], colW[K][V];
 #pragma unroll
         for (int k = 0; k < K; ++k)
 #pragma unroll
-          for (int v = 0; v < V; ++v) colU[k][v] = colW[k][v] = 0.0f;
+          for (int v = 0; v < V; ++v) colU[k][v] = colW[k][v] = Acc(0);
         for (int64_t r = r0; r < r1; ++r) {
           const float invR = 1.0f / rowR[r - r0];
 #pragma unroll
           for (int k = 0; k < K; ++k) {
-            const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * kThreads) * V;
+            const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
             if (c0 < C) {
-              float x[V];
-              load_vec<TG, V>(g + r * C + c0, x);
+              Chunk<TG, V> x;
+              x.load(g + r * C + c0);
 #pragma unroll
               for (int v = 0; v < V; ++v) {
                 const float gg = x[v] * x[v];
-                colU[k][v] += gg + hp.eps0;
-                colW[k][v] += gg * invR;
+                colU[k][v] += Acc(gg + hp.eps0);
+                colW[k][v] += Acc(gg * invR);
               }
             }
           }
         }
 #pragma unroll
         for (int k = 0; k < K; ++k) {
-          const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * kThreads) * V;
+          const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
           if (c0 < C) {
 #pragma unroll
             for (int v = 0; v < V; ++v) {
-              pU[c0 + v] = colU[k][v];
-              pW[c0 + v] = colW[k][v];
+              pU[c0 + v] = float(colU[k][v]);
+              pW[c0 + v] = float(colW[k][v]);
             }
           }
         }
@@ -316,146 +403,177 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass1(const DevTensor* __rest
 
 // ---------------- P2 ----------------
 // Per element: u = (r_i*c_j)*g / clip; m = fma(u, 1-b1, m_old*b1); res = (u-m)^2 + eps1.
-template <int V>
-__device__ __forceinline__ void load_codes(const int8_t* __restrict__ q, float (&out)[V]) {
-  if constexpr (V == 8) {
-    const uint2 raw = *reinterpret_cast<const uint2*>(q);
-    const int8_t* s = reinterpret_cast<const int8_t*>(&raw);
-#pragma unroll
-    for (int v = 0; v < 8; ++v) out[v] = float(s[v]);
-  } else if constexpr (V == 4) {
-    const uint32_t raw = *reinterpret_cast<const uint32_t*>(q);
-    const int8_t* s = reinterpret_cast<const int8_t*>(&raw);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) out[v] = float(s[v]);
-  } else {
-#pragma unroll
-    for (int v = 0; v < V; ++v) out[v] = float(q[v]);
-  }
-}
-
-template <typename TG, int V, int K>
-__global__ __launch_bounds__(kThreads) void k_fact_pass2(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
-                                                         const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+template <typename TG, int V, int K, int TPB>
+__global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                    const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using GS = typename TG::storage;
-  constexpr int S = BandShape<V, K>::S;
-  __shared__ float red[2][16][4];
+  using Acc = ColAcc<V, K>;
+  constexpr int NW = TPB / kWave;
+  constexpr int S = Stage<TG, V, K>::S;
+  constexpr int64_t segw = int64_t(TPB) * V * K;
+  __shared__ float red[2][16][NW];
   const int tid = threadIdx.x;
   int par = 0;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
-    const int slot = find_slot(wstart, ntens, w);
-    const DevTensor& t = T[tids[slot]];
-    const int64_t local = w - wstart[slot];
-    const int64_t b = local / t.nbands;
-    const int64_t band = local - b * t.nbands;
-    const int64_t R = t.R, C = t.C;
-    const int64_t r0 = band * t.rb;
-    const int64_t r1 = (r0 + t.rb < R) ? (r0 + t.rb) : R;
+    const BandItem it = band_item(T, tids, wstart, ntens, w);
+    const DevTensor& t = *it.t;
+    const int64_t R = t.R, C = t.C, b = it.b, r0 = it.r0, r1 = it.r1;
     const int64_t ebase = (b * R) * C;
     const GS* __restrict__ g = static_cast<const GS*>(t.g) + ebase;
     const int8_t* __restrict__ mq = t.mq + ebase;
     const float* __restrict__ cf = t.cfac + b * C;
-    const float clip = t.clip[0];
+    const float clip = t.clip[0], crcp = t.clip[1];
     const float fC = float(C);
-    constexpr int64_t segw = int64_t(kThreads) * V * K;
     const int64_t nseg = (C + segw - 1) / segw;
-    float* __restrict__ pR = t.partRes + (b * t.nbands + band) * C;
+    float* __restrict__ pR = t.partRes + (b * t.nbands + it.band) * C;
     const int64_t PR = t.P * R;
 
-    for (int64_t seg = 0; seg < nseg; ++seg) {
-      // column factors for this thread's columns
+    // residual of one element, and of a V-chunk (V > 1 chunks lie inside one quantisation block)
+    auto res_of = [&](float ri, float cj, float x, float q, float scale) {
+      const float u = div_rcp((ri * cj) * x, clip, crcp);
+      const float m = fmaf(u, hp.a1, (q * scale) * hp.b1);
+      const float d = u - m;
+      return d * d + hp.eps1;
+    };
+    auto row_state = [&](int64_t row, float tot) {
+      const float RRold = deq_u8(t.rq[PR + row], t.ra[t.nbr + blk_of(row, hp)]);
+      t.RRn[row] = fmaf(tot / fC, hp.a3, RRold * hp.b3);
+    };
+
+    if (nseg == 1) {
       float cj[K][V];
 #pragma unroll
       for (int k = 0; k < K; ++k) {
-        const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * kThreads) * V;
+        const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
 #pragma unroll
         for (int v = 0; v < V; ++v) cj[k][v] = (c0 + v < C) ? cf[c0 + v] : 0.0f;
       }
-      ColAcc<V, K> colR[K][V];
+      Acc colR[K][V];
 #pragma unroll
       for (int k = 0; k < K; ++k)
 #pragma unroll
-        for (int v = 0; v < V; ++v) colR[k][v] = 0;
-      for (int64_t r = r0; r < r1; r += S) {
+        for (int v = 0; v < V; ++v) colR[k][v] = Acc(0);
+      Chunk<TG, V> gA[S][K], gB[S][K];
+      CodeChunk<V> qA[S][K], qB[S][K];
+      auto load_stage = [&](Chunk<TG, V> (&gb)[S][K], CodeChunk<V> (&qb)[S][K], int64_t r) {
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
+            if (r + s < r1 && c0 < C) {
+              gb[s][k].load(g + (r + s) * C + c0);
+              qb[s][k].load(mq + (r + s) * C + c0);
+            }
+          }
+      };
+      auto process = [&](const Chunk<TG, V> (&gb)[S][K], const CodeChunk<V> (&qb)[S][K], int64_t r) {
         float ps[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           ps[s] = 0.0f;
           if (r + s < r1) {
-            const int64_t row = b * R + r + s;
-            const float ri = t.rfac[row];
+            const float ri = t.rfac[b * R + r + s];
 #pragma unroll
             for (int k = 0; k < K; ++k) {
-              const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * kThreads) * V;
+              const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
               if (c0 < C) {
                 const int64_t e = (r + s) * C + c0;
-                float x[V], q[V];
-                load_vec<TG, V>(g + e, x);
-                load_codes<V>(mq + e, q);
+                float scale = t.ma[blk_of(ebase + e, hp)] / kSignedQ;
 #pragma unroll
                 for (int v = 0; v < V; ++v) {
-                  const float scale = t.ma[blk_of(ebase + e + v, hp)] / kSignedQ;
-                  const float u = ((ri * cj[k][v]) * x[v]) / clip;
-                  const float m = fmaf(u, hp.a1, (q[v] * scale) * hp.b1);
-                  const float d = u - m;
-                  const float res = d * d + hp.eps1;
+                  if (V == 1 && v > 0) scale = t.ma[blk_of(ebase + e + v, hp)] / kSignedQ;
+                  const float res = res_of(ri, cj[k][v], gb[s][k][v], float(qb[s][k].s[v]), scale);
                   ps[s] += res;
-                  colR[k][v] += ColAcc<V, K>(res);
+                  colR[k][v] += Acc(res);
                 }
               }
             }
           }
         }
-        if (nseg == 1) {
-          float tot[S];
-          block_row_sums<S>(ps, red, par, tot);
-          par ^= 1;
+        float tot[S];
+        block_row_sums<S, NW>(ps, red, par, tot);
+        par ^= 1;
 #pragma unroll
-          for (int s = 0; s < S; ++s) {
-            if (r + s < r1 && tid == 0) {
-              const int64_t row = b * R + r + s;
-              const float RRold = deq_u8(t.rq[PR + row], t.ra[t.nbr + blk_of(row, hp)]);
-              t.RRn[row] = fmaf(tot[s] / fC, hp.a3, RRold * hp.b3);
-            }
-          }
+        for (int s = 0; s < S; ++s)
+          if (r + s < r1 && tid == 0) row_state(b * R + r + s, tot[s]);
+      };
+      load_stage(gA, qA, r0);
+      for (int64_t r = r0; r < r1; r += 2 * S) {
+        if (r + S < r1) load_stage(gB, qB, r + S);
+        process(gA, qA, r);
+        if (r + S < r1) {
+          if (r + 2 * S < r1) load_stage(gA, qA, r + 2 * S);
+          process(gB, qB, r + S);
         }
       }
 #pragma unroll
       for (int k = 0; k < K; ++k) {
-        const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * kThreads) * V;
+        const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
         if (c0 < C) {
 #pragma unroll
           for (int v = 0; v < V; ++v) pR[c0 + v] = float(colR[k][v]);
         }
       }
-    }
-    if (nseg > 1) {
-      // row sums of the residual over the whole row (second sweep for wide rows)
+    } else {
+      // column partials, segment by segment
+      for (int64_t seg = 0; seg < nseg; ++seg) {
+        Acc colR[K][V];
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+#pragma unroll
+          for (int v = 0; v < V; ++v) colR[k][v] = Acc(0);
+        for (int64_t r = r0; r < r1; ++r) {
+          const float ri = t.rfac[b * R + r];
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
+            if (c0 < C) {
+              const int64_t e = r * C + c0;
+              Chunk<TG, V> x;
+              CodeChunk<V> q;
+              x.load(g + e);
+              q.load(mq + e);
+#pragma unroll
+              for (int v = 0; v < V; ++v) {
+                const float scale = t.ma[blk_of(ebase + e + v, hp)] / kSignedQ;
+                colR[k][v] += Acc(res_of(ri, cf[c0 + v], x[v], float(q.s[v]), scale));
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
+          if (c0 < C) {
+#pragma unroll
+            for (int v = 0; v < V; ++v) pR[c0 + v] = float(colR[k][v]);
+          }
+        }
+      }
+      // row sums over whole rows
       for (int64_t r = r0; r < r1; r += S) {
         float ps[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           ps[s] = 0.0f;
           if (r + s < r1) {
-            const int64_t row = b * R + r + s;
-            const float ri = t.rfac[row];
+            const float ri = t.rfac[b * R + r + s];
             for (int64_t seg = 0; seg < nseg; ++seg) {
 #pragma unroll
               for (int k = 0; k < K; ++k) {
-                const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * kThreads) * V;
+                const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
                 if (c0 < C) {
                   const int64_t e = (r + s) * C + c0;
-                  float x[V], q[V];
-                  load_vec<TG, V>(g + e, x);
-                  load_codes<V>(mq + e, q);
+                  Chunk<TG, V> x;
+                  CodeChunk<V> q;
+                  x.load(g + e);
+                  q.load(mq + e);
 #pragma unroll
                   for (int v = 0; v < V; ++v) {
                     const float scale = t.ma[blk_of(ebase + e + v, hp)] / kSignedQ;
-                    const float u = ((ri * cf[c0 + v]) * x[v]) / clip;
-                    const float m = fmaf(u, hp.a1, (q[v] * scale) * hp.b1);
-                    const float d = u - m;
-                    ps[s] += d * d + hp.eps1;
+                    ps[s] += res_of(ri, cf[c0 + v], x[v], float(q.s[v]), scale);
                   }
                 }
               }
@@ -463,16 +581,11 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass2(const DevTensor* __rest
           }
         }
         float tot[S];
-        block_row_sums<S>(ps, red, par, tot);
+        block_row_sums<S, NW>(ps, red, par, tot);
         par ^= 1;
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-          if (r + s < r1 && tid == 0) {
-            const int64_t row = b * R + r + s;
-            const float RRold = deq_u8(t.rq[PR + row], t.ra[t.nbr + blk_of(row, hp)]);
-            t.RRn[row] = fmaf(tot[s] / fC, hp.a3, RRold * hp.b3);
-          }
-        }
+        for (int s = 0; s < S; ++s)
+          if (r + s < r1 && tid == 0) row_state(b * R + r + s, tot[s]);
       }
     }
   }
@@ -577,14 +690,15 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
         if (!RES) t.clip_part[blk] = ((ssum[0] + ssum[1]) + ssum[2]) + ssum[3];
       }
     }
+    const float arcp = rcp_for_div(amax);
     if (is_row) {
       const float* __restrict__ Rsrc = RES ? t.RRn : t.Rn;
       uint8_t* __restrict__ q = t.rq + (RES ? t.P * t.R : 0);
-      for (int64_t i = i0 + tid; i < i1; i += kThreads) q[i] = quant_u8(Rsrc[i], amax);
+      for (int64_t i = i0 + tid; i < i1; i += kThreads) q[i] = quant_u8_r(Rsrc[i], amax, arcp);
     } else {
       const float* __restrict__ Csrc = RES ? t.CRn : t.Cn;
       uint8_t* __restrict__ q = t.cq + (RES ? t.P * t.C : 0);
-      for (int64_t i = i0 + tid; i < i1; i += kThreads) q[i] = quant_u8(Csrc[i], amax);
+      for (int64_t i = i0 + tid; i < i1; i += kThreads) q[i] = quant_u8_r(Csrc[i], amax, arcp);
     }
     __syncthreads();  // smax / ssum reused by the next item
   }
@@ -651,7 +765,9 @@ __global__ __launch_bounds__(kThreads) void k_clip(const DevTensor* __restrict__
     __syncthreads();
     if (tid == 0) {
       const double tot = ((ssum[0] + ssum[1]) + ssum[2]) + ssum[3];
-      t.clip[0] = clip_from_norm(float(sqrt(tot)), t.N, hp);
+      const float c = clip_from_norm(float(sqrt(tot)), t.N, hp);
+      t.clip[0] = c;
+      t.clip[1] = rcp_for_div(c);
     }
     __syncthreads();
   }
@@ -705,7 +821,9 @@ __global__ __launch_bounds__(kThreads) void k_clip_refnorm(const DevTensor* __re
         const float uu = u * u;
         bsum = bsum + uu;
       }
-      t.clip[0] = clip_from_norm(sqrtf(bsum), N, hp);
+      const float c = clip_from_norm(sqrtf(bsum), N, hp);
+      t.clip[0] = c;
+      t.clip[1] = rcp_for_div(c);
     }
     __syncthreads();
   }
@@ -734,7 +852,7 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
     const int64_t N = t.N, C = t.C, R = t.R;
     PS* __restrict__ p = static_cast<PS*>(t.p);
     const GS* __restrict__ g = static_cast<const GS*>(t.g);
-    const float clip = t.clip[0];
+    const float clip = t.clip[0], crcp = t.clip[1];
     float m[8], pv[8];
     const bool full = t.vec_ok && (e0 + 8 <= N);
     if (e0 < N) {
@@ -753,28 +871,48 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
         }
       }
       const float scale = t.ma[blk_of(e0, hp)] / kSignedQ;  // 8 elements share a block (B >= 8)
-      int64_t row = e0 / C;
+      int64_t row, bb;
+      if (t.idx32) {
+        const uint32_t r32 = udiv_magic(uint32_t(e0), t.mC, t.sC);
+        row = r32;
+        bb = udiv_magic(r32, t.mR, t.sR);
+      } else {
+        row = e0 / C;
+        bb = row / R;
+      }
       int64_t j = e0 - row * C;
-      int64_t bb = row / R;
-      int64_t i = row - bb * R;
+      if (full && t.c8) {
+        // the 8 elements share a row; their column factors are contiguous and 32-byte aligned
+        const float ri = t.rfac[row], rri = t.rrfac[row];
+        float cj[8], crj[8];
+        load8<F32>(t.cfac + bb * C + j, cj);
+        load8<F32>(t.crfac + bb * C + j, crj);
 #pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        if (e0 + v < N) {
-          const float ri = t.rfac[row], rri = t.rrfac[row];
-          const float cj = t.cfac[bb * C + j], crj = t.crfac[bb * C + j];
-          const float u = ((ri * cj) * gv[v]) / clip;
+        for (int v = 0; v < 8; ++v) {
+          const float u = div_rcp((ri * cj[v]) * gv[v], clip, crcp);
           m[v] = fmaf(u, hp.a1, (q[v] * scale) * hp.b1);
-          const float step = (rri * crj) * m[v];
-          pv[v] = param_update<TP>(pv[v], step, hp);
-        } else {
-          m[v] = 0.0f;
+          pv[v] = param_update<TP>(pv[v], (rri * crj[v]) * m[v], hp);
         }
-        if (++j == C) {
-          j = 0;
-          ++row;
-          if (++i == R) {
-            i = 0;
-            ++bb;
+      } else {
+        int64_t i = row - bb * R;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          if (e0 + v < N) {
+            const float ri = t.rfac[row], rri = t.rrfac[row];
+            const float cj = t.cfac[bb * C + j], crj = t.crfac[bb * C + j];
+            const float u = div_rcp((ri * cj) * gv[v], clip, crcp);
+            m[v] = fmaf(u, hp.a1, (q[v] * scale) * hp.b1);
+            pv[v] = param_update<TP>(pv[v], (rri * crj) * m[v], hp);
+          } else {
+            m[v] = 0.0f;
+          }
+          if (++j == C) {
+            j = 0;
+            ++row;
+            if (++i == R) {
+              i = 0;
+              ++bb;
+            }
           }
         }
       }
@@ -799,20 +937,21 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
       par ^= 1;
     }
     amax = fix_absmax(amax);
+    const float arcp = rcp_for_div(amax);
     if (e0 < N) {
       if (((e0 & (hp.B - 1)) == 0)) t.ma[blk_of(e0, hp)] = amax;
       if (full) {
         uint2 raw;
         int8_t* s = reinterpret_cast<int8_t*>(&raw);
 #pragma unroll
-        for (int v = 0; v < 8; ++v) s[v] = quant_s8(m[v], amax);
+        for (int v = 0; v < 8; ++v) s[v] = quant_s8_r(m[v], amax, arcp);
         *reinterpret_cast<uint2*>(t.mq + e0) = raw;
         store8<TP>(p + e0, pv);
       } else {
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
           if (e0 + v < N) {
-            t.mq[e0 + v] = quant_s8(m[v], amax);
+            t.mq[e0 + v] = quant_s8_r(m[v], amax, arcp);
             p[e0 + v] = TP::store(pv[v]);
           }
         }
@@ -842,7 +981,7 @@ __global__ __launch_bounds__(kThreads) void k_vec_passB(const DevTensor* __restr
     const int64_t N = t.N;
     PS* __restrict__ p = static_cast<PS*>(t.p);
     const GS* __restrict__ g = static_cast<const GS*>(t.g);
-    const float clip = t.clip[0];
+    const float clip = t.clip[0], crcp = t.clip[1];
     float m[8], vv[8], pv[8];
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
@@ -850,7 +989,7 @@ __global__ __launch_bounds__(kThreads) void k_vec_passB(const DevTensor* __restr
       if (e < N) {
         const float gv = TG::load(g[e]);
         vv[v] = vec_v_new<TG>(t, e, gv, hp);
-        const float u = (rsqrt_ref(vv[v]) * gv) / clip;
+        const float u = div_rcp(rsqrt_ref(vv[v]) * gv, clip, crcp);
         const float mold = deq_s8(t.mq[e], t.ma[blk_of(e, hp)]);
         m[v] = fmaf(u, hp.a1, mold * hp.b1);
         pv[v] = param_update<TP>(TP::load(p[e]), m[v], hp);
@@ -888,6 +1027,7 @@ __global__ __launch_bounds__(kThreads) void k_vec_passB(const DevTensor* __restr
     }
     am = fix_absmax(am);
     av = fix_absmax(av);
+    const float amr = rcp_for_div(am), avr = rcp_for_div(av);
     if (e0 < N && ((e0 & (hp.B - 1)) == 0)) {
       t.ma[blk_of(e0, hp)] = am;
       t.ra[blk_of(e0, hp)] = av;
@@ -896,8 +1036,8 @@ __global__ __launch_bounds__(kThreads) void k_vec_passB(const DevTensor* __restr
     for (int v = 0; v < 8; ++v) {
       const int64_t e = e0 + v;
       if (e < N) {
-        t.mq[e] = quant_s8(m[v], am);
-        t.rq[e] = quant_u8(vv[v], av);
+        t.mq[e] = quant_s8_r(m[v], am, amr);
+        t.rq[e] = quant_u8_r(vv[v], av, avr);
         p[e] = TP::store(pv[v]);
       }
     }
