@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "../../include/came8.h"
+#include "came8_dispatch.h"
 #include "came8_kernels.h"
 
 using namespace came8;
@@ -166,6 +167,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     if (t.prefix < 1 || t.rows < 1 || t.cols < 1) return fail(CAME8_EINVAL, who + "empty or negative shape");
     if (!t.factored && (t.prefix != 1 || t.rows != 1)) return fail(CAME8_EINVAL, who + "1-D tensors take prefix = rows = 1");
     if (t.factored && (!t.col_q || !t.col_absmax)) return fail(CAME8_EINVAL, who + "null column state");
+    if ((B & (B - 1)) != 0 && t.prefix * t.rows * t.cols >= (int64_t(1) << 31))
+      return fail(CAME8_EINVAL, who + "block sizes that are not powers of two need fewer than 2^31 elements");
     DevTensor& d = plan.dev[i];
     d.p = t.param;
     d.g = t.grad;
@@ -194,6 +197,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       size_t Rn, rfac, RRn, rrfac, Cn, cfac, CRn, crfac, pU, pW, pR, rm, rmr, clipp, clip;
     } o{};
     d.idx32 = d.N < (int64_t(1) << 31) ? 1 : 0;
+    d.rowal = (d.C % B) == 0 ? 1 : 0;
     d.c8 = (d.C % 8 == 0) ? 1 : 0;
     magic_div(d.C, d.mC, d.sC);
     magic_div(d.R, d.mR, d.sR);
@@ -358,41 +362,26 @@ Hp make_hp(const came8_hparams& h) {
   hp.wd = h.weight_decay != 0.0 ? 1 : 0;
   hp.B = h.block_size;
   hp.log2B = log2_or_minus1(h.block_size);
+  if (hp.log2B >= 0) {
+    hp.mB = 1;
+    hp.sB = uint32_t(hp.log2B);
+  } else {
+    magic_div(h.block_size, hp.mB, hp.sB);
+  }
   return hp;
 }
 
 // ---------------------------------------------------------------------------
 // kernel-variant dispatch
 // ---------------------------------------------------------------------------
-using BandFn = void (*)(const DevTensor*, const int32_t*, const int64_t*, int, Hp);
-
-template <typename TG, int V, int K, int TPB>
-BandFn band_pick(bool pass2) {
-  return pass2 ? k_fact_pass2<TG, V, K, TPB> : k_fact_pass1<TG, V, K, TPB>;
-}
-
-// the (V, K, TPB) variants band_variant() can choose
-template <typename TG, int VW>
-BandFn band_fn(bool pass2, int V, int K, int TPB) {
-  if (V == 1 && TPB == 256) {
-    switch (K) {
-      case 1: return band_pick<TG, 1, 1, 256>(pass2);
-      case 2: return band_pick<TG, 1, 2, 256>(pass2);
-      case 4: return band_pick<TG, 1, 4, 256>(pass2);
-      case 8: return band_pick<TG, 1, 8, 256>(pass2);
-      case 16: return band_pick<TG, 1, 16, 256>(pass2);
-      case 32: return band_pick<TG, 1, 32, 256>(pass2);
-      default: return nullptr;
-    }
+// band-pass kernels are instantiated in came8_band.hip (one translation unit per family)
+BandFn band_fn(int gdt, bool pass2, int V, int K, int TPB) {
+  switch (gdt) {
+    case CAME8_F32: return pass2 ? band_fn_F32_p2(V, K, TPB) : band_fn_F32_p1(V, K, TPB);
+    case CAME8_BF16: return pass2 ? band_fn_BF16_p2(V, K, TPB) : band_fn_BF16_p1(V, K, TPB);
+    case CAME8_F16: return pass2 ? band_fn_F16_p2(V, K, TPB) : band_fn_F16_p1(V, K, TPB);
+    default: return nullptr;
   }
-  if (V == VW) {
-    if (TPB == 256 && K == 1) return band_pick<TG, VW, 1, 256>(pass2);
-    if (TPB == 256 && K == 2) return band_pick<TG, VW, 2, 256>(pass2);
-    if (TPB == 512 && K == 2) return band_pick<TG, VW, 2, 512>(pass2);
-    if (TPB == 512 && K == 3) return band_pick<TG, VW, 3, 512>(pass2);
-    if (TPB == 512 && K == 4) return band_pick<TG, VW, 4, 512>(pass2);
-  }
-  return nullptr;
 }
 
 using GenFn = void (*)(const DevTensor*, const int32_t*, const int64_t*, int, Hp);
@@ -604,9 +593,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     const BandKey& k = kv.first;
     const WorkList& wl = kv.second;
     BandFn fn = nullptr;
-    if (k.gdt == CAME8_F32) fn = band_fn<F32, 4>(false, k.V, k.K, k.TPB);
-    if (k.gdt == CAME8_BF16) fn = band_fn<BF16, 8>(false, k.V, k.K, k.TPB);
-    if (k.gdt == CAME8_F16) fn = band_fn<F16, 8>(false, k.V, k.K, k.TPB);
+    fn = band_fn(k.gdt, false, k.V, k.K, k.TPB);
     if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
     { PhaseTimer pt(PH_PASS1, alg_bytes(plan, wl, tensors, PH_PASS1), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
@@ -645,7 +632,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     }
   } else {
     PhaseTimer pt(PH_CLIP, 0.0, stream);
-    hipLaunchKernelGGL(k_clip, dim3(grid_for(n_tensors)), blk, 0, stream, dT, int(n_tensors), hp);
+    hipLaunchKernelGGL(k_clip<>, dim3(grid_for(n_tensors)), blk, 0, stream, dT, int(n_tensors), hp);
     if ((rc = check_launch("clip")) != CAME8_OK) return rc;
   }
   // ---- P2, residual factors ----
@@ -654,9 +641,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       const BandKey& k = kv.first;
       const WorkList& wl = kv.second;
       BandFn fn = nullptr;
-      if (k.gdt == CAME8_F32) fn = band_fn<F32, 4>(true, k.V, k.K, k.TPB);
-      if (k.gdt == CAME8_BF16) fn = band_fn<BF16, 8>(true, k.V, k.K, k.TPB);
-      if (k.gdt == CAME8_F16) fn = band_fn<F16, 8>(true, k.V, k.K, k.TPB);
+      fn = band_fn(k.gdt, true, k.V, k.K, k.TPB);
       if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
       { PhaseTimer pt(PH_PASS2, alg_bytes(plan, wl, tensors, PH_PASS2), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);

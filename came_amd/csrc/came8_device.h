@@ -14,13 +14,25 @@ namespace came8 {
 constexpr int kThreads = 256;  // four 64-lane wavefronts per workgroup
 constexpr int kWave = 64;
 
+// Global-memory view of a pointer taken from a descriptor (loads and stores through it are
+// global_* instructions instead of flat_* ones, which also wait on the LDS counter).
+#define CAME8_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ CAME8_GLOBAL T* gbl(T* p) {
+  return (CAME8_GLOBAL T*)p;
+}
+
 // ---------------------------------------------------------------------------
 // element types: storage + exact conversions (float <-> storage)
 // ---------------------------------------------------------------------------
+//
+// elem(w, v): element v of consecutive elements packed little-endian in 32-bit words (one
+// instruction each: a move, a shift or mask, or a half-precision convert of a word half).
 struct F32 {
   using storage = float;
   static __device__ __forceinline__ float load(storage v) { return v; }
   static __device__ __forceinline__ storage store(float f) { return f; }
+  static __device__ __forceinline__ float elem(const uint32_t* w, int v) { return __uint_as_float(w[v]); }
 };
 
 // bfloat16: the conversion from fp32 rounds to nearest even (gfx950's v_cvt_pk_bf16_f32), the
@@ -29,6 +41,9 @@ struct BF16 {
   using storage = uint16_t;
   static __device__ __forceinline__ float load(storage v) { return __uint_as_float(uint32_t(v) << 16); }
   static __device__ __forceinline__ storage store(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+  static __device__ __forceinline__ float elem(const uint32_t* w, int v) {
+    return (v & 1) ? __uint_as_float(w[v >> 1] & 0xffff0000u) : __uint_as_float(w[v >> 1] << 16);
+  }
 };
 
 // IEEE half, round-to-nearest-even conversion.
@@ -36,49 +51,50 @@ struct F16 {
   using storage = uint16_t;
   static __device__ __forceinline__ float load(storage v) { return float(__builtin_bit_cast(_Float16, v)); }
   static __device__ __forceinline__ storage store(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+  static __device__ __forceinline__ float elem(const uint32_t* w, int v) {
+    return float(__builtin_bit_cast(_Float16, uint16_t(w[v >> 1] >> (16 * (v & 1)))));
+  }
 };
 
-// Load V consecutive elements (V * sizeof(storage) == 16 bytes when V > 1, 16-byte aligned).
-template <typename T, int V>
-__device__ __forceinline__ void load_vec(const typename T::storage* __restrict__ p, float (&out)[V]) {
-  if constexpr (V == 1) {
-    out[0] = T::load(p[0]);
-  } else {
-    static_assert(V * sizeof(typename T::storage) == 16, "vector chunk must be 16 bytes");
-    const uint4 raw = *reinterpret_cast<const uint4*>(p);
-    const typename T::storage* s = reinterpret_cast<const typename T::storage*>(&raw);
-#pragma unroll
-    for (int v = 0; v < V; ++v) out[v] = T::load(s[v]);
-  }
+// signed byte v of consecutive int8 codes packed in 32-bit words, as a float
+__device__ __forceinline__ float code_elem(const uint32_t* w, int v) {
+  return float(int32_t(w[v >> 2] << (24 - 8 * (v & 3))) >> 24);
 }
+
+// native vector types (HIP's float4 / uint4 classes cannot bind to global-address-space objects)
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Load / store 8 consecutive elements (16 or 32 bytes, aligned) of any element type.
 template <typename T>
-__device__ __forceinline__ void load8(const typename T::storage* __restrict__ p, float (&out)[8]) {
+__device__ __forceinline__ void load8(const CAME8_GLOBAL typename T::storage* __restrict__ p, float (&out)[8]) {
   if constexpr (sizeof(typename T::storage) == 4) {
-    const float4 a = reinterpret_cast<const float4*>(p)[0];
-    const float4 b = reinterpret_cast<const float4*>(p)[1];
+    const CAME8_GLOBAL f32x4* q = (const CAME8_GLOBAL f32x4*)p;
+    const f32x4 a = q[0];
+    const f32x4 b = q[1];
     out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
     out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
   } else {
-    const uint4 raw = *reinterpret_cast<const uint4*>(p);
-    const typename T::storage* s = reinterpret_cast<const typename T::storage*>(&raw);
+    const u32x4 raw = *(const CAME8_GLOBAL u32x4*)p;
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
-    for (int v = 0; v < 8; ++v) out[v] = T::load(s[v]);
+    for (int v = 0; v < 8; ++v) out[v] = T::elem(w, v);
   }
 }
 
 template <typename T>
-__device__ __forceinline__ void store8(typename T::storage* __restrict__ p, const float (&in)[8]) {
+__device__ __forceinline__ void store8(CAME8_GLOBAL typename T::storage* __restrict__ p, const float (&in)[8]) {
   if constexpr (sizeof(typename T::storage) == 4) {
-    reinterpret_cast<float4*>(p)[0] = make_float4(in[0], in[1], in[2], in[3]);
-    reinterpret_cast<float4*>(p)[1] = make_float4(in[4], in[5], in[6], in[7]);
+    CAME8_GLOBAL f32x4* q = (CAME8_GLOBAL f32x4*)p;
+    q[0] = f32x4{in[0], in[1], in[2], in[3]};
+    q[1] = f32x4{in[4], in[5], in[6], in[7]};
   } else {
-    uint4 raw;
+    u32x4 raw;
     typename T::storage* s = reinterpret_cast<typename T::storage*>(&raw);
 #pragma unroll
     for (int v = 0; v < 8; ++v) s[v] = T::store(in[v]);
-    *reinterpret_cast<uint4*>(p) = raw;
+    *(CAME8_GLOBAL u32x4*)p = raw;
   }
 }
 
@@ -90,6 +106,33 @@ __device__ __forceinline__ F wave_sum(F v) {
 #pragma unroll
   for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
   return v;
+}
+
+// Cross-lane moves without index arithmetic.  Each pattern is an involution (a lane's partner's
+// partner is itself), so a butterfly over them leaves every lane of a group with the same value.
+// DPP: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2), row_half_mirror (within 8
+// lanes, i <-> 7 - i), row_mirror (within 16 lanes, i <-> 15 - i); ds_swizzle bit mode: lane ^ 16.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xb1, kDppXor2 = 0x4e, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+__device__ __forceinline__ uint32_t swz_xor16_u32(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), 0x401f));
+}
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int lane) {
+  return uint32_t(__builtin_amdgcn_readlane(int(v), lane));
+}
+
+// Sum over the 64 lanes in a fixed order (pairs, quads, 8, 16, 32 lanes, then lane 0's half plus
+// lane 32's half); every lane returns the same value.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += __uint_as_float(dpp_u32<kDppXor1>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<kDppXor2>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<kDppHalfMirror>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<kDppMirror>(__float_as_uint(v)));
+  v += __uint_as_float(swz_xor16_u32(__float_as_uint(v)));
+  return __uint_as_float(readlane_u32(__float_as_uint(v), 0)) + __uint_as_float(readlane_u32(__float_as_uint(v), 32));
 }
 
 // max that propagates NaN (torch.amax semantics)
@@ -107,6 +150,33 @@ __device__ __forceinline__ float group_max_rt(float v, int L) {
   for (int o = L / 2; o > 0; o >>= 1) v = nan_max(v, __shfl_xor(v, o, kWave));
   return v;
 }
+
+// unsigned max over aligned groups of L lanes (L a power of two <= 64); every lane of a group
+// returns the group's maximum
+template <int L>
+__device__ __forceinline__ uint32_t group_max_bits(uint32_t v) {
+  if constexpr (L >= 2) v = max(v, dpp_u32<kDppXor1>(v));
+  if constexpr (L >= 4) v = max(v, dpp_u32<kDppXor2>(v));
+  if constexpr (L >= 8) v = max(v, dpp_u32<kDppHalfMirror>(v));
+  if constexpr (L >= 16) v = max(v, dpp_u32<kDppMirror>(v));
+  if constexpr (L >= 32) v = max(v, swz_xor16_u32(v));
+  if constexpr (L >= 64) v = max(readlane_u32(v, 0), readlane_u32(v, 32));
+  return v;
+}
+__device__ __forceinline__ uint32_t group_max_bits_rt(uint32_t v, int L) {
+  switch (L) {
+    case 1: return v;
+    case 2: return group_max_bits<2>(v);
+    case 4: return group_max_bits<4>(v);
+    case 8: return group_max_bits<8>(v);
+    case 16: return group_max_bits<16>(v);
+    case 32: return group_max_bits<32>(v);
+    default: return group_max_bits<64>(v);
+  }
+}
+
+// a value every lane holds alike, moved to a scalar register (lets branches on it be scalar)
+__device__ __forceinline__ float uniform_f32(float v) { return __uint_as_float(readlane_u32(__float_as_uint(v), 0)); }
 
 // ---------------------------------------------------------------------------
 // blockwise quantisation (reference blockwise_quantization.py:66-82,112-124)
@@ -132,39 +202,71 @@ __device__ __forceinline__ uint8_t quant_u8(float x, float absmax) {
 __device__ __forceinline__ float deq_s8(int8_t q, float absmax) { return float(q) * (absmax / kSignedQ); }
 __device__ __forceinline__ float deq_u8(uint8_t q, float absmax) { return float(q) * (absmax / kUnsignedQ); }
 
-// a / b for b > 0 given y = rcp_for_div(b): q0 = a*y, r = a - q0*b (exact, fused), q1 = q0 + r*y
-// (fused) is the correctly rounded quotient when a, b and q1 are normal numbers in [2^-100, 2^100]
-// (checked exhaustively over every significand of a for hundreds of divisors, _work-free test in
-// tests/test_div_rcp.py); zeros pass through with their sign, every other case takes the IEEE division.
-__device__ __forceinline__ float div_rcp(float a, float b, float y) {
+// Division by a block's absmax in quantisation.  With y = RN(1/b), q0 = RN(a*y), r = a - q0*b
+// (exact, fused) and q1 = RN(q0 + r*y) (fused) is the correctly rounded a/b whenever a, b and the
+// quotient are normal numbers in [2^-100, 2^100] (checked exhaustively over every significand of a
+// for hundreds of divisors, tests/test_div_rcp.py).  In quantisation |a| <= b, and only quotients
+// |a/b| >= 2^-8 can round to a nonzero code; with b in [2^-40, 2^60] those lie in the exact range,
+// and smaller ones give code 0 either way.  Blocks whose absmax is outside that range divide.
+__device__ __forceinline__ float div_fast(float a, float b, float y) {
   const float q0 = a * y;
   const float r = fmaf(-q0, b, a);
-  float q = fmaf(r, y, q0);
-  const float aa = fabsf(a), aq = fabsf(q);
-  const bool fast = aa >= 0x1p-100f && aa <= 0x1p100f && aq >= 0x1p-100f && aq <= 0x1p100f;
-  if (a == 0.0f) {
-    q = a;
-  } else if (__builtin_expect(!fast, 0)) {
-    q = a / b;
-  }
-  return q;
+  return fmaf(r, y, q0);
 }
 
-// the reciprocal div_rcp expects; NaN (forcing the IEEE division) for divisors outside [2^-100, 2^100]
+// the reciprocal div_fast expects; NaN for divisors outside [2^-40, 2^60] (callers then divide)
 __device__ __forceinline__ float rcp_for_div(float b) {
-  return (b >= 0x1p-100f && b <= 0x1p100f) ? 1.0f / b : __builtin_nanf("");
+  return (b >= 0x1p-40f && b <= 0x1p60f) ? 1.0f / b : __builtin_nanf("");
 }
 
-// quantisation with the block's reciprocal absmax precomputed (same results as quant_s8/quant_u8)
-__device__ __forceinline__ int8_t quant_s8_r(float x, float absmax, float rcp) {
-  float q = rintf(div_rcp(x, absmax, rcp) * kSignedQ);
+// quantisation with rcp = rcp_for_div(absmax) finite (same results as quant_s8 / quant_u8)
+__device__ __forceinline__ int8_t quant_s8_fast(float x, float absmax, float rcp) {
+  float q = rintf(div_fast(x, absmax, rcp) * kSignedQ);
   q = q < -kSignedQ ? -kSignedQ : (q > kSignedQ ? kSignedQ : q);
   return int8_t(int(q));
 }
-__device__ __forceinline__ uint8_t quant_u8_r(float x, float absmax, float rcp) {
-  float q = rintf(div_rcp(x, absmax, rcp) * kUnsignedQ);
+__device__ __forceinline__ uint8_t quant_u8_fast(float x, float absmax, float rcp) {
+  float q = rintf(div_fast(x, absmax, rcp) * kUnsignedQ);
   q = q < 0.0f ? 0.0f : (q > kUnsignedQ ? kUnsignedQ : q);
   return uint8_t(int(q));
+}
+// Division by the clip divisor (in [1, 2^60], shared by a whole tensor) with y = rcp_for_div(clip):
+// the fast path is exact for zero and for every finite numerator with |a| >= 2^-40, whose quotient
+// is then a normal number (tests/test_div_rcp.py); it fails only for tiny numerators with subnormal
+// quotients and for infinities.  Callers keep a DivGuard per chunk and redo the rare chunks that
+// hold other numerators with the IEEE division, element by element, out of the hot path.
+__device__ __forceinline__ bool div_exact_needed(float a) {
+  const float aa = fabsf(a);
+  return !(aa >= 0x1p-40f && aa <= 0x1.fffffep127f) && a != 0.0f;
+}
+
+// Range of the nonzero |a| over a chunk, one test per chunk: lo is the least (bits(a) << 1) - 1
+// (the sign shifted out; zeros wrap to the largest value and drop out), hi the largest |a|.
+struct DivGuard {
+  uint32_t lo = 0xffffffffu;
+  float hi = 0.0f;
+  __device__ __forceinline__ void add(float a) {
+    lo = min(lo, (__float_as_uint(a) << 1) - 1u);
+    hi = fmaxf(hi, fabsf(a));
+  }
+  // every numerator is zero or has 2^-40 <= |a| <= FLT_MAX (0x56ffffff = (bits(2^-40) << 1) - 1)
+  __device__ __forceinline__ bool fast() const { return lo >= 0x56ffffffu && hi <= 0x1.fffffep127f; }
+};
+
+// absmax / 127 for dequantisation: the reciprocal form equals the IEEE quotient for every finite
+// absmax (checked over all finite floats); infinities and NaNs divide.
+constexpr float kRcpSignedQ = 1.0f / kSignedQ;
+__device__ __forceinline__ float scale_s8(float absmax) {
+  if (__builtin_expect(!(fabsf(absmax) <= 0x1.fffffep127f), 0)) return absmax / kSignedQ;
+  return div_fast(absmax, kSignedQ, kRcpSignedQ);
+}
+
+// any rcp (NaN divides)
+__device__ __forceinline__ int8_t quant_s8_r(float x, float absmax, float rcp) {
+  return rcp == rcp ? quant_s8_fast(x, absmax, rcp) : quant_s8(x, absmax);
+}
+__device__ __forceinline__ uint8_t quant_u8_r(float x, float absmax, float rcp) {
+  return rcp == rcp ? quant_u8_fast(x, absmax, rcp) : quant_u8(x, absmax);
 }
 
 // n / d for n < 2^31 with the host-precomputed magic m = floor(2^s / d) + 1, s = 32 + ceil(log2 d)

@@ -67,6 +67,7 @@ struct DevTensor {
   uint64_t mC, mR;    // magic multipliers for n / C and n / R (n < 2^31)
   uint32_t sC, sR;    // and their shifts
   int32_t idx32;      // N < 2^31: flat indices fit the magic division
+  int32_t rowal;      // the quantisation block size divides C (every row starts a block)
   int32_t c8;         // C % 8 == 0: 8 consecutive elements never cross a row
   int32_t vec_ok;     // p, g, codes 16-byte aligned (flat passes may use vector access)
   int32_t factored;
@@ -84,10 +85,12 @@ struct Hp {
   int32_t wd;      // weight_decay != 0
   int32_t B;       // quantisation block size
   int32_t log2B;   // log2(B) if B is a power of two, else -1
+  uint32_t sB;     // magic division by B (indices < 2^31, which the host guarantees for
+  uint64_t mB;     // block sizes that are not powers of two)
 };
 
 __device__ __forceinline__ int64_t blk_of(int64_t e, const Hp& hp) {
-  return hp.log2B >= 0 ? (e >> hp.log2B) : (e / hp.B);
+  return hp.log2B >= 0 ? (e >> hp.log2B) : int64_t(udiv_magic(uint32_t(e), hp.mB, hp.sB));
 }
 
 // wstart has n+1 entries, wstart[0] = 0; returns k with wstart[k] <= w < wstart[k+1]
@@ -129,42 +132,52 @@ constexpr int kMaxBandRows = 256;
 // register buffers).  Wider rows are handled in column segments after a first
 // sweep that forms the row sums.
 
+// V consecutive gradient elements, kept as raw 32-bit words until used (V = 1, or 16 bytes).
 template <typename TG, int V>
 struct Chunk {
-  typename TG::storage s[V];
-  __device__ __forceinline__ void load(const typename TG::storage* __restrict__ p) {
+  static constexpr int NWD = V == 1 ? 1 : 4;
+  uint32_t w[NWD];
+  __device__ __forceinline__ void load(const CAME8_GLOBAL typename TG::storage* __restrict__ p) {
     if constexpr (V == 1) {
-      s[0] = p[0];
+      if constexpr (sizeof(typename TG::storage) == 4) w[0] = __float_as_uint(p[0]);
+      else w[0] = uint32_t(p[0]);
     } else {
       static_assert(V * sizeof(typename TG::storage) == 16, "vector chunk must be 16 bytes");
-      *reinterpret_cast<uint4*>(s) = *reinterpret_cast<const uint4*>(p);
+      const u32x4 r = *(const CAME8_GLOBAL u32x4*)p;
+      w[0] = r.x; w[1] = r.y; w[2] = r.z; w[3] = r.w;
     }
   }
-  __device__ __forceinline__ float operator[](int v) const { return TG::load(s[v]); }
+  __device__ __forceinline__ float operator[](int v) const { return TG::elem(w, v); }
 };
 
+// V consecutive int8 codes (V-byte aligned for V = 4, 8), as raw words.
 template <int V>
 struct CodeChunk {
-  int8_t s[V];
-  __device__ __forceinline__ void load(const int8_t* __restrict__ p) {
+  static constexpr int NWD = (V + 3) / 4;
+  uint32_t w[NWD];
+  __device__ __forceinline__ void load(const CAME8_GLOBAL int8_t* __restrict__ p) {
     if constexpr (V == 8) {
-      *reinterpret_cast<uint2*>(s) = *reinterpret_cast<const uint2*>(p);
+      const u32x2 r = *(const CAME8_GLOBAL u32x2*)p;
+      w[0] = r.x; w[1] = r.y;
     } else if constexpr (V == 4) {
-      *reinterpret_cast<uint32_t*>(s) = *reinterpret_cast<const uint32_t*>(p);
+      w[0] = *(const CAME8_GLOBAL uint32_t*)p;
     } else {
 #pragma unroll
-      for (int v = 0; v < V; ++v) s[v] = p[v];
+      for (int i = 0; i < NWD; ++i) w[i] = 0;
+#pragma unroll
+      for (int v = 0; v < V; ++v) w[v >> 2] |= uint32_t(uint8_t(p[v])) << (8 * (v & 3));
     }
   }
+  __device__ __forceinline__ float operator[](int v) const { return code_elem(w, v); }
 };
 
 // V int8 codes as floats (V consecutive, V-byte aligned)
 template <int V>
-__device__ __forceinline__ void load_codes(const int8_t* __restrict__ q, float (&out)[V]) {
+__device__ __forceinline__ void load_codes(const CAME8_GLOBAL int8_t* __restrict__ q, float (&out)[V]) {
   CodeChunk<V> c;
   c.load(q);
 #pragma unroll
-  for (int v = 0; v < V; ++v) out[v] = float(c.s[v]);
+  for (int v = 0; v < V; ++v) out[v] = c[v];
 }
 
 // Rows per register stage: about 64 bytes of gradient per thread, 1..16 rows.
@@ -236,11 +249,14 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
     const BandItem it = band_item(T, tids, wstart, ntens, w);
     const DevTensor& t = *it.t;
     const int64_t R = t.R, C = t.C, b = it.b, r0 = it.r0, r1 = it.r1;
-    const GS* __restrict__ g = static_cast<const GS*>(t.g) + (b * R) * C;
+    const CAME8_GLOBAL GS* __restrict__ g = gbl(static_cast<const GS*>(t.g) + (b * R) * C);
+    const CAME8_GLOBAL uint8_t* __restrict__ rq = gbl(t.rq);
+    const CAME8_GLOBAL float* __restrict__ ra = gbl(t.ra);
+    CAME8_GLOBAL float* __restrict__ Rn = gbl(t.Rn);
     const float fC = float(C);
     const int64_t nseg = (C + segw - 1) / segw;
-    float* __restrict__ pU = t.partU + (b * t.nbands + it.band) * C;
-    float* __restrict__ pW = t.partW + (b * t.nbands + it.band) * C;
+    CAME8_GLOBAL float* __restrict__ pU = gbl(t.partU + (b * t.nbands + it.band) * C);
+    CAME8_GLOBAL float* __restrict__ pW = gbl(t.partW + (b * t.nbands + it.band) * C);
 
     if (nseg == 1) {
       Acc colU[K][V], colW[K][V];
@@ -249,14 +265,19 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
 #pragma unroll
         for (int v = 0; v < V; ++v) colU[k][v] = colW[k][v] = Acc(0);
       Chunk<TG, V> A[S][K], Bf[S][K];
+      int32_t coff[K];  // this thread's column offsets; coff[k] < C when chunk k exists
+#pragma unroll
+      for (int k = 0; k < K; ++k) coff[k] = (tid + k * TPB) * V;
       auto load_stage = [&](Chunk<TG, V> (&buf)[S][K], int64_t r) {
 #pragma unroll
-        for (int s = 0; s < S; ++s)
+        for (int s = 0; s < S; ++s) {
+          if (r + s < r1) {
+            const CAME8_GLOBAL GS* __restrict__ grow = g + (r + s) * C;
 #pragma unroll
-          for (int k = 0; k < K; ++k) {
-            const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
-            if (r + s < r1 && c0 < C) buf[s][k].load(g + (r + s) * C + c0);
+            for (int k = 0; k < K; ++k)
+              if (coff[k] < C) buf[s][k].load(grow + coff[k]);
           }
+        }
       };
       auto process = [&](const Chunk<TG, V> (&buf)[S][K], int64_t r) {
         float ps[S];
@@ -265,8 +286,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
           ps[s] = 0.0f;
 #pragma unroll
           for (int k = 0; k < K; ++k) {
-            const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
-            if (r + s < r1 && c0 < C) {
+            if (r + s < r1 && coff[k] < C) {
 #pragma unroll
               for (int v = 0; v < V; ++v) {
                 const float x = buf[s][k][v];
@@ -282,14 +302,13 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
         for (int s = 0; s < S; ++s) {
           if (r + s < r1) {
             const int64_t row = b * R + r + s;
-            const float Rold = deq_u8(t.rq[row], t.ra[blk_of(row, hp)]);
+            const float Rold = deq_u8(rq[row], ra[blk_of(row, hp)]);
             const float Rnew = fmaf(tot[s] / fC, hp.a2, Rold * hp.b2);
-            if (tid == 0) t.Rn[row] = Rnew;
+            if (tid == 0) Rn[row] = Rnew;
             const float invR = 1.0f / Rnew;
 #pragma unroll
             for (int k = 0; k < K; ++k) {
-              const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
-              if (c0 < C) {
+              if (coff[k] < C) {
 #pragma unroll
                 for (int v = 0; v < V; ++v) {
                   const float x = buf[s][k][v];
@@ -350,10 +369,10 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
         for (int s = 0; s < S; ++s) {
           if (r + s < r1) {
             const int64_t row = b * R + r + s;
-            const float Rold = deq_u8(t.rq[row], t.ra[blk_of(row, hp)]);
+            const float Rold = deq_u8(rq[row], ra[blk_of(row, hp)]);
             const float Rnew = fmaf(tot[s] / fC, hp.a2, Rold * hp.b2);
             if (tid == 0) {
-              t.Rn[row] = Rnew;
+              Rn[row] = Rnew;
               rowR[r + s - r0] = Rnew;
             }
           }
@@ -412,36 +431,69 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
   constexpr int S = Stage<TG, V, K>::S;
   constexpr int64_t segw = int64_t(TPB) * V * K;
   __shared__ float red[2][16][NW];
-  const int tid = threadIdx.x;
-  int par = 0;
+  __shared__ float rowpart[2][kMaxBandRows][NW];  // per-wave row sums of a band (fast path)
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  int par = 0, bpar = 0;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
     const BandItem it = band_item(T, tids, wstart, ntens, w);
     const DevTensor& t = *it.t;
     const int64_t R = t.R, C = t.C, b = it.b, r0 = it.r0, r1 = it.r1;
     const int64_t ebase = (b * R) * C;
-    const GS* __restrict__ g = static_cast<const GS*>(t.g) + ebase;
-    const int8_t* __restrict__ mq = t.mq + ebase;
-    const float* __restrict__ cf = t.cfac + b * C;
-    const float clip = t.clip[0], crcp = t.clip[1];
+    const CAME8_GLOBAL GS* __restrict__ g = gbl(static_cast<const GS*>(t.g) + ebase);
+    const CAME8_GLOBAL int8_t* __restrict__ mq = gbl(t.mq + ebase);
+    const CAME8_GLOBAL float* __restrict__ ma = gbl(t.ma);
+    const CAME8_GLOBAL float* __restrict__ cf = gbl(t.cfac + b * C);
+    const CAME8_GLOBAL float* __restrict__ rfac = gbl(t.rfac);
+    const CAME8_GLOBAL uint8_t* __restrict__ rq = gbl(t.rq);
+    const CAME8_GLOBAL float* __restrict__ ra = gbl(t.ra);
+    CAME8_GLOBAL float* __restrict__ RRn = gbl(t.RRn);
+    const float clip = uniform_f32(t.clip[0]), crcp = uniform_f32(t.clip[1]);
+    const bool clip_fast = crcp == crcp;
     const float fC = float(C);
     const int64_t nseg = (C + segw - 1) / segw;
-    float* __restrict__ pR = t.partRes + (b * t.nbands + it.band) * C;
+    CAME8_GLOBAL float* __restrict__ pR = gbl(t.partRes + (b * t.nbands + it.band) * C);
     const int64_t PR = t.P * R;
 
-    // residual of one element, and of a V-chunk (V > 1 chunks lie inside one quantisation block)
+    // residual of one element (the reference's u, m_new and (u - m_new)^2 + eps1)
     auto res_of = [&](float ri, float cj, float x, float q, float scale) {
-      const float u = div_rcp((ri * cj) * x, clip, crcp);
+      const float a = (ri * cj) * x;
+      float u = a / clip;
+      if (clip_fast && !div_exact_needed(a)) u = div_fast(a, clip, crcp);
       const float m = fmaf(u, hp.a1, (q * scale) * hp.b1);
       const float d = u - m;
       return d * d + hp.eps1;
     };
+    // Residuals of a V-chunk (V > 1 chunks lie inside one quantisation block) with the reciprocal
+    // divisions only; `bad` records a numerator or an absmax outside their exact range, after which
+    // the band is recomputed by the general path below.
+    auto res_chunk = [&](float ri, const float (&cjv)[V], const Chunk<TG, V>& x, const CodeChunk<V>& qc,
+                         float amax, float (&res)[V], bool& bad) {
+      const float scale = div_fast(amax, kSignedQ, kRcpSignedQ);
+      float a[V];
+      DivGuard gd;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        a[v] = (ri * cjv[v]) * x[v];
+        gd.add(a[v]);
+      }
+      bad |= !gd.fast() || !(fabsf(amax) <= 0x1.fffffep127f);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float u = div_fast(a[v], clip, crcp);
+        const float m = fmaf(u, hp.a1, (qc[v] * scale) * hp.b1);
+        const float d = u - m;
+        res[v] = d * d + hp.eps1;
+      }
+    };
     auto row_state = [&](int64_t row, float tot) {
-      const float RRold = deq_u8(t.rq[PR + row], t.ra[t.nbr + blk_of(row, hp)]);
-      t.RRn[row] = fmaf(tot / fC, hp.a3, RRold * hp.b3);
+      const float RRold = deq_u8(rq[PR + row], ra[t.nbr + blk_of(row, hp)]);
+      RRn[row] = fmaf(tot / fC, hp.a3, RRold * hp.b3);
     };
 
-    if (nseg == 1) {
+    bool general = nseg > 1 || !clip_fast;
+    if (!general) {
+      bool bad = false;
       float cj[K][V];
 #pragma unroll
       for (int k = 0; k < K; ++k) {
@@ -456,58 +508,76 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
         for (int v = 0; v < V; ++v) colR[k][v] = Acc(0);
       Chunk<TG, V> gA[S][K], gB[S][K];
       CodeChunk<V> qA[S][K], qB[S][K];
+      int32_t coff[K];  // this thread's column offsets; coff[k] < C when chunk k exists
+#pragma unroll
+      for (int k = 0; k < K; ++k) coff[k] = (tid + k * TPB) * V;
       auto load_stage = [&](Chunk<TG, V> (&gb)[S][K], CodeChunk<V> (&qb)[S][K], int64_t r) {
 #pragma unroll
-        for (int s = 0; s < S; ++s)
+        for (int s = 0; s < S; ++s) {
+          if (r + s < r1) {
+            const CAME8_GLOBAL GS* __restrict__ grow = g + (r + s) * C;
+            const CAME8_GLOBAL int8_t* __restrict__ qrow = mq + (r + s) * C;
 #pragma unroll
-          for (int k = 0; k < K; ++k) {
-            const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
-            if (r + s < r1 && c0 < C) {
-              gb[s][k].load(g + (r + s) * C + c0);
-              qb[s][k].load(mq + (r + s) * C + c0);
+            for (int k = 0; k < K; ++k) {
+              if (coff[k] < C) {
+                gb[s][k].load(grow + coff[k]);
+                qb[s][k].load(qrow + coff[k]);
+              }
             }
           }
+        }
       };
-      auto process = [&](const Chunk<TG, V> (&gb)[S][K], const CodeChunk<V> (&qb)[S][K], int64_t r) {
+      // When B divides C a row starts a block: the block of chunk k is the row's first block plus
+      // the chunk's (per-thread) block offset cbk[k].
+      int32_t cbk[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) cbk[k] = t.rowal ? int32_t(blk_of(coff[k], hp)) : 0;
+      auto process = [&](auto AL, const Chunk<TG, V> (&gb)[S][K], const CodeChunk<V> (&qb)[S][K],
+                         int64_t r) __attribute__((always_inline)) {
+        constexpr bool kAligned = decltype(AL)::value;
         float ps[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           ps[s] = 0.0f;
           if (r + s < r1) {
-            const float ri = t.rfac[b * R + r + s];
+            const float ri = rfac[b * R + r + s];
+            const int64_t erow = ebase + (r + s) * C;
+            const CAME8_GLOBAL float* __restrict__ marow = kAligned ? ma + blk_of(erow, hp) : ma;
 #pragma unroll
             for (int k = 0; k < K; ++k) {
-              const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
-              if (c0 < C) {
-                const int64_t e = (r + s) * C + c0;
-                float scale = t.ma[blk_of(ebase + e, hp)] / kSignedQ;
+              if (coff[k] < C) {
+                const float amax = kAligned ? marow[cbk[k]] : ma[blk_of(erow + coff[k], hp)];
+                float res[V];
+                res_chunk(ri, cj[k], gb[s][k], qb[s][k], amax, res, bad);
 #pragma unroll
                 for (int v = 0; v < V; ++v) {
-                  if (V == 1 && v > 0) scale = t.ma[blk_of(ebase + e + v, hp)] / kSignedQ;
-                  const float res = res_of(ri, cj[k][v], gb[s][k][v], float(qb[s][k].s[v]), scale);
-                  ps[s] += res;
-                  colR[k][v] += Acc(res);
+                  ps[s] += res[v];
+                  colR[k][v] += Acc(res[v]);
                 }
               }
             }
           }
         }
-        float tot[S];
-        block_row_sums<S, NW>(ps, red, par, tot);
-        par ^= 1;
+        // each wave's share of the row sums; the band's rows are combined after its last stage
 #pragma unroll
-        for (int s = 0; s < S; ++s)
-          if (r + s < r1 && tid == 0) row_state(b * R + r + s, tot[s]);
-      };
-      load_stage(gA, qA, r0);
-      for (int64_t r = r0; r < r1; r += 2 * S) {
-        if (r + S < r1) load_stage(gB, qB, r + S);
-        process(gA, qA, r);
-        if (r + S < r1) {
-          if (r + 2 * S < r1) load_stage(gA, qA, r + 2 * S);
-          process(gB, qB, r + S);
+        for (int s = 0; s < S; ++s) {
+          const float wsum = wave_sum(ps[s]);
+          if (lane == 0 && r + s < r1) rowpart[bpar][r + s - r0][wid] = wsum;
         }
-      }
+      };
+      auto run = [&](auto AL) __attribute__((always_inline)) {
+        load_stage(gA, qA, r0);
+        for (int64_t r = r0; r < r1; r += 2 * S) {
+          if (r + S < r1) load_stage(gB, qB, r + S);
+          process(AL, gA, qA, r);
+          if (r + S < r1) {
+            if (r + 2 * S < r1) load_stage(gA, qA, r + 2 * S);
+            process(AL, gB, qB, r + S);
+          }
+        }
+      };
+      if (t.rowal) run(std::true_type{});
+      else run(std::false_type{});
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
@@ -516,8 +586,20 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
           for (int v = 0; v < V; ++v) pR[c0 + v] = float(colR[k][v]);
         }
       }
-    } else {
-      // column partials, segment by segment
+      general = __syncthreads_or(bad);  // rare: the general path rewrites this band's outputs
+      if (!general) {
+        // row totals over the waves in a fixed order
+        for (int rr = tid; rr < r1 - r0; rr += TPB) {
+          float tot = rowpart[bpar][rr][0];
+#pragma unroll
+          for (int w2 = 1; w2 < NW; ++w2) tot += rowpart[bpar][rr][w2];
+          row_state(b * R + r0 + rr, tot);
+        }
+      }
+      bpar ^= 1;  // the next band writes the other half (after this band's barrier above)
+    }
+    if (general) {
+      // general path (wide rows, or exact divisions needed): column partials, segment by segment
       for (int64_t seg = 0; seg < nseg; ++seg) {
         Acc colR[K][V];
 #pragma unroll
@@ -525,7 +607,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
 #pragma unroll
           for (int v = 0; v < V; ++v) colR[k][v] = Acc(0);
         for (int64_t r = r0; r < r1; ++r) {
-          const float ri = t.rfac[b * R + r];
+          const float ri = rfac[b * R + r];
 #pragma unroll
           for (int k = 0; k < K; ++k) {
             const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
@@ -537,8 +619,8 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
               q.load(mq + e);
 #pragma unroll
               for (int v = 0; v < V; ++v) {
-                const float scale = t.ma[blk_of(ebase + e + v, hp)] / kSignedQ;
-                colR[k][v] += Acc(res_of(ri, cf[c0 + v], x[v], float(q.s[v]), scale));
+                const float scale = scale_s8(ma[blk_of(ebase + e + v, hp)]);
+                colR[k][v] += Acc(res_of(ri, cf[c0 + v], x[v], q[v], scale));
               }
             }
           }
@@ -559,7 +641,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
         for (int s = 0; s < S; ++s) {
           ps[s] = 0.0f;
           if (r + s < r1) {
-            const float ri = t.rfac[b * R + r + s];
+            const float ri = rfac[b * R + r + s];
             for (int64_t seg = 0; seg < nseg; ++seg) {
 #pragma unroll
               for (int k = 0; k < K; ++k) {
@@ -572,8 +654,8 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
                   q.load(mq + e);
 #pragma unroll
                   for (int v = 0; v < V; ++v) {
-                    const float scale = t.ma[blk_of(ebase + e + v, hp)] / kSignedQ;
-                    ps[s] += res_of(ri, cf[c0 + v], x[v], float(q.s[v]), scale);
+                    const float scale = scale_s8(ma[blk_of(ebase + e + v, hp)]);
+                    ps[s] += res_of(ri, cf[c0 + v], x[v], q[v], scale);
                   }
                 }
               }
@@ -753,6 +835,7 @@ __device__ __forceinline__ float clip_from_norm(float norm, int64_t N, const Hp&
   return q < 1.0f ? 1.0f : q;
 }
 
+template <int = 0>  // a template only so that every translation unit may include this header
 __global__ __launch_bounds__(kThreads) void k_clip(const DevTensor* __restrict__ T, int ntens, Hp hp) {
   __shared__ double ssum[4];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -834,77 +917,150 @@ __global__ __launch_bounds__(kThreads) void k_clip_refnorm(const DevTensor* __re
 // ===========================================================================
 // 2048-element tiles, 8 consecutive elements per thread, L = B/8 lanes per
 // quantisation block (B a power of two in [8, 2048]).
+//
+// A tile that lies inside its tensor, of a tensor whose rows hold whole 8-element groups and whose
+// buffers are 16-byte aligned, takes the fast path: one branch per tile on a workgroup-uniform
+// condition, vector loads and stores, the reciprocal divisions, and the rare elements outside their
+// exact range handled by selects.  Other tiles (tensor tails, ragged shapes) take the general
+// per-element path.  Both give the same values.
+
+// Maximum of per-thread values over the L lanes of each quantisation block (L = B/8 <= 256); every
+// thread of the workgroup must call it (L > 64 synchronises through LDS).
+__device__ __forceinline__ uint32_t block_max_bits(uint32_t v, int L, uint32_t (*wmax)[4], int& par) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (L <= 64) return group_max_bits_rt(v, L);
+  v = group_max_bits<64>(v);
+  if (lane == 0) wmax[par][wid] = v;
+  __syncthreads();
+  const int wpb = L >> 6;  // waves per block
+  const int w0 = (wid / wpb) * wpb;
+  v = wmax[par][w0];
+  for (int k = 1; k < wpb; ++k) v = max(v, wmax[par][w0 + k]);
+  par ^= 1;
+  return v;
+}
+
+// |m| as an ordered bit pattern (a NaN orders above every number, so a maximum propagates it as
+// torch.amax does)
+__device__ __forceinline__ uint32_t abs_bits(float m) { return __float_as_uint(m) & 0x7fffffffu; }
+
+// 8 codes packed little-endian into two words
+__device__ __forceinline__ u32x2 pack_codes(const int32_t (&c)[8]) {
+  u32x2 r;
+  r.x = __builtin_amdgcn_perm(uint32_t(c[1]), uint32_t(c[0]), 0x0c0c0400u) |
+        __builtin_amdgcn_perm(uint32_t(c[3]), uint32_t(c[2]), 0x04000c0cu);
+  r.y = __builtin_amdgcn_perm(uint32_t(c[5]), uint32_t(c[4]), 0x0c0c0400u) |
+        __builtin_amdgcn_perm(uint32_t(c[7]), uint32_t(c[6]), 0x04000c0cu);
+  return r;
+}
+
 template <typename TP, typename TG>
 __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                          const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using PS = typename TP::storage;
   using GS = typename TG::storage;
-  __shared__ float wmax[2][4];
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  __shared__ uint32_t wmax[2][4];
+  const int tid = threadIdx.x;
   const int L = hp.B >> 3;  // lanes per block
   int par = 0;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
     const int slot = find_slot(wstart, ntens, w);
     const DevTensor& t = T[tids[slot]];
-    const int64_t tile = w - wstart[slot];
-    const int64_t e0 = tile * kTile + int64_t(tid) * 8;
+    const int64_t base = (w - wstart[slot]) * kTile;
+    const int64_t e0 = base + int64_t(tid) * 8;
     const int64_t N = t.N, C = t.C, R = t.R;
-    PS* __restrict__ p = static_cast<PS*>(t.p);
-    const GS* __restrict__ g = static_cast<const GS*>(t.g);
-    const float clip = t.clip[0], crcp = t.clip[1];
-    float m[8], pv[8];
-    const bool full = t.vec_ok && (e0 + 8 <= N);
-    if (e0 < N) {
-      float gv[8], q[8];
-      if (full) {
-        load8<TG>(g + e0, gv);
-        load8<TP>(p + e0, pv);
-        load_codes<8>(t.mq + e0, q);
+    CAME8_GLOBAL PS* __restrict__ p = gbl(static_cast<PS*>(t.p));
+    const CAME8_GLOBAL GS* __restrict__ g = gbl(static_cast<const GS*>(t.g));
+    CAME8_GLOBAL int8_t* __restrict__ mq = gbl(t.mq);
+    CAME8_GLOBAL float* __restrict__ ma = gbl(t.ma);
+    const CAME8_GLOBAL float* __restrict__ rfac = gbl(t.rfac);
+    const CAME8_GLOBAL float* __restrict__ rrfac = gbl(t.rrfac);
+    const CAME8_GLOBAL float* __restrict__ cfac = gbl(t.cfac);
+    const CAME8_GLOBAL float* __restrict__ crfac = gbl(t.crfac);
+    const float clip = uniform_f32(t.clip[0]), crcp = uniform_f32(t.clip[1]);
+    const bool clip_fast = crcp == crcp;
+    const int64_t blk = blk_of(e0, hp);  // 8 elements share a block (B >= 8)
+    int64_t row, bb;
+    if (t.idx32) {
+      const uint32_t r32 = udiv_magic(uint32_t(e0), t.mC, t.sC);
+      row = r32;
+      bb = udiv_magic(r32, t.mR, t.sR);
+    } else {
+      row = e0 / C;
+      bb = row / R;
+    }
+    int64_t j = e0 - row * C;
+
+    if (t.vec_ok && t.c8 && base + kTile <= N) {
+      // ---- fast tile: the 8 elements share a row; their column factors are contiguous ----
+      float gv[8], pv[8], q[8], cj[8], crj[8], m[8];
+      load8<TG>(g + e0, gv);
+      load8<TP>(p + e0, pv);
+      load_codes<8>(mq + e0, q);
+      const float amax_old = ma[blk];
+      const float ri = rfac[row], rri = rrfac[row];
+      load8<F32>(cfac + bb * C + j, cj);
+      load8<F32>(crfac + bb * C + j, crj);
+      float a[8];
+      DivGuard gd;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        a[v] = (ri * cj[v]) * gv[v];
+        gd.add(a[v]);
+      }
+      if (__builtin_expect(clip_fast && gd.fast() && fabsf(amax_old) <= 0x1.fffffep127f, 1)) {
+        const float scale = div_fast(amax_old, kSignedQ, kRcpSignedQ);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) m[v] = fmaf(div_fast(a[v], clip, crcp), hp.a1, (q[v] * scale) * hp.b1);
       } else {
+        // numerators or an absmax outside the reciprocal forms' exact range (selects, no branches)
+        const float scale = amax_old / kSignedQ;
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
-          const bool ok = e0 + v < N;
-          gv[v] = ok ? TG::load(g[e0 + v]) : 0.0f;
-          pv[v] = ok ? TP::load(p[e0 + v]) : 0.0f;
-          q[v] = ok ? float(t.mq[e0 + v]) : 0.0f;
-        }
-      }
-      const float scale = t.ma[blk_of(e0, hp)] / kSignedQ;  // 8 elements share a block (B >= 8)
-      int64_t row, bb;
-      if (t.idx32) {
-        const uint32_t r32 = udiv_magic(uint32_t(e0), t.mC, t.sC);
-        row = r32;
-        bb = udiv_magic(r32, t.mR, t.sR);
-      } else {
-        row = e0 / C;
-        bb = row / R;
-      }
-      int64_t j = e0 - row * C;
-      if (full && t.c8) {
-        // the 8 elements share a row; their column factors are contiguous and 32-byte aligned
-        const float ri = t.rfac[row], rri = t.rrfac[row];
-        float cj[8], crj[8];
-        load8<F32>(t.cfac + bb * C + j, cj);
-        load8<F32>(t.crfac + bb * C + j, crj);
-#pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          const float u = div_rcp((ri * cj[v]) * gv[v], clip, crcp);
+          const float u = (clip_fast && !div_exact_needed(a[v])) ? div_fast(a[v], clip, crcp) : a[v] / clip;
           m[v] = fmaf(u, hp.a1, (q[v] * scale) * hp.b1);
-          pv[v] = param_update<TP>(pv[v], (rri * crj[v]) * m[v], hp);
         }
+      }
+#pragma unroll
+      for (int v = 0; v < 8; ++v) pv[v] = param_update<TP>(pv[v], (rri * crj[v]) * m[v], hp);
+      store8<TP>(p + e0, pv);
+
+      uint32_t abits = 0;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) abits = max(abits, abs_bits(m[v]));
+      abits = block_max_bits(abits, L, wmax, par);
+      const float amax = fix_absmax(__uint_as_float(abits));
+      const float arcp = rcp_for_div(amax);
+      if ((e0 & (hp.B - 1)) == 0) ma[blk] = amax;
+      int32_t c[8];
+      if (__builtin_expect(arcp == arcp && abits <= 0x7f800000u, 1)) {
+        // |m| <= amax, so |m / amax| <= 1 and the code needs no clamp
+#pragma unroll
+        for (int v = 0; v < 8; ++v) c[v] = int32_t(rintf(div_fast(m[v], amax, arcp) * kSignedQ));
       } else {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) c[v] = quant_s8(m[v], amax);
+      }
+      *(CAME8_GLOBAL u32x2*)(mq + e0) = pack_codes(c);
+    } else {
+      // ---- general tile: element by element ----
+      float m[8], pv[8];
+      if (e0 < N) {
+        const float scale = ma[blk] / kSignedQ;
         int64_t i = row - bb * R;
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
           if (e0 + v < N) {
-            const float ri = t.rfac[row], rri = t.rrfac[row];
-            const float cj = t.cfac[bb * C + j], crj = t.crfac[bb * C + j];
-            const float u = div_rcp((ri * cj) * gv[v], clip, crcp);
-            m[v] = fmaf(u, hp.a1, (q[v] * scale) * hp.b1);
+            pv[v] = TP::load(p[e0 + v]);
+            const float ri = rfac[row], rri = rrfac[row];
+            const float cj = cfac[bb * C + j], crj = crfac[bb * C + j];
+            const float u = ((ri * cj) * TG::load(g[e0 + v])) / clip;
+            m[v] = fmaf(u, hp.a1, (float(mq[e0 + v]) * scale) * hp.b1);
             pv[v] = param_update<TP>(pv[v], (rri * crj) * m[v], hp);
           } else {
             m[v] = 0.0f;
+            pv[v] = 0.0f;
           }
           if (++j == C) {
             j = 0;
@@ -915,43 +1071,21 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
             }
           }
         }
-      }
-    } else {
-#pragma unroll
-      for (int v = 0; v < 8; ++v) m[v] = 0.0f;
-    }
-    // block absmax of |m|
-    float amax = 0.0f;
-#pragma unroll
-    for (int v = 0; v < 8; ++v) amax = nan_max(amax, fabsf(m[v]));
-    if (L <= 64) {
-      amax = group_max_rt(amax, L);
-    } else {
-      amax = group_max<64>(amax);
-      if (lane == 0) wmax[par][wid] = amax;
-      __syncthreads();
-      const int wpb = L >> 6;  // waves per block
-      const int w0 = (wid / wpb) * wpb;
-      amax = wmax[par][w0];
-      for (int k = 1; k < wpb; ++k) amax = nan_max(amax, wmax[par][w0 + k]);
-      par ^= 1;
-    }
-    amax = fix_absmax(amax);
-    const float arcp = rcp_for_div(amax);
-    if (e0 < N) {
-      if (((e0 & (hp.B - 1)) == 0)) t.ma[blk_of(e0, hp)] = amax;
-      if (full) {
-        uint2 raw;
-        int8_t* s = reinterpret_cast<int8_t*>(&raw);
-#pragma unroll
-        for (int v = 0; v < 8; ++v) s[v] = quant_s8_r(m[v], amax, arcp);
-        *reinterpret_cast<uint2*>(t.mq + e0) = raw;
-        store8<TP>(p + e0, pv);
       } else {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) m[v] = pv[v] = 0.0f;
+      }
+      uint32_t abits = 0;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) abits = max(abits, abs_bits(m[v]));
+      abits = block_max_bits(abits, L, wmax, par);
+      const float amax = fix_absmax(__uint_as_float(abits));
+      if (e0 < N) {
+        if ((e0 & (hp.B - 1)) == 0) ma[blk] = amax;
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
           if (e0 + v < N) {
-            t.mq[e0 + v] = quant_s8_r(m[v], amax, arcp);
+            mq[e0 + v] = quant_s8(m[v], amax);
             p[e0 + v] = TP::store(pv[v]);
           }
         }
@@ -981,7 +1115,7 @@ __global__ __launch_bounds__(kThreads) void k_vec_passB(const DevTensor* __restr
     const int64_t N = t.N;
     PS* __restrict__ p = static_cast<PS*>(t.p);
     const GS* __restrict__ g = static_cast<const GS*>(t.g);
-    const float clip = t.clip[0], crcp = t.clip[1];
+    const float clip = t.clip[0];
     float m[8], vv[8], pv[8];
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
@@ -989,7 +1123,7 @@ __global__ __launch_bounds__(kThreads) void k_vec_passB(const DevTensor* __restr
       if (e < N) {
         const float gv = TG::load(g[e]);
         vv[v] = vec_v_new<TG>(t, e, gv, hp);
-        const float u = div_rcp(rsqrt_ref(vv[v]) * gv, clip, crcp);
+        const float u = (rsqrt_ref(vv[v]) * gv) / clip;
         const float mold = deq_s8(t.mq[e], t.ma[blk_of(e, hp)]);
         m[v] = fmaf(u, hp.a1, mold * hp.b1);
         pv[v] = param_update<TP>(TP::load(p[e]), m[v], hp);
