@@ -38,6 +38,13 @@ sys.path.insert(0, HERE)
 METRIC = "CAME8bit step time (ms) + achieved HBM GB/s, Llama-7B param set, 1 MI355X"
 HBM_PEAK_GBS = 8000.0
 
+# HBM-side bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this
+# bench (calibrated against a copy of known size: fetch x2, write x1); the summary, with its commands,
+# is the file named in "source".  Re-measured whenever that kernel changes.
+PROFILED_TRAFFIC = {
+    ("c4", "pass3"): {"read": 52.659e9, "write": 20.398e9, "source": "profiles/c4_step_hbm_traffic.md"},
+}
+
 
 # ------------------------------------------------------------------------------------ workloads
 def llama_shapes(layers, d, ffn, vocab):
@@ -234,7 +241,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": (PROFILED_TRAFFIC[(args.config, dname)]["read"] + PROFILED_TRAFFIC[(args.config, dname)]["write"])
+            if (args.config, dname) in PROFILED_TRAFFIC else None,
+            "traffic_source": PROFILED_TRAFFIC.get((args.config, dname), {}).get("source"),
             "alg_bytes_per_launch": dbytes / dl,
             "avg_launch_ms": round(dms / dl, 4),
         },
