@@ -81,7 +81,8 @@ struct WorkList {
 struct Plan {
   std::vector<DevTensor> dev;
   std::map<BandKey, WorkList> band;      // P1 / P2
-  std::map<TypeKey, WorkList> upd;       // P3 (fast block sizes)
+  std::map<TypeKey, WorkList> upd;       // P3, tile form (fast block sizes)
+  std::map<TypeKey, WorkList> updb;      // P3, band form
   std::map<TypeKey, WorkList> vecB;      // 1-D pass B (fast block sizes)
   std::map<int, WorkList> vecA;          // 1-D pass A, by grad type
   std::map<TypeKey, WorkList> generic;   // P3 / B for other block sizes (per quantisation block)
@@ -100,6 +101,9 @@ void add_item(WorkList& wl, int32_t tid, int64_t count) {
 }
 
 bool fast_block(int B) { return B >= 8 && B <= kTile && (B & (B - 1)) == 0; }
+
+constexpr int kP3BandRows = 32;       // rows per work item of the band form of P3
+constexpr int64_t kP3BandMinCols = 1024;  // narrower rows leave too many of a workgroup's lanes idle
 
 int log2_or_minus1(int B) {
   if (B <= 0 || (B & (B - 1)) != 0) return -1;
@@ -199,6 +203,16 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     d.idx32 = d.N < (int64_t(1) << 31) ? 1 : 0;
     d.rowal = (d.C % B) == 0 ? 1 : 0;
     d.c8 = (d.C % 8 == 0) ? 1 : 0;
+    // band form of P3: rows start blocks, vector access, rows wide enough to occupy the lanes
+    d.p3_rb = 0;
+    d.p3_nseg = 0;
+    d.p3_nbands = 0;
+    if (t.factored && fast_block(B) && d.rowal && d.vec_ok && d.C >= kP3BandMinCols) {
+      const int64_t bpr = d.C / B, bmax = kTile / B;  // blocks per row, per segment
+      d.p3_nseg = int32_t(ceil_div(bpr, bmax));
+      d.p3_rb = kP3BandRows;
+      d.p3_nbands = ceil_div(d.R, int64_t(kP3BandRows));
+    }
     magic_div(d.C, d.mC, d.sC);
     magic_div(d.R, d.mR, d.sR);
     if (t.factored) {
@@ -250,7 +264,10 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       add_item(plan.band[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB}], i, d.P * d.nbands);
       add_item(plan.rowmean, i, d.P);
       add_item(plan.factor, i, d.nbr + d.nbc);
-      if (fastB) add_item(plan.upd[tk], i, ceil_div(d.N, kTile));
+      if (fastB) {
+        if (d.p3_nbands > 0) add_item(plan.updb[tk], i, d.P * d.p3_nbands * d.p3_nseg);
+        else add_item(plan.upd[tk], i, ceil_div(d.N, kTile));
+      }
     } else {
       add_item(plan.vecA[t.grad_dtype], i, d.nclip);
       if (fastB) add_item(plan.vecB[tk], i, ceil_div(d.N, kTile));
@@ -269,6 +286,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
   };
   for (auto& kv : plan.band) place(kv.second);
   for (auto& kv : plan.upd) place(kv.second);
+  for (auto& kv : plan.updb) place(kv.second);
   for (auto& kv : plan.vecB) place(kv.second);
   for (auto& kv : plan.vecA) place(kv.second);
   for (auto& kv : plan.generic) place(kv.second);
@@ -303,6 +321,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     };
     for (auto& kv : plan.band) put(kv.second);
     for (auto& kv : plan.upd) put(kv.second);
+    for (auto& kv : plan.updb) put(kv.second);
     for (auto& kv : plan.vecB) put(kv.second);
     for (auto& kv : plan.vecA) put(kv.second);
     for (auto& kv : plan.generic) put(kv.second);
@@ -664,6 +683,14 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       const WorkList& wl = kv.second;
       GenFn fn;
       CAME8_TYPE_SWITCH2(k_fact_pass3, kv.first.pdt, kv.first.gdt, fn);
+      { PhaseTimer pt(PH_PASS3, alg_bytes(plan, wl, tensors, PH_PASS3), stream);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      if ((rc = check_launch("pass3")) != CAME8_OK) return rc; }
+    }
+    for (auto& kv : plan.updb) {
+      const WorkList& wl = kv.second;
+      GenFn fn;
+      CAME8_TYPE_SWITCH2(k_fact_pass3b, kv.first.pdt, kv.first.gdt, fn);
       { PhaseTimer pt(PH_PASS3, alg_bytes(plan, wl, tensors, PH_PASS3), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("pass3")) != CAME8_OK) return rc; }

@@ -68,6 +68,9 @@ struct DevTensor {
   uint32_t sC, sR;    // and their shifts
   int32_t idx32;      // N < 2^31: flat indices fit the magic division
   int32_t rowal;      // the quantisation block size divides C (every row starts a block)
+  int32_t p3_rb;      // band form of P3: rows per work item,
+  int32_t p3_nseg;    // column segments per row,
+  int64_t p3_nbands;  // row bands per matrix (0: the tensor uses the tile form)
   int32_t c8;         // C % 8 == 0: 8 consecutive elements never cross a row
   int32_t vec_ok;     // p, g, codes 16-byte aligned (flat passes may use vector access)
   int32_t factored;
@@ -954,6 +957,51 @@ __device__ __forceinline__ u32x2 pack_codes(const int32_t (&c)[8]) {
   return r;
 }
 
+// m_new and the updated parameters of 8 elements that share a row and a quantisation block
+// (reference CAME8bitFull.py:1032-1036 and 1047-1056): the reciprocal divisions, and the rare
+// operands outside their exact range through selects.
+template <typename TP>
+__device__ __forceinline__ void p3_math8(const float (&gv)[8], const float (&q)[8], float (&pv)[8], float (&m)[8],
+                                         float amax_old, float ri, float rri, const float (&cj)[8],
+                                         const float (&crj)[8], float clip, float crcp, bool clip_fast, const Hp& hp) {
+  float a[8];
+  DivGuard gd;
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    a[v] = (ri * cj[v]) * gv[v];
+    gd.add(a[v]);
+  }
+  if (__builtin_expect(clip_fast && gd.fast() && fabsf(amax_old) <= 0x1.fffffep127f, 1)) {
+    const float scale = div_fast(amax_old, kSignedQ, kRcpSignedQ);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) m[v] = fmaf(div_fast(a[v], clip, crcp), hp.a1, (q[v] * scale) * hp.b1);
+  } else {
+    const float scale = amax_old / kSignedQ;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const float u = (clip_fast && !div_exact_needed(a[v])) ? div_fast(a[v], clip, crcp) : a[v] / clip;
+      m[v] = fmaf(u, hp.a1, (q[v] * scale) * hp.b1);
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < 8; ++v) pv[v] = param_update<TP>(pv[v], (rri * crj[v]) * m[v], hp);
+}
+
+// int8 codes of 8 values of a block whose absmax is amax (abits: the block maximum of |m| as bits)
+__device__ __forceinline__ u32x2 p3_quant8(const float (&m)[8], float amax, uint32_t abits) {
+  const float arcp = rcp_for_div(amax);
+  int32_t c[8];
+  if (__builtin_expect(arcp == arcp && abits <= 0x7f800000u, 1)) {
+    // |m| <= amax, so |m / amax| <= 1 and the code needs no clamp
+#pragma unroll
+    for (int v = 0; v < 8; ++v) c[v] = int32_t(rintf(div_fast(m[v], amax, arcp) * kSignedQ));
+  } else {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) c[v] = quant_s8(m[v], amax);
+  }
+  return pack_codes(c);
+}
+
 template <typename TP, typename TG>
 __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                          const int64_t* __restrict__ wstart, int ntens, Hp hp) {
@@ -1002,28 +1050,7 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
       const float ri = rfac[row], rri = rrfac[row];
       load8<F32>(cfac + bb * C + j, cj);
       load8<F32>(crfac + bb * C + j, crj);
-      float a[8];
-      DivGuard gd;
-#pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        a[v] = (ri * cj[v]) * gv[v];
-        gd.add(a[v]);
-      }
-      if (__builtin_expect(clip_fast && gd.fast() && fabsf(amax_old) <= 0x1.fffffep127f, 1)) {
-        const float scale = div_fast(amax_old, kSignedQ, kRcpSignedQ);
-#pragma unroll
-        for (int v = 0; v < 8; ++v) m[v] = fmaf(div_fast(a[v], clip, crcp), hp.a1, (q[v] * scale) * hp.b1);
-      } else {
-        // numerators or an absmax outside the reciprocal forms' exact range (selects, no branches)
-        const float scale = amax_old / kSignedQ;
-#pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          const float u = (clip_fast && !div_exact_needed(a[v])) ? div_fast(a[v], clip, crcp) : a[v] / clip;
-          m[v] = fmaf(u, hp.a1, (q[v] * scale) * hp.b1);
-        }
-      }
-#pragma unroll
-      for (int v = 0; v < 8; ++v) pv[v] = param_update<TP>(pv[v], (rri * crj[v]) * m[v], hp);
+      p3_math8<TP>(gv, q, pv, m, amax_old, ri, rri, cj, crj, clip, crcp, clip_fast, hp);
       store8<TP>(p + e0, pv);
 
       uint32_t abits = 0;
@@ -1031,18 +1058,8 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
       for (int v = 0; v < 8; ++v) abits = max(abits, abs_bits(m[v]));
       abits = block_max_bits(abits, L, wmax, par);
       const float amax = fix_absmax(__uint_as_float(abits));
-      const float arcp = rcp_for_div(amax);
       if ((e0 & (hp.B - 1)) == 0) ma[blk] = amax;
-      int32_t c[8];
-      if (__builtin_expect(arcp == arcp && abits <= 0x7f800000u, 1)) {
-        // |m| <= amax, so |m / amax| <= 1 and the code needs no clamp
-#pragma unroll
-        for (int v = 0; v < 8; ++v) c[v] = int32_t(rintf(div_fast(m[v], amax, arcp) * kSignedQ));
-      } else {
-#pragma unroll
-        for (int v = 0; v < 8; ++v) c[v] = quant_s8(m[v], amax);
-      }
-      *(CAME8_GLOBAL u32x2*)(mq + e0) = pack_codes(c);
+      *(CAME8_GLOBAL u32x2*)(mq + e0) = p3_quant8(m, amax, abits);
     } else {
       // ---- general tile: element by element ----
       float m[8], pv[8];
@@ -1089,6 +1106,122 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
             p[e0 + v] = TP::store(pv[v]);
           }
         }
+      }
+    }
+  }
+}
+
+// ===========================================================================
+// P3, band form: rows stream through a workgroup that keeps its columns' factors in registers
+// ===========================================================================
+// For tensors whose rows start quantisation blocks (B divides C; B a power of two in [8, 2048]) and
+// whose buffers are 16-byte aligned.  A work item is (matrix, band of p3_rb rows, column segment
+// of whole blocks, at most 2048 columns); thread t owns 8 consecutive columns of the segment, loads
+// their c and cr factors once, and walks the band's rows with the next row's loads in flight.
+// The arithmetic is p3_math8 / p3_quant8, as in the tile kernel.
+
+// 8 consecutive elements of type T kept as raw 32-bit words until used
+template <typename T>
+struct Raw8 {
+  static constexpr int NWD = int(sizeof(typename T::storage)) * 2;
+  uint32_t w[NWD];
+  __device__ __forceinline__ void load(const CAME8_GLOBAL typename T::storage* __restrict__ p) {
+    const CAME8_GLOBAL u32x4* q = (const CAME8_GLOBAL u32x4*)p;
+#pragma unroll
+    for (int i = 0; i < NWD / 4; ++i) {
+      const u32x4 r = q[i];
+      w[4 * i] = r.x; w[4 * i + 1] = r.y; w[4 * i + 2] = r.z; w[4 * i + 3] = r.w;
+    }
+  }
+  __device__ __forceinline__ float operator[](int v) const { return T::elem(w, v); }
+};
+
+template <typename TP, typename TG>
+__global__ __launch_bounds__(kThreads) void k_fact_pass3b(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                          const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using PS = typename TP::storage;
+  using GS = typename TG::storage;
+  __shared__ uint32_t wmax[2][4];
+  const int tid = threadIdx.x;
+  const int L = hp.B >> 3;  // lanes per block
+  int par = 0;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t R = t.R, C = t.C;
+    const int64_t nseg = t.p3_nseg;
+    const int64_t local = w - wstart[slot];
+    const int64_t per_mat = t.p3_nbands * nseg;
+    const int64_t b = local / per_mat;
+    const int64_t rem = local - b * per_mat;
+    const int64_t band = rem / nseg, seg = rem - band * nseg;
+    const int64_t r0 = band * t.p3_rb;
+    const int64_t r1 = (r0 + t.p3_rb < R) ? (r0 + t.p3_rb) : R;
+    const int64_t bpr = C >> hp.log2B;  // blocks per row
+    const int64_t blk0 = seg * bpr / nseg, blk1 = (seg + 1) * bpr / nseg;
+    const bool active = tid < (blk1 - blk0) * L;
+    const int64_t col = (blk0 << hp.log2B) + int64_t(tid) * 8;
+    const int64_t cblk = blk0 + (tid >> (hp.log2B - 3));  // this thread's block within a row
+
+    CAME8_GLOBAL PS* __restrict__ p = gbl(static_cast<PS*>(t.p));
+    const CAME8_GLOBAL GS* __restrict__ g = gbl(static_cast<const GS*>(t.g));
+    CAME8_GLOBAL int8_t* __restrict__ mq = gbl(t.mq);
+    CAME8_GLOBAL float* __restrict__ ma = gbl(t.ma);
+    const CAME8_GLOBAL float* __restrict__ rfac = gbl(t.rfac);
+    const CAME8_GLOBAL float* __restrict__ rrfac = gbl(t.rrfac);
+    const float clip = uniform_f32(t.clip[0]), crcp = uniform_f32(t.clip[1]);
+    const bool clip_fast = crcp == crcp;
+
+    float cj[8], crj[8];
+    if (active) {
+      load8<F32>(gbl(t.cfac) + b * C + col, cj);
+      load8<F32>(gbl(t.crfac) + b * C + col, crj);
+    }
+    Raw8<TG> gA, gB;
+    Raw8<TP> pA, pB;
+    CodeChunk<8> qA, qB;
+    float aA = 0.0f, aB = 0.0f;
+    auto load_row = [&](int64_t r, Raw8<TG>& gr, Raw8<TP>& pr, CodeChunk<8>& qr, float& am) {
+      const int64_t e = (b * R + r) * C + col;
+      gr.load(g + e);
+      pr.load(p + e);
+      qr.load(mq + e);
+      am = ma[(b * R + r) * bpr + cblk];
+    };
+    auto do_row = [&](int64_t r, const Raw8<TG>& gr, const Raw8<TP>& pr, const CodeChunk<8>& qr, float am) {
+      const int64_t row = b * R + r;
+      const float ri = uniform_f32(rfac[row]), rri = uniform_f32(rrfac[row]);
+      float m[8], pv[8];
+      uint32_t abits = 0;
+      if (active) {
+        float gv[8], q[8];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          gv[v] = gr[v];
+          q[v] = qr[v];
+          pv[v] = pr[v];
+        }
+        p3_math8<TP>(gv, q, pv, m, am, ri, rri, cj, crj, clip, crcp, clip_fast, hp);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) abits = max(abits, abs_bits(m[v]));
+      }
+      abits = block_max_bits(abits, L, wmax, par);
+      if (active) {
+        const int64_t e = row * C + col;
+        store8<TP>(p + e, pv);
+        const float amax = fix_absmax(__uint_as_float(abits));
+        if ((tid & (L - 1)) == 0) ma[row * bpr + cblk] = amax;
+        *(CAME8_GLOBAL u32x2*)(mq + e) = p3_quant8(m, amax, abits);
+      }
+    };
+    if (active) load_row(r0, gA, pA, qA, aA);
+    for (int64_t r = r0; r < r1; r += 2) {
+      if (active && r + 1 < r1) load_row(r + 1, gB, pB, qB, aB);
+      do_row(r, gA, pA, qA, aA);
+      if (r + 1 < r1) {
+        if (active && r + 2 < r1) load_row(r + 2, gA, pA, qA, aA);
+        do_row(r + 1, gB, pB, qB, aB);
       }
     }
   }

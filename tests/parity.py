@@ -146,13 +146,13 @@ def compare_states(gpu_state: dict, ref_state: dict, *, code_frac: float, abs_re
             frac, mx = code_mismatch(g, r)
             report[k] = (frac, mx)
             assert mx <= max_code_diff, f"{where}/{k}: a code differs by {mx}"
-            n = max(1, g.numel())
-            assert frac * n <= max(2.0, code_frac * n), f"{where}/{k}: {frac:.3e} of codes differ (bound {code_frac})"
             if ref_fp32 is not None and tie_tol is not None and mx > 0:
                 dist = tie_distance(k, ref_state, ref_fp32, block)
                 diff = g.to(torch.int32) != r.to(torch.int32)
                 worst = dist[diff].max().item()
                 assert worst <= tie_tol, f"{where}/{k}: a differing code is {worst:.2e} from a rounding tie (> {tie_tol})"
+            n = max(1, g.numel())
+            assert frac * n <= max(2.0, code_frac * n), f"{where}/{k}: {frac:.3e} of codes differ (bound {code_frac})"
         else:
             m, _ = rel_err(g, r)
             report[k] = m
