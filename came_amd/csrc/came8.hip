@@ -87,7 +87,6 @@ struct Plan {
   std::map<int, WorkList> vecA;          // 1-D pass A, by grad type
   std::map<TypeKey, WorkList> generic;   // P3 / B for other block sizes (per quantisation block)
   std::map<int, WorkList> refnorm;       // parity-mode clip, by grad type
-  WorkList rowmean;                      // F1a / F2a (per matrix)
   WorkList factor;                       // F1b / F2b (per state block)
   size_t plan_bytes = 0;
   size_t total_bytes = 0;
@@ -227,7 +226,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       o.Rn = take(pr); o.rfac = take(pr); o.RRn = take(pr); o.rrfac = take(pr);
       o.Cn = take(pc); o.cfac = take(pc); o.CRn = take(pc); o.crfac = take(pc);
       o.pU = take(part); o.pW = take(part); o.pR = take(part);
-      o.rm = take(size_t(d.P) * 4); o.rmr = take(size_t(d.P) * 4);
+      o.rm = take(size_t(d.P * d.nbands) * 4); o.rmr = take(size_t(d.P * d.nbands) * 4);
       o.clipp = take(size_t(d.nclip) * 8);
       o.clip = take(8);
     } else {
@@ -246,7 +245,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       d.Rn = at(o.Rn); d.rfac = at(o.rfac); d.RRn = at(o.RRn); d.rrfac = at(o.rrfac);
       d.Cn = at(o.Cn); d.cfac = at(o.cfac); d.CRn = at(o.CRn); d.crfac = at(o.crfac);
       d.partU = at(o.pU); d.partW = at(o.pW); d.partRes = at(o.pR);
-      d.rm = at(o.rm); d.rmr = at(o.rmr);
+      d.rsum = at(o.rm); d.rrsum = at(o.rmr);
     }
     d.clip_part = reinterpret_cast<double*>(scr + o.clipp);
     d.clip = at(o.clip);
@@ -262,7 +261,6 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     if (t.factored) {
       const BandShapeSel sel = band_variant(t, d.C, B);
       add_item(plan.band[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB}], i, d.P * d.nbands);
-      add_item(plan.rowmean, i, d.P);
       add_item(plan.factor, i, d.nbr + d.nbc);
       if (fastB) {
         if (d.p3_nbands > 0) add_item(plan.updb[tk], i, d.P * d.p3_nbands * d.p3_nseg);
@@ -291,7 +289,6 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
   for (auto& kv : plan.vecA) place(kv.second);
   for (auto& kv : plan.generic) place(kv.second);
   for (auto& kv : plan.refnorm) place(kv.second);
-  place(plan.rowmean);
   place(plan.factor);
   plan.plan_bytes = align_up(off);
   plan.total_bytes = plan.plan_bytes + scr;
@@ -308,7 +305,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
         rebase(d.Rn); rebase(d.rfac); rebase(d.RRn); rebase(d.rrfac);
         rebase(d.Cn); rebase(d.cfac); rebase(d.CRn); rebase(d.crfac);
         rebase(d.partU); rebase(d.partW); rebase(d.partRes);
-        rebase(d.rm); rebase(d.rmr);
+        rebase(d.rsum); rebase(d.rrsum);
       }
       rebase(d.clip_part);
       rebase(d.clip);
@@ -326,7 +323,6 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     for (auto& kv : plan.vecA) put(kv.second);
     for (auto& kv : plan.generic) put(kv.second);
     for (auto& kv : plan.refnorm) put(kv.second);
-    put(plan.rowmean);
     put(plan.factor);
   }
   return CAME8_OK;
@@ -626,13 +622,8 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
     if ((rc = check_launch("vec_passA")) != CAME8_OK) return rc; }
   }
-  const bool any_fact = !plan.rowmean.tids.empty();
+  const bool any_fact = !plan.factor.tids.empty();
   if (any_fact) {
-    const WorkList& rm = plan.rowmean;
-    { PhaseTimer pt(PH_ROWMEAN, alg_bytes(plan, rm, tensors, PH_ROWMEAN), stream);
-    hipLaunchKernelGGL(k_row_mean<false>, dim3(grid_for(rm.total(), 4)), blk, 0, stream, dT, tids(rm), wst(rm),
-                       int(rm.tids.size()));
-    if ((rc = check_launch("row_mean")) != CAME8_OK) return rc; }
     const WorkList& fb = plan.factor;
     { PhaseTimer pt(PH_FACTOR, alg_bytes(plan, fb, tensors, PH_FACTOR), stream);
     hipLaunchKernelGGL(k_factor_blocks<false>, dim3(grid_for(fb.total())), blk, 0, stream, dT, tids(fb), wst(fb),
@@ -666,11 +657,6 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("pass2")) != CAME8_OK) return rc; }
     }
-    const WorkList& rm = plan.rowmean;
-    { PhaseTimer pt(PH_ROWMEAN_RES, alg_bytes(plan, rm, tensors, PH_ROWMEAN_RES), stream);
-    hipLaunchKernelGGL(k_row_mean<true>, dim3(grid_for(rm.total(), 4)), blk, 0, stream, dT, tids(rm), wst(rm),
-                       int(rm.tids.size()));
-    if ((rc = check_launch("row_mean_res")) != CAME8_OK) return rc; }
     const WorkList& fb = plan.factor;
     { PhaseTimer pt(PH_FACTOR_RES, alg_bytes(plan, fb, tensors, PH_FACTOR_RES), stream);
     hipLaunchKernelGGL(k_factor_blocks<true>, dim3(grid_for(fb.total())), blk, 0, stream, dT, tids(fb), wst(fb),

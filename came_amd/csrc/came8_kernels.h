@@ -59,8 +59,8 @@ struct DevTensor {
   float* partU;   // column partials of g^2+eps0     [P*nbands*C]
   float* partW;   // column partials of g^2/R_i      [P*nbands*C]
   float* partRes; // column partials of residual     [P*nbands*C]
-  float* rm;      // mean row state per matrix       [P]
-  float* rmr;     // mean residual row state         [P]
+  float* rsum;    // row states summed per band      [P*nbands]  (mean row state: their sum / R)
+  float* rrsum;   // residual row states per band    [P*nbands]
   double* clip_part;  // clip numerator partials     [nclip]
   float* clip;        // clip divisor and rcp_for_div of it [2]
   int64_t nclip;
@@ -260,6 +260,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
     const int64_t nseg = (C + segw - 1) / segw;
     CAME8_GLOBAL float* __restrict__ pU = gbl(t.partU + (b * t.nbands + it.band) * C);
     CAME8_GLOBAL float* __restrict__ pW = gbl(t.partW + (b * t.nbands + it.band) * C);
+    float bandR = 0.0f;  // sum of this band's new row states, in row order (every thread alike)
 
     if (nseg == 1) {
       Acc colU[K][V], colW[K][V];
@@ -308,6 +309,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
             const float Rold = deq_u8(rq[row], ra[blk_of(row, hp)]);
             const float Rnew = fmaf(tot[s] / fC, hp.a2, Rold * hp.b2);
             if (tid == 0) Rn[row] = Rnew;
+            bandR += Rnew;
             const float invR = 1.0f / Rnew;
 #pragma unroll
             for (int k = 0; k < K; ++k) {
@@ -374,6 +376,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
             const int64_t row = b * R + r + s;
             const float Rold = deq_u8(rq[row], ra[blk_of(row, hp)]);
             const float Rnew = fmaf(tot[s] / fC, hp.a2, Rold * hp.b2);
+            bandR += Rnew;
             if (tid == 0) {
               Rn[row] = Rnew;
               rowR[r + s - r0] = Rnew;
@@ -420,6 +423,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
       }
       __syncthreads();  // rowR is reused by the next work item
     }
+    if (tid == 0) t.rsum[b * t.nbands + it.band] = bandR;
   }
 }
 
@@ -435,6 +439,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
   constexpr int64_t segw = int64_t(TPB) * V * K;
   __shared__ float red[2][16][NW];
   __shared__ float rowpart[2][kMaxBandRows][NW];  // per-wave row sums of a band (fast path)
+  __shared__ float rowval[kMaxBandRows];           // the band's new residual row states
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   int par = 0, bpar = 0;
   const int64_t total = wstart[ntens];
@@ -491,7 +496,9 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
     };
     auto row_state = [&](int64_t row, float tot) {
       const float RRold = deq_u8(rq[PR + row], ra[t.nbr + blk_of(row, hp)]);
-      RRn[row] = fmaf(tot / fC, hp.a3, RRold * hp.b3);
+      const float RRnew = fmaf(tot / fC, hp.a3, RRold * hp.b3);
+      RRn[row] = RRnew;
+      return RRnew;
     };
 
     bool general = nseg > 1 || !clip_fast;
@@ -591,17 +598,25 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
       }
       general = __syncthreads_or(bad);  // rare: the general path rewrites this band's outputs
       if (!general) {
-        // row totals over the waves in a fixed order
+        // row totals over the waves in a fixed order; the new residual row states go through
+        // LDS so that one thread can add them up in row order
         for (int rr = tid; rr < r1 - r0; rr += TPB) {
           float tot = rowpart[bpar][rr][0];
 #pragma unroll
           for (int w2 = 1; w2 < NW; ++w2) tot += rowpart[bpar][rr][w2];
-          row_state(b * R + r0 + rr, tot);
+          rowval[rr] = row_state(b * R + r0 + rr, tot);
+        }
+        __syncthreads();
+        if (tid == 0) {
+          float sum = 0.0f;
+          for (int64_t rr = 0; rr < r1 - r0; ++rr) sum += rowval[rr];
+          t.rrsum[b * t.nbands + it.band] = sum;
         }
       }
       bpar ^= 1;  // the next band writes the other half (after this band's barrier above)
     }
     if (general) {
+      float bandRR = 0.0f;  // sum of the band's new residual row states (thread 0, row order)
       // general path (wide rows, or exact divisions needed): column partials, segment by segment
       for (int64_t seg = 0; seg < nseg; ++seg) {
         Acc colR[K][V];
@@ -670,29 +685,10 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
         par ^= 1;
 #pragma unroll
         for (int s = 0; s < S; ++s)
-          if (r + s < r1 && tid == 0) row_state(b * R + r + s, tot[s]);
+          if (r + s < r1 && tid == 0) bandRR += row_state(b * R + r + s, tot[s]);
       }
+      if (tid == 0) t.rrsum[b * t.nbands + it.band] = bandRR;
     }
-  }
-}
-
-// ===========================================================================
-// F1a / F2a: mean of the new row state per matrix (one wavefront per matrix)
-// ===========================================================================
-template <bool RES>
-__global__ __launch_bounds__(kThreads) void k_row_mean(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
-                                                       const int64_t* __restrict__ wstart, int ntens) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int64_t total = wstart[ntens];
-  for (int64_t w = int64_t(blockIdx.x) * 4 + wid; w < total; w += int64_t(gridDim.x) * 4) {
-    const int slot = find_slot(wstart, ntens, w);
-    const DevTensor& t = T[tids[slot]];
-    const int64_t b = w - wstart[slot];
-    const float* __restrict__ src = (RES ? t.RRn : t.Rn) + b * t.R;
-    float s = 0.0f;
-    for (int64_t i = lane; i < t.R; i += kWave) s += src[i];
-    s = wave_sum(s);
-    if (lane == 0) (RES ? t.rmr : t.rm)[b] = clamp_min_tiny(s / float(t.R));
   }
 }
 
@@ -701,6 +697,29 @@ __global__ __launch_bounds__(kThreads) void k_row_mean(const DevTensor* __restri
 // ===========================================================================
 // Work item = one quantisation block of the row state (first nbr items of a
 // tensor) or of the column state (next nbc items).
+
+// Mean row state of matrix b, max(mean, 1e-30): the per-band sums the band pass wrote, added in band
+// order (the reference: R.mean(dim=-1, keepdim=True).clamp_min(1e-30), CAME8bitFull.py:1021,1044).
+__device__ __forceinline__ float matrix_row_mean(const DevTensor& t, const float* __restrict__ bandsum, int64_t b) {
+  const float* __restrict__ src = bandsum + b * t.nbands;
+  float s = 0.0f;
+  for (int64_t k = 0; k < t.nbands; ++k) s += src[k];
+  return clamp_min_tiny(s / float(t.R));
+}
+
+// sum over the nbands band partials of one column (stride C), four interleaved accumulators
+__device__ __forceinline__ double band_column_sum(const float* __restrict__ pp, int64_t nbands, int64_t C) {
+  double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+  int64_t k = 0;
+  for (; k + 4 <= nbands; k += 4) {
+    a0 += double(pp[k * C]);
+    a1 += double(pp[(k + 1) * C]);
+    a2 += double(pp[(k + 2) * C]);
+    a3 += double(pp[(k + 3) * C]);
+  }
+  for (; k < nbands; ++k) a0 += double(pp[k * C]);
+  return (a0 + a1) + (a2 + a3);
+}
 template <bool RES>
 __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                             const int64_t* __restrict__ wstart, int ntens, Hp hp) {
@@ -725,10 +744,17 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
     if (is_row) {
       const float* __restrict__ Rsrc = RES ? t.RRn : t.Rn;
       float* __restrict__ fac = RES ? t.rrfac : t.rfac;
-      const float* __restrict__ mean = RES ? t.rmr : t.rm;
+      const float* __restrict__ bsum = RES ? t.rrsum : t.rsum;
+      int64_t mb = i0 / t.R;  // matrix of the block's first row; blocks may span matrices
+      float mean = matrix_row_mean(t, bsum, mb);
       for (int64_t i = i0 + tid; i < i1; i += kThreads) {
+        const int64_t bi = i / t.R;
+        if (bi != mb) {
+          mb = bi;
+          mean = matrix_row_mean(t, bsum, mb);
+        }
         const float v = Rsrc[i];
-        fac[i] = rsqrt_ref(v / mean[i / t.R]);
+        fac[i] = rsqrt_ref(v / mean);
         vmax = nan_max(vmax, v);
       }
     } else {
@@ -738,12 +764,13 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
       float* __restrict__ Cdst = RES ? t.CRn : t.Cn;
       float* __restrict__ fac = RES ? t.crfac : t.cfac;
       const float fR = float(t.R);
+      int64_t cmb = -1;  // matrix whose mean row state crm holds
+      float crm = 0.0f;
       for (int64_t i = i0 + tid; i < i1; i += kThreads) {
         const int64_t b = i / t.C;
         const int64_t j = i - b * t.C;
         const float* __restrict__ pp = part + (b * t.nbands) * t.C + j;
-        double s = 0.0;
-        for (int64_t band = 0; band < t.nbands; ++band) s += double(pp[band * t.C]);
+        const double s = band_column_sum(pp, t.nbands, t.C);
         const float Cold = deq_u8(t.cq[off + i], t.ca[aoff + blk_of(i, hp)]);
         const float Cv = clamp_min_tiny(fmaf(float(s) / fR, alpha, Cold * beta));
         const float c = rsqrt_ref(Cv);
@@ -752,9 +779,12 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
         vmax = nan_max(vmax, Cv);
         if (!RES) {
           const float* __restrict__ pw = t.partW + (b * t.nbands) * t.C + j;
-          double W = 0.0;
-          for (int64_t band = 0; band < t.nbands; ++band) W += double(pw[band * t.C]);
-          csum += double(t.rm[b]) * double(c) * double(c) * W;
+          const double W = band_column_sum(pw, t.nbands, t.C);
+          if (b != cmb) {
+            cmb = b;
+            crm = matrix_row_mean(t, t.rsum, b);
+          }
+          csum += double(crm) * double(c) * double(c) * W;
         }
       }
     }
