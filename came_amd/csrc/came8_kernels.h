@@ -236,7 +236,7 @@ __device__ __forceinline__ BandItem band_item(const DevTensor* __restrict__ T, c
 
 // ---------------- P1 ----------------
 template <typename TG, int V, int K, int TPB>
-__global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+__global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(TPB == 256 ? 5 : 3))) void k_fact_pass1(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                     const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using GS = typename TG::storage;
   using Acc = ColAcc<V, K>;
