@@ -75,6 +75,9 @@ CONFIGS = {
            dict(lr=2e-4, weight_decay=1e-2)),
     "c1": ("2048x2048+2048/CAME8bit/fp32", lambda: [(2048, 2048), (2048,)], torch.float32, torch.float32, 1e-3,
            "CAME8bit", dict(lr=2e-4, weight_decay=1e-2)),
+    # the same Llama-7B set stepped by CAMECUDA (fp32 optimizer states)
+    "c4fp": ("llama7b-shape/CAMECUDA/bf16", lambda: llama_shapes(32, 4096, 11008, 32000), torch.bfloat16,
+             torch.bfloat16, 2e-4, "CAMECUDA", dict(lr=2e-4, weight_decay=1e-2, betas=(0.9, 0.999, 0.9999))),
 }
 
 
@@ -82,11 +85,18 @@ def esize(dt):
     return torch.tensor([], dtype=dt).element_size()
 
 
-def compulsory_bytes(shapes, pdt, gdt, block=256):
+def compulsory_bytes(shapes, pdt, gdt, block=256, fp32_state=False):
     sg, sp = esize(gdt), esize(pdt)
     tot = 0
     for s in shapes:
         n = math.prod(s)
+        if fp32_state:  # fp32 momentum (and 1-D second moment) read and written; fp32 row/col states
+            if len(s) >= 2:
+                pr, pc = math.prod(s[:-1]), math.prod(s[:-2]) * s[-1]
+                tot += n * (sg + 2 * sp + 8) + 16 * (pr + pc)
+            else:
+                tot += n * (sg + 2 * sp + 16)
+            continue
         if len(s) >= 2:
             pr, pc = math.prod(s[:-1]), math.prod(s[:-2]) * s[-1]
             tot += n * (sg + 2 * sp + 2) + 8 * math.ceil(n / block) + 4 * (pr + pc) \
@@ -97,7 +107,7 @@ def compulsory_bytes(shapes, pdt, gdt, block=256):
 
 
 # --------------------------------------------------------------------------------- CPU baseline
-def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp):
+def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False):
     """Time the CPU oracle on a bounded sample of the workload; returns the cpu_baseline object."""
     from oracle import came8_oracle as orc
 
@@ -112,15 +122,21 @@ def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp):
     b1, b2, b3 = hp.get("betas", (0.9, 0.999, 0.9999))
     ohp = dict(beta1=b1, beta2=b2, beta3=b3, eps0=1e-30, eps1=1e-16, lr=hp["lr"], clip_threshold=1.0,
                weight_decay=hp.get("weight_decay", 0.0), block_size=256)
-    states = [orc.init_full8bit_state(s) for s in sample]
+    if fp32_state:
+        states = [orc.init_fp32_state(s) for s in sample]
+        ohp.pop("block_size")
+        step_fn = orc.fp32_state_step
+    else:
+        states = [orc.init_full8bit_state(s) for s in sample]
+        step_fn = orc.full8bit_step
     times = []
     for it in range(3):
         t0 = time.perf_counter()
         for p, g, st in zip(params, grads, states):
-            orc.full8bit_step(p, g, st, **ohp)
+            step_fn(p, g, st, **ohp)
         times.append(time.perf_counter() - t0)
     t = sorted(times[1:])[0]  # first step allocates; best of the next two
-    nbytes = compulsory_bytes(sample, pdt, gdt)
+    nbytes = compulsory_bytes(sample, pdt, gdt, fp32_state=fp32_state)
     n_sample = sum(math.prod(s) for s in sample)
     n_total = sum(math.prod(s) for s in shapes)
     return {
@@ -211,7 +227,8 @@ def main():
     _lib.profile_enable(False)
 
     ms = (t1 - t0) * 1e3 / args.steps
-    nbytes = compulsory_bytes(shapes, pdt, gdt)
+    fp32_state = cls_name == "CAMECUDA"
+    nbytes = compulsory_bytes(shapes, pdt, gdt, fp32_state=fp32_state)
     value = nbytes / (ms / 1e3) / 1e9
     dom = max(phases.items(), key=lambda kv: kv[1][1])
     dname, (dl, dms, dbytes) = dom
@@ -238,7 +255,8 @@ def main():
             "params": sum(math.prod(s) for s in shapes),
             "param_dtype": str(pdt).replace("torch.", ""),
             "grad_dtype": str(gdt).replace("torch.", ""),
-            "state": "int8 momentum + uint8 row/col factors, block 256",
+            "state": "fp32 momentum + fp32 row/col factors" if fp32_state
+            else "int8 momentum + uint8 row/col factors, block 256",
             "compulsory_bytes_per_step": nbytes,
             "step_roofline_frac": round(value / HBM_PEAK_GBS, 4),
         },
@@ -259,7 +277,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle on a sample", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(args.config, shapes, pdt, gdt, gstd, hp)
+        out["cpu_baseline"] = cpu_baseline(args.config, shapes, pdt, gdt, gstd, hp, fp32_state=fp32_state)
     print(json.dumps(out), flush=True)
 
 

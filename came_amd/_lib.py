@@ -15,7 +15,10 @@ LIB_PATH = os.path.join(HERE, "lib", "libcame8.so")
 
 CAME8_F32, CAME8_BF16, CAME8_F16 = 0, 1, 2
 CAME8_OK, CAME8_EINVAL, CAME8_ESPACE, CAME8_EHIP = 0, -1, -2, -3
+ABI_VERSION = 2  # include/came8.h: CAME8_ABI_VERSION
 CAME8_FLAG_REFERENCE_NORM = 1
+CAME8_STATE_Q8 = 0
+CAME8_STATE_FP32 = 1
 
 # every symbol include/came8.h declares
 EXPORTED_SYMBOLS = (
@@ -50,7 +53,7 @@ class Came8Tensor(ctypes.Structure):
         ("param_dtype", ctypes.c_int32),
         ("grad_dtype", ctypes.c_int32),
         ("factored", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("state_kind", ctypes.c_int32),
     ]
 
 
@@ -135,8 +138,8 @@ def load(path: str | None = None) -> ctypes.CDLL:
         lib.came8_quantize_blockwise.argtypes = [vp, i64, i32, i32, vp, vp, vp]
         lib.came8_dequantize_blockwise.restype = ctypes.c_int
         lib.came8_dequantize_blockwise.argtypes = [vp, vp, i64, i32, i32, vp, vp]
-        if lib.came8_abi_version() != 1:
-            raise RuntimeError(f"came_amd: {p} has ABI {lib.came8_abi_version()}, expected 1")
+        if lib.came8_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"came_amd: {p} has ABI {lib.came8_abi_version()}, expected {ABI_VERSION}")
         _lib = lib
         return lib
 

@@ -67,8 +67,8 @@ struct BandKey {
   }
 };
 struct TypeKey {
-  int pdt, gdt;
-  bool operator<(const TypeKey& o) const { return std::tie(pdt, gdt) < std::tie(o.pdt, o.gdt); }
+  int pdt, gdt, st = 0;  // st: fp32 states
+  bool operator<(const TypeKey& o) const { return std::tie(pdt, gdt, st) < std::tie(o.pdt, o.gdt, o.st); }
 };
 
 struct WorkList {
@@ -163,8 +163,14 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
   for (int i = 0; i < n; ++i) {
     const came8_tensor& t = ts[i];
     const std::string who = "came8: tensor " + std::to_string(i) + ": ";
-    if (!t.param || !t.grad || !t.exp_avg_q || !t.exp_avg_absmax || !t.row_q || !t.row_absmax)
+    if (t.state_kind != CAME8_STATE_Q8 && t.state_kind != CAME8_STATE_FP32)
+      return fail(CAME8_EINVAL, who + "unknown state_kind " + std::to_string(t.state_kind));
+    const bool f32st = t.state_kind == CAME8_STATE_FP32;
+    if (!t.param || !t.grad || !t.exp_avg_q || !t.row_q || (!f32st && !t.exp_avg_absmax) ||
+        ((!f32st || t.factored) && !t.row_absmax))
       return fail(CAME8_EINVAL, who + "null pointer");
+    if (f32st && !fast_block(B))
+      return fail(CAME8_EINVAL, who + "fp32 states need a power-of-two block size in [8, 2048]");
     for (int dt : {t.param_dtype, t.grad_dtype})
       if (dt != CAME8_F32 && dt != CAME8_BF16 && dt != CAME8_F16) return fail(CAME8_EINVAL, who + "unsupported dtype");
     if (t.prefix < 1 || t.rows < 1 || t.cols < 1) return fail(CAME8_EINVAL, who + "empty or negative shape");
@@ -187,6 +193,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     d.N = t.prefix * t.rows * t.cols;
     d.nbm = std::max<int64_t>(1, ceil_div(d.N, B));
     d.factored = t.factored ? 1 : 0;
+    d.fp32st = f32st ? 1 : 0;
     const uintptr_t pp = reinterpret_cast<uintptr_t>(t.param), gp = reinterpret_cast<uintptr_t>(t.grad),
                     mp = reinterpret_cast<uintptr_t>(t.exp_avg_q);
     d.vec_ok = (pp % 16 == 0 && gp % 16 == 0 && mp % 8 == 0) ? 1 : 0;
@@ -257,7 +264,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
   for (int i = 0; i < n; ++i) {
     const came8_tensor& t = ts[i];
     const DevTensor& d = plan.dev[i];
-    const TypeKey tk{t.param_dtype, t.grad_dtype};
+    const TypeKey tk{t.param_dtype, t.grad_dtype, d.fp32st};
     if (t.factored) {
       const BandShapeSel sel = band_variant(t, d.C, B);
       add_item(plan.band[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB}], i, d.P * d.nbands);
@@ -401,6 +408,15 @@ BandFn band_fn(int gdt, bool pass2, int V, int K, int TPB) {
 
 using GenFn = void (*)(const DevTensor*, const int32_t*, const int64_t*, int, Hp);
 
+template <typename TP, typename TG>
+constexpr GenFn k_fact_pass3_q8 = k_fact_pass3<TP, TG, false>;
+template <typename TP, typename TG>
+constexpr GenFn k_fact_pass3_f32st = k_fact_pass3<TP, TG, true>;
+template <typename TP, typename TG>
+constexpr GenFn k_fact_pass3b_q8 = k_fact_pass3b<TP, TG, false>;
+template <typename TP, typename TG>
+constexpr GenFn k_fact_pass3b_f32st = k_fact_pass3b<TP, TG, true>;
+
 #define CAME8_TYPE_SWITCH2(KERNEL, pdt, gdt, out)                                       \
   do {                                                                                  \
     out = nullptr;                                                                      \
@@ -413,6 +429,16 @@ using GenFn = void (*)(const DevTensor*, const int32_t*, const int64_t*, int, Hp
     if (pdt == CAME8_F16 && gdt == CAME8_F32) out = KERNEL<F16, F32>;                   \
     if (pdt == CAME8_F16 && gdt == CAME8_BF16) out = KERNEL<F16, BF16>;                 \
     if (pdt == CAME8_F16 && gdt == CAME8_F16) out = KERNEL<F16, F16>;                   \
+  } while (0)
+
+// KERNEL<TP, TG, fp32 states>
+#define CAME8_TYPE_SWITCH3(KERNEL, pdt, gdt, st, out)            \
+  do {                                                           \
+    if (st) {                                                    \
+      CAME8_TYPE_SWITCH2(KERNEL##_f32st, pdt, gdt, out);         \
+    } else {                                                     \
+      CAME8_TYPE_SWITCH2(KERNEL##_q8, pdt, gdt, out);            \
+    }                                                            \
   } while (0)
 
 #define CAME8_TYPE_SWITCH1(KERNEL, gdt, out)           \
@@ -508,12 +534,14 @@ double alg_bytes(const Plan& plan, const WorkList& wl, const came8_tensor* ts, i
     const DevTensor& d = plan.dev[i];
     const double N = double(d.N), sg = elem_bytes(ts[i].grad_dtype), sp = elem_bytes(ts[i].param_dtype);
     const double nbm = double(d.nbm);
+    const double mb = d.fp32st ? 4.0 : 1.0;  // momentum bytes per element
+    const double vb = d.fp32st ? 4.0 : 1.0;  // 1-D second-moment bytes per element
     switch (phase) {
       case PH_PASS1: tot += N * sg + double(d.P * d.R) + 4.0 * double(d.nbr); break;              // g, old row codes
-      case PH_PASS2: tot += N * (sg + 1.0) + 4.0 * nbm; break;                                     // g, m codes
-      case PH_PASS3: tot += N * (sg + 2.0 * sp + 2.0) + 8.0 * nbm; break;                          // g, p rw, m rw
-      case PH_VECA: tot += N * (sg + 1.0) + 4.0 * nbm; break;                                      // g, v codes
-      case PH_VECB: tot += N * (sg + 2.0 * sp + 4.0) + 16.0 * nbm; break;                          // g, p, m, v
+      case PH_PASS2: tot += N * (sg + mb) + (d.fp32st ? 0.0 : 4.0 * nbm); break;                  // g, m
+      case PH_PASS3: tot += N * (sg + 2.0 * sp + 2.0 * mb) + (d.fp32st ? 0.0 : 8.0 * nbm); break;  // g, p rw, m rw
+      case PH_VECA: tot += N * (sg + vb) + (d.fp32st ? 0.0 : 4.0 * nbm); break;                   // g, v
+      case PH_VECB: tot += N * (sg + 2.0 * sp + 2.0 * (mb + vb)) + (d.fp32st ? 0.0 : 16.0 * nbm); break;
       case PH_GENERIC:
         tot += d.factored ? N * (sg + 2.0 * sp + 2.0) + 8.0 * nbm : N * (sg + 2.0 * sp + 4.0) + 16.0 * nbm;
         break;
@@ -668,7 +696,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     for (auto& kv : plan.upd) {
       const WorkList& wl = kv.second;
       GenFn fn;
-      CAME8_TYPE_SWITCH2(k_fact_pass3, kv.first.pdt, kv.first.gdt, fn);
+      CAME8_TYPE_SWITCH3(k_fact_pass3, kv.first.pdt, kv.first.gdt, kv.first.st, fn);
       { PhaseTimer pt(PH_PASS3, alg_bytes(plan, wl, tensors, PH_PASS3), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("pass3")) != CAME8_OK) return rc; }
@@ -676,7 +704,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     for (auto& kv : plan.updb) {
       const WorkList& wl = kv.second;
       GenFn fn;
-      CAME8_TYPE_SWITCH2(k_fact_pass3b, kv.first.pdt, kv.first.gdt, fn);
+      CAME8_TYPE_SWITCH3(k_fact_pass3b, kv.first.pdt, kv.first.gdt, kv.first.st, fn);
       { PhaseTimer pt(PH_PASS3, alg_bytes(plan, wl, tensors, PH_PASS3), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("pass3")) != CAME8_OK) return rc; }

@@ -74,7 +74,14 @@ struct DevTensor {
   int32_t c8;         // C % 8 == 0: 8 consecutive elements never cross a row
   int32_t vec_ok;     // p, g, codes 16-byte aligned (flat passes may use vector access)
   int32_t factored;
+  int32_t fp32st;     // fp32 states (CAMECUDA layout): mq -> float m, rq/ra -> float second-moment /
+                      // residual rows (rq -> float v for 1-D), cq/ca -> float columns; ma unused
 };
+
+// fp32-state views of the state pointers
+__device__ __forceinline__ float* st_m(const DevTensor& t) { return reinterpret_cast<float*>(t.mq); }
+__device__ __forceinline__ float* st_sq_row(const DevTensor& t) { return reinterpret_cast<float*>(t.rq); }
+__device__ __forceinline__ float* st_sq_col(const DevTensor& t) { return reinterpret_cast<float*>(t.cq); }
 
 // Hyper-parameters as the fp32 constants the reference's CPU ops use.
 struct Hp {
@@ -172,6 +179,27 @@ struct CodeChunk {
     }
   }
   __device__ __forceinline__ float operator[](int v) const { return code_elem(w, v); }
+  // dequantised old momentum: code * (absmax / 127), the scale rounded first
+  __device__ __forceinline__ float mold(int v, float scale) const { return code_elem(w, v) * scale; }
+};
+
+// V consecutive fp32 momentum values (fp32-state layout), V-element aligned for V = 4, 8
+template <int V>
+struct M32Chunk {
+  float m[V];
+  __device__ __forceinline__ void load(const CAME8_GLOBAL float* __restrict__ p) {
+    if constexpr (V % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < V / 4; ++i) {
+        const f32x4 r = ((const CAME8_GLOBAL f32x4*)p)[i];
+        m[4 * i] = r.x; m[4 * i + 1] = r.y; m[4 * i + 2] = r.z; m[4 * i + 3] = r.w;
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < V; ++v) m[v] = p[v];
+    }
+  }
+  __device__ __forceinline__ float mold(int v, float) const { return m[v]; }
 };
 
 // V int8 codes as floats (V consecutive, V-byte aligned)
@@ -306,7 +334,7 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(TPB == 256 
         for (int s = 0; s < S; ++s) {
           if (r + s < r1) {
             const int64_t row = b * R + r + s;
-            const float Rold = deq_u8(rq[row], ra[blk_of(row, hp)]);
+            const float Rold = t.fp32st ? st_sq_row(t)[row] : deq_u8(rq[row], ra[blk_of(row, hp)]);
             const float Rnew = fmaf(tot[s] / fC, hp.a2, Rold * hp.b2);
             if (tid == 0) Rn[row] = Rnew;
             bandR += Rnew;
@@ -374,7 +402,7 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(TPB == 256 
         for (int s = 0; s < S; ++s) {
           if (r + s < r1) {
             const int64_t row = b * R + r + s;
-            const float Rold = deq_u8(rq[row], ra[blk_of(row, hp)]);
+            const float Rold = t.fp32st ? st_sq_row(t)[row] : deq_u8(rq[row], ra[blk_of(row, hp)]);
             const float Rnew = fmaf(tot[s] / fC, hp.a2, Rold * hp.b2);
             bandR += Rnew;
             if (tid == 0) {
@@ -464,20 +492,22 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
     const int64_t PR = t.P * R;
 
     // residual of one element (the reference's u, m_new and (u - m_new)^2 + eps1)
-    auto res_of = [&](float ri, float cj, float x, float q, float scale) {
+    auto res_of = [&](float ri, float cj, float x, float mold) {
       const float a = (ri * cj) * x;
       float u = a / clip;
       if (clip_fast && !div_exact_needed(a)) u = div_fast(a, clip, crcp);
-      const float m = fmaf(u, hp.a1, (q * scale) * hp.b1);
+      const float m = fmaf(u, hp.a1, mold * hp.b1);
       const float d = u - m;
       return d * d + hp.eps1;
     };
     // Residuals of a V-chunk (V > 1 chunks lie inside one quantisation block) with the reciprocal
     // divisions only; `bad` records a numerator or an absmax outside their exact range, after which
     // the band is recomputed by the general path below.
-    auto res_chunk = [&](float ri, const float (&cjv)[V], const Chunk<TG, V>& x, const CodeChunk<V>& qc,
-                         float amax, float (&res)[V], bool& bad) {
-      const float scale = div_fast(amax, kSignedQ, kRcpSignedQ);
+    // (fp32 states: the old momentum is read as is and amax is not used)
+    auto res_chunk = [&](float ri, const float (&cjv)[V], const Chunk<TG, V>& x, const auto& qc,
+                         float amax, float (&res)[V], bool& bad) __attribute__((always_inline)) {
+      constexpr bool kF32 = std::is_same<std::decay_t<decltype(qc)>, M32Chunk<V>>::value;
+      const float scale = kF32 ? 0.0f : div_fast(amax, kSignedQ, kRcpSignedQ);
       float a[V];
       DivGuard gd;
 #pragma unroll
@@ -485,17 +515,17 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
         a[v] = (ri * cjv[v]) * x[v];
         gd.add(a[v]);
       }
-      bad |= !gd.fast() || !(fabsf(amax) <= 0x1.fffffep127f);
+      bad |= !gd.fast() || (!kF32 && !(fabsf(amax) <= 0x1.fffffep127f));
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         const float u = div_fast(a[v], clip, crcp);
-        const float m = fmaf(u, hp.a1, (qc[v] * scale) * hp.b1);
+        const float m = fmaf(u, hp.a1, qc.mold(v, scale) * hp.b1);
         const float d = u - m;
         res[v] = d * d + hp.eps1;
       }
     };
     auto row_state = [&](int64_t row, float tot) {
-      const float RRold = deq_u8(rq[PR + row], ra[t.nbr + blk_of(row, hp)]);
+      const float RRold = t.fp32st ? t.ra[row] : deq_u8(rq[PR + row], ra[t.nbr + blk_of(row, hp)]);
       const float RRnew = fmaf(tot / fC, hp.a3, RRold * hp.b3);
       RRn[row] = RRnew;
       return RRnew;
@@ -516,35 +546,40 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
       for (int k = 0; k < K; ++k)
 #pragma unroll
         for (int v = 0; v < V; ++v) colR[k][v] = Acc(0);
-      Chunk<TG, V> gA[S][K], gB[S][K];
-      CodeChunk<V> qA[S][K], qB[S][K];
       int32_t coff[K];  // this thread's column offsets; coff[k] < C when chunk k exists
 #pragma unroll
       for (int k = 0; k < K; ++k) coff[k] = (tid + k * TPB) * V;
-      auto load_stage = [&](Chunk<TG, V> (&gb)[S][K], CodeChunk<V> (&qb)[S][K], int64_t r) {
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          if (r + s < r1) {
-            const CAME8_GLOBAL GS* __restrict__ grow = g + (r + s) * C;
-            const CAME8_GLOBAL int8_t* __restrict__ qrow = mq + (r + s) * C;
-#pragma unroll
-            for (int k = 0; k < K; ++k) {
-              if (coff[k] < C) {
-                gb[s][k].load(grow + coff[k]);
-                qb[s][k].load(qrow + coff[k]);
-              }
-            }
-          }
-        }
-      };
       // When B divides C a row starts a block: the block of chunk k is the row's first block plus
       // the chunk's (per-thread) block offset cbk[k].
       int32_t cbk[K];
 #pragma unroll
       for (int k = 0; k < K; ++k) cbk[k] = t.rowal ? int32_t(blk_of(coff[k], hp)) : 0;
-      auto process = [&](auto AL, const Chunk<TG, V> (&gb)[S][K], const CodeChunk<V> (&qb)[S][K],
+      const CAME8_GLOBAL float* __restrict__ m32 = gbl(static_cast<const float*>(st_m(t)) + ebase);
+      // AL: rows start quantisation blocks; ST: fp32 states
+      auto run = [&](auto AL, auto ST) __attribute__((always_inline)) {
+      constexpr bool kF32 = decltype(ST)::value;
+      using MB = typename std::conditional<kF32, M32Chunk<V>, CodeChunk<V>>::type;
+      Chunk<TG, V> gA[S][K], gB[S][K];
+      MB qA[S][K], qB[S][K];
+      auto load_stage = [&](Chunk<TG, V> (&gb)[S][K], MB (&qb)[S][K], int64_t r) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          if (r + s < r1) {
+            const CAME8_GLOBAL GS* __restrict__ grow = g + (r + s) * C;
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+              if (coff[k] < C) {
+                gb[s][k].load(grow + coff[k]);
+                if constexpr (kF32) qb[s][k].load(m32 + (r + s) * C + coff[k]);
+                else qb[s][k].load(mq + (r + s) * C + coff[k]);
+              }
+            }
+          }
+        }
+      };
+      auto process = [&](const Chunk<TG, V> (&gb)[S][K], const MB (&qb)[S][K],
                          int64_t r) __attribute__((always_inline)) {
-        constexpr bool kAligned = decltype(AL)::value;
+        constexpr bool kAligned = decltype(AL)::value && !kF32;
         float ps[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
@@ -556,7 +591,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
 #pragma unroll
             for (int k = 0; k < K; ++k) {
               if (coff[k] < C) {
-                const float amax = kAligned ? marow[cbk[k]] : ma[blk_of(erow + coff[k], hp)];
+                const float amax = kF32 ? 0.0f : (kAligned ? marow[cbk[k]] : ma[blk_of(erow + coff[k], hp)]);
                 float res[V];
                 res_chunk(ri, cj[k], gb[s][k], qb[s][k], amax, res, bad);
 #pragma unroll
@@ -575,19 +610,19 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
           if (lane == 0 && r + s < r1) rowpart[bpar][r + s - r0][wid] = wsum;
         }
       };
-      auto run = [&](auto AL) __attribute__((always_inline)) {
         load_stage(gA, qA, r0);
         for (int64_t r = r0; r < r1; r += 2 * S) {
           if (r + S < r1) load_stage(gB, qB, r + S);
-          process(AL, gA, qA, r);
+          process(gA, qA, r);
           if (r + S < r1) {
             if (r + 2 * S < r1) load_stage(gA, qA, r + 2 * S);
-            process(AL, gB, qB, r + S);
+            process(gB, qB, r + S);
           }
         }
       };
-      if (t.rowal) run(std::true_type{});
-      else run(std::false_type{});
+      if (t.fp32st) run(std::false_type{}, std::true_type{});
+      else if (t.rowal) run(std::true_type{}, std::false_type{});
+      else run(std::false_type{}, std::false_type{});
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
@@ -616,6 +651,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
       bpar ^= 1;  // the next band writes the other half (after this band's barrier above)
     }
     if (general) {
+      const CAME8_GLOBAL float* __restrict__ m32g = gbl(static_cast<const float*>(st_m(t)) + ebase);
       float bandRR = 0.0f;  // sum of the band's new residual row states (thread 0, row order)
       // general path (wide rows, or exact divisions needed): column partials, segment by segment
       for (int64_t seg = 0; seg < nseg; ++seg) {
@@ -637,8 +673,8 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
               q.load(mq + e);
 #pragma unroll
               for (int v = 0; v < V; ++v) {
-                const float scale = scale_s8(ma[blk_of(ebase + e + v, hp)]);
-                colR[k][v] += Acc(res_of(ri, cf[c0 + v], x[v], q[v], scale));
+                const float mold = t.fp32st ? m32g[e + v] : q[v] * scale_s8(ma[blk_of(ebase + e + v, hp)]);
+                colR[k][v] += Acc(res_of(ri, cf[c0 + v], x[v], mold));
               }
             }
           }
@@ -672,8 +708,8 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
                   q.load(mq + e);
 #pragma unroll
                   for (int v = 0; v < V; ++v) {
-                    const float scale = scale_s8(ma[blk_of(ebase + e + v, hp)]);
-                    ps[s] += res_of(ri, cf[c0 + v], x[v], q[v], scale);
+                    const float mold = t.fp32st ? m32g[e + v] : q[v] * scale_s8(ma[blk_of(ebase + e + v, hp)]);
+                    ps[s] += res_of(ri, cf[c0 + v], x[v], mold);
                   }
                 }
               }
@@ -756,6 +792,7 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
         const float v = Rsrc[i];
         fac[i] = rsqrt_ref(v / mean);
         vmax = nan_max(vmax, v);
+        if (t.fp32st) (RES ? t.ra : st_sq_row(t))[i] = v;  // the fp32 row state itself
       }
     } else {
       const int64_t off = RES ? t.P * t.C : 0;
@@ -771,11 +808,13 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
         const int64_t j = i - b * t.C;
         const float* __restrict__ pp = part + (b * t.nbands) * t.C + j;
         const double s = band_column_sum(pp, t.nbands, t.C);
-        const float Cold = deq_u8(t.cq[off + i], t.ca[aoff + blk_of(i, hp)]);
+        float* __restrict__ cst = RES ? t.ca : st_sq_col(t);  // fp32 column state
+        const float Cold = t.fp32st ? cst[i] : deq_u8(t.cq[off + i], t.ca[aoff + blk_of(i, hp)]);
         const float Cv = clamp_min_tiny(fmaf(float(s) / fR, alpha, Cold * beta));
         const float c = rsqrt_ref(Cv);
         Cdst[i] = Cv;
         fac[i] = c;
+        if (t.fp32st) cst[i] = Cv;
         vmax = nan_max(vmax, Cv);
         if (!RES) {
           const float* __restrict__ pw = t.partW + (b * t.nbands) * t.C + j;
@@ -798,15 +837,16 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
     __syncthreads();
     const float amax = fix_absmax(nan_max(nan_max(smax[0], smax[1]), nan_max(smax[2], smax[3])));
     if (tid == 0) {
-      if (is_row) {
-        t.ra[(RES ? t.nbr : 0) + blk] = amax;
-      } else {
-        t.ca[(RES ? t.nbc : 0) + blk] = amax;
-        if (!RES) t.clip_part[blk] = ((ssum[0] + ssum[1]) + ssum[2]) + ssum[3];
+      if (!RES && !is_row) t.clip_part[blk] = ((ssum[0] + ssum[1]) + ssum[2]) + ssum[3];
+      if (!t.fp32st) {
+        if (is_row) t.ra[(RES ? t.nbr : 0) + blk] = amax;
+        else t.ca[(RES ? t.nbc : 0) + blk] = amax;
       }
     }
     const float arcp = rcp_for_div(amax);
-    if (is_row) {
+    if (t.fp32st) {
+      // fp32 states were written above; no codes
+    } else if (is_row) {
       const float* __restrict__ Rsrc = RES ? t.RRn : t.Rn;
       uint8_t* __restrict__ q = t.rq + (RES ? t.P * t.R : 0);
       for (int64_t i = i0 + tid; i < i1; i += kThreads) q[i] = quant_u8_r(Rsrc[i], amax, arcp);
@@ -824,7 +864,7 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
 // ===========================================================================
 template <typename TG>
 __device__ __forceinline__ float vec_v_new(const DevTensor& t, int64_t e, float gv, const Hp& hp) {
-  const float vold = deq_u8(t.rq[e], t.ra[blk_of(e, hp)]);
+  const float vold = t.fp32st ? st_sq_row(t)[e] : deq_u8(t.rq[e], t.ra[blk_of(e, hp)]);
   return clamp_min_tiny(fmaf(gv * gv + hp.eps0, hp.a2, vold * hp.b2));
 }
 
@@ -990,7 +1030,9 @@ __device__ __forceinline__ u32x2 pack_codes(const int32_t (&c)[8]) {
 // m_new and the updated parameters of 8 elements that share a row and a quantisation block
 // (reference CAME8bitFull.py:1032-1036 and 1047-1056): the reciprocal divisions, and the rare
 // operands outside their exact range through selects.
-template <typename TP>
+// With F32ST (fp32 states) q holds the old momentum values and amax_old is not used; otherwise q
+// holds the int8 codes of a block whose absmax is amax_old.
+template <typename TP, bool F32ST>
 __device__ __forceinline__ void p3_math8(const float (&gv)[8], const float (&q)[8], float (&pv)[8], float (&m)[8],
                                          float amax_old, float ri, float rri, const float (&cj)[8],
                                          const float (&crj)[8], float clip, float crcp, bool clip_fast, const Hp& hp) {
@@ -1001,16 +1043,17 @@ __device__ __forceinline__ void p3_math8(const float (&gv)[8], const float (&q)[
     a[v] = (ri * cj[v]) * gv[v];
     gd.add(a[v]);
   }
-  if (__builtin_expect(clip_fast && gd.fast() && fabsf(amax_old) <= 0x1.fffffep127f, 1)) {
-    const float scale = div_fast(amax_old, kSignedQ, kRcpSignedQ);
+  if (__builtin_expect(clip_fast && gd.fast() && (F32ST || fabsf(amax_old) <= 0x1.fffffep127f), 1)) {
+    const float scale = F32ST ? 0.0f : div_fast(amax_old, kSignedQ, kRcpSignedQ);
 #pragma unroll
-    for (int v = 0; v < 8; ++v) m[v] = fmaf(div_fast(a[v], clip, crcp), hp.a1, (q[v] * scale) * hp.b1);
+    for (int v = 0; v < 8; ++v)
+      m[v] = fmaf(div_fast(a[v], clip, crcp), hp.a1, (F32ST ? q[v] : q[v] * scale) * hp.b1);
   } else {
-    const float scale = amax_old / kSignedQ;
+    const float scale = F32ST ? 0.0f : amax_old / kSignedQ;
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
       const float u = (clip_fast && !div_exact_needed(a[v])) ? div_fast(a[v], clip, crcp) : a[v] / clip;
-      m[v] = fmaf(u, hp.a1, (q[v] * scale) * hp.b1);
+      m[v] = fmaf(u, hp.a1, (F32ST ? q[v] : q[v] * scale) * hp.b1);
     }
   }
 #pragma unroll
@@ -1032,7 +1075,7 @@ __device__ __forceinline__ u32x2 p3_quant8(const float (&m)[8], float amax, uint
   return pack_codes(c);
 }
 
-template <typename TP, typename TG>
+template <typename TP, typename TG, bool F32ST>
 __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                          const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using PS = typename TP::storage;
@@ -1075,13 +1118,18 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
       float gv[8], pv[8], q[8], cj[8], crj[8], m[8];
       load8<TG>(g + e0, gv);
       load8<TP>(p + e0, pv);
-      load_codes<8>(mq + e0, q);
-      const float amax_old = ma[blk];
+      if constexpr (F32ST) load8<F32>(gbl(st_m(t)) + e0, q);
+      else load_codes<8>(mq + e0, q);
+      const float amax_old = F32ST ? 0.0f : ma[blk];
       const float ri = rfac[row], rri = rrfac[row];
       load8<F32>(cfac + bb * C + j, cj);
       load8<F32>(crfac + bb * C + j, crj);
-      p3_math8<TP>(gv, q, pv, m, amax_old, ri, rri, cj, crj, clip, crcp, clip_fast, hp);
+      p3_math8<TP, F32ST>(gv, q, pv, m, amax_old, ri, rri, cj, crj, clip, crcp, clip_fast, hp);
       store8<TP>(p + e0, pv);
+      if constexpr (F32ST) {
+        store8<F32>(gbl(st_m(t)) + e0, m);
+        continue;
+      }
 
       uint32_t abits = 0;
 #pragma unroll
@@ -1094,7 +1142,7 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
       // ---- general tile: element by element ----
       float m[8], pv[8];
       if (e0 < N) {
-        const float scale = ma[blk] / kSignedQ;
+        const float scale = F32ST ? 0.0f : ma[blk] / kSignedQ;
         int64_t i = row - bb * R;
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
@@ -1103,7 +1151,8 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
             const float ri = rfac[row], rri = rrfac[row];
             const float cj = cfac[bb * C + j], crj = crfac[bb * C + j];
             const float u = ((ri * cj) * TG::load(g[e0 + v])) / clip;
-            m[v] = fmaf(u, hp.a1, (float(mq[e0 + v]) * scale) * hp.b1);
+            const float mold = F32ST ? st_m(t)[e0 + v] : float(mq[e0 + v]) * scale;
+            m[v] = fmaf(u, hp.a1, mold * hp.b1);
             pv[v] = param_update<TP>(pv[v], (rri * crj) * m[v], hp);
           } else {
             m[v] = 0.0f;
@@ -1121,6 +1170,16 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
       } else {
 #pragma unroll
         for (int v = 0; v < 8; ++v) m[v] = pv[v] = 0.0f;
+      }
+      if constexpr (F32ST) {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          if (e0 + v < N) {
+            st_m(t)[e0 + v] = m[v];
+            p[e0 + v] = TP::store(pv[v]);
+          }
+        }
+        continue;
       }
       uint32_t abits = 0;
 #pragma unroll
@@ -1166,7 +1225,7 @@ struct Raw8 {
   __device__ __forceinline__ float operator[](int v) const { return T::elem(w, v); }
 };
 
-template <typename TP, typename TG>
+template <typename TP, typename TG, bool F32ST>
 __global__ __launch_bounds__(kThreads) void k_fact_pass3b(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                           const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using PS = typename TP::storage;
@@ -1208,18 +1267,23 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3b(const DevTensor* __res
       load8<F32>(gbl(t.cfac) + b * C + col, cj);
       load8<F32>(gbl(t.crfac) + b * C + col, crj);
     }
+    using MB = typename std::conditional<F32ST, M32Chunk<8>, CodeChunk<8>>::type;
     Raw8<TG> gA, gB;
     Raw8<TP> pA, pB;
-    CodeChunk<8> qA, qB;
+    MB qA, qB;
     float aA = 0.0f, aB = 0.0f;
-    auto load_row = [&](int64_t r, Raw8<TG>& gr, Raw8<TP>& pr, CodeChunk<8>& qr, float& am) {
+    auto load_row = [&](int64_t r, Raw8<TG>& gr, Raw8<TP>& pr, MB& qr, float& am) {
       const int64_t e = (b * R + r) * C + col;
       gr.load(g + e);
       pr.load(p + e);
-      qr.load(mq + e);
-      am = ma[(b * R + r) * bpr + cblk];
+      if constexpr (F32ST) {
+        qr.load(gbl(st_m(t)) + e);
+      } else {
+        qr.load(mq + e);
+        am = ma[(b * R + r) * bpr + cblk];
+      }
     };
-    auto do_row = [&](int64_t r, const Raw8<TG>& gr, const Raw8<TP>& pr, const CodeChunk<8>& qr, float am) {
+    auto do_row = [&](int64_t r, const Raw8<TG>& gr, const Raw8<TP>& pr, const MB& qr, float am) {
       const int64_t row = b * R + r;
       const float ri = uniform_f32(rfac[row]), rri = uniform_f32(rrfac[row]);
       float m[8], pv[8];
@@ -1229,13 +1293,20 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3b(const DevTensor* __res
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
           gv[v] = gr[v];
-          q[v] = qr[v];
+          q[v] = qr.mold(v, 1.0f);  // the code itself, or the fp32 momentum
           pv[v] = pr[v];
         }
-        p3_math8<TP>(gv, q, pv, m, am, ri, rri, cj, crj, clip, crcp, clip_fast, hp);
+        p3_math8<TP, F32ST>(gv, q, pv, m, am, ri, rri, cj, crj, clip, crcp, clip_fast, hp);
+        if constexpr (F32ST) {
+          const int64_t e = row * C + col;
+          store8<TP>(p + e, pv);
+          store8<F32>(gbl(st_m(t)) + e, m);
+          return;
+        }
 #pragma unroll
         for (int v = 0; v < 8; ++v) abits = max(abits, abs_bits(m[v]));
       }
+      if constexpr (F32ST) return;
       abits = block_max_bits(abits, L, wmax, par);
       if (active) {
         const int64_t e = row * C + col;
@@ -1287,13 +1358,25 @@ __global__ __launch_bounds__(kThreads) void k_vec_passB(const DevTensor* __restr
         const float gv = TG::load(g[e]);
         vv[v] = vec_v_new<TG>(t, e, gv, hp);
         const float u = (rsqrt_ref(vv[v]) * gv) / clip;
-        const float mold = deq_s8(t.mq[e], t.ma[blk_of(e, hp)]);
+        const float mold = t.fp32st ? st_m(t)[e] : deq_s8(t.mq[e], t.ma[blk_of(e, hp)]);
         m[v] = fmaf(u, hp.a1, mold * hp.b1);
         pv[v] = param_update<TP>(TP::load(p[e]), m[v], hp);
       } else {
         m[v] = 0.0f;
         vv[v] = 0.0f;
       }
+    }
+    if (t.fp32st) {  // fp32 states: store the values (uniform per work item)
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const int64_t e = e0 + v;
+        if (e < N) {
+          st_m(t)[e] = m[v];
+          st_sq_row(t)[e] = vv[v];
+          p[e] = TP::store(pv[v]);
+        }
+      }
+      continue;
     }
     float am = 0.0f, av = 0.0f;
 #pragma unroll

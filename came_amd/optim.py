@@ -64,6 +64,10 @@ def _release_workspace(ptr: int) -> None:
 class _Came8Base(torch.optim.Optimizer):
     """Shared step machinery: state layout, descriptor table, workspace, one library call per group."""
 
+    _MODE = "full8bit"                 # state["_mode"] of this optimizer's layout
+    _STATE_KIND = _lib.CAME8_STATE_Q8  # how the library reads the state pointers
+    _KEEP_DTYPES = _STATE_DTYPES       # state tensors whose dtype a checkpoint load must keep
+
     def _validate_and_defaults(self, lr, eps, clip_threshold, betas, weight_decay, block_size):
         # came_pytorch/CAME8bitFull.py:73-91
         if lr is None or lr <= 0.0:
@@ -141,7 +145,7 @@ class _Came8Base(torch.optim.Optimizer):
             if p is None or p not in self.state:
                 continue
             live = self.state[p]
-            for key, dt in _STATE_DTYPES.items():
+            for key, dt in self._KEEP_DTYPES.items():
                 v = st.get(key)
                 if isinstance(v, torch.Tensor):
                     live[key] = v.detach().to(device=p.device, dtype=dt).clone()
@@ -151,8 +155,11 @@ class _Came8Base(torch.optim.Optimizer):
             for key, v in st.items():
                 if isinstance(v, (str, bool, int, float)):
                     live[key] = v
-            if live.get("factored") and "factored_row_q" in live:
-                self._bind_factored_views(live)
+            self._after_load(live)
+
+    def _after_load(self, state: dict) -> None:
+        if state.get("factored") and "factored_row_q" in state:
+            self._bind_factored_views(state)
 
     # ------------------------------------------------------------------- step
     def _group_hparams(self, group: dict) -> _lib.Came8HParams:
@@ -196,15 +203,31 @@ class _Came8Base(torch.optim.Optimizer):
         if grad.shape != p.shape:
             raise RuntimeError(f"grad shape {tuple(grad.shape)} does not match param shape {tuple(p.shape)}")
         state = self.state[p]
-        if len(state) == 0 or state.get("_mode") != "full8bit":
+        if len(state) == 0 or state.get("_mode") != self._MODE:
             state.clear()
             self._init_state(state, grad, block_size)
         self._check_state(p, state, block_size)
         return state, grad
 
+    def _group_block_size(self, group: dict) -> int:
+        return int(group["block_size"])
+
+    def _fill_desc(self, d, p: torch.Tensor, state: dict) -> None:
+        """State pointers of one tensor in the full8bit layout (include/came8.h: came8_tensor)."""
+        d.exp_avg_q = state["exp_avg_q"].data_ptr()
+        d.exp_avg_absmax = state["exp_avg_absmax"].data_ptr()
+        if state["factored"]:
+            d.row_q = state["factored_row_q"].data_ptr()
+            d.row_absmax = state["factored_row_absmax"].data_ptr()
+            d.col_q = state["factored_col_q"].data_ptr()
+            d.col_absmax = state["factored_col_absmax"].data_ptr()
+        else:
+            d.row_q = state["exp_avg_sq_q"].data_ptr()
+            d.row_absmax = state["exp_avg_sq_absmax"].data_ptr()
+
     @torch.no_grad()
     def _step_group(self, group: dict, params: list) -> None:
-        block_size = int(group["block_size"])
+        block_size = self._group_block_size(group)
         hp = self._group_hparams(group)
         by_device: dict = defaultdict(list)
         for p in params:
@@ -233,24 +256,18 @@ class _Came8Base(torch.optim.Optimizer):
                 d = descs[i]
                 d.param = pd.data_ptr()
                 d.grad = g.data_ptr()
-                d.exp_avg_q = state["exp_avg_q"].data_ptr()
-                d.exp_avg_absmax = state["exp_avg_absmax"].data_ptr()
                 d.param_dtype = _DTYPE_CODE[p.dtype]
                 d.grad_dtype = _DTYPE_CODE[g.dtype]
+                d.state_kind = self._STATE_KIND
                 if state["factored"]:
                     shape = tuple(p.shape)
                     d.prefix = math.prod(shape[:-2])
                     d.rows, d.cols = shape[-2], shape[-1]
                     d.factored = 1
-                    d.row_q = state["factored_row_q"].data_ptr()
-                    d.row_absmax = state["factored_row_absmax"].data_ptr()
-                    d.col_q = state["factored_col_q"].data_ptr()
-                    d.col_absmax = state["factored_col_absmax"].data_ptr()
                 else:
                     d.prefix, d.rows, d.cols = 1, 1, p.numel()
                     d.factored = 0
-                    d.row_q = state["exp_avg_sq_q"].data_ptr()
-                    d.row_absmax = state["exp_avg_sq_absmax"].data_ptr()
+                self._fill_desc(d, p, state)
             ws, tag = self._workspace(device, descs, n, block_size)
             with torch.cuda.device(device):
                 stream = torch.cuda.current_stream(device).cuda_stream
@@ -507,3 +524,119 @@ class CAME8bit(CAME8bitFull):
                 if not (p.data.is_contiguous() and p.grad.is_contiguous()):
                     raise RuntimeError("CUDA graph capture requires contiguous parameter and gradient tensors.")
                 self._prepare_param(p, block_size)
+
+
+# state tensors of the fp32-state layout (all fp32, whatever the parameter dtype)
+_FP32_STATE_KEYS = ("exp_avg", "exp_avg_sq_row", "exp_avg_sq_col", "exp_avg_res_row", "exp_avg_res_col", "exp_avg_sq")
+
+
+class CAMECUDA(_Came8Base):
+    """CAME with fp32 optimizer state (reference came_pytorch/CAMECUDA.py:16).
+
+    Same constructor arguments, ``ValueError`` texts, param-group keys and per-parameter state as
+    the reference (CAMECUDA.py:27-56, 83-104: ``step``, ``_mode`` = "cudafp", ``factored``,
+    ``exp_avg`` and ``exp_avg_sq_row/col`` + ``exp_avg_res_row/col`` for ndim >= 2 or ``exp_avg_sq``
+    for 1-D, all fp32).  The arithmetic is the reference's ``_step_param_generic``
+    (CAMECUDA.py:275-326) -- the 8-bit step's with the states kept in fp32 -- run for every
+    parameter of a group by one ``came8_step`` call with fp32 states.  The reference's per-tensor
+    CUDA scratch buffers (``scratch_fp32`` and the like) are not kept: the library's workspace
+    replaces them, and a state dict without them loads in the reference (it then takes its
+    generic path).
+    """
+
+    _MODE = "cudafp"
+    _STATE_KIND = _lib.CAME8_STATE_FP32
+    _KEEP_DTYPES = {k: torch.float32 for k in _FP32_STATE_KEYS}
+    _WORK_BLOCK = 256  # shapes the library's work decomposition only; fp32 states have no blocks
+
+    def __init__(
+        self,
+        params,
+        lr: float,
+        eps: tuple[float, float] = (1e-30, 1e-16),
+        clip_threshold: float = 1.0,
+        betas: tuple[float, float, float] = (0.9, 0.999, 0.9999),
+        weight_decay: float = 0.0,
+    ):
+        # came_pytorch/CAMECUDA.py:37-56
+        if lr is None or lr <= 0.0:
+            raise ValueError(f"lr must be > 0, got {lr}")
+        if clip_threshold <= 0.0:
+            raise ValueError(f"clip_threshold must be > 0, got {clip_threshold}")
+        if len(eps) != 2:
+            raise ValueError(f"eps must be a tuple of length 2, got eps={eps}")
+        if len(betas) != 3:
+            raise ValueError(f"betas must be a tuple of length 3, got betas={betas}")
+        if not all(0.0 <= beta <= 1.0 for beta in betas):
+            raise ValueError(f"betas must be in [0, 1], got betas={betas}")
+        defaults = dict(
+            lr=float(lr),
+            eps=(float(eps[0]), float(eps[1])),
+            clip_threshold=float(clip_threshold),
+            betas=(float(betas[0]), float(betas[1]), float(betas[2])),
+            weight_decay=float(weight_decay),
+        )
+        super().__init__(params, defaults)
+        self.reference_norm = False
+
+    @property
+    def supports_memory_efficient_fp16(self):
+        return True
+
+    @property
+    def supports_flat_params(self):
+        return False
+
+    def _group_block_size(self, group: dict) -> int:
+        return self._WORK_BLOCK
+
+    def _group_hparams(self, group: dict) -> _lib.Came8HParams:
+        b1, b2, b3 = group["betas"]
+        e0, e1 = group["eps"]
+        flags = _lib.CAME8_FLAG_REFERENCE_NORM if getattr(self, "reference_norm", False) else 0
+        return _lib.Came8HParams(float(group["lr"]), float(b1), float(b2), float(b3), float(e0), float(e1),
+                                 float(group["clip_threshold"]), float(group["weight_decay"]),
+                                 self._WORK_BLOCK, flags)
+
+    def _init_state(self, state: dict, grad: torch.Tensor, block_size: int) -> None:
+        """The reference's fp32 layout (CAMECUDA.py:83-104)."""
+        state["step"] = 0
+        state["_mode"] = "cudafp"
+        state["factored"] = grad.dim() >= 2
+        shape = tuple(grad.shape)
+        state["exp_avg"] = torch.zeros(shape, device=grad.device, dtype=torch.float32)
+        if state["factored"]:
+            row_shape, col_shape = shape[:-1], shape[:-2] + shape[-1:]
+            for k, sh in (("exp_avg_sq_row", row_shape), ("exp_avg_sq_col", col_shape),
+                          ("exp_avg_res_row", row_shape), ("exp_avg_res_col", col_shape)):
+                state[k] = torch.zeros(sh, device=grad.device, dtype=torch.float32)
+        else:
+            state["exp_avg_sq"] = torch.zeros(shape, device=grad.device, dtype=torch.float32)
+
+    def _check_state(self, p: torch.Tensor, state: dict, block_size: int) -> None:
+        if tuple(state["exp_avg"].shape) != tuple(p.shape):
+            raise RuntimeError("Parameter shape changed; the optimizer state no longer matches it.")
+        for k in _FP32_STATE_KEYS:
+            v = state.get(k)
+            if v is None:
+                continue
+            if v.device != p.device:
+                raise RuntimeError("optimizer state lives on a different device than its parameter")
+            if v.dtype != torch.float32 or not v.is_contiguous():
+                state[k] = v.to(dtype=torch.float32).contiguous()
+
+    def _fill_desc(self, d, p: torch.Tensor, state: dict) -> None:
+        """fp32 state pointers (include/came8.h: came8_tensor with CAME8_STATE_FP32)."""
+        d.exp_avg_q = state["exp_avg"].data_ptr()
+        d.exp_avg_absmax = None
+        if state["factored"]:
+            d.row_q = state["exp_avg_sq_row"].data_ptr()
+            d.row_absmax = state["exp_avg_res_row"].data_ptr()
+            d.col_q = state["exp_avg_sq_col"].data_ptr()
+            d.col_absmax = state["exp_avg_res_col"].data_ptr()
+        else:
+            d.row_q = state["exp_avg_sq"].data_ptr()
+            d.row_absmax = None
+
+    def _after_load(self, state: dict) -> None:
+        pass

@@ -17,7 +17,11 @@
  *                           came_full_factored_step_multitensor_same_shape_ptrs came_bindings.cpp:1795-1907
  *                           came_full_nonfactored_step_multitensor_ptrs        came_bindings.cpp:1170-1222
  *                         (Python wrappers: came_pytorch/came_cuda/__init__.py:253-963;
- *                          arithmetic: came_pytorch/CAME8bitFull.py:1006-1075).
+ *                          arithmetic: came_pytorch/CAME8bitFull.py:1006-1075);
+ *                         and, with fp32 states, CAMECUDA's steps:
+ *                           came_fp_factored_step               came_bindings.cpp:1692-1760
+ *                         (Python: came_cuda/__init__.py:820-860; arithmetic:
+ *                          came_pytorch/CAMECUDA.py:275-326).
  *   came8_quantize_blockwise / came8_dequantize_blockwise
  *                        -- blockwise_quant / blockwise_dequant
  *                           came_bindings.cpp:756-801 (Python: came_cuda/__init__.py:205-228;
@@ -37,7 +41,7 @@
 extern "C" {
 #endif
 
-#define CAME8_ABI_VERSION 1
+#define CAME8_ABI_VERSION 2
 
 /* element types of parameters and gradients */
 #define CAME8_F32 0
@@ -49,6 +53,10 @@ extern "C" {
 #define CAME8_EINVAL (-1)   /* bad argument: shape, dtype, block size, null pointer */
 #define CAME8_ESPACE (-2)   /* workspace smaller than came8_workspace_size() */
 #define CAME8_EHIP (-3)     /* a HIP runtime call failed */
+
+/* came8_tensor.state_kind */
+#define CAME8_STATE_Q8 0   /* 8-bit states, full8bit layout (CAME8bit, CAME8bitFull, CAME8bitMemory) */
+#define CAME8_STATE_FP32 1 /* fp32 states, CAMECUDA layout */
 
 /* flags for came8_hparams.flags */
 #define CAME8_FLAG_REFERENCE_NORM 1u /* clip RMS summed in the reference CPU order (slow; parity runs) */
@@ -72,6 +80,19 @@ extern "C" {
  *     col_q, col_absmax unused (NULL)
  *
  * param and grad are contiguous; param is updated in place.
+ *
+ * With state_kind = CAME8_STATE_FP32 the states are the fp32 tensors of the
+ * reference's CAMECUDA (came_pytorch/CAMECUDA.py:83-104), passed through the
+ * same fields (cast to the field types):
+ *   exp_avg_q      -> exp_avg          float [N]
+ *   row_q          -> exp_avg_sq_row   float [P*R]   (1-D: exp_avg_sq float [N])
+ *   row_absmax     -> exp_avg_res_row  float [P*R]   (1-D: unused)
+ *   col_q          -> exp_avg_sq_col   float [P*C]
+ *   col_absmax     -> exp_avg_res_col  float [P*C]
+ *   exp_avg_absmax    unused (may be NULL)
+ * The arithmetic is CAMECUDA._step_param_generic (CAMECUDA.py:275-326): the
+ * 8-bit step's, with the states kept in fp32 and no quantisation.  block_size
+ * then only shapes the work decomposition (a power of two in [8, 2048]).
  */
 typedef struct came8_tensor {
   void* param;
@@ -88,7 +109,7 @@ typedef struct came8_tensor {
   int32_t param_dtype; /* CAME8_F32 / CAME8_BF16 / CAME8_F16 */
   int32_t grad_dtype;
   int32_t factored;    /* 1 for ndim >= 2, 0 for 1-D */
-  int32_t reserved;
+  int32_t state_kind;  /* CAME8_STATE_Q8 (0) or CAME8_STATE_FP32 */
 } came8_tensor;
 
 /* Hyper-parameters of one param group (the reference's group keys, as Python floats). */

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     assert set(declared) == set(L.EXPORTED_SYMBOLS), declared
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.came8_abi_version() == 1
+    assert lib.came8_abi_version() == 2
     assert b"gfx950" in lib.came8_version()
 
 
@@ -175,3 +175,71 @@ def test_load_state_dict_keeps_dtypes_mode_and_copies():
                     assert b[k].data_ptr() != v.data_ptr(), k
         if a["factored"]:
             assert b["exp_avg_res_row_q"].data_ptr() == b["factored_row_q"][1].data_ptr()
+
+
+# ---------------------------------------------------------------------------------- CAMECUDA
+@pytest.mark.parametrize("kw,msg", [
+    (dict(lr=0.0), "lr must be > 0"),
+    (dict(lr=1e-3, clip_threshold=0.0), "clip_threshold must be > 0"),
+    (dict(lr=1e-3, eps=(1e-30,)), "eps must be a tuple of length 2"),
+    (dict(lr=1e-3, betas=(0.9, 0.99)), "betas must be a tuple of length 3"),
+    (dict(lr=1e-3, betas=(0.9, 1.5, 0.99)), r"betas must be in \[0, 1\]"),
+])
+def test_camecuda_constructor_validation(kw, msg):
+    with pytest.raises(ValueError, match=msg):
+        came_amd.CAMECUDA(P0, **kw)
+
+
+def test_camecuda_group_keys_and_properties():
+    opt = came_amd.CAMECUDA(P0, lr=1e-3, weight_decay=0.1)
+    assert set(opt.param_groups[0]) == {"params", "lr", "eps", "clip_threshold", "betas", "weight_decay"}
+    assert opt.supports_memory_efficient_fp16 and not opt.supports_flat_params
+
+
+@pytest.mark.parametrize("shape", [(7,), (5, 9), (2, 3, 5, 7)])
+def test_camecuda_state_layout_matches_reference(shape):
+    opt = came_amd.CAMECUDA([torch.nn.Parameter(torch.zeros(shape))], lr=1e-3)
+    st = {}
+    opt._init_state(st, torch.zeros(shape), 256)
+    ref = orc.init_fp32_state(shape)
+    assert set(st) == set(ref)
+    for k, v in ref.items():
+        if isinstance(v, torch.Tensor):
+            assert st[k].dtype == torch.float32 and tuple(st[k].shape) == tuple(v.shape), k
+        else:
+            assert st[k] == v, k
+
+
+def test_camecuda_load_state_dict_keeps_fp32_states():
+    ps = [torch.nn.Parameter(torch.randn(30, 20).bfloat16()), torch.nn.Parameter(torch.randn(20).bfloat16())]
+    opt = came_amd.CAMECUDA(ps, lr=2e-4)
+    for p in ps:
+        opt._init_state(opt.state[p], p, 256)
+        opt.state[p]["exp_avg"].normal_()
+        opt.state[p]["step"] = 3
+    ps2 = [torch.nn.Parameter(p.data.clone()) for p in ps]
+    opt2 = came_amd.CAMECUDA(ps2, lr=2e-4)
+    opt2.load_state_dict(opt.state_dict())
+    for p, p2 in zip(ps, ps2):
+        a, b = opt.state[p], opt2.state[p2]
+        assert b["_mode"] == "cudafp" and b["step"] == 3
+        for k, v in a.items():
+            if isinstance(v, torch.Tensor):
+                assert b[k].dtype == torch.float32 and torch.equal(b[k], v), k
+
+
+def test_fp32_state_kind_checks():
+    lib = L.load()
+    size = ctypes.c_size_t(0)
+    d = _desc((64, 64))
+    d.state_kind = 7
+    assert lib.came8_workspace_size((L.Came8Tensor * 1)(d), 1, 256, ctypes.byref(size)) == L.CAME8_EINVAL
+    assert b"state_kind" in lib.came8_last_error()
+    d.state_kind = L.CAME8_STATE_FP32
+    d.exp_avg_absmax = None  # not used by fp32 states
+    assert lib.came8_workspace_size((L.Came8Tensor * 1)(d), 1, 256, ctypes.byref(size)) == L.CAME8_OK
+    assert lib.came8_workspace_size((L.Came8Tensor * 1)(d), 1, 100, ctypes.byref(size)) == L.CAME8_EINVAL
+    v = _desc((33,))
+    v.state_kind = L.CAME8_STATE_FP32
+    v.exp_avg_absmax = v.row_absmax = None
+    assert lib.came8_workspace_size((L.Came8Tensor * 1)(v), 1, 256, ctypes.byref(size)) == L.CAME8_OK
