@@ -13,6 +13,8 @@ pure-PyTorch CPU path:
   (CPU branch; ``CAME8bitMemory.py:390-447`` uses the same shapes)
 * one full8bit parameter step     -- reference ``came_pytorch/CAME8bitFull.py:939-1075`` (CPU branch)
 * the fp32-state CAMECUDA step    -- reference ``came_pytorch/CAMECUDA.py:275-326`` (generic branch)
+* the 8bit2d step (16x16-tile momentum) -- reference CUDA kernels, ``came_cuda/csrc/came_kernels.cu``
+  (see ``came8bit2d_step``; parity unpinned against the reference, which cannot run here)
 
 The op sequence is kept identical to the reference because the point of the
 oracle is bit-level agreement with it: each rounding step (``mul_`` then
@@ -27,6 +29,8 @@ from __future__ import annotations
 
 import math
 from typing import Dict
+
+import numpy as np
 
 import torch
 
@@ -257,3 +261,174 @@ def fp32_state_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], 
     if weight_decay != 0.0:
         p.add_(p, alpha=-weight_decay * lr)
     p.add_(step_dir, alpha=-lr)
+
+
+# --------------------------------------------------------------------------
+# 8bit2d step (reference CAME8bit2D / the CUDA 2-D path of CAME8bit)
+# --------------------------------------------------------------------------
+# The reference's 8bit2d step exists only as CUDA kernels (came_cuda/csrc/came_kernels.cu:
+# kUpdateSqRowQuantized :60-96, kUpdateSqColQuantizedFinalize :198-243, kFinalizeQuantizedRFactor
+# :298-333, kSumUpdateSq :595-619, kUpdateExpAvgQuantAndResSumsTiled :2584-2684,
+# kUpdateResRowQuantized :2685-2707, kReduceRow/ColTilePartials :2708-2741,
+# kUpdateResColQuantizedFinalize :2742-2780, kParamUpdateTiled :3333-3367; launch order
+# :3598-4040).  This is a CPU restatement written from that source, with its float32 operation
+# order; PARITY UNPINNED against the reference itself (it cannot run here): its reductions are
+# CUB block sums and float atomics of unfixed order, its rsqrtf is not correctly rounded and its
+# compiler may contract multiply-adds.  Here: sums in a fixed order (sequential where the kernel is
+# sequential), correctly rounded 1/sqrt, no contraction except the final parameter write (a fused
+# multiply-add, as torch's add_(alpha=) and the GPU both do), and the update-RMS sum in fp64.
+TILE_2D = 16
+
+
+def init_8bit2d_state(shape, block_size: int = 256) -> Dict[str, object]:
+    """Reference came8bit2d_state.py:33-75, persistent part (the scratch tensors it also allocates are
+    listed in SCRATCH_8BIT2D_KEYS)."""
+    rows, cols = (int(s) for s in shape)
+    tr, tc = math.ceil(rows / TILE_2D), math.ceil(cols / TILE_2D)
+    st: Dict[str, object] = {"_mode": "8bit2d"}
+    st["exp_avg_q"] = torch.zeros((rows, cols), dtype=torch.int8)
+    st["exp_avg_absmax"] = torch.zeros(tr * tc, dtype=torch.float32)  # 0: "no momentum yet"
+    for k, n in (("exp_avg_sq_row", rows), ("exp_avg_sq_col", cols), ("exp_avg_res_row", rows),
+                 ("exp_avg_res_col", cols)):
+        st[k + "_q"] = torch.zeros(n, dtype=torch.uint8)
+        st[k + "_absmax"] = torch.ones(num_blocks(n, block_size), dtype=torch.float32)
+    st.update(rows=rows, cols=cols, tile_rows=tr, tile_cols=tc, num_tiles=tr * tc)
+    return st
+
+
+SCRATCH_8BIT2D_KEYS = ("r_factor", "c_factor", "r_res_factor", "c_res_factor", "res_row_sum", "res_col_sum",
+                       "res_row_partial", "res_col_partial", "sum_sq_row", "sum_update", "sum_update_partial",
+                       "sum_res_row")
+
+
+def _f32(x) -> np.float32:
+    return np.float32(x)
+
+
+def _quant_inv(x: torch.Tensor, absmax: torch.Tensor, signed: bool) -> torch.Tensor:
+    """came_kernels.cu:833-847: rint((x * (1 / absmax)) * Q), clamped; each product rounded."""
+    inv = (torch.ones_like(absmax) / absmax)
+    qmax = SIGNED_QMAX if signed else UNSIGNED_QMAX
+    q = torch.round((x * inv) * qmax).clamp(-qmax if signed else 0.0, qmax)
+    return q.to(torch.int8 if signed else torch.uint8)
+
+
+def _block_fix(v: torch.Tensor, block_size: int) -> torch.Tensor:
+    """Per flat block of ``v`` (>= 0 values): max over the block, 0 -> 1; one value per element."""
+    n = v.numel()
+    nb = num_blocks(n, block_size)
+    buf = torch.zeros(nb * block_size, dtype=torch.float32)
+    buf[:n] = v
+    a = buf.view(nb, block_size).amax(dim=1)
+    a = torch.where(a > 0, a, torch.ones_like(a))
+    return a
+
+
+def _ema_f32(old: torch.Tensor, mean: torch.Tensor, beta: float) -> torch.Tensor:
+    """(old * beta) + ((1.0f - beta) * mean) in float32, unfused (came_kernels.cu:91, 229, 2701, 2764)."""
+    b = _f32(beta)
+    a = _f32(1.0) - b
+    return (old * float(b)) + (mean * float(a))
+
+
+def _rsqrt(x: torch.Tensor) -> torch.Tensor:
+    return torch.ones_like(x) / torch.sqrt(x)
+
+
+@torch.no_grad()
+def came8bit2d_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *, beta1: float, beta2: float,
+                    beta3: float, eps0: float, eps1: float, lr: float, clip_threshold: float, weight_decay: float,
+                    block_size: int = 256, capture: Dict[str, torch.Tensor] | None = None) -> None:
+    """One 8bit2d step on a 2-D parameter ``p`` (in place) and state ``st`` (in place)."""
+    rows, cols = p.shape
+    bs = block_size
+    g = grad.float()
+    U = (g * g) + float(_f32(eps0))
+    # row second moment (kUpdateSqRowQuantized)
+    old_r = dequantize_blockwise(st["exp_avg_sq_row_q"], st["exp_avg_sq_row_absmax"], signed=False, block_size=bs)
+    row_mean = U.sum(dim=1) / float(cols)
+    upd_r = _ema_f32(old_r, row_mean, beta2)
+    sum_sq_row = upd_r.sum()
+    # column second moment, summed row after row (kUpdateSqColQuantizedFinalize)
+    col_acc = torch.zeros(cols, dtype=torch.float32)
+    for i in range(rows):
+        col_acc = col_acc + U[i]
+    old_c = dequantize_blockwise(st["exp_avg_sq_col_q"], st["exp_avg_sq_col_absmax"], signed=False, block_size=bs)
+    upd_c = _ema_f32(old_c, col_acc / float(rows), beta2)
+    ca = _block_fix(upd_c, bs)
+    st["exp_avg_sq_col_absmax"].copy_(ca)
+    st["exp_avg_sq_col_q"].copy_(_quant_inv(upd_c, ca.repeat_interleave(bs)[:cols], signed=False))
+    c = _rsqrt(upd_c)
+    # row factors (kFinalizeQuantizedRFactor)
+    ra = _block_fix(upd_r, bs)
+    st["exp_avg_sq_row_absmax"].copy_(ra)
+    st["exp_avg_sq_row_q"].copy_(_quant_inv(upd_r, ra.repeat_interleave(bs)[:rows], signed=False))
+    mean = sum_sq_row / float(rows)
+    mean = mean if float(mean) > 0 else torch.tensor(1.0)
+    r = _rsqrt(upd_r / mean)
+    # update RMS (kSumUpdateSq; the sum in fp64 here) and clip
+    u0 = (g * r[:, None]) * c[None, :]
+    sum_update = _f32(float((u0.double() ** 2).sum()))
+    rms = np.sqrt(_f32(sum_update / _f32(rows * cols)), dtype=np.float32)
+    clip = max(_f32(1.0), _f32(rms / _f32(clip_threshold)))
+    upd = u0 / float(clip)
+    # momentum in 16x16 tiles (kUpdateExpAvgQuantAndResSumsTiled)
+    tr, tc = st["tile_rows"], st["tile_cols"]
+    tile = (torch.arange(rows)[:, None] // TILE_2D) * tc + (torch.arange(cols)[None, :] // TILE_2D)
+    old_am = st["exp_avg_absmax"][tile]
+    m_old = torch.where(old_am > 0, st["exp_avg_q"].float() * (old_am / SIGNED_QMAX), torch.zeros(()))
+    b1 = _f32(beta1)
+    m_new = (m_old * float(b1)) + (upd * float(_f32(1.0) - b1))
+    diff = upd - m_new
+    res = (diff * diff) + float(_f32(eps1))
+    am = torch.zeros(tr * tc, dtype=torch.float32).scatter_reduce(0, tile.reshape(-1), m_new.abs().reshape(-1),
+                                                                   reduce="amax", include_self=True)
+    am = torch.where(am > 0, am, torch.ones_like(am))
+    st["exp_avg_absmax"].copy_(am)
+    q_new = _quant_inv(m_new, am[tile], signed=True)
+    st["exp_avg_q"].copy_(q_new)
+    # residual sums: 16 elements of a tile in order, then tiles in order (kReduceRow/ColTilePartials)
+    pad_r, pad_c = tr * TILE_2D, tc * TILE_2D
+    rp = torch.zeros(pad_r, pad_c)
+    rp[:rows, :cols] = res
+    row_part = torch.zeros(pad_r, tc)
+    col_part = torch.zeros(tr, pad_c)
+    for j in range(TILE_2D):
+        row_part = row_part + rp.view(pad_r, tc, TILE_2D)[:, :, j]
+        col_part = col_part + rp.view(tr, TILE_2D, pad_c)[:, j, :]
+    res_row_sum = torch.zeros(pad_r)
+    for tx in range(tc):
+        res_row_sum = res_row_sum + row_part[:, tx]
+    res_col_sum = torch.zeros(pad_c)
+    for ty in range(tr):
+        res_col_sum = res_col_sum + col_part[ty]
+    res_row_sum, res_col_sum = res_row_sum[:rows], res_col_sum[:cols]
+    # multiplicative weight decay, rounded to the parameter type
+    if weight_decay != 0.0:
+        fac = _f32(1.0) - _f32(lr) * _f32(weight_decay)
+        p.copy_((p.float() * float(fac)).to(p.dtype))
+    # residual factors (kUpdateResRowQuantized, kUpdateResColQuantizedFinalize, kFinalizeQuantizedRFactor)
+    old_rr = dequantize_blockwise(st["exp_avg_res_row_q"], st["exp_avg_res_row_absmax"], signed=False, block_size=bs)
+    upd_rr = _ema_f32(old_rr, res_row_sum / float(cols), beta3)
+    sum_res_row = upd_rr.sum()
+    old_rc = dequantize_blockwise(st["exp_avg_res_col_q"], st["exp_avg_res_col_absmax"], signed=False, block_size=bs)
+    upd_rc = _ema_f32(old_rc, res_col_sum / float(rows), beta3)
+    cra = _block_fix(upd_rc, bs)
+    st["exp_avg_res_col_absmax"].copy_(cra)
+    st["exp_avg_res_col_q"].copy_(_quant_inv(upd_rc, cra.repeat_interleave(bs)[:cols], signed=False))
+    cr = _rsqrt(upd_rc)
+    rra = _block_fix(upd_rr, bs)
+    st["exp_avg_res_row_absmax"].copy_(rra)
+    st["exp_avg_res_row_q"].copy_(_quant_inv(upd_rr, rra.repeat_interleave(bs)[:rows], signed=False))
+    rmean = sum_res_row / float(rows)
+    rmean = rmean if float(rmean) > 0 else torch.tensor(1.0)
+    rr = _rsqrt(upd_rr / rmean)
+    # parameter write from the requantised momentum (kParamUpdateTiled): p - lr * ((m * rr) * cr), fused
+    m_q = q_new.float() * (am[tile] / SIGNED_QMAX)
+    update2 = (m_q * rr[:, None]) * cr[None, :]
+    pf = p.float()
+    pf.add_(update2, alpha=-lr)
+    p.copy_(pf.to(p.dtype))
+    if capture is not None:
+        capture.update(clip=torch.tensor(float(clip)), exp_avg=m_new.clone(), sq_row=upd_r.clone(),
+                       sq_col=upd_c.clone(), res_row=upd_rr.clone(), res_col=upd_rc.clone(), update=upd.clone())
