@@ -5,7 +5,7 @@ constructor arguments, ``step()`` semantics and state layout; the step itself
 runs in ``libcame8.so`` (hand-written HIP kernels behind the C ABI in
 ``include/came8.h``).
 """
-from .optim import CAME8bit, CAME8bitFull, CAME8bitMemory, CAMECUDA  # noqa: F401
+from .optim import CAME8bit, CAME8bit2D, CAME8bitFull, CAME8bitMemory, CAMECUDA  # noqa: F401
 
-__all__ = ["CAME8bit", "CAME8bitFull", "CAME8bitMemory", "CAMECUDA"]
+__all__ = ["CAME8bit", "CAME8bit2D", "CAME8bitFull", "CAME8bitMemory", "CAMECUDA"]
 __version__ = "0.1.0"

@@ -15,10 +15,11 @@ LIB_PATH = os.path.join(HERE, "lib", "libcame8.so")
 
 CAME8_F32, CAME8_BF16, CAME8_F16 = 0, 1, 2
 CAME8_OK, CAME8_EINVAL, CAME8_ESPACE, CAME8_EHIP = 0, -1, -2, -3
-ABI_VERSION = 2  # include/came8.h: CAME8_ABI_VERSION
+ABI_VERSION = 3  # include/came8.h: CAME8_ABI_VERSION
 CAME8_FLAG_REFERENCE_NORM = 1
 CAME8_STATE_Q8 = 0
 CAME8_STATE_FP32 = 1
+CAME8_STATE_8BIT2D = 2
 
 # every symbol include/came8.h declares
 EXPORTED_SYMBOLS = (
@@ -54,6 +55,12 @@ class Came8Tensor(ctypes.Structure):
         ("grad_dtype", ctypes.c_int32),
         ("factored", ctypes.c_int32),
         ("state_kind", ctypes.c_int32),
+        ("res_row_q", ctypes.c_void_p),
+        ("res_row_absmax", ctypes.c_void_p),
+        ("res_col_q", ctypes.c_void_p),
+        ("res_col_absmax", ctypes.c_void_p),
+        ("res_row_partial", ctypes.c_void_p),
+        ("res_col_partial", ctypes.c_void_p),
     ]
 
 

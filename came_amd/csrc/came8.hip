@@ -80,7 +80,8 @@ struct WorkList {
 
 struct Plan {
   std::vector<DevTensor> dev;
-  std::map<BandKey, WorkList> band;      // P1 / P2
+  std::map<BandKey, WorkList> band;      // P1 (every factored tensor)
+  std::map<BandKey, WorkList> band2;     // P2 (factored tensors of the full8bit / fp32 layouts)
   std::map<TypeKey, WorkList> upd;       // P3, tile form (fast block sizes)
   std::map<TypeKey, WorkList> updb;      // P3, band form
   std::map<TypeKey, WorkList> vecB;      // 1-D pass B (fast block sizes)
@@ -88,6 +89,9 @@ struct Plan {
   std::map<TypeKey, WorkList> generic;   // P3 / B for other block sizes (per quantisation block)
   std::map<int, WorkList> refnorm;       // parity-mode clip, by grad type
   WorkList factor;                       // F1b / F2b (per state block)
+  std::map<TypeKey, WorkList> tiles2d;   // 8bit2d momentum pass (per 16 rows x 256 columns)
+  WorkList res2d;                        // 8bit2d residual row states (per band)
+  std::map<int, WorkList> param2d;       // 8bit2d parameter write, by param type
   size_t plan_bytes = 0;
   size_t total_bytes = 0;
   std::vector<uint8_t> blob;
@@ -163,9 +167,18 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
   for (int i = 0; i < n; ++i) {
     const came8_tensor& t = ts[i];
     const std::string who = "came8: tensor " + std::to_string(i) + ": ";
-    if (t.state_kind != CAME8_STATE_Q8 && t.state_kind != CAME8_STATE_FP32)
+    if (t.state_kind != CAME8_STATE_Q8 && t.state_kind != CAME8_STATE_FP32 && t.state_kind != CAME8_STATE_8BIT2D)
       return fail(CAME8_EINVAL, who + "unknown state_kind " + std::to_string(t.state_kind));
     const bool f32st = t.state_kind == CAME8_STATE_FP32;
+    const bool s2d = t.state_kind == CAME8_STATE_8BIT2D;
+    if (s2d) {
+      if (!t.factored || t.prefix != 1) return fail(CAME8_EINVAL, who + "8bit2d states need a 2-D tensor (factored, prefix 1)");
+      if (B != 256) return fail(CAME8_EINVAL, who + "8bit2d states support block_size=256 only, got " + std::to_string(B));
+      if (!t.res_row_q || !t.res_row_absmax || !t.res_col_q || !t.res_col_absmax)
+        return fail(CAME8_EINVAL, who + "null residual state");
+      if ((t.res_row_partial == nullptr) != (t.res_col_partial == nullptr))
+        return fail(CAME8_EINVAL, who + "give both tile partial buffers or neither");
+    }
     if (!t.param || !t.grad || !t.exp_avg_q || !t.row_q || (!f32st && !t.exp_avg_absmax) ||
         ((!f32st || t.factored) && !t.row_absmax))
       return fail(CAME8_EINVAL, who + "null pointer");
@@ -194,6 +207,15 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     d.nbm = std::max<int64_t>(1, ceil_div(d.N, B));
     d.factored = t.factored ? 1 : 0;
     d.fp32st = f32st ? 1 : 0;
+    d.mode2d = s2d ? 1 : 0;
+    if (s2d) {
+      d.tr = int32_t(ceil_div(t.rows, 16));
+      d.tc = int32_t(ceil_div(t.cols, 16));
+      d.rrq = t.res_row_q;
+      d.rra = t.res_row_absmax;
+      d.rcq = t.res_col_q;
+      d.rca = t.res_col_absmax;
+    }
     const uintptr_t pp = reinterpret_cast<uintptr_t>(t.param), gp = reinterpret_cast<uintptr_t>(t.grad),
                     mp = reinterpret_cast<uintptr_t>(t.exp_avg_q);
     d.vec_ok = (pp % 16 == 0 && gp % 16 == 0 && mp % 8 == 0) ? 1 : 0;
@@ -204,7 +226,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       return o;
     };
     struct Offs {
-      size_t Rn, rfac, RRn, rrfac, Cn, cfac, CRn, crfac, pU, pW, pR, rm, rmr, clipp, clip;
+      size_t Rn, rfac, RRn, rrfac, Cn, cfac, CRn, crfac, pU, pW, pR, rm, rmr, clipp, clip, t2r, t2c;
     } o{};
     d.idx32 = d.N < (int64_t(1) << 31) ? 1 : 0;
     d.rowal = (d.C % B) == 0 ? 1 : 0;
@@ -213,7 +235,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     d.p3_rb = 0;
     d.p3_nseg = 0;
     d.p3_nbands = 0;
-    if (t.factored && fast_block(B) && d.rowal && d.vec_ok && d.C >= kP3BandMinCols) {
+    if (t.factored && !s2d && fast_block(B) && d.rowal && d.vec_ok && d.C >= kP3BandMinCols) {
       const int64_t bpr = d.C / B, bmax = kTile / B;  // blocks per row, per segment
       d.p3_nseg = int32_t(ceil_div(bpr, bmax));
       d.p3_rb = kP3BandRows;
@@ -232,7 +254,15 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       const size_t part = size_t(d.P * d.nbands * d.C) * 4;
       o.Rn = take(pr); o.rfac = take(pr); o.RRn = take(pr); o.rrfac = take(pr);
       o.Cn = take(pc); o.cfac = take(pc); o.CRn = take(pc); o.crfac = take(pc);
-      o.pU = take(part); o.pW = take(part); o.pR = take(part);
+      o.pU = take(part); o.pW = take(part);
+      if (s2d) {  // tile residual sums per row [R*tc] and per column [C*tr], unless the caller's
+        if (!t.res_row_partial) {
+          o.t2r = take(size_t(d.R) * size_t(d.tc) * 4);
+          o.t2c = take(size_t(d.C) * size_t(d.tr) * 4);
+        }
+      } else {
+        o.pR = take(part);
+      }
       o.rm = take(size_t(d.P * d.nbands) * 4); o.rmr = take(size_t(d.P * d.nbands) * 4);
       o.clipp = take(size_t(d.nclip) * 8);
       o.clip = take(8);
@@ -251,7 +281,13 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     if (t.factored) {
       d.Rn = at(o.Rn); d.rfac = at(o.rfac); d.RRn = at(o.RRn); d.rrfac = at(o.rrfac);
       d.Cn = at(o.Cn); d.cfac = at(o.cfac); d.CRn = at(o.CRn); d.crfac = at(o.crfac);
-      d.partU = at(o.pU); d.partW = at(o.pW); d.partRes = at(o.pR);
+      d.partU = at(o.pU); d.partW = at(o.pW);
+      if (s2d) {
+        d.t2row = t.res_row_partial ? t.res_row_partial : at(o.t2r);
+        d.t2col = t.res_col_partial ? t.res_col_partial : at(o.t2c);
+      } else {
+        d.partRes = at(o.pR);
+      }
       d.rsum = at(o.rm); d.rrsum = at(o.rmr);
     }
     d.clip_part = reinterpret_cast<double*>(scr + o.clipp);
@@ -265,9 +301,20 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     const came8_tensor& t = ts[i];
     const DevTensor& d = plan.dev[i];
     const TypeKey tk{t.param_dtype, t.grad_dtype, d.fp32st};
+    if (d.mode2d) {
+      const BandShapeSel sel = band_variant(t, d.C, B);
+      add_item(plan.band[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB}], i, d.nbands);
+      add_item(plan.factor, i, d.nbr + d.nbc);
+      add_item(plan.tiles2d[tk], i, int64_t(d.tr) * ceil_div(d.C, 256));
+      add_item(plan.res2d, i, d.nbands);
+      add_item(plan.param2d[t.param_dtype], i, ceil_div(d.N, kTile));
+      continue;  // the clip of this layout has no parity-mode variant (the reference sums it with float atomics)
+    }
     if (t.factored) {
       const BandShapeSel sel = band_variant(t, d.C, B);
-      add_item(plan.band[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB}], i, d.P * d.nbands);
+      const BandKey bk{t.grad_dtype, sel.V, sel.K, sel.TPB};
+      add_item(plan.band[bk], i, d.P * d.nbands);
+      add_item(plan.band2[bk], i, d.P * d.nbands);
       add_item(plan.factor, i, d.nbr + d.nbc);
       if (fastB) {
         if (d.p3_nbands > 0) add_item(plan.updb[tk], i, d.P * d.p3_nbands * d.p3_nseg);
@@ -290,6 +337,10 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     off = align_up(off + wl.wstart.size() * 8, 16);
   };
   for (auto& kv : plan.band) place(kv.second);
+  for (auto& kv : plan.band2) place(kv.second);
+  for (auto& kv : plan.tiles2d) place(kv.second);
+  for (auto& kv : plan.param2d) place(kv.second);
+  place(plan.res2d);
   for (auto& kv : plan.upd) place(kv.second);
   for (auto& kv : plan.updb) place(kv.second);
   for (auto& kv : plan.vecB) place(kv.second);
@@ -311,7 +362,15 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       if (d.factored) {
         rebase(d.Rn); rebase(d.rfac); rebase(d.RRn); rebase(d.rrfac);
         rebase(d.Cn); rebase(d.cfac); rebase(d.CRn); rebase(d.crfac);
-        rebase(d.partU); rebase(d.partW); rebase(d.partRes);
+        rebase(d.partU); rebase(d.partW);
+        if (d.mode2d) {
+          if (!ts[i].res_row_partial) {  // workspace offsets (caller buffers are absolute)
+            rebase(d.t2row);
+            rebase(d.t2col);
+          }
+        } else {
+          rebase(d.partRes);
+        }
         rebase(d.rsum); rebase(d.rrsum);
       }
       rebase(d.clip_part);
@@ -324,6 +383,10 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       std::memcpy(plan.blob.data() + wl.wstart_off, wl.wstart.data(), wl.wstart.size() * 8);
     };
     for (auto& kv : plan.band) put(kv.second);
+    for (auto& kv : plan.band2) put(kv.second);
+    for (auto& kv : plan.tiles2d) put(kv.second);
+    for (auto& kv : plan.param2d) put(kv.second);
+    put(plan.res2d);
     for (auto& kv : plan.upd) put(kv.second);
     for (auto& kv : plan.updb) put(kv.second);
     for (auto& kv : plan.vecB) put(kv.second);
@@ -382,6 +445,12 @@ Hp make_hp(const came8_hparams& h) {
   hp.alr = float(-h.lr);
   hp.thr = float(h.clip_threshold);
   hp.wd = h.weight_decay != 0.0 ? 1 : 0;
+  // 8bit2d: the reference computes these in float (came_kernels.cu:91, 2623, 2678)
+  hp.a1f = 1.0f - float(h.beta1);
+  hp.a2f = 1.0f - float(h.beta2);
+  hp.a3f = 1.0f - float(h.beta3);
+  const float lr_wd = float(h.lr) * float(h.weight_decay);
+  hp.wdfac = 1.0f - lr_wd;
   hp.B = h.block_size;
   hp.log2B = log2_or_minus1(h.block_size);
   if (hp.log2B >= 0) {
@@ -467,10 +536,10 @@ int check_launch(const char* what) {
 // ---------------------------------------------------------------------------
 const char* const kPhaseNames[] = {"pass1", "vec_passA", "row_mean", "factor_blocks", "clip", "clip_refnorm",
                                    "pass2", "row_mean_res", "factor_blocks_res", "pass3", "vec_passB",
-                                   "generic_update"};
+                                   "generic_update", "tiles2d", "res_rows2d", "param2d"};
 constexpr int kNumPhases = sizeof(kPhaseNames) / sizeof(kPhaseNames[0]);
 enum Phase { PH_PASS1, PH_VECA, PH_ROWMEAN, PH_FACTOR, PH_CLIP, PH_CLIP_REF, PH_PASS2, PH_ROWMEAN_RES,
-             PH_FACTOR_RES, PH_PASS3, PH_VECB, PH_GENERIC };
+             PH_FACTOR_RES, PH_PASS3, PH_VECB, PH_GENERIC, PH_TILES2D, PH_RES2D, PH_PARAM2D };
 
 struct Pending {
   int phase;
@@ -528,7 +597,7 @@ struct PhaseTimer {
 double elem_bytes(int dt) { return dt == CAME8_F32 ? 4.0 : 2.0; }
 
 // Algorithmic bytes of one launch: every operand the kernel must touch, counted once.
-double alg_bytes(const Plan& plan, const WorkList& wl, const came8_tensor* ts, int phase) {
+double alg_bytes(const Plan& plan, const WorkList& wl, const came8_tensor* ts, int phase, bool wd = false) {
   double tot = 0.0;
   for (int32_t i : wl.tids) {
     const DevTensor& d = plan.dev[i];
@@ -544,6 +613,16 @@ double alg_bytes(const Plan& plan, const WorkList& wl, const came8_tensor* ts, i
       case PH_VECB: tot += N * (sg + 2.0 * sp + 2.0 * (mb + vb)) + (d.fp32st ? 0.0 : 16.0 * nbm); break;
       case PH_GENERIC:
         tot += d.factored ? N * (sg + 2.0 * sp + 2.0) + 8.0 * nbm : N * (sg + 2.0 * sp + 4.0) + 16.0 * nbm;
+        break;
+      case PH_TILES2D:  // g, m rw, p rw (weight decay), tile scales rw, tile residual sums written
+        tot += N * (sg + 2.0 + (wd ? 2.0 * sp : 0.0)) + 8.0 * double(d.tr) * double(d.tc) +
+               4.0 * (double(d.R) * d.tc + double(d.C) * d.tr);
+        break;
+      case PH_RES2D:  // tile residual row sums, residual row codes and scales, new row states
+        tot += 4.0 * double(d.R) * d.tc + double(d.R) + 4.0 * double(d.nbr) + 4.0 * double(d.R);
+        break;
+      case PH_PARAM2D:  // m, tile scales, p rw
+        tot += N * (1.0 + 2.0 * sp) + 4.0 * double(d.tr) * double(d.tc);
         break;
       case PH_FACTOR: case PH_FACTOR_RES:  // one row + one column state: codes rw, scales rw
         tot += 2.0 * double(d.P * d.R + d.P * d.C) + 8.0 * double(d.nbr + d.nbc);
@@ -668,14 +747,15 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     hipLaunchKernelGGL(fn, dim3(grid_for(int64_t(wl.tids.size()))), blk, 0, stream, dT, tids(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("clip_refnorm")) != CAME8_OK) return rc; }
     }
-  } else {
+  }
+  if (!refnorm || !plan.tiles2d.empty()) {  // parity mode: only the 8bit2d tensors take this divisor
     PhaseTimer pt(PH_CLIP, 0.0, stream);
-    hipLaunchKernelGGL(k_clip<>, dim3(grid_for(n_tensors)), blk, 0, stream, dT, int(n_tensors), hp);
+    hipLaunchKernelGGL(k_clip<>, dim3(grid_for(n_tensors)), blk, 0, stream, dT, int(n_tensors), int(refnorm), hp);
     if ((rc = check_launch("clip")) != CAME8_OK) return rc;
   }
   // ---- P2, residual factors ----
   if (any_fact) {
-    for (auto& kv : plan.band) {
+    for (auto& kv : plan.band2) {
       const BandKey& k = kv.first;
       const WorkList& wl = kv.second;
       BandFn fn = nullptr;
@@ -685,6 +765,21 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("pass2")) != CAME8_OK) return rc; }
     }
+    for (auto& kv : plan.tiles2d) {
+      const WorkList& wl = kv.second;
+      GenFn fn;
+      CAME8_TYPE_SWITCH2(k_2d_tiles, kv.first.pdt, kv.first.gdt, fn);
+      { PhaseTimer pt(PH_TILES2D, alg_bytes(plan, wl, tensors, PH_TILES2D, h.weight_decay != 0.0), stream);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      if ((rc = check_launch("tiles2d")) != CAME8_OK) return rc; }
+    }
+    if (!plan.res2d.tids.empty()) {
+      const WorkList& wl = plan.res2d;
+      PhaseTimer pt(PH_RES2D, alg_bytes(plan, wl, tensors, PH_RES2D), stream);
+      hipLaunchKernelGGL(k_2d_res_rows<>, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl),
+                         int(wl.tids.size()), hp);
+      if ((rc = check_launch("res_rows2d")) != CAME8_OK) return rc;
+    }
     const WorkList& fb = plan.factor;
     { PhaseTimer pt(PH_FACTOR_RES, alg_bytes(plan, fb, tensors, PH_FACTOR_RES), stream);
     hipLaunchKernelGGL(k_factor_blocks<true>, dim3(grid_for(fb.total())), blk, 0, stream, dT, tids(fb), wst(fb),
@@ -692,6 +787,14 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     if ((rc = check_launch("factor_blocks_res")) != CAME8_OK) return rc; }
   }
   // ---- P3 and 1-D pass B ----
+  for (auto& kv : plan.param2d) {
+    const WorkList& wl = kv.second;
+    GenFn fn;
+    CAME8_TYPE_SWITCH1(k_2d_param, kv.first, fn);
+    { PhaseTimer pt(PH_PARAM2D, alg_bytes(plan, wl, tensors, PH_PARAM2D), stream);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+    if ((rc = check_launch("param2d")) != CAME8_OK) return rc; }
+  }
   if (fastB) {
     for (auto& kv : plan.upd) {
       const WorkList& wl = kv.second;

@@ -261,6 +261,17 @@ __device__ __forceinline__ float scale_s8(float absmax) {
   return div_fast(absmax, kSignedQ, kRcpSignedQ);
 }
 
+// The 8bit2d layout's quantisation (reference came_kernels.cu:833-847): x times the rounded reciprocal
+// of absmax, times Q, each product rounded, then rint and a clamp through fminf / fmaxf.
+__device__ __forceinline__ int8_t quant_s8_inv(float x, float inv) {
+  const float q = rintf((x * inv) * kSignedQ);
+  return int8_t(fminf(kSignedQ, fmaxf(-kSignedQ, q)));
+}
+__device__ __forceinline__ uint8_t quant_u8_inv(float x, float inv) {
+  const float q = rintf((x * inv) * kUnsignedQ);
+  return uint8_t(fminf(kUnsignedQ, fmaxf(0.0f, q)));
+}
+
 // any rcp (NaN divides)
 __device__ __forceinline__ int8_t quant_s8_r(float x, float absmax, float rcp) {
   return rcp == rcp ? quant_s8_fast(x, absmax, rcp) : quant_s8(x, absmax);

@@ -76,6 +76,17 @@ struct DevTensor {
   int32_t factored;
   int32_t fp32st;     // fp32 states (CAMECUDA layout): mq -> float m, rq/ra -> float second-moment /
                       // residual rows (rq -> float v for 1-D), cq/ca -> float columns; ma unused
+  // 8bit2d layout (reference CAME8bit2D): ma holds one absmax per 16x16 tile of m; rq/ra, cq/ca are
+  // the second-moment row / column states and rrq/rra, rcq/rca the residual ones; t2row / t2col
+  // receive each tile's residual sums per row [R*tc] and per column [C*tr]
+  int32_t mode2d;
+  int32_t tr, tc;     // tile rows, tile columns
+  uint8_t* rrq;
+  float* rra;
+  uint8_t* rcq;
+  float* rca;
+  float* t2row;
+  float* t2col;
 };
 
 // fp32-state views of the state pointers
@@ -97,6 +108,8 @@ struct Hp {
   int32_t log2B;   // log2(B) if B is a power of two, else -1
   uint32_t sB;     // magic division by B (indices < 2^31, which the host guarantees for
   uint64_t mB;     // block sizes that are not powers of two)
+  float a1f, a2f, a3f;  // 8bit2d: 1 - beta computed in float
+  float wdfac;          // 8bit2d: multiplicative weight decay 1 - lr * wd, computed in float
 };
 
 __device__ __forceinline__ int64_t blk_of(int64_t e, const Hp& hp) {
@@ -335,7 +348,7 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(TPB == 256 
           if (r + s < r1) {
             const int64_t row = b * R + r + s;
             const float Rold = t.fp32st ? st_sq_row(t)[row] : deq_u8(rq[row], ra[blk_of(row, hp)]);
-            const float Rnew = fmaf(tot[s] / fC, hp.a2, Rold * hp.b2);
+            const float Rnew = t.mode2d ? (Rold * hp.b2) + (hp.a2f * (tot[s] / fC)) : fmaf(tot[s] / fC, hp.a2, Rold * hp.b2);
             if (tid == 0) Rn[row] = Rnew;
             bandR += Rnew;
             const float invR = 1.0f / Rnew;
@@ -403,7 +416,7 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(TPB == 256 
           if (r + s < r1) {
             const int64_t row = b * R + r + s;
             const float Rold = t.fp32st ? st_sq_row(t)[row] : deq_u8(rq[row], ra[blk_of(row, hp)]);
-            const float Rnew = fmaf(tot[s] / fC, hp.a2, Rold * hp.b2);
+            const float Rnew = t.mode2d ? (Rold * hp.b2) + (hp.a2f * (tot[s] / fC)) : fmaf(tot[s] / fC, hp.a2, Rold * hp.b2);
             bandR += Rnew;
             if (tid == 0) {
               Rn[row] = Rnew;
@@ -740,7 +753,9 @@ __device__ __forceinline__ float matrix_row_mean(const DevTensor& t, const float
   const float* __restrict__ src = bandsum + b * t.nbands;
   float s = 0.0f;
   for (int64_t k = 0; k < t.nbands; ++k) s += src[k];
-  return clamp_min_tiny(s / float(t.R));
+  const float m = s / float(t.R);
+  if (t.mode2d) return m > 0.0f ? m : 1.0f;  // 8bit2d: a mean that is not positive counts as 1
+  return clamp_min_tiny(m);
 }
 
 // sum over the nbands band partials of one column (stride C), four interleaved accumulators
@@ -777,6 +792,7 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
     double csum = 0.0;
     const float beta = RES ? hp.b3 : hp.b2;
     const float alpha = RES ? hp.a3 : hp.a2;
+    const float alpha_f = RES ? hp.a3f : hp.a2f;
     if (is_row) {
       const float* __restrict__ Rsrc = RES ? t.RRn : t.Rn;
       float* __restrict__ fac = RES ? t.rrfac : t.rfac;
@@ -806,11 +822,24 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
       for (int64_t i = i0 + tid; i < i1; i += kThreads) {
         const int64_t b = i / t.C;
         const int64_t j = i - b * t.C;
-        const float* __restrict__ pp = part + (b * t.nbands) * t.C + j;
-        const double s = band_column_sum(pp, t.nbands, t.C);
         float* __restrict__ cst = RES ? t.ca : st_sq_col(t);  // fp32 column state
-        const float Cold = t.fp32st ? cst[i] : deq_u8(t.cq[off + i], t.ca[aoff + blk_of(i, hp)]);
-        const float Cv = clamp_min_tiny(fmaf(float(s) / fR, alpha, Cold * beta));
+        float Cold, Cv;
+        if (t.mode2d) {
+          // 8bit2d: residual column sums come from the tile partials (tiles in order); no clamp
+          float s2 = 0.0f;
+          if (RES) {
+            for (int64_t ty = 0; ty < t.tr; ++ty) s2 += t.t2col[i * t.tr + ty];
+          } else {
+            s2 = float(band_column_sum(part + (b * t.nbands) * t.C + j, t.nbands, t.C));
+          }
+          Cold = RES ? deq_u8(t.rcq[i], t.rca[blk_of(i, hp)]) : deq_u8(t.cq[i], t.ca[blk_of(i, hp)]);
+          Cv = (Cold * beta) + (alpha_f * (s2 / fR));
+        } else {
+          const float* __restrict__ pp = part + (b * t.nbands) * t.C + j;
+          const double s = band_column_sum(pp, t.nbands, t.C);
+          Cold = t.fp32st ? cst[i] : deq_u8(t.cq[off + i], t.ca[aoff + blk_of(i, hp)]);
+          Cv = clamp_min_tiny(fmaf(float(s) / fR, alpha, Cold * beta));
+        }
         const float c = rsqrt_ref(Cv);
         Cdst[i] = Cv;
         fac[i] = c;
@@ -838,7 +867,10 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
     const float amax = fix_absmax(nan_max(nan_max(smax[0], smax[1]), nan_max(smax[2], smax[3])));
     if (tid == 0) {
       if (!RES && !is_row) t.clip_part[blk] = ((ssum[0] + ssum[1]) + ssum[2]) + ssum[3];
-      if (!t.fp32st) {
+      if (t.mode2d) {
+        if (is_row) (RES ? t.rra : t.ra)[blk] = amax;
+        else (RES ? t.rca : t.ca)[blk] = amax;
+      } else if (!t.fp32st) {
         if (is_row) t.ra[(RES ? t.nbr : 0) + blk] = amax;
         else t.ca[(RES ? t.nbc : 0) + blk] = amax;
       }
@@ -846,6 +878,11 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
     const float arcp = rcp_for_div(amax);
     if (t.fp32st) {
       // fp32 states were written above; no codes
+    } else if (t.mode2d) {
+      const float inv = 1.0f / amax;
+      const float* __restrict__ src = is_row ? (RES ? t.RRn : t.Rn) : (RES ? t.CRn : t.Cn);
+      uint8_t* __restrict__ q = is_row ? (RES ? t.rrq : t.rq) : (RES ? t.rcq : t.cq);
+      for (int64_t i = i0 + tid; i < i1; i += kThreads) q[i] = quant_u8_inv(src[i], inv);
     } else if (is_row) {
       const float* __restrict__ Rsrc = RES ? t.RRn : t.Rn;
       uint8_t* __restrict__ q = t.rq + (RES ? t.P * t.R : 0);
@@ -908,12 +945,15 @@ __device__ __forceinline__ float clip_from_norm(float norm, int64_t N, const Hp&
   return q < 1.0f ? 1.0f : q;
 }
 
+// only2d: leave every tensor but those of the 8bit2d layout alone (their divisor comes from the
+// parity-mode kernel)
 template <int = 0>  // a template only so that every translation unit may include this header
-__global__ __launch_bounds__(kThreads) void k_clip(const DevTensor* __restrict__ T, int ntens, Hp hp) {
+__global__ __launch_bounds__(kThreads) void k_clip(const DevTensor* __restrict__ T, int ntens, int only2d, Hp hp) {
   __shared__ double ssum[4];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   for (int k = blockIdx.x; k < ntens; k += gridDim.x) {
     const DevTensor& t = T[k];
+    if (only2d && !t.mode2d) continue;  // uniform over the workgroup
     double s = 0.0;
     for (int64_t i = tid; i < t.nclip; i += kThreads) s += t.clip_part[i];
     s = wave_sum(s);
@@ -921,7 +961,13 @@ __global__ __launch_bounds__(kThreads) void k_clip(const DevTensor* __restrict__
     __syncthreads();
     if (tid == 0) {
       const double tot = ((ssum[0] + ssum[1]) + ssum[2]) + ssum[3];
-      const float c = clip_from_norm(float(sqrt(tot)), t.N, hp);
+      float c;
+      if (t.mode2d) {  // 8bit2d: sqrtf(sum / n) in float (came_kernels.cu:2619-2620)
+        const float q = sqrtf(float(tot) / float(t.N)) / hp.thr;
+        c = q < 1.0f ? 1.0f : q;
+      } else {
+        c = clip_from_norm(float(sqrt(tot)), t.N, hp);
+      }
       t.clip[0] = c;
       t.clip[1] = rcp_for_div(c);
     }
@@ -1489,6 +1535,154 @@ __global__ __launch_bounds__(kThreads) void k_generic_update(const DevTensor* __
       if (!t.factored) t.ra[blk] = av;
     }
     __syncthreads();
+  }
+}
+
+// ===========================================================================
+// 8bit2d layout: momentum quantised in 16x16 tiles (reference CAME8bit2D; arithmetic order of
+// came_kernels.cu:2584-2684, 2685-2780, 3333-3367)
+// ===========================================================================
+constexpr int kTile2 = 16;
+
+// Momentum pass.  Work item = (tensor, tile row ty, group of 256 columns); wave w owns columns
+// [256*cg + 64*w, +64) of the tile row's 16 rows, one column per lane, so a tile is 16 lanes of one
+// wave.  u = (g*r)*c / clip; m = m_old*b1 + u*(1-b1) (m_old = 0 in a tile whose absmax is 0);
+// res = (u - m)^2 + eps1; the tile's absmax and int8 codes; each tile's residual sums per row and
+// per column (16 terms in order); and p <- p * (1 - lr*wd) when wd != 0.
+template <typename TP, typename TG>
+__global__ __launch_bounds__(kThreads) void k_2d_tiles(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                       const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using PS = typename TP::storage;
+  using GS = typename TG::storage;
+  __shared__ float lres[4][kTile2][kWave + 1];  // +1: rows of a tile fall in different banks
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t R = t.R, C = t.C;
+    const int64_t ncg = (C + 255) / 256;
+    const int64_t local = w - wstart[slot];
+    const int64_t ty = local / ncg, cg = local - ty * ncg;
+    const int64_t r0 = ty * kTile2;
+    const int nrows = int((R - r0) < kTile2 ? (R - r0) : kTile2);
+    const int64_t col = cg * 256 + int64_t(wid) * kWave + lane;
+    const bool cvalid = col < C;
+    const int64_t tile = ty * t.tc + (col >> 4);
+    CAME8_GLOBAL PS* __restrict__ p = gbl(static_cast<PS*>(t.p));
+    const CAME8_GLOBAL GS* __restrict__ g = gbl(static_cast<const GS*>(t.g));
+    CAME8_GLOBAL int8_t* __restrict__ mq = gbl(t.mq);
+    const float clip = uniform_f32(t.clip[0]);
+    const float cj = cvalid ? t.cfac[col] : 0.0f;
+    const float am_old = cvalid ? t.ma[tile] : 0.0f;
+    const float sc_old = am_old / kSignedQ;
+    float m[kTile2], res[kTile2];
+    uint32_t abits = 0;
+#pragma unroll
+    for (int i = 0; i < kTile2; ++i) {
+      m[i] = 0.0f;
+      res[i] = 0.0f;
+      if (i < nrows && cvalid) {
+        const int64_t e = (r0 + i) * C + col;
+        const float ri = t.rfac[r0 + i];
+        const float u = ((TG::load(g[e]) * ri) * cj) / clip;
+        const float mo = am_old > 0.0f ? float(mq[e]) * sc_old : 0.0f;
+        const float mn = (mo * hp.b1) + (u * hp.a1f);
+        const float d = u - mn;
+        m[i] = mn;
+        res[i] = (d * d) + hp.eps1;
+        if (hp.wd) p[e] = TP::store(TP::load(p[e]) * hp.wdfac);
+      }
+      abits = max(abits, abs_bits(m[i]));
+    }
+    abits = group_max_bits<kTile2>(abits);
+    const float amax = fix_absmax(__uint_as_float(abits));
+    const float inv = 1.0f / amax;
+    if (cvalid) {
+      if ((lane & (kTile2 - 1)) == 0) t.ma[tile] = amax;
+      float csum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kTile2; ++i) {
+        if (i < nrows) mq[(r0 + i) * C + col] = quant_s8_inv(m[i], inv);
+        csum += res[i];
+      }
+      t.t2col[col * t.tr + ty] = csum;
+    }
+    // per-row sums of each tile: the 16 columns in order, through LDS
+#pragma unroll
+    for (int i = 0; i < kTile2; ++i) lres[wid][i][lane] = res[i];
+    __syncthreads();
+    {
+      const int i = lane & (kTile2 - 1), k = lane >> 4;
+      const int64_t c0 = cg * 256 + int64_t(wid) * kWave + k * kTile2;
+      float rsum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kTile2; ++j) rsum += lres[wid][i][k * kTile2 + j];
+      if (i < nrows && c0 < C) t.t2row[(r0 + i) * t.tc + (c0 >> 4)] = rsum;
+    }
+    __syncthreads();  // lres is reused by the next work item
+  }
+}
+
+// Residual row states of the 8bit2d layout.  Work item = (tensor, band of rb rows): each row's sum
+// over its tiles in order, mean, new state RR = RR_old*b3 + (1-b3)*mean; the band's states summed
+// in row order for the mean row state.
+template <int = 0>  // a template only so that every translation unit may include this header
+__global__ __launch_bounds__(kThreads) void k_2d_res_rows(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                          const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  __shared__ float rowval[kMaxBandRows];
+  const int tid = threadIdx.x;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t band = w - wstart[slot];
+    const int64_t r0 = band * t.rb;
+    const int64_t r1 = (r0 + t.rb < t.R) ? (r0 + t.rb) : t.R;
+    for (int64_t i = tid; i < r1 - r0; i += kThreads) {
+      const int64_t row = r0 + i;
+      float s = 0.0f;
+      for (int64_t tx = 0; tx < t.tc; ++tx) s += t.t2row[row * t.tc + tx];
+      const float old = deq_u8(t.rrq[row], t.rra[blk_of(row, hp)]);
+      const float v = (old * hp.b3) + (hp.a3f * (s / float(t.C)));
+      t.RRn[row] = v;
+      rowval[i] = v;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      float s = 0.0f;
+      for (int64_t i = 0; i < r1 - r0; ++i) s += rowval[i];
+      t.rrsum[band] = s;
+    }
+    __syncthreads();
+  }
+}
+
+// Parameter write of the 8bit2d layout from the requantised momentum: p <- p - lr*((m_q*rr)*cr),
+// one fused multiply-add; 2048 elements per work item.
+template <typename TP>
+__global__ __launch_bounds__(kThreads) void k_2d_param(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                       const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using PS = typename TP::storage;
+  const int tid = threadIdx.x;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t e0 = (w - wstart[slot]) * kTile + int64_t(tid) * 8;
+    PS* __restrict__ p = static_cast<PS*>(t.p);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int64_t e = e0 + v;
+      if (e < t.N) {
+        const int64_t row = t.idx32 ? int64_t(udiv_magic(uint32_t(e), t.mC, t.sC)) : e / t.C;
+        const int64_t col = e - row * t.C;
+        const float am = t.ma[(row >> 4) * t.tc + (col >> 4)];
+        const float mqv = float(t.mq[e]) * (am / kSignedQ);
+        const float step = (mqv * t.rrfac[row]) * t.crfac[col];
+        p[e] = TP::store(fmaf(step, hp.alr, TP::load(p[e])));
+      }
+    }
   }
 }
 

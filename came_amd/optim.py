@@ -212,6 +212,14 @@ class _Came8Base(torch.optim.Optimizer):
     def _group_block_size(self, group: dict) -> int:
         return int(group["block_size"])
 
+    @staticmethod
+    def _is_factored(state: dict) -> bool:
+        return bool(state["factored"])
+
+    @staticmethod
+    def _count_step(state: dict) -> None:
+        state["step"] += 1
+
     def _fill_desc(self, d, p: torch.Tensor, state: dict) -> None:
         """State pointers of one tensor in the full8bit layout (include/came8.h: came8_tensor)."""
         d.exp_avg_q = state["exp_avg_q"].data_ptr()
@@ -237,7 +245,7 @@ class _Came8Base(torch.optim.Optimizer):
             items = []
             for p in plist:
                 state, grad = self._prepare_param(p, block_size)
-                state["step"] += 1
+                self._count_step(state)
                 if p.numel() == 0:
                     continue
                 items.append((p, state, grad))
@@ -259,7 +267,7 @@ class _Came8Base(torch.optim.Optimizer):
                 d.param_dtype = _DTYPE_CODE[p.dtype]
                 d.grad_dtype = _DTYPE_CODE[g.dtype]
                 d.state_kind = self._STATE_KIND
-                if state["factored"]:
+                if self._is_factored(state):
                     shape = tuple(p.shape)
                     d.prefix = math.prod(shape[:-2])
                     d.rows, d.cols = shape[-2], shape[-1]
@@ -640,3 +648,198 @@ class CAMECUDA(_Came8Base):
 
     def _after_load(self, state: dict) -> None:
         pass
+
+
+# state tensors of the 8bit2d layout and their dtypes (came_pytorch/came8bit2d_state.py:40-68)
+_STATE_DTYPES_2D = {
+    "exp_avg_q": torch.int8,
+    "exp_avg_absmax": torch.float32,
+    **{f"exp_avg_{k}_q": torch.uint8 for k in ("sq_row", "sq_col", "res_row", "res_col")},
+    **{f"exp_avg_{k}_absmax": torch.float32 for k in ("sq_row", "sq_col", "res_row", "res_col")},
+    **{k: torch.float32 for k in ("r_factor", "c_factor", "r_res_factor", "c_res_factor", "res_row_sum",
+                                  "res_col_sum", "res_row_partial", "res_col_partial", "sum_sq_row", "sum_update",
+                                  "sum_update_partial", "sum_res_row")},
+}
+_TILE_2D = 16
+
+
+def init_8bit2d_state(state: dict, p_data: torch.Tensor, *, block_size: int = 256) -> None:
+    """The reference's 8bit2d state of a 2-D parameter (came_pytorch/came8bit2d_state.py:33-75): the
+    persistent tensors, the per-parameter scratch tensors the reference keeps in the state (the
+    library uses ``res_row_partial`` / ``res_col_partial`` as its tile sums; the others stay
+    unwritten, so a state dict saved here steps unchanged in the reference) and the shape keys.
+    There is no ``step`` key."""
+    rows, cols = p_data.shape
+    dev = p_data.device
+    tr, tc = math.ceil(rows / _TILE_2D), math.ceil(cols / _TILE_2D)
+    state["_mode"] = "8bit2d"
+    state["exp_avg_q"] = torch.zeros_like(p_data, dtype=torch.int8)
+    state["exp_avg_absmax"] = torch.zeros((tr * tc,), device=dev, dtype=torch.float32)  # 0: no momentum yet
+    for k, n in (("sq_row", rows), ("sq_col", cols), ("res_row", rows), ("res_col", cols)):
+        state[f"exp_avg_{k}_q"], state[f"exp_avg_{k}_absmax"] = init_qstate(
+            (n,), device=dev, signed=False, block_size=block_size)
+    f32 = dict(device=dev, dtype=torch.float32)
+    for k, n in (("r_factor", rows), ("c_factor", cols), ("r_res_factor", rows), ("c_res_factor", cols),
+                 ("res_row_sum", rows), ("res_col_sum", cols), ("res_row_partial", tc * rows),
+                 ("res_col_partial", tr * cols), ("sum_sq_row", 1), ("sum_update", 1),
+                 ("sum_update_partial", (rows * cols + 255) // 256), ("sum_res_row", 1)):
+        state[k] = torch.empty((n,), **f32)
+    state.update(rows=rows, cols=cols, tile_rows=tr, tile_cols=tc, num_tiles=tr * tc)
+
+
+def validate_8bit2d_state(state: dict, p_data: torch.Tensor) -> None:
+    """came_pytorch/came8bit2d_state.py:78-87 (same messages)."""
+    rows, cols = p_data.shape
+    tr, tc = math.ceil(rows / _TILE_2D), math.ceil(cols / _TILE_2D)
+    if state["rows"] != rows or state["cols"] != cols:
+        raise RuntimeError("Parameter shape changed; this optimizer does not support resizing 8-bit state.")
+    if state["tile_rows"] != tr or state["tile_cols"] != tc or state["num_tiles"] != tr * tc:
+        raise RuntimeError("Tile layout changed; this optimizer does not support resizing 8-bit state.")
+
+
+class CAME8bit2D(_Came8Base):
+    """CAME with int8 momentum in 16x16 tiles, 2-D CUDA parameters only (reference
+    came_pytorch/CAME8bit2D.py:9).
+
+    Same constructor arguments, defaults and errors (CAME8bit2D.py:19-50, 52-72, 74-131), same
+    state keys (came8bit2d_state.py:33-75; no ``step``).  The arithmetic is the reference's CUDA
+    8bit2d step (``came2d_step``, came_cuda/csrc/came_bindings.cpp:617-759): float32 EMAs of the row
+    and column states, momentum quantised per 16x16 tile with a tile absmax that starts at 0,
+    multiplicative weight decay and the parameter written from the requantised momentum.  Every
+    parameter of a param group is stepped by one ``came8_step`` call.
+    """
+
+    _MODE = "8bit2d"
+    _STATE_KIND = _lib.CAME8_STATE_8BIT2D
+    _KEEP_DTYPES = _STATE_DTYPES_2D
+
+    def __init__(
+        self,
+        params,
+        lr: float,
+        eps: tuple[float, float] = (1e-30, 1e-16),
+        clip_threshold: float = 1.0,
+        betas: tuple[float, float, float] = (0.9, 0.999, 0.9999),
+        weight_decay: float = 0.0,
+        block_size: int = 256,
+        cuda_graph_compatible: bool = False,
+    ):
+        # came_pytorch/CAME8bit2D.py:30-50
+        if lr is None or lr <= 0.0:
+            raise ValueError(f"lr must be > 0, got {lr}")
+        if clip_threshold <= 0.0:
+            raise ValueError(f"clip_threshold must be > 0, got {clip_threshold}")
+        if len(eps) != 2:
+            raise ValueError(f"eps must be a tuple of length 2, got eps={eps}")
+        if len(betas) != 3:
+            raise ValueError(f"betas must be a tuple of length 3, got betas={betas}")
+        if block_size != 256:
+            raise ValueError("Only block_size=256 is supported in this minimal implementation.")
+        defaults = dict(
+            lr=float(lr),
+            eps=(float(eps[0]), float(eps[1])),
+            clip_threshold=float(clip_threshold),
+            betas=(float(betas[0]), float(betas[1]), float(betas[2])),
+            weight_decay=float(weight_decay),
+            block_size=int(block_size),
+        )
+        super().__init__(params, defaults)
+        self.cuda_graph_compatible = bool(cuda_graph_compatible)
+
+    @staticmethod
+    def _is_factored(state: dict) -> bool:
+        return True
+
+    @staticmethod
+    def _count_step(state: dict) -> None:
+        pass  # the 8bit2d state keeps no step count
+
+    def _check_grad(self, p: torch.Tensor) -> None:
+        # came_pytorch/CAME8bit2D.py:89-101
+        if p.dim() != 2:
+            raise NotImplementedError("CAME8bit2D currently supports 2D parameters only.")
+        if not p.is_cuda:
+            raise NotImplementedError("CAME8bit2D requires CUDA parameters.")
+        if p.grad.is_sparse:
+            raise RuntimeError("CAME does not support sparse gradients.")
+        if p.grad.dtype != p.dtype:
+            raise RuntimeError(f"Expected g.dtype == p.dtype, got {p.grad.dtype} vs {p.dtype}")
+        if self.cuda_graph_compatible and not (p.data.is_contiguous() and p.grad.is_contiguous()):
+            raise RuntimeError("CUDA graph capture requires contiguous parameter and gradient tensors.")
+
+    def _init_state(self, state: dict, grad: torch.Tensor, block_size: int) -> None:
+        init_8bit2d_state(state, grad, block_size=block_size)
+
+    def _check_state(self, p: torch.Tensor, state: dict, block_size: int) -> None:
+        """Shape keys as the reference checks them, then every buffer the library will write: dtype,
+        device, contiguity and size (the reference's own checks, came_bindings.cpp:657-714)."""
+        validate_8bit2d_state(state, p.data)
+        rows, cols = p.shape
+        tr, tc = state["tile_rows"], state["tile_cols"]
+        nbr, nbc = num_blocks(rows, block_size), num_blocks(cols, block_size)
+        need = {"exp_avg_q": (torch.int8, rows * cols), "exp_avg_absmax": (torch.float32, tr * tc),
+                "exp_avg_sq_row_q": (torch.uint8, rows), "exp_avg_res_row_q": (torch.uint8, rows),
+                "exp_avg_sq_col_q": (torch.uint8, cols), "exp_avg_res_col_q": (torch.uint8, cols),
+                "exp_avg_sq_row_absmax": (torch.float32, nbr), "exp_avg_res_row_absmax": (torch.float32, nbr),
+                "exp_avg_sq_col_absmax": (torch.float32, nbc), "exp_avg_res_col_absmax": (torch.float32, nbc),
+                "res_row_partial": (torch.float32, tc * rows), "res_col_partial": (torch.float32, tr * cols)}
+        for k, (dt, n) in need.items():
+            v = state.get(k)
+            if not isinstance(v, torch.Tensor):
+                raise RuntimeError(f"8bit2d state is missing {k}")
+            if v.device != p.device:
+                raise RuntimeError("optimizer state lives on a different device than its parameter")
+            if v.dtype != dt:
+                raise RuntimeError(f"{k} must be {str(dt).replace('torch.', '')}, got {v.dtype}")
+            if not v.is_contiguous():
+                raise RuntimeError(f"{k} must be contiguous")
+            if v.numel() < n:
+                raise RuntimeError(f"{k} is too small: {v.numel()} < {n}")
+        if tuple(state["exp_avg_q"].shape) != tuple(p.shape):
+            raise RuntimeError("exp_avg_q.shape must match p.shape")
+
+    def _fill_desc(self, d, p: torch.Tensor, state: dict) -> None:
+        """8bit2d state pointers (include/came8.h: came8_tensor with CAME8_STATE_8BIT2D)."""
+        d.exp_avg_q = state["exp_avg_q"].data_ptr()
+        d.exp_avg_absmax = state["exp_avg_absmax"].data_ptr()
+        d.row_q = state["exp_avg_sq_row_q"].data_ptr()
+        d.row_absmax = state["exp_avg_sq_row_absmax"].data_ptr()
+        d.col_q = state["exp_avg_sq_col_q"].data_ptr()
+        d.col_absmax = state["exp_avg_sq_col_absmax"].data_ptr()
+        d.res_row_q = state["exp_avg_res_row_q"].data_ptr()
+        d.res_row_absmax = state["exp_avg_res_row_absmax"].data_ptr()
+        d.res_col_q = state["exp_avg_res_col_q"].data_ptr()
+        d.res_col_absmax = state["exp_avg_res_col_absmax"].data_ptr()
+        d.res_row_partial = state["res_row_partial"].data_ptr()
+        d.res_col_partial = state["res_col_partial"].data_ptr()
+
+    def _after_load(self, state: dict) -> None:
+        pass
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        for group in self.param_groups:
+            for p in group["params"]:
+                if p.grad is not None:
+                    self._check_grad(p)
+        return super().step(closure)
+
+    @torch.no_grad()
+    def prime_for_cuda_graph(self) -> None:
+        """Create every state before capture (came_pytorch/CAME8bit2D.py:52-72, same messages)."""
+        for group in self.param_groups:
+            block_size = group["block_size"]
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                if p.dim() != 2:
+                    raise RuntimeError("CUDA graph capture for CAME8bit2D requires 2D parameters.")
+                if not p.is_cuda:
+                    raise RuntimeError("CUDA graph capture for CAME8bit2D requires CUDA parameters.")
+                if p.grad.is_sparse:
+                    raise RuntimeError("CAME does not support sparse gradients.")
+                if p.grad.dtype != p.dtype:
+                    raise RuntimeError(f"Expected g.dtype == p.dtype, got {p.grad.dtype} vs {p.dtype}")
+                if not (p.data.is_contiguous() and p.grad.is_contiguous()):
+                    raise RuntimeError("CUDA graph capture requires contiguous parameter and gradient tensors.")
+                self._prepare_param(p, block_size)

@@ -21,7 +21,11 @@
  *                         and, with fp32 states, CAMECUDA's steps:
  *                           came_fp_factored_step               came_bindings.cpp:1692-1760
  *                         (Python: came_cuda/__init__.py:820-860; arithmetic:
- *                          came_pytorch/CAMECUDA.py:275-326).
+ *                          came_pytorch/CAMECUDA.py:275-326);
+ *                         and, with the 8bit2d state layout, CAME8bit2D's step:
+ *                           came2d_step                         came_bindings.cpp:617-759
+ *                         (Python: came_pytorch/CAME8bit2D.py; kernels:
+ *                          came_cuda/csrc/came_kernels.cu:3599-4040).
  *   came8_quantize_blockwise / came8_dequantize_blockwise
  *                        -- blockwise_quant / blockwise_dequant
  *                           came_bindings.cpp:756-801 (Python: came_cuda/__init__.py:205-228;
@@ -41,7 +45,7 @@
 extern "C" {
 #endif
 
-#define CAME8_ABI_VERSION 2
+#define CAME8_ABI_VERSION 3
 
 /* element types of parameters and gradients */
 #define CAME8_F32 0
@@ -57,6 +61,7 @@ extern "C" {
 /* came8_tensor.state_kind */
 #define CAME8_STATE_Q8 0   /* 8-bit states, full8bit layout (CAME8bit, CAME8bitFull, CAME8bitMemory) */
 #define CAME8_STATE_FP32 1 /* fp32 states, CAMECUDA layout */
+#define CAME8_STATE_8BIT2D 2 /* 8-bit states, 8bit2d layout (CAME8bit2D): momentum in 16x16 tiles */
 
 /* flags for came8_hparams.flags */
 #define CAME8_FLAG_REFERENCE_NORM 1u /* clip RMS summed in the reference CPU order (slow; parity runs) */
@@ -93,6 +98,26 @@ extern "C" {
  * The arithmetic is CAMECUDA._step_param_generic (CAMECUDA.py:275-326): the
  * 8-bit step's, with the states kept in fp32 and no quantisation.  block_size
  * then only shapes the work decomposition (a power of two in [8, 2048]).
+ *
+ * With state_kind = CAME8_STATE_8BIT2D the tensor is a 2-D matrix (prefix 1,
+ * factored 1) with the reference's 8bit2d state (came_pytorch/came8bit2d_state.py:33-75):
+ *   exp_avg_q        int8   [R*C]            row-major momentum codes
+ *   exp_avg_absmax   f32    [ceil(R/16)*ceil(C/16)]  one absmax per 16x16 tile,
+ *                                            tile (ty, tx) at ty*ceil(C/16)+tx; 0 = no momentum yet
+ *   row_q, row_absmax          exp_avg_sq_row   uint8 [R], f32 [ceil(R/B)]
+ *   col_q, col_absmax          exp_avg_sq_col   uint8 [C], f32 [ceil(C/B)]
+ *   res_row_q, res_row_absmax  exp_avg_res_row  uint8 [R], f32 [ceil(R/B)]
+ *   res_col_q, res_col_absmax  exp_avg_res_col  uint8 [C], f32 [ceil(C/B)]
+ *   res_row_partial  f32 [R*ceil(C/16)], res_col_partial f32 [C*ceil(R/16)]: the
+ *                    reference's state-resident scratch for each tile's residual sums
+ *                    per row and per column; used as such when both are given, else
+ *                    the workspace holds them (NULL both)
+ * and the arithmetic of the reference's CUDA 8bit2d step (came_pytorch/came_cuda/csrc/
+ * came_kernels.cu:60-96, 198-243, 298-333, 595-619, 2584-2780, 3333-3367; launch order
+ * came_kernels.cu:3599-4040): float32 EMAs (old*beta)+((1-beta)*mean), momentum
+ * requantised per tile, multiplicative weight decay p*(1-lr*wd), and the parameter written
+ * from the requantised momentum.  block_size must be 256, as the reference requires
+ * (came_bindings.cpp:690).  The res_* fields are used only by this kind.
  */
 typedef struct came8_tensor {
   void* param;
@@ -109,7 +134,13 @@ typedef struct came8_tensor {
   int32_t param_dtype; /* CAME8_F32 / CAME8_BF16 / CAME8_F16 */
   int32_t grad_dtype;
   int32_t factored;    /* 1 for ndim >= 2, 0 for 1-D */
-  int32_t state_kind;  /* CAME8_STATE_Q8 (0) or CAME8_STATE_FP32 */
+  int32_t state_kind;  /* CAME8_STATE_Q8 (0), CAME8_STATE_FP32 or CAME8_STATE_8BIT2D */
+  uint8_t* res_row_q;  /* CAME8_STATE_8BIT2D only (NULL otherwise) */
+  float* res_row_absmax;
+  uint8_t* res_col_q;
+  float* res_col_absmax;
+  float* res_row_partial;  /* CAME8_STATE_8BIT2D only, optional (NULL: workspace) */
+  float* res_col_partial;
 } came8_tensor;
 
 /* Hyper-parameters of one param group (the reference's group keys, as Python floats). */

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     assert set(declared) == set(L.EXPORTED_SYMBOLS), declared
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.came8_abi_version() == 2
+    assert lib.came8_abi_version() == 3
     assert b"gfx950" in lib.came8_version()
 
 
@@ -243,3 +243,82 @@ def test_fp32_state_kind_checks():
     v.state_kind = L.CAME8_STATE_FP32
     v.exp_avg_absmax = v.row_absmax = None
     assert lib.came8_workspace_size((L.Came8Tensor * 1)(v), 1, 256, ctypes.byref(size)) == L.CAME8_OK
+
+
+# ---------------------------------------------------------------------------------- CAME8bit2D
+def _desc2d(shape, fake=0x100000):
+    d = _desc(shape, fake=fake)
+    d.state_kind = L.CAME8_STATE_8BIT2D
+    d.res_row_q, d.res_row_absmax = fake + 0x80000000, fake + 0x90000000
+    d.res_col_q, d.res_col_absmax = fake + 0xA0000000, fake + 0xB0000000
+    return d
+
+
+def test_8bit2d_state_kind_checks():
+    """came2d_step's rules (came_bindings.cpp:617-714): 2-D only, block_size 256, every state given."""
+    lib = L.load()
+    size = ctypes.c_size_t(0)
+    d = _desc2d((100, 300))
+    assert lib.came8_workspace_size((L.Came8Tensor * 1)(d), 1, 256, ctypes.byref(size)) == L.CAME8_OK
+    ws_own = size.value
+    assert lib.came8_workspace_size((L.Came8Tensor * 1)(d), 1, 128, ctypes.byref(size)) == L.CAME8_EINVAL
+    assert b"block_size=256" in lib.came8_last_error()
+    d.res_col_absmax = None
+    assert lib.came8_workspace_size((L.Came8Tensor * 1)(d), 1, 256, ctypes.byref(size)) == L.CAME8_EINVAL
+    assert b"residual" in lib.came8_last_error()
+    n = _desc2d((2, 3, 5, 7))
+    assert lib.came8_workspace_size((L.Came8Tensor * 1)(n), 1, 256, ctypes.byref(size)) == L.CAME8_EINVAL
+    v = _desc2d((33,))
+    assert lib.came8_workspace_size((L.Came8Tensor * 1)(v), 1, 256, ctypes.byref(size)) == L.CAME8_EINVAL
+    # the caller's tile partial buffers replace the workspace's copy: R*ceil(C/16) + C*ceil(R/16) floats
+    d = _desc2d((100, 300))
+    d.res_row_partial = 0x7000000000
+    assert lib.came8_workspace_size((L.Came8Tensor * 1)(d), 1, 256, ctypes.byref(size)) == L.CAME8_EINVAL
+    d.res_col_partial = 0x7100000000
+    assert lib.came8_workspace_size((L.Came8Tensor * 1)(d), 1, 256, ctypes.byref(size)) == L.CAME8_OK
+    assert ws_own - size.value >= 4 * (100 * 19 + 300 * 7)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(lr=0.0), "lr must be > 0"),
+    (dict(lr=1e-3, clip_threshold=0.0), "clip_threshold must be > 0"),
+    (dict(lr=1e-3, eps=(1e-30,)), "eps must be a tuple of length 2"),
+    (dict(lr=1e-3, betas=(0.9, 0.999)), "betas must be a tuple of length 3"),
+    (dict(lr=1e-3, block_size=128), "Only block_size=256 is supported"),
+])
+def test_came8bit2d_constructor_validation(kw, msg):
+    with pytest.raises(ValueError, match=msg):
+        came_amd.CAME8bit2D([torch.nn.Parameter(torch.zeros(4, 4))], **kw)
+
+
+def test_came8bit2d_group_keys_and_cpu_refusal():
+    p = torch.nn.Parameter(torch.zeros(4, 4))
+    opt = came_amd.CAME8bit2D([p], lr=1e-3, weight_decay=0.1, cuda_graph_compatible=True)
+    g = opt.param_groups[0]
+    assert {k: g[k] for k in ("lr", "eps", "clip_threshold", "betas", "weight_decay", "block_size")} == dict(
+        lr=1e-3, eps=(1e-30, 1e-16), clip_threshold=1.0, betas=(0.9, 0.999, 0.9999), weight_decay=0.1,
+        block_size=256)
+    assert opt.cuda_graph_compatible is True
+    p.grad = torch.zeros(4, 4)
+    with pytest.raises(NotImplementedError, match="requires CUDA parameters"):
+        opt.step()
+    with pytest.raises(RuntimeError, match="requires CUDA parameters"):
+        opt.prime_for_cuda_graph()
+
+
+def test_came8bit2d_state_layout_matches_oracle_init():
+    """init_8bit2d_state (the product) and the oracle's restatement of came8bit2d_state.py:33-75 agree on
+    every persistent key, dtype, shape and initial value; the reference's scratch keys are present."""
+    from came_amd.optim import init_8bit2d_state
+    for shape in [(37, 50), (1, 1), (16, 33), (4097, 129)]:
+        st = {}
+        init_8bit2d_state(st, torch.zeros(shape))
+        ref = orc.init_8bit2d_state(shape)
+        for k, v in ref.items():
+            if isinstance(v, torch.Tensor):
+                assert st[k].dtype == v.dtype and st[k].shape == v.shape and torch.equal(st[k], v), k
+            else:
+                assert st[k] == v, k
+        extra = set(st) - set(ref)
+        assert extra == set(orc.SCRATCH_8BIT2D_KEYS)
+        assert "step" not in st
