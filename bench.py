@@ -75,6 +75,10 @@ CONFIGS = {
            dict(lr=2e-4, weight_decay=1e-2)),
     "c1": ("2048x2048+2048/CAME8bit/fp32", lambda: [(2048, 2048), (2048,)], torch.float32, torch.float32, 1e-3,
            "CAME8bit", dict(lr=2e-4, weight_decay=1e-2)),
+    # the Llama-7B matrices stepped by CAME8bit2D (8bit2d layout: momentum in 16x16 tiles; 2-D only)
+    "c4_2d": ("llama7b-shape matrices/CAME8bit2D/bf16",
+              lambda: [s for s in llama_shapes(32, 4096, 11008, 32000) if len(s) == 2], torch.bfloat16,
+              torch.bfloat16, 2e-4, "CAME8bit2D", dict(lr=2e-4, weight_decay=1e-2, betas=(0.9, 0.999, 0.9999))),
     # the same Llama-7B set stepped by CAMECUDA (fp32 optimizer states)
     "c4fp": ("llama7b-shape/CAMECUDA/bf16", lambda: llama_shapes(32, 4096, 11008, 32000), torch.bfloat16,
              torch.bfloat16, 2e-4, "CAMECUDA", dict(lr=2e-4, weight_decay=1e-2, betas=(0.9, 0.999, 0.9999))),
@@ -85,11 +89,18 @@ def esize(dt):
     return torch.tensor([], dtype=dt).element_size()
 
 
-def compulsory_bytes(shapes, pdt, gdt, block=256, fp32_state=False):
+def compulsory_bytes(shapes, pdt, gdt, block=256, fp32_state=False, tiles=False):
+    """Bytes every step must move: gradient read, parameter and momentum codes read and written, momentum
+    scales (one per block of 256, or per 16x16 tile with `tiles`) read and written, row/column states."""
     sg, sp = esize(gdt), esize(pdt)
     tot = 0
     for s in shapes:
         n = math.prod(s)
+        if tiles:
+            r, c = s
+            tot += n * (sg + 2 * sp + 2) + 8 * math.ceil(r / 16) * math.ceil(c / 16) + 4 * (r + c) \
+                + 16 * (math.ceil(r / block) + math.ceil(c / block))
+            continue
         if fp32_state:  # fp32 momentum (and 1-D second moment) read and written; fp32 row/col states
             if len(s) >= 2:
                 pr, pc = math.prod(s[:-1]), math.prod(s[:-2]) * s[-1]
@@ -107,7 +118,7 @@ def compulsory_bytes(shapes, pdt, gdt, block=256, fp32_state=False):
 
 
 # --------------------------------------------------------------------------------- CPU baseline
-def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False):
+def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False, tiles=False):
     """Time the CPU oracle on a bounded sample of the workload; returns the cpu_baseline object."""
     from oracle import came8_oracle as orc
 
@@ -126,6 +137,9 @@ def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False):
         states = [orc.init_fp32_state(s) for s in sample]
         ohp.pop("block_size")
         step_fn = orc.fp32_state_step
+    elif tiles:
+        states = [orc.init_8bit2d_state(s) for s in sample]
+        step_fn = orc.came8bit2d_step
     else:
         states = [orc.init_full8bit_state(s) for s in sample]
         step_fn = orc.full8bit_step
@@ -136,7 +150,7 @@ def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False):
             step_fn(p, g, st, **ohp)
         times.append(time.perf_counter() - t0)
     t = sorted(times[1:])[0]  # first step allocates; best of the next two
-    nbytes = compulsory_bytes(sample, pdt, gdt, fp32_state=fp32_state)
+    nbytes = compulsory_bytes(sample, pdt, gdt, fp32_state=fp32_state, tiles=tiles)
     n_sample = sum(math.prod(s) for s in sample)
     n_total = sum(math.prod(s) for s in shapes)
     return {
@@ -228,7 +242,8 @@ def main():
 
     ms = (t1 - t0) * 1e3 / args.steps
     fp32_state = cls_name == "CAMECUDA"
-    nbytes = compulsory_bytes(shapes, pdt, gdt, fp32_state=fp32_state)
+    tiles = cls_name == "CAME8bit2D"
+    nbytes = compulsory_bytes(shapes, pdt, gdt, fp32_state=fp32_state, tiles=tiles)
     value = nbytes / (ms / 1e3) / 1e9
     dom = max(phases.items(), key=lambda kv: kv[1][1])
     dname, (dl, dms, dbytes) = dom
@@ -256,6 +271,7 @@ def main():
             "param_dtype": str(pdt).replace("torch.", ""),
             "grad_dtype": str(gdt).replace("torch.", ""),
             "state": "fp32 momentum + fp32 row/col factors" if fp32_state
+            else "int8 momentum in 16x16 tiles + uint8 row/col factors, block 256" if tiles
             else "int8 momentum + uint8 row/col factors, block 256",
             "compulsory_bytes_per_step": nbytes,
             "step_roofline_frac": round(value / HBM_PEAK_GBS, 4),
@@ -277,7 +293,8 @@ def main():
     }
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle on a sample", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(args.config, shapes, pdt, gdt, gstd, hp, fp32_state=fp32_state)
+        out["cpu_baseline"] = cpu_baseline(args.config, shapes, pdt, gdt, gstd, hp, fp32_state=fp32_state,
+                                           tiles=tiles)
     print(json.dumps(out), flush=True)
 
 

@@ -89,9 +89,11 @@ struct Plan {
   std::map<TypeKey, WorkList> generic;   // P3 / B for other block sizes (per quantisation block)
   std::map<int, WorkList> refnorm;       // parity-mode clip, by grad type
   WorkList factor;                       // F1b / F2b (per state block)
-  std::map<TypeKey, WorkList> tiles2d;   // 8bit2d momentum pass (per 16 rows x 256 columns)
-  WorkList res2d;                        // 8bit2d residual row states (per band)
-  std::map<int, WorkList> param2d;       // 8bit2d parameter write, by param type
+  std::map<int, WorkList> tiles2d_v;     // 8bit2d momentum pass, vector form (per tile row), by grad type
+  std::map<int, WorkList> tiles2d;       // 8bit2d momentum pass, scalar form (per 16 rows x 256 columns)
+  WorkList res2d;                        // 8bit2d residual row states after the scalar form (per tile row)
+  std::map<int, WorkList> param2d_v;     // 8bit2d parameter write, vector form, by param type
+  std::map<int, WorkList> param2d;       // 8bit2d parameter write, scalar form, by param type
   size_t plan_bytes = 0;
   size_t total_bytes = 0;
   std::vector<uint8_t> blob;
@@ -208,7 +210,12 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     d.factored = t.factored ? 1 : 0;
     d.fp32st = f32st ? 1 : 0;
     d.mode2d = s2d ? 1 : 0;
+    bool v2d = false, v2dp = false;  // vector forms of the 8bit2d momentum pass / parameter write
     if (s2d) {
+      const uintptr_t a16 = 15;
+      const bool c16 = t.cols % 16 == 0, mq16 = (reinterpret_cast<uintptr_t>(t.exp_avg_q) & a16) == 0;
+      v2d = c16 && mq16 && (reinterpret_cast<uintptr_t>(t.grad) & a16) == 0;
+      v2dp = c16 && mq16 && (reinterpret_cast<uintptr_t>(t.param) & a16) == 0;
       d.tr = int32_t(ceil_div(t.rows, 16));
       d.tc = int32_t(ceil_div(t.cols, 16));
       d.rrq = t.res_row_q;
@@ -255,15 +262,16 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       o.Rn = take(pr); o.rfac = take(pr); o.RRn = take(pr); o.rrfac = take(pr);
       o.Cn = take(pc); o.cfac = take(pc); o.CRn = take(pc); o.crfac = take(pc);
       o.pU = take(part); o.pW = take(part);
-      if (s2d) {  // tile residual sums per row [R*tc] and per column [C*tr], unless the caller's
+      if (s2d) {  // tile residual sums per column [tr][C] and (scalar pass) per row [R][tc], unless the caller's
         if (!t.res_row_partial) {
-          o.t2r = take(size_t(d.R) * size_t(d.tc) * 4);
+          if (!v2d) o.t2r = take(size_t(d.R) * size_t(d.tc) * 4);
           o.t2c = take(size_t(d.C) * size_t(d.tr) * 4);
         }
       } else {
         o.pR = take(part);
       }
-      o.rm = take(size_t(d.P * d.nbands) * 4); o.rmr = take(size_t(d.P * d.nbands) * 4);
+      o.rm = take(size_t(d.P * d.nbands) * 4);
+      o.rmr = take(size_t(d.P * (s2d ? std::max<int64_t>(d.nbands, d.tr) : d.nbands)) * 4);
       o.clipp = take(size_t(d.nclip) * 8);
       o.clip = take(8);
     } else {
@@ -283,8 +291,10 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       d.Cn = at(o.Cn); d.cfac = at(o.cfac); d.CRn = at(o.CRn); d.crfac = at(o.crfac);
       d.partU = at(o.pU); d.partW = at(o.pW);
       if (s2d) {
-        d.t2row = t.res_row_partial ? t.res_row_partial : at(o.t2r);
+        d.t2row = t.res_row_partial ? t.res_row_partial : (v2d ? nullptr : at(o.t2r));
         d.t2col = t.res_col_partial ? t.res_col_partial : at(o.t2c);
+        d.v2d = v2d ? 1 : 0;
+        d.v2dp = v2dp ? 1 : 0;
       } else {
         d.partRes = at(o.pR);
       }
@@ -305,9 +315,14 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       const BandShapeSel sel = band_variant(t, d.C, B);
       add_item(plan.band[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB}], i, d.nbands);
       add_item(plan.factor, i, d.nbr + d.nbc);
-      add_item(plan.tiles2d[tk], i, int64_t(d.tr) * ceil_div(d.C, 256));
-      add_item(plan.res2d, i, d.nbands);
-      add_item(plan.param2d[t.param_dtype], i, ceil_div(d.N, kTile));
+      if (d.v2d) {
+        add_item(plan.tiles2d_v[t.grad_dtype], i, d.tr);
+      } else {
+        add_item(plan.tiles2d[t.grad_dtype], i, int64_t(d.tr) * ceil_div(d.C, 256));
+        add_item(plan.res2d, i, d.tr);
+      }
+      if (d.v2dp) add_item(plan.param2d_v[t.param_dtype], i, ceil_div(d.N, kParam2Items));
+      else add_item(plan.param2d[t.param_dtype], i, ceil_div(d.N, kTile));
       continue;  // the clip of this layout has no parity-mode variant (the reference sums it with float atomics)
     }
     if (t.factored) {
@@ -338,7 +353,9 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
   };
   for (auto& kv : plan.band) place(kv.second);
   for (auto& kv : plan.band2) place(kv.second);
+  for (auto& kv : plan.tiles2d_v) place(kv.second);
   for (auto& kv : plan.tiles2d) place(kv.second);
+  for (auto& kv : plan.param2d_v) place(kv.second);
   for (auto& kv : plan.param2d) place(kv.second);
   place(plan.res2d);
   for (auto& kv : plan.upd) place(kv.second);
@@ -365,7 +382,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
         rebase(d.partU); rebase(d.partW);
         if (d.mode2d) {
           if (!ts[i].res_row_partial) {  // workspace offsets (caller buffers are absolute)
-            rebase(d.t2row);
+            if (!d.v2d) rebase(d.t2row);
             rebase(d.t2col);
           }
         } else {
@@ -384,7 +401,9 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     };
     for (auto& kv : plan.band) put(kv.second);
     for (auto& kv : plan.band2) put(kv.second);
+    for (auto& kv : plan.tiles2d_v) put(kv.second);
     for (auto& kv : plan.tiles2d) put(kv.second);
+    for (auto& kv : plan.param2d_v) put(kv.second);
     for (auto& kv : plan.param2d) put(kv.second);
     put(plan.res2d);
     for (auto& kv : plan.upd) put(kv.second);
@@ -614,15 +633,16 @@ double alg_bytes(const Plan& plan, const WorkList& wl, const came8_tensor* ts, i
       case PH_GENERIC:
         tot += d.factored ? N * (sg + 2.0 * sp + 2.0) + 8.0 * nbm : N * (sg + 2.0 * sp + 4.0) + 16.0 * nbm;
         break;
-      case PH_TILES2D:  // g, m rw, p rw (weight decay), tile scales rw, tile residual sums written
-        tot += N * (sg + 2.0 + (wd ? 2.0 * sp : 0.0)) + 8.0 * double(d.tr) * double(d.tc) +
-               4.0 * (double(d.R) * d.tc + double(d.C) * d.tr);
+      case PH_TILES2D:  // g, m rw, tile scales rw, column tile sums written (+ row tile sums, scalar form)
+        tot += N * (sg + 2.0) + 8.0 * double(d.tr) * double(d.tc) + 4.0 * double(d.C) * d.tr +
+               (d.v2d ? 0.0 : 4.0 * double(d.R) * d.tc);
         break;
-      case PH_RES2D:  // tile residual row sums, residual row codes and scales, new row states
+      case PH_RES2D:  // row tile sums, residual row codes and scales, new row states
         tot += 4.0 * double(d.R) * d.tc + double(d.R) + 4.0 * double(d.nbr) + 4.0 * double(d.R);
         break;
-      case PH_PARAM2D:  // m, tile scales, p rw
+      case PH_PARAM2D:  // m, tile scales, p rw (weight decay folded in)
         tot += N * (1.0 + 2.0 * sp) + 4.0 * double(d.tr) * double(d.tc);
+        (void)wd;
         break;
       case PH_FACTOR: case PH_FACTOR_RES:  // one row + one column state: codes rw, scales rw
         tot += 2.0 * double(d.P * d.R + d.P * d.C) + 8.0 * double(d.nbr + d.nbc);
@@ -748,7 +768,8 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       if ((rc = check_launch("clip_refnorm")) != CAME8_OK) return rc; }
     }
   }
-  if (!refnorm || !plan.tiles2d.empty()) {  // parity mode: only the 8bit2d tensors take this divisor
+  const bool any2d = !plan.tiles2d.empty() || !plan.tiles2d_v.empty();
+  if (!refnorm || any2d) {  // parity mode: only the 8bit2d tensors take this divisor
     PhaseTimer pt(PH_CLIP, 0.0, stream);
     hipLaunchKernelGGL(k_clip<>, dim3(grid_for(n_tensors)), blk, 0, stream, dT, int(n_tensors), int(refnorm), hp);
     if ((rc = check_launch("clip")) != CAME8_OK) return rc;
@@ -765,11 +786,19 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("pass2")) != CAME8_OK) return rc; }
     }
+    for (auto& kv : plan.tiles2d_v) {
+      const WorkList& wl = kv.second;
+      GenFn fn;
+      CAME8_TYPE_SWITCH1(k_2d_rows, kv.first, fn);
+      { PhaseTimer pt(PH_TILES2D, alg_bytes(plan, wl, tensors, PH_TILES2D), stream);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      if ((rc = check_launch("tiles2d")) != CAME8_OK) return rc; }
+    }
     for (auto& kv : plan.tiles2d) {
       const WorkList& wl = kv.second;
       GenFn fn;
-      CAME8_TYPE_SWITCH2(k_2d_tiles, kv.first.pdt, kv.first.gdt, fn);
-      { PhaseTimer pt(PH_TILES2D, alg_bytes(plan, wl, tensors, PH_TILES2D, h.weight_decay != 0.0), stream);
+      CAME8_TYPE_SWITCH1(k_2d_tiles, kv.first, fn);
+      { PhaseTimer pt(PH_TILES2D, alg_bytes(plan, wl, tensors, PH_TILES2D), stream);
       hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("tiles2d")) != CAME8_OK) return rc; }
     }
@@ -787,11 +816,19 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     if ((rc = check_launch("factor_blocks_res")) != CAME8_OK) return rc; }
   }
   // ---- P3 and 1-D pass B ----
+  for (auto& kv : plan.param2d_v) {
+    const WorkList& wl = kv.second;
+    GenFn fn;
+    CAME8_TYPE_SWITCH1(k_2d_param_v, kv.first, fn);
+    { PhaseTimer pt(PH_PARAM2D, alg_bytes(plan, wl, tensors, PH_PARAM2D, h.weight_decay != 0.0), stream);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+    if ((rc = check_launch("param2d")) != CAME8_OK) return rc; }
+  }
   for (auto& kv : plan.param2d) {
     const WorkList& wl = kv.second;
     GenFn fn;
     CAME8_TYPE_SWITCH1(k_2d_param, kv.first, fn);
-    { PhaseTimer pt(PH_PARAM2D, alg_bytes(plan, wl, tensors, PH_PARAM2D), stream);
+    { PhaseTimer pt(PH_PARAM2D, alg_bytes(plan, wl, tensors, PH_PARAM2D, h.weight_decay != 0.0), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
     if ((rc = check_launch("param2d")) != CAME8_OK) return rc; }
   }

@@ -77,8 +77,9 @@ struct DevTensor {
   int32_t fp32st;     // fp32 states (CAMECUDA layout): mq -> float m, rq/ra -> float second-moment /
                       // residual rows (rq -> float v for 1-D), cq/ca -> float columns; ma unused
   // 8bit2d layout (reference CAME8bit2D): ma holds one absmax per 16x16 tile of m; rq/ra, cq/ca are
-  // the second-moment row / column states and rrq/rra, rcq/rca the residual ones; t2row / t2col
-  // receive each tile's residual sums per row [R*tc] and per column [C*tr]
+  // the second-moment row / column states and rrq/rra, rcq/rca the residual ones; t2col receives
+  // each tile's residual sums per column [tr][C], t2row (scalar momentum pass only) per row [R][tc];
+  // rrsum then holds one sum of residual row states per tile row
   int32_t mode2d;
   int32_t tr, tc;     // tile rows, tile columns
   uint8_t* rrq;
@@ -87,6 +88,7 @@ struct DevTensor {
   float* rca;
   float* t2row;
   float* t2col;
+  int32_t v2d, v2dp;  // vector forms of the momentum pass / parameter write apply
 };
 
 // fp32-state views of the state pointers
@@ -749,10 +751,11 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
 
 // Mean row state of matrix b, max(mean, 1e-30): the per-band sums the band pass wrote, added in band
 // order (the reference: R.mean(dim=-1, keepdim=True).clamp_min(1e-30), CAME8bitFull.py:1021,1044).
-__device__ __forceinline__ float matrix_row_mean(const DevTensor& t, const float* __restrict__ bandsum, int64_t b) {
-  const float* __restrict__ src = bandsum + b * t.nbands;
+__device__ __forceinline__ float matrix_row_mean(const DevTensor& t, const float* __restrict__ bandsum, int64_t b,
+                                                 int64_t nb) {
+  const float* __restrict__ src = bandsum + b * nb;
   float s = 0.0f;
-  for (int64_t k = 0; k < t.nbands; ++k) s += src[k];
+  for (int64_t k = 0; k < nb; ++k) s += src[k];
   const float m = s / float(t.R);
   if (t.mode2d) return m > 0.0f ? m : 1.0f;  // 8bit2d: a mean that is not positive counts as 1
   return clamp_min_tiny(m);
@@ -797,13 +800,15 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
       const float* __restrict__ Rsrc = RES ? t.RRn : t.Rn;
       float* __restrict__ fac = RES ? t.rrfac : t.rfac;
       const float* __restrict__ bsum = RES ? t.rrsum : t.rsum;
+      // the 8bit2d momentum pass sums its residual row states per tile row
+      const int64_t nsum = (RES && t.mode2d) ? int64_t(t.tr) : t.nbands;
       int64_t mb = i0 / t.R;  // matrix of the block's first row; blocks may span matrices
-      float mean = matrix_row_mean(t, bsum, mb);
+      float mean = matrix_row_mean(t, bsum, mb, nsum);
       for (int64_t i = i0 + tid; i < i1; i += kThreads) {
         const int64_t bi = i / t.R;
         if (bi != mb) {
           mb = bi;
-          mean = matrix_row_mean(t, bsum, mb);
+          mean = matrix_row_mean(t, bsum, mb, nsum);
         }
         const float v = Rsrc[i];
         fac[i] = rsqrt_ref(v / mean);
@@ -828,7 +833,7 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
           // 8bit2d: residual column sums come from the tile partials (tiles in order); no clamp
           float s2 = 0.0f;
           if (RES) {
-            for (int64_t ty = 0; ty < t.tr; ++ty) s2 += t.t2col[i * t.tr + ty];
+            for (int64_t ty = 0; ty < t.tr; ++ty) s2 += t.t2col[ty * t.C + i];
           } else {
             s2 = float(band_column_sum(part + (b * t.nbands) * t.C + j, t.nbands, t.C));
           }
@@ -850,7 +855,7 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
           const double W = band_column_sum(pw, t.nbands, t.C);
           if (b != cmb) {
             cmb = b;
-            crm = matrix_row_mean(t, t.rsum, b);
+            crm = matrix_row_mean(t, t.rsum, b, t.nbands);
           }
           csum += double(crm) * double(c) * double(c) * W;
         }
@@ -1543,16 +1548,149 @@ __global__ __launch_bounds__(kThreads) void k_generic_update(const DevTensor* __
 // came_kernels.cu:2584-2684, 2685-2780, 3333-3367)
 // ===========================================================================
 constexpr int kTile2 = 16;
+constexpr int kParam2Items = 4096;  // elements per work item of the vector parameter write
 
-// Momentum pass.  Work item = (tensor, tile row ty, group of 256 columns); wave w owns columns
-// [256*cg + 64*w, +64) of the tile row's 16 rows, one column per lane, so a tile is 16 lanes of one
-// wave.  u = (g*r)*c / clip; m = m_old*b1 + u*(1-b1) (m_old = 0 in a tile whose absmax is 0);
-// res = (u - m)^2 + eps1; the tile's absmax and int8 codes; each tile's residual sums per row and
-// per column (16 terms in order); and p <- p * (1 - lr*wd) when wd != 0.
-template <typename TP, typename TG>
+// one element of the momentum pass: u = (g*r)*c / clip; m = m_old*b1 + u*(1-b1); res = (u - m)^2 + eps1
+__device__ __forceinline__ void m2d_elem(float gv, float ri, float cj, float clip, float mold, const Hp& hp, float& m,
+                                         float& res) {
+  const float u = ((gv * ri) * cj) / clip;
+  const float mn = (mold * hp.b1) + (u * hp.a1f);
+  const float d = u - mn;
+  m = mn;
+  res = (d * d) + hp.eps1;
+}
+
+// residual row state of one row from its sum over the tiles: RR_old*b3 + (1-b3)*(sum/C)
+__device__ __forceinline__ float rr2d_new(const DevTensor& t, int64_t row, float sum, const Hp& hp) {
+  const float old = deq_u8(t.rrq[row], t.rra[blk_of(row, hp)]);
+  return (old * hp.b3) + (hp.a3f * (sum / float(t.C)));
+}
+
+// Momentum pass, vector form (C a multiple of 16; gradient and codes 16-byte aligned).  Work item =
+// (tensor, tile row ty): rows [16*ty, +16) across all columns, 16 tiles at a time.  Lane l of wave w
+// holds row l%16 of tile 4*w + l/16 of the chunk: 16 consecutive elements, loaded as vectors.  Per
+// tile: the absmax of the new momentum (a max over the tile's 16 lanes, 0 -> 1) and its int8
+// codes; each tile row's residual sum (in-lane, columns in order) and each tile column's (rows in
+// order, through LDS, written to t2col[ty*C + col]).  The rows' tile sums are added in tile order
+// chunk by chunk; at the end of the item come the residual row states and their sum over the
+// item's rows (rrsum[ty]).  An inactive lane (a row or tile past the edge) carries zeros.
+template <typename TG>
+__global__ __launch_bounds__(kThreads) void k_2d_rows(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                      const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using GS = typename TG::storage;
+  __shared__ float xres[4][kWave][kTile2 + 1];  // per wave: 4 tiles x 16 rows x 16 residuals (+1: banks)
+  __shared__ float rpart[kTile2][kTile2];       // [row][tile of the chunk]: each tile row's residual sum
+  __shared__ float racc[kTile2];                // running row sums, tiles in order
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int i = lane & (kTile2 - 1), s = lane >> 4;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t R = t.R, C = t.C, tc = t.tc;
+    const int64_t ty = w - wstart[slot];
+    const int64_t r0 = ty * kTile2;
+    const int nrows = int((R - r0) < kTile2 ? (R - r0) : kTile2);
+    const bool rvalid = i < nrows;
+    const int64_t row = r0 + (rvalid ? i : 0);
+    const CAME8_GLOBAL GS* __restrict__ grow = gbl(static_cast<const GS*>(t.g) + row * C);
+    CAME8_GLOBAL int8_t* __restrict__ qrow = gbl(t.mq + row * C);
+    const CAME8_GLOBAL float* __restrict__ cf = gbl(static_cast<const float*>(t.cfac));
+    CAME8_GLOBAL float* __restrict__ ma = gbl(t.ma + ty * tc);
+    const float clip = uniform_f32(t.clip[0]);
+    const float ri = t.rfac[row];
+    if (tid < kTile2) racc[tid] = 0.0f;
+    for (int64_t tx0 = 0; tx0 < tc; tx0 += kTile2) {
+      const int64_t tx = tx0 + wid * 4 + s;
+      const bool tvalid = tx < tc;
+      const bool act = tvalid && rvalid;
+      const int64_t c0 = tx * kTile2;
+      float m[kTile2], res[kTile2];
+      uint32_t abits = 0;
+      float rsum = 0.0f;
+      if (act) {
+        Raw8<TG> ga, gb;
+        ga.load(grow + c0);
+        gb.load(grow + c0 + 8);
+        const u32x4 q = *(const CAME8_GLOBAL u32x4*)(qrow + c0);
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+        const float am_old = ma[tx];
+        const float sc_old = am_old / kSignedQ;
+        const bool have_m = am_old > 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const f32x4 c4 = *(const CAME8_GLOBAL f32x4*)(cf + c0 + 4 * k);
+          const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int j = 4 * k + v;
+            const float gv = j < 8 ? ga[j] : gb[j - 8];
+            const float mold = have_m ? code_elem(qw, j) * sc_old : 0.0f;
+            m2d_elem(gv, ri, cv[v], clip, mold, hp, m[j], res[j]);
+            abits = max(abits, abs_bits(m[j]));
+            rsum += res[j];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kTile2; ++j) m[j] = res[j] = 0.0f;
+      }
+      abits = group_max_bits<kTile2>(abits);  // the tile's 16 rows are 16 consecutive lanes
+      if (act) {
+        const float amax = fix_absmax(__uint_as_float(abits));
+        const float inv = 1.0f / amax;
+        uint32_t ow[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          uint32_t wv = 0;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) wv |= uint32_t(uint8_t(quant_s8_inv(m[4 * k + v], inv))) << (8 * v);
+          ow[k] = wv;
+        }
+        *(CAME8_GLOBAL u32x4*)(qrow + c0) = u32x4{ow[0], ow[1], ow[2], ow[3]};
+        if (i == 0) ma[tx] = amax;
+      }
+#pragma unroll
+      for (int j = 0; j < kTile2; ++j) xres[wid][lane][j] = res[j];
+      rpart[i][wid * 4 + s] = rsum;
+      __syncthreads();
+      if (tvalid) {  // lane (s, i): column i of its tile, the 16 rows in order
+        float cs = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kTile2; ++k) cs += xres[wid][s * kTile2 + k][i];
+        t.t2col[ty * C + c0 + i] = cs;
+      }
+      if (tid < nrows) {
+        float a = racc[tid];
+        const int64_t nt = (tc - tx0) < kTile2 ? (tc - tx0) : kTile2;
+        for (int64_t k = 0; k < nt; ++k) a += rpart[tid][k];
+        racc[tid] = a;
+      }
+      __syncthreads();
+    }
+    if (tid < nrows) {
+      const float v = rr2d_new(t, r0 + tid, racc[tid], hp);
+      t.RRn[r0 + tid] = v;
+      racc[tid] = v;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      float sum = 0.0f;
+      for (int k = 0; k < nrows; ++k) sum += racc[k];
+      t.rrsum[ty] = sum;
+    }
+    __syncthreads();  // racc / LDS reused by the next item
+  }
+}
+
+// Momentum pass, scalar form (any C and alignment).  Work item = (tensor, tile row ty, group of 256
+// columns); wave w owns columns [256*cg + 64*w, +64) of the tile row's 16 rows, one column per lane,
+// so a tile is 16 lanes of one wave.  The same per-element arithmetic and tile codes as the vector
+// form; each tile's residual sums per column go to t2col[ty*C + col] and per row to
+// t2row[row*tc + tx], which k_2d_res_rows then adds in tile order.
+template <typename TG>
 __global__ __launch_bounds__(kThreads) void k_2d_tiles(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                        const int64_t* __restrict__ wstart, int ntens, Hp hp) {
-  using PS = typename TP::storage;
   using GS = typename TG::storage;
   __shared__ float lres[4][kTile2][kWave + 1];  // +1: rows of a tile fall in different banks
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -1569,7 +1707,6 @@ __global__ __launch_bounds__(kThreads) void k_2d_tiles(const DevTensor* __restri
     const int64_t col = cg * 256 + int64_t(wid) * kWave + lane;
     const bool cvalid = col < C;
     const int64_t tile = ty * t.tc + (col >> 4);
-    CAME8_GLOBAL PS* __restrict__ p = gbl(static_cast<PS*>(t.p));
     const CAME8_GLOBAL GS* __restrict__ g = gbl(static_cast<const GS*>(t.g));
     CAME8_GLOBAL int8_t* __restrict__ mq = gbl(t.mq);
     const float clip = uniform_f32(t.clip[0]);
@@ -1584,14 +1721,8 @@ __global__ __launch_bounds__(kThreads) void k_2d_tiles(const DevTensor* __restri
       res[i] = 0.0f;
       if (i < nrows && cvalid) {
         const int64_t e = (r0 + i) * C + col;
-        const float ri = t.rfac[r0 + i];
-        const float u = ((TG::load(g[e]) * ri) * cj) / clip;
-        const float mo = am_old > 0.0f ? float(mq[e]) * sc_old : 0.0f;
-        const float mn = (mo * hp.b1) + (u * hp.a1f);
-        const float d = u - mn;
-        m[i] = mn;
-        res[i] = (d * d) + hp.eps1;
-        if (hp.wd) p[e] = TP::store(TP::load(p[e]) * hp.wdfac);
+        const float mold = am_old > 0.0f ? float(mq[e]) * sc_old : 0.0f;
+        m2d_elem(TG::load(g[e]), t.rfac[r0 + i], cj, clip, mold, hp, m[i], res[i]);
       }
       abits = max(abits, abs_bits(m[i]));
     }
@@ -1606,7 +1737,7 @@ __global__ __launch_bounds__(kThreads) void k_2d_tiles(const DevTensor* __restri
         if (i < nrows) mq[(r0 + i) * C + col] = quant_s8_inv(m[i], inv);
         csum += res[i];
       }
-      t.t2col[col * t.tr + ty] = csum;
+      t.t2col[ty * C + col] = csum;
     }
     // per-row sums of each tile: the 16 columns in order, through LDS
 #pragma unroll
@@ -1624,42 +1755,84 @@ __global__ __launch_bounds__(kThreads) void k_2d_tiles(const DevTensor* __restri
   }
 }
 
-// Residual row states of the 8bit2d layout.  Work item = (tensor, band of rb rows): each row's sum
-// over its tiles in order, mean, new state RR = RR_old*b3 + (1-b3)*mean; the band's states summed
-// in row order for the mean row state.
+// Residual row states after the scalar momentum pass.  Work item = (tensor, tile row ty): each of its
+// rows' sum over the tiles in order, the new state, and the states' sum over the rows (rrsum[ty]).
 template <int = 0>  // a template only so that every translation unit may include this header
 __global__ __launch_bounds__(kThreads) void k_2d_res_rows(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                           const int64_t* __restrict__ wstart, int ntens, Hp hp) {
-  __shared__ float rowval[kMaxBandRows];
+  __shared__ float rowval[kTile2];
   const int tid = threadIdx.x;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
     const int slot = find_slot(wstart, ntens, w);
     const DevTensor& t = T[tids[slot]];
-    const int64_t band = w - wstart[slot];
-    const int64_t r0 = band * t.rb;
-    const int64_t r1 = (r0 + t.rb < t.R) ? (r0 + t.rb) : t.R;
-    for (int64_t i = tid; i < r1 - r0; i += kThreads) {
-      const int64_t row = r0 + i;
+    const int64_t ty = w - wstart[slot];
+    const int64_t r0 = ty * kTile2;
+    const int nrows = int((t.R - r0) < kTile2 ? (t.R - r0) : kTile2);
+    if (tid < nrows) {
+      const int64_t row = r0 + tid;
       float s = 0.0f;
       for (int64_t tx = 0; tx < t.tc; ++tx) s += t.t2row[row * t.tc + tx];
-      const float old = deq_u8(t.rrq[row], t.rra[blk_of(row, hp)]);
-      const float v = (old * hp.b3) + (hp.a3f * (s / float(t.C)));
+      const float v = rr2d_new(t, row, s, hp);
       t.RRn[row] = v;
-      rowval[i] = v;
+      rowval[tid] = v;
     }
     __syncthreads();
     if (tid == 0) {
       float s = 0.0f;
-      for (int64_t i = 0; i < r1 - r0; ++i) s += rowval[i];
-      t.rrsum[band] = s;
+      for (int k = 0; k < nrows; ++k) s += rowval[k];
+      t.rrsum[ty] = s;
     }
     __syncthreads();
   }
 }
 
-// Parameter write of the 8bit2d layout from the requantised momentum: p <- p - lr*((m_q*rr)*cr),
-// one fused multiply-add; 2048 elements per work item.
+// parameter write of one element: p <- round(p * (1 - lr*wd)) when wd != 0 (the reference does this
+// in its momentum pass; nothing reads p in between), then p <- round(p - lr*((m_q*rr)*cr)), one
+// fused multiply-add, m_q = code * (tile absmax / 127)
+template <typename TP>
+__device__ __forceinline__ float p2d_new(float pv, float code, float sc, float rr, float cr, const Hp& hp) {
+  if (hp.wd) pv = TP::load(TP::store(pv * hp.wdfac));
+  const float step = ((code * sc) * rr) * cr;
+  return fmaf(step, hp.alr, pv);
+}
+
+// Parameter write, vector form (C a multiple of 16; parameter and codes 16-byte aligned): a thread
+// takes one tile row of 16 elements, 4096 elements per work item.
+template <typename TP>
+__global__ __launch_bounds__(kThreads) void k_2d_param_v(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                         const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using PS = typename TP::storage;
+  const int tid = threadIdx.x;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t e0 = (w - wstart[slot]) * kParam2Items + int64_t(tid) * kTile2;
+    if (e0 >= t.N) continue;
+    const int64_t row = t.idx32 ? int64_t(udiv_magic(uint32_t(e0), t.mC, t.sC)) : e0 / t.C;
+    const int64_t c0 = e0 - row * t.C;
+    CAME8_GLOBAL PS* __restrict__ p = gbl(static_cast<PS*>(t.p) + e0);
+    const u32x4 q = *(const CAME8_GLOBAL u32x4*)gbl(t.mq + e0);
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+    const float sc = t.ma[(row >> 4) * t.tc + (c0 >> 4)] / kSignedQ;
+    const float rr = t.rrfac[row];
+    const CAME8_GLOBAL float* __restrict__ crp = gbl(static_cast<const float*>(t.crfac) + c0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float pv[8];
+      load8<TP>(p + 8 * h, pv);
+      const f32x4 ca = *(const CAME8_GLOBAL f32x4*)(crp + 8 * h);
+      const f32x4 cb = *(const CAME8_GLOBAL f32x4*)(crp + 8 * h + 4);
+      const float cr[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
+#pragma unroll
+      for (int v = 0; v < 8; ++v) pv[v] = p2d_new<TP>(pv[v], code_elem(qw, 8 * h + v), sc, rr, cr[v], hp);
+      store8<TP>(p + 8 * h, pv);
+    }
+  }
+}
+
+// Parameter write, scalar form (any C and alignment): 8 consecutive elements per thread, 2048 per item.
 template <typename TP>
 __global__ __launch_bounds__(kThreads) void k_2d_param(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                        const int64_t* __restrict__ wstart, int ntens, Hp hp) {
@@ -1677,10 +1850,8 @@ __global__ __launch_bounds__(kThreads) void k_2d_param(const DevTensor* __restri
       if (e < t.N) {
         const int64_t row = t.idx32 ? int64_t(udiv_magic(uint32_t(e), t.mC, t.sC)) : e / t.C;
         const int64_t col = e - row * t.C;
-        const float am = t.ma[(row >> 4) * t.tc + (col >> 4)];
-        const float mqv = float(t.mq[e]) * (am / kSignedQ);
-        const float step = (mqv * t.rrfac[row]) * t.crfac[col];
-        p[e] = TP::store(fmaf(step, hp.alr, TP::load(p[e])));
+        const float sc = t.ma[(row >> 4) * t.tc + (col >> 4)] / kSignedQ;
+        p[e] = TP::store(p2d_new<TP>(TP::load(p[e]), float(t.mq[e]), sc, t.rrfac[row], t.crfac[col], hp));
       }
     }
   }

@@ -33,7 +33,7 @@ TIE_TOL = 1e-3
 EXACT_TIE = 1e-4
 CODE_FRAC = 2e-2
 SHAPES = [(64, 2048), (1000, 3), (3, 5000), (33, 5461), (130, 1024), (17, 17), (1, 1), (16, 16), (257, 129),
-          (4097, 129), (48, 4100)]
+          (4097, 129), (48, 4100), (37, 400), (5, 48)]
 
 
 def _ohp(hp):
@@ -217,3 +217,52 @@ def test_8bit2d_errors_match_reference():
     opt.state[p3]["res_row_partial"] = torch.zeros(3, device="cuda")  # too small for 8 rows x 1 tile column
     with pytest.raises(RuntimeError, match="res_row_partial is too small"):
         opt.step()
+
+
+def _misaligned(t: torch.Tensor) -> torch.Tensor:
+    """A contiguous copy of `t` that starts one element past a 16-byte boundary."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    v = buf[1:].view(t.shape)
+    v.copy_(t)
+    return v
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_8bit2d_vector_and_scalar_forms_agree_bitwise(dtype):
+    """Rows that are a whole number of tiles (C % 16 == 0) with 16-byte aligned buffers take the vector
+    momentum pass and parameter write; a parameter one element off a 16-byte boundary takes the scalar
+    parameter write, and momentum codes 8 bytes off one take the scalar momentum pass too (pass 1,
+    which needs only 8-byte aligned codes, stays the same).  Both forms run the same arithmetic in
+    the same order, so three steps must agree bit for bit."""
+    dt = getattr(torch, dtype)
+    shapes = [(64, 2048), (37, 400), (5, 48), (130, 1024)]
+    refs = P.make_params(shapes, dt, seed=81)
+    gen = torch.Generator().manual_seed(82)
+    grads = [[P.heavy_grad(gen, s, dt) for s in shapes] for _ in range(3)]
+    runs = {}
+    for mode in ("aligned", "param_off", "codes_off"):
+        ps = []
+        for r in refs:
+            d = r.clone().cuda()
+            ps.append(torch.nn.Parameter(_misaligned(d) if mode == "param_off" else d))
+        opt = came_amd.CAME8bit2D(ps, lr=1e-3, weight_decay=1e-2)
+        for p, g in zip(ps, grads[0]):
+            p.grad = g.cuda()
+        opt.prime_for_cuda_graph()  # creates the states
+        if mode == "codes_off":
+            for p in ps:
+                q = opt.state[p]["exp_avg_q"]
+                buf = torch.zeros(q.numel() + 8, dtype=torch.int8, device="cuda")
+                opt.state[p]["exp_avg_q"] = buf[8:].view(q.shape)
+                assert opt.state[p]["exp_avg_q"].data_ptr() % 16 == 8
+        for step in range(3):
+            for p, g in zip(ps, grads[step]):
+                p.grad = g.cuda()
+            opt.step()
+        torch.cuda.synchronize()
+        runs[mode] = [(p.data.cpu(), {k: opt.state[p][k].cpu() for k in PERSIST}) for p in ps]
+    for mode in ("param_off", "codes_off"):
+        for i, ((pa, sa), (pb, sb)) in enumerate(zip(runs["aligned"], runs[mode])):
+            assert torch.equal(pa, pb), f"{mode} tensor {i}: parameters differ"
+            for k in PERSIST:
+                assert torch.equal(sa[k], sb[k]), f"{mode} tensor {i}: {k} differs"
