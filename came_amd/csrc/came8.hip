@@ -61,9 +61,9 @@ float round_to_f16(float f) { return float(_Float16(f)); }
 
 // Kernel-variant keys.
 struct BandKey {
-  int gdt, V, K, TPB;
+  int gdt, V, K, TPB, st = 0;  // st: fp32 states (pass 2 only)
   bool operator<(const BandKey& o) const {
-    return std::tie(gdt, V, K, TPB) < std::tie(o.gdt, o.V, o.K, o.TPB);
+    return std::tie(gdt, V, K, TPB, st) < std::tie(o.gdt, o.V, o.K, o.TPB, o.st);
   }
 };
 struct TypeKey {
@@ -327,9 +327,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     }
     if (t.factored) {
       const BandShapeSel sel = band_variant(t, d.C, B);
-      const BandKey bk{t.grad_dtype, sel.V, sel.K, sel.TPB};
-      add_item(plan.band[bk], i, d.P * d.nbands);
-      add_item(plan.band2[bk], i, d.P * d.nbands);
+      add_item(plan.band[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB}], i, d.P * d.nbands);
+      add_item(plan.band2[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB, d.fp32st}], i, d.P * d.nbands);
       add_item(plan.factor, i, d.nbr + d.nbc);
       if (fastB) {
         if (d.p3_nbands > 0) add_item(plan.updb[tk], i, d.P * d.p3_nbands * d.p3_nseg);
@@ -485,11 +484,11 @@ Hp make_hp(const came8_hparams& h) {
 // kernel-variant dispatch
 // ---------------------------------------------------------------------------
 // band-pass kernels are instantiated in came8_band.hip (one translation unit per family)
-BandFn band_fn(int gdt, bool pass2, int V, int K, int TPB) {
+BandFn band_fn(int gdt, bool pass2, int V, int K, int TPB, int st) {
   switch (gdt) {
-    case CAME8_F32: return pass2 ? band_fn_F32_p2(V, K, TPB) : band_fn_F32_p1(V, K, TPB);
-    case CAME8_BF16: return pass2 ? band_fn_BF16_p2(V, K, TPB) : band_fn_BF16_p1(V, K, TPB);
-    case CAME8_F16: return pass2 ? band_fn_F16_p2(V, K, TPB) : band_fn_F16_p1(V, K, TPB);
+    case CAME8_F32: return pass2 ? band_fn_F32_p2(V, K, TPB, st) : band_fn_F32_p1(V, K, TPB, st);
+    case CAME8_BF16: return pass2 ? band_fn_BF16_p2(V, K, TPB, st) : band_fn_BF16_p1(V, K, TPB, st);
+    case CAME8_F16: return pass2 ? band_fn_F16_p2(V, K, TPB, st) : band_fn_F16_p1(V, K, TPB, st);
     default: return nullptr;
   }
 }
@@ -735,7 +734,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     const BandKey& k = kv.first;
     const WorkList& wl = kv.second;
     BandFn fn = nullptr;
-    fn = band_fn(k.gdt, false, k.V, k.K, k.TPB);
+    fn = band_fn(k.gdt, false, k.V, k.K, k.TPB, 0);
     if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
     { PhaseTimer pt(PH_PASS1, alg_bytes(plan, wl, tensors, PH_PASS1), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
@@ -780,7 +779,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       const BandKey& k = kv.first;
       const WorkList& wl = kv.second;
       BandFn fn = nullptr;
-      fn = band_fn(k.gdt, true, k.V, k.K, k.TPB);
+      fn = band_fn(k.gdt, true, k.V, k.K, k.TPB, k.st);
       if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
       { PhaseTimer pt(PH_PASS2, alg_bytes(plan, wl, tensors, PH_PASS2), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);

@@ -16,31 +16,31 @@ using TG = CAME8_BAND_TYPE;
 constexpr int kVW = 16 / int(sizeof(TG::storage));  // elements per 16-byte chunk
 
 template <int V, int K, int TPB>
-BandFn pick() {
-  if constexpr (CAME8_BAND_PASS == 2) return k_fact_pass2<TG, V, K, TPB>;
-  else return k_fact_pass1<TG, V, K, TPB>;
+BandFn pick(int st) {
+  if constexpr (CAME8_BAND_PASS == 2) return st ? k_fact_pass2<TG, V, K, TPB, true> : k_fact_pass2<TG, V, K, TPB, false>;
+  else return (void)st, k_fact_pass1<TG, V, K, TPB>;
 }
 }  // namespace
 
-// the (V, K, TPB) variants the host's band_variant() can choose
-BandFn CAME8_BAND_SELECTOR(CAME8_BAND_TYPE, CAME8_BAND_PASS)(int V, int K, int TPB) {
+// the (V, K, TPB) variants the host's band_variant() can choose; st selects fp32 states (pass 2)
+BandFn CAME8_BAND_SELECTOR(CAME8_BAND_TYPE, CAME8_BAND_PASS)(int V, int K, int TPB, int st) {
   if (V == 1 && TPB == 256) {
     switch (K) {
-      case 1: return pick<1, 1, 256>();
-      case 2: return pick<1, 2, 256>();
-      case 4: return pick<1, 4, 256>();
-      case 8: return pick<1, 8, 256>();
-      case 16: return pick<1, 16, 256>();
-      case 32: return pick<1, 32, 256>();
+      case 1: return pick<1, 1, 256>(st);
+      case 2: return pick<1, 2, 256>(st);
+      case 4: return pick<1, 4, 256>(st);
+      case 8: return pick<1, 8, 256>(st);
+      case 16: return pick<1, 16, 256>(st);
+      case 32: return pick<1, 32, 256>(st);
       default: return nullptr;
     }
   }
   if (V == kVW) {
-    if (TPB == 256 && K == 1) return pick<kVW, 1, 256>();
-    if (TPB == 256 && K == 2) return pick<kVW, 2, 256>();
-    if (TPB == 512 && K == 2) return pick<kVW, 2, 512>();
-    if (TPB == 512 && K == 3) return pick<kVW, 3, 512>();
-    if (TPB == 512 && K == 4) return pick<kVW, 4, 512>();
+    if (TPB == 256 && K == 1) return pick<kVW, 1, 256>(st);
+    if (TPB == 256 && K == 2) return pick<kVW, 2, 256>(st);
+    if (TPB == 512 && K == 2) return pick<kVW, 2, 512>(st);
+    if (TPB == 512 && K == 3) return pick<kVW, 3, 512>(st);
+    if (TPB == 512 && K == 4) return pick<kVW, 4, 512>(st);
   }
   return nullptr;
 }

@@ -175,6 +175,12 @@ __device__ __forceinline__ uint32_t group_max_bits_rt(uint32_t v, int L) {
   }
 }
 
+// s_waitcnt vmcnt(0) alone (gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15).  vmcnt counts stores as
+// well as loads; while stores are outstanding the compiler cannot tell which load has returned and
+// waits for every one at the first use.  Waiting for the stores once, before a prefetching loop
+// that issues only loads, lets it wait for exactly one stage inside the loop.
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // a value every lane holds alike, moved to a scalar register (lets branches on it be scalar)
 __device__ __forceinline__ float uniform_f32(float v) { return __uint_as_float(readlane_u32(__float_as_uint(v), 0)); }
 

@@ -117,6 +117,11 @@ struct Hp {
 __device__ __forceinline__ int64_t blk_of(int64_t e, const Hp& hp) {
   return hp.log2B >= 0 ? (e >> hp.log2B) : int64_t(udiv_magic(uint32_t(e), hp.mB, hp.sB));
 }
+// the same without a branch: (e * mB) >> sB is e >> log2(B) for a power of two (mB = 1) and the
+// magic division otherwise (e < 2^31 then, so the product stays below 2^64)
+__device__ __forceinline__ int64_t blk_of_nb(int64_t e, const Hp& hp) {
+  return int64_t((uint64_t(e) * hp.mB) >> hp.sB);
+}
 
 // wstart has n+1 entries, wstart[0] = 0; returns k with wstart[k] <= w < wstart[k+1]
 __device__ __forceinline__ int find_slot(const int64_t* __restrict__ wstart, int n, int64_t w) {
@@ -233,25 +238,28 @@ struct Stage {
   static constexpr int S = (64 / bytes) < 1 ? 1 : ((64 / bytes) > 16 ? 16 : (64 / bytes));
 };
 
-// Column accumulators: fp64 when a thread owns few columns (short rows, so a band spans many rows),
-// fp32 otherwise (a band is at most 256 rows).
+// Row and column accumulators of the band passes: fp64.  A row or column of heavy-tailed gradients
+// can hold one element that outweighs the rest by ten orders of magnitude; fp32 partial sums then
+// keep only what the dominant term's last few ulps allow, in an order-dependent way, while fp64
+// sums are exact for every practical purpose (fp64 fused multiply-adds issue at the fp32 rate on
+// CDNA4).  A band's column partials are rounded to fp32 once when stored.
 template <int V, int K>
-using ColAcc = typename std::conditional<(V * K <= 8), double, float>::type;
+using ColAcc = double;
 
 // Sum S per-thread row partials over the workgroup (NW wavefronts) in a fixed order;
 // red is a [2][16][NW] LDS buffer whose half alternates between calls.
 template <int S, int NW>
-__device__ __forceinline__ void block_row_sums(const float (&ps)[S], float (*red)[16][NW], int par, float (&tot)[S]) {
+__device__ __forceinline__ void block_row_sums(const double (&ps)[S], double (*red)[16][NW], int par, double (&tot)[S]) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    const float w = wave_sum(ps[s]);
+    const double w = wave_sum(ps[s]);
     if (lane == 0) red[par][s][wid] = w;
   }
   __syncthreads();
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    float t = red[par][s][0];
+    double t = red[par][s][0];
 #pragma unroll
     for (int w = 1; w < NW; ++w) t += red[par][s][w];
     tot[s] = t;
@@ -277,17 +285,35 @@ __device__ __forceinline__ BandItem band_item(const DevTensor* __restrict__ T, c
   return it;
 }
 
+// a + x*y in the accumulator's type (one fused multiply-add)
+template <typename Acc>
+__device__ __forceinline__ Acc acc_fma(Acc a, float x, float y) {
+  if constexpr (std::is_same<Acc, double>::value) return fma(double(x), double(y), a);
+  else return fmaf(x, y, a);
+}
+// a + x*x*w, the product formed in the accumulator's type
+template <typename Acc>
+__device__ __forceinline__ Acc acc_fma_w(Acc a, float x, float w) {
+  if constexpr (std::is_same<Acc, double>::value) return fma(double(x) * double(w), double(x), a);
+  else return fmaf(x * w, x, a);
+}
+
 // ---------------- P1 ----------------
+// Row sums of g^2 (whole rows per workgroup, so the new row state R_i is known locally) and, per
+// band, the column partial sums of g^2 + eps0 and of g^2/R_i.  These sums feed the factors, which
+// are held to a relative tolerance rather than a bit pattern: each element costs one fused
+// multiply-add per sum, and eps0 is added once per summed element count instead of per element.
 template <typename TG, int V, int K, int TPB>
-__global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(TPB == 256 ? 5 : 3))) void k_fact_pass1(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+__global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                     const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using GS = typename TG::storage;
   using Acc = ColAcc<V, K>;
   constexpr int NW = TPB / kWave;
   constexpr int S = Stage<TG, V, K>::S;
   constexpr int64_t segw = int64_t(TPB) * V * K;
-  __shared__ float red[2][16][NW];
+  __shared__ double red[2][16][NW];
   __shared__ float rowR[kMaxBandRows];
+  __shared__ float rowold[kMaxBandRows];  // the band's old row states
   const int tid = threadIdx.x;
   int par = 0;
   const int64_t total = wstart[ntens];
@@ -304,95 +330,113 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(TPB == 256 
     CAME8_GLOBAL float* __restrict__ pU = gbl(t.partU + (b * t.nbands + it.band) * C);
     CAME8_GLOBAL float* __restrict__ pW = gbl(t.partW + (b * t.nbands + it.band) * C);
     float bandR = 0.0f;  // sum of this band's new row states, in row order (every thread alike)
+    const float band_eps = float(r1 - r0) * hp.eps0;  // eps0 of each element of a column partial
+    // new row state from the row's sum of g^2 (eps0 added once per element count)
+    // the old row states go through LDS: a per-row global load inside the stage loop would wait for
+    // the next stage's loads as well
+    for (int64_t rr = tid; rr < r1 - r0; rr += TPB) {
+      const int64_t row = b * R + r0 + rr;
+      rowold[rr] = t.fp32st ? st_sq_row(t)[row] : deq_u8(rq[row], ra[blk_of(row, hp)]);
+    }
+    __syncthreads();
+    auto row_state = [&](int64_t row, double sum_g2) {
+      const float tot = float(sum_g2 + double(C) * double(hp.eps0));
+      const float Rold = rowold[row - b * R - r0];
+      return t.mode2d ? (Rold * hp.b2) + (hp.a2f * (tot / fC)) : fmaf(tot / fC, hp.a2, Rold * hp.b2);
+    };
 
     if (nseg == 1) {
+      // The stage loop issues only loads (the new row states stay in LDS until after it) and issues
+      // them unconditionally, so that the compiler waits for exactly one stage while the next is in
+      // flight: a chunk past the row end (cok false) loads the row's first chunk and is skipped, a
+      // row past the band end loads the band's last row and is ignored.
       Acc colU[K][V], colW[K][V];
 #pragma unroll
       for (int k = 0; k < K; ++k)
 #pragma unroll
         for (int v = 0; v < V; ++v) colU[k][v] = colW[k][v] = Acc(0);
       Chunk<TG, V> A[S][K], Bf[S][K];
-      int32_t coff[K];  // this thread's column offsets; coff[k] < C when chunk k exists
+      int32_t coff[K];
+      bool cok[K];
 #pragma unroll
-      for (int k = 0; k < K; ++k) coff[k] = (tid + k * TPB) * V;
-      auto load_stage = [&](Chunk<TG, V> (&buf)[S][K], int64_t r) {
+      for (int k = 0; k < K; ++k) {
+        const int32_t c = (tid + k * TPB) * V;
+        cok[k] = c < C;  // V > 1: C % V == 0, so a chunk that starts inside the row ends inside it
+        coff[k] = cok[k] ? c : 0;
+      }
+      auto load_stage = [&](Chunk<TG, V> (&buf)[S][K], int64_t r) __attribute__((always_inline)) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-          if (r + s < r1) {
-            const CAME8_GLOBAL GS* __restrict__ grow = g + (r + s) * C;
+          const int64_t rs = (r + s < r1) ? (r + s) : (r1 - 1);
+          const CAME8_GLOBAL GS* __restrict__ grow = g + rs * C;
 #pragma unroll
-            for (int k = 0; k < K; ++k)
-              if (coff[k] < C) buf[s][k].load(grow + coff[k]);
-          }
+          for (int k = 0; k < K; ++k) buf[s][k].load(grow + coff[k]);
         }
       };
-      auto process = [&](const Chunk<TG, V> (&buf)[S][K], int64_t r) {
-        float ps[S];
+      auto process = [&](const Chunk<TG, V> (&buf)[S][K], int64_t r) __attribute__((always_inline)) {
+        double ps[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           ps[s] = 0.0f;
 #pragma unroll
           for (int k = 0; k < K; ++k) {
-            if (r + s < r1 && coff[k] < C) {
+            if (cok[k]) {
 #pragma unroll
               for (int v = 0; v < V; ++v) {
                 const float x = buf[s][k][v];
-                ps[s] += x * x + hp.eps0;
+                ps[s] = acc_fma(ps[s], x, x);
               }
             }
           }
         }
-        float tot[S];
+        double tot[S];
         block_row_sums<S, NW>(ps, red, par, tot);
         par ^= 1;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           if (r + s < r1) {
-            const int64_t row = b * R + r + s;
-            const float Rold = t.fp32st ? st_sq_row(t)[row] : deq_u8(rq[row], ra[blk_of(row, hp)]);
-            const float Rnew = t.mode2d ? (Rold * hp.b2) + (hp.a2f * (tot[s] / fC)) : fmaf(tot[s] / fC, hp.a2, Rold * hp.b2);
-            if (tid == 0) Rn[row] = Rnew;
+            const float Rnew = row_state(b * R + r + s, tot[s]);
+            if (tid == 0) rowR[r + s - r0] = Rnew;
             bandR += Rnew;
             const float invR = 1.0f / Rnew;
 #pragma unroll
             for (int k = 0; k < K; ++k) {
-              if (coff[k] < C) {
+              if (cok[k]) {
 #pragma unroll
                 for (int v = 0; v < V; ++v) {
                   const float x = buf[s][k][v];
-                  const float gg = x * x;
-                  colU[k][v] += Acc(gg + hp.eps0);
-                  colW[k][v] += Acc(gg * invR);
+                  colU[k][v] = acc_fma(colU[k][v], x, x);
+                  colW[k][v] = acc_fma_w(colW[k][v], x, invR);
                 }
               }
             }
           }
         }
       };
+      wait_vm_all();
       load_stage(A, r0);
       for (int64_t r = r0; r < r1; r += 2 * S) {
-        if (r + S < r1) load_stage(Bf, r + S);
+        load_stage(Bf, r + S);
         process(A, r);
-        if (r + S < r1) {
-          if (r + 2 * S < r1) load_stage(A, r + 2 * S);
-          process(Bf, r + S);
-        }
+        load_stage(A, r + 2 * S);
+        process(Bf, r + S);
       }
 #pragma unroll
       for (int k = 0; k < K; ++k) {
-        const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
-        if (c0 < C) {
+        if (cok[k]) {
 #pragma unroll
           for (int v = 0; v < V; ++v) {
-            pU[c0 + v] = float(colU[k][v]);
-            pW[c0 + v] = float(colW[k][v]);
+            pU[coff[k] + v] = float(colU[k][v]) + band_eps;
+            pW[coff[k] + v] = float(colW[k][v]);
           }
         }
       }
+      __syncthreads();
+      for (int64_t rr = tid; rr < r1 - r0; rr += TPB) Rn[b * R + r0 + rr] = rowR[rr];
     } else {
       // phase A: row sums over all segments
       for (int64_t r = r0; r < r1; r += S) {
-        float ps[S];
+        double ps[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) ps[s] = 0.0f;
         for (int64_t seg = 0; seg < nseg; ++seg) {
@@ -405,20 +449,19 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(TPB == 256 
                 Chunk<TG, V> x;
                 x.load(g + (r + s) * C + c0);
 #pragma unroll
-                for (int v = 0; v < V; ++v) ps[s] += x[v] * x[v] + hp.eps0;
+                for (int v = 0; v < V; ++v) ps[s] = acc_fma(ps[s], x[v], x[v]);
               }
             }
           }
         }
-        float tot[S];
+        double tot[S];
         block_row_sums<S, NW>(ps, red, par, tot);
         par ^= 1;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           if (r + s < r1) {
             const int64_t row = b * R + r + s;
-            const float Rold = t.fp32st ? st_sq_row(t)[row] : deq_u8(rq[row], ra[blk_of(row, hp)]);
-            const float Rnew = t.mode2d ? (Rold * hp.b2) + (hp.a2f * (tot[s] / fC)) : fmaf(tot[s] / fC, hp.a2, Rold * hp.b2);
+            const float Rnew = row_state(row, tot[s]);
             bandR += Rnew;
             if (tid == 0) {
               Rn[row] = Rnew;
@@ -445,9 +488,8 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(TPB == 256 
               x.load(g + r * C + c0);
 #pragma unroll
               for (int v = 0; v < V; ++v) {
-                const float gg = x[v] * x[v];
-                colU[k][v] += Acc(gg + hp.eps0);
-                colW[k][v] += Acc(gg * invR);
+                colU[k][v] = acc_fma(colU[k][v], x[v], x[v]);
+                colW[k][v] = acc_fma_w(colW[k][v], x[v], invR);
               }
             }
           }
@@ -458,7 +500,7 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(TPB == 256 
           if (c0 < C) {
 #pragma unroll
             for (int v = 0; v < V; ++v) {
-              pU[c0 + v] = float(colU[k][v]);
+              pU[c0 + v] = float(colU[k][v]) + band_eps;
               pW[c0 + v] = float(colW[k][v]);
             }
           }
@@ -467,12 +509,20 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(TPB == 256 
       __syncthreads();  // rowR is reused by the next work item
     }
     if (tid == 0) t.rsum[b * t.nbands + it.band] = bandR;
+    __syncthreads();  // rowold is rewritten by the next work item
   }
 }
 
 // ---------------- P2 ----------------
-// Per element: u = (r_i*c_j)*g / clip; m = fma(u, 1-b1, m_old*b1); res = (u-m)^2 + eps1.
-template <typename TG, int V, int K, int TPB>
+// Residual row and column sums of a band.  Per element the reference forms u = (r_i*c_j)*g / clip,
+// m = fma(u, 1-b1, m_old*b1) and res = (u - m)^2 + eps1 (CAME8bitFull.py:1032-1036) and keeps only
+// the means of res along rows and columns; the momentum itself is formed again, and kept, in pass 3.
+// This pass forms u and m with the reference's own operations and roundings (the division by the
+// clip divisor through its reciprocal, exact for the numerators that matter; m_old = code*(absmax/127)),
+// so d = u - m is the reference's; it then sums d*d with fused multiply-adds and adds eps1 once per
+// summed element count.  The sums differ from the reference's only in the order of addition and the
+// rounding of d*d: a few 1e-8 relative even where one element dominates a short column.
+template <typename TG, int V, int K, int TPB, bool F32ST>
 __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                     const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using GS = typename TG::storage;
@@ -480,9 +530,10 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
   constexpr int NW = TPB / kWave;
   constexpr int S = Stage<TG, V, K>::S;
   constexpr int64_t segw = int64_t(TPB) * V * K;
-  __shared__ float red[2][16][NW];
-  __shared__ float rowpart[2][kMaxBandRows][NW];  // per-wave row sums of a band (fast path)
+  __shared__ double red[2][16][NW];
+  __shared__ double rowpart[2][kMaxBandRows + 1][NW];  // per-wave row sums of a band (+1: a dummy row)
   __shared__ float rowval[kMaxBandRows];           // the band's new residual row states
+  __shared__ float rowsc[kMaxBandRows];            // the band's row factors r_i
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   int par = 0, bpar = 0;
   const int64_t total = wstart[ntens];
@@ -493,182 +544,175 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
     const int64_t ebase = (b * R) * C;
     const CAME8_GLOBAL GS* __restrict__ g = gbl(static_cast<const GS*>(t.g) + ebase);
     const CAME8_GLOBAL int8_t* __restrict__ mq = gbl(t.mq + ebase);
+    const CAME8_GLOBAL float* __restrict__ m32 = gbl(static_cast<const float*>(st_m(t)) + ebase);
     const CAME8_GLOBAL float* __restrict__ ma = gbl(t.ma);
     const CAME8_GLOBAL float* __restrict__ cf = gbl(t.cfac + b * C);
     const CAME8_GLOBAL float* __restrict__ rfac = gbl(t.rfac);
     const CAME8_GLOBAL uint8_t* __restrict__ rq = gbl(t.rq);
     const CAME8_GLOBAL float* __restrict__ ra = gbl(t.ra);
     CAME8_GLOBAL float* __restrict__ RRn = gbl(t.RRn);
-    const float clip = uniform_f32(t.clip[0]), crcp = uniform_f32(t.clip[1]);
-    const bool clip_fast = crcp == crcp;
+    const float clip = uniform_f32(t.clip[0]);
+    const float crcp = 1.0f / clip;  // the clip divisor is >= 1, so division through it is exact or 1 ulp off
     const float fC = float(C);
+    const float band_eps = float(r1 - r0) * hp.eps1;  // eps1 of each element of a column partial
     const int64_t nseg = (C + segw - 1) / segw;
     CAME8_GLOBAL float* __restrict__ pR = gbl(t.partRes + (b * t.nbands + it.band) * C);
     const int64_t PR = t.P * R;
+    constexpr bool f32st = F32ST;  // fp32 states (CAMECUDA layout); the host keys the launch by it
 
-    // residual of one element (the reference's u, m_new and (u - m_new)^2 + eps1)
-    auto res_of = [&](float ri, float cj, float x, float mold) {
-      const float a = (ri * cj) * x;
-      float u = a / clip;
-      if (clip_fast && !div_exact_needed(a)) u = div_fast(a, clip, crcp);
-      const float m = fmaf(u, hp.a1, mold * hp.b1);
-      const float d = u - m;
-      return d * d + hp.eps1;
+    // d = u - m of one element (x the gradient, mo the dequantised old momentum)
+    auto d_of = [&](float ri, float cj, float x, float mo) __attribute__((always_inline)) {
+      const float u = div_fast((ri * cj) * x, clip, crcp);
+      const float m = fmaf(u, hp.a1, mo * hp.b1);
+      return u - m;
     };
-    // Residuals of a V-chunk (V > 1 chunks lie inside one quantisation block) with the reciprocal
-    // divisions only; `bad` records a numerator or an absmax outside their exact range, after which
-    // the band is recomputed by the general path below.
-    // (fp32 states: the old momentum is read as is and amax is not used)
-    auto res_chunk = [&](float ri, const float (&cjv)[V], const Chunk<TG, V>& x, const auto& qc,
-                         float amax, float (&res)[V], bool& bad) __attribute__((always_inline)) {
-      constexpr bool kF32 = std::is_same<std::decay_t<decltype(qc)>, M32Chunk<V>>::value;
-      const float scale = kF32 ? 0.0f : div_fast(amax, kSignedQ, kRcpSignedQ);
-      float a[V];
-      DivGuard gd;
-#pragma unroll
-      for (int v = 0; v < V; ++v) {
-        a[v] = (ri * cjv[v]) * x[v];
-        gd.add(a[v]);
-      }
-      bad |= !gd.fast() || (!kF32 && !(fabsf(amax) <= 0x1.fffffep127f));
-#pragma unroll
-      for (int v = 0; v < V; ++v) {
-        const float u = div_fast(a[v], clip, crcp);
-        const float m = fmaf(u, hp.a1, qc.mold(v, scale) * hp.b1);
-        const float d = u - m;
-        res[v] = d * d + hp.eps1;
-      }
-    };
-    auto row_state = [&](int64_t row, float tot) {
-      const float RRold = t.fp32st ? t.ra[row] : deq_u8(rq[PR + row], ra[t.nbr + blk_of(row, hp)]);
+    auto row_state = [&](int64_t row, double sum_e2) {
+      const float tot = float(sum_e2 + double(C) * double(hp.eps1));
+      const float RRold = f32st ? t.ra[row] : deq_u8(rq[PR + row], ra[t.nbr + blk_of(row, hp)]);
       const float RRnew = fmaf(tot / fC, hp.a3, RRold * hp.b3);
       RRn[row] = RRnew;
       return RRnew;
     };
 
-    bool general = nseg > 1 || !clip_fast;
-    if (!general) {
-      bool bad = false;
+    // the row scalars go through LDS: a per-row global load inside the stage loop would wait for the
+    // next stage's loads as well
+    for (int64_t rr = tid; rr < r1 - r0; rr += TPB) rowsc[rr] = rfac[b * R + r0 + rr];
+    __syncthreads();
+    if (nseg == 1) {
+      // The stage loop is branch-free, so that the compiler can wait for exactly one stage's loads
+      // while the next stage's are in flight: a chunk past the row end (cok false) loads the row's
+      // first chunk instead, and a row past the band end loads the band's last row; both contribute
+      // zero (their r_i, c_j and momentum scale are zero) and their sums are never stored.
       float cj[K][V];
+      int32_t coff[K];
+      bool cok[K];
 #pragma unroll
       for (int k = 0; k < K; ++k) {
-        const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
+        const int32_t c = (tid + k * TPB) * V;
+        cok[k] = c < C;  // V > 1: C % V == 0, so a chunk that starts inside the row ends inside it
+        coff[k] = cok[k] ? c : 0;
 #pragma unroll
-        for (int v = 0; v < V; ++v) cj[k][v] = (c0 + v < C) ? cf[c0 + v] : 0.0f;
+        for (int v = 0; v < V; ++v) cj[k][v] = cok[k] ? cf[c + v] : 0.0f;
       }
       Acc colR[K][V];
 #pragma unroll
       for (int k = 0; k < K; ++k)
 #pragma unroll
         for (int v = 0; v < V; ++v) colR[k][v] = Acc(0);
-      int32_t coff[K];  // this thread's column offsets; coff[k] < C when chunk k exists
-#pragma unroll
-      for (int k = 0; k < K; ++k) coff[k] = (tid + k * TPB) * V;
       // When B divides C a row starts a block: the block of chunk k is the row's first block plus
       // the chunk's (per-thread) block offset cbk[k].
       int32_t cbk[K];
 #pragma unroll
       for (int k = 0; k < K; ++k) cbk[k] = t.rowal ? int32_t(blk_of(coff[k], hp)) : 0;
-      const CAME8_GLOBAL float* __restrict__ m32 = gbl(static_cast<const float*>(st_m(t)) + ebase);
       // AL: rows start quantisation blocks; ST: fp32 states
       auto run = [&](auto AL, auto ST) __attribute__((always_inline)) {
-      constexpr bool kF32 = decltype(ST)::value;
-      using MB = typename std::conditional<kF32, M32Chunk<V>, CodeChunk<V>>::type;
-      Chunk<TG, V> gA[S][K], gB[S][K];
-      MB qA[S][K], qB[S][K];
-      auto load_stage = [&](Chunk<TG, V> (&gb)[S][K], MB (&qb)[S][K], int64_t r) __attribute__((always_inline)) {
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          if (r + s < r1) {
-            const CAME8_GLOBAL GS* __restrict__ grow = g + (r + s) * C;
-#pragma unroll
-            for (int k = 0; k < K; ++k) {
-              if (coff[k] < C) {
-                gb[s][k].load(grow + coff[k]);
-                if constexpr (kF32) qb[s][k].load(m32 + (r + s) * C + coff[k]);
-                else qb[s][k].load(mq + (r + s) * C + coff[k]);
-              }
-            }
-          }
-        }
-      };
-      auto process = [&](const Chunk<TG, V> (&gb)[S][K], const MB (&qb)[S][K],
-                         int64_t r) __attribute__((always_inline)) {
+        constexpr bool kF32 = decltype(ST)::value;
         constexpr bool kAligned = decltype(AL)::value && !kF32;
-        float ps[S];
+        using MB = typename std::conditional<kF32, M32Chunk<V>, CodeChunk<V>>::type;
+        // a stage: S rows of gradient chunks, momentum chunks and (8-bit states) the chunks' block
+        // absmax, all issued together so that waiting for one stage never waits for the next
+        Chunk<TG, V> gA[S][K], gB[S][K];
+        MB qA[S][K], qB[S][K];
+        float aA[S][K], aB[S][K];
+        auto load_stage = [&](Chunk<TG, V> (&gb)[S][K], MB (&qb)[S][K], float (&ab)[S][K], int64_t r) __attribute__((always_inline)) {
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-          ps[s] = 0.0f;
-          if (r + s < r1) {
-            const float ri = rfac[b * R + r + s];
-            const int64_t erow = ebase + (r + s) * C;
-            const CAME8_GLOBAL float* __restrict__ marow = kAligned ? ma + blk_of(erow, hp) : ma;
+          for (int s = 0; s < S; ++s) {
+            const int64_t rs = (r + s < r1) ? (r + s) : (r1 - 1);
+            const int64_t erow = ebase + rs * C;
+            const CAME8_GLOBAL float* __restrict__ marow = kAligned ? ma + blk_of_nb(erow, hp) : ma;
 #pragma unroll
             for (int k = 0; k < K; ++k) {
-              if (coff[k] < C) {
-                const float amax = kF32 ? 0.0f : (kAligned ? marow[cbk[k]] : ma[blk_of(erow + coff[k], hp)]);
-                float res[V];
-                res_chunk(ri, cj[k], gb[s][k], qb[s][k], amax, res, bad);
-#pragma unroll
-                for (int v = 0; v < V; ++v) {
-                  ps[s] += res[v];
-                  colR[k][v] += Acc(res[v]);
-                }
+              gb[s][k].load(g + rs * C + coff[k]);
+              if constexpr (kF32) {
+                qb[s][k].load(m32 + rs * C + coff[k]);
+              } else {
+                qb[s][k].load(mq + rs * C + coff[k]);
+                ab[s][k] = kAligned ? marow[cbk[k]] : ma[blk_of_nb(erow + coff[k], hp)];
               }
             }
           }
-        }
-        // each wave's share of the row sums; the band's rows are combined after its last stage
+        };
+        auto process = [&](const Chunk<TG, V> (&gb)[S][K], const MB (&qb)[S][K], const float (&ab)[S][K], int64_t r) __attribute__((always_inline)) {
+          double ps[S];
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-          const float wsum = wave_sum(ps[s]);
-          if (lane == 0 && r + s < r1) rowpart[bpar][r + s - r0][wid] = wsum;
-        }
-      };
-        load_stage(gA, qA, r0);
-        for (int64_t r = r0; r < r1; r += 2 * S) {
-          if (r + S < r1) load_stage(gB, qB, r + S);
-          process(gA, qA, r);
-          if (r + S < r1) {
-            if (r + 2 * S < r1) load_stage(gA, qA, r + 2 * S);
-            process(gB, qB, r + S);
+          for (int s = 0; s < S; ++s) {
+            ps[s] = 0.0f;
+            const bool rok = r + s < r1;
+            const float ri_l = rowsc[(rok ? (r + s) : (r1 - 1)) - r0];
+            const float ri = rok ? ri_l : 0.0f;
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+              const bool ok = rok && cok[k];
+              // momentum scale absmax/127 (fp32 states: 1), zero for a chunk that counts for nothing
+              float sc;
+              if constexpr (kF32) sc = ok ? 1.0f : 0.0f;
+              else sc = ok ? div_fast(ab[s][k], kSignedQ, kRcpSignedQ) : 0.0f;
+#pragma unroll
+              for (int v = 0; v < V; ++v) {
+                float mo;
+                if constexpr (kF32) mo = qb[s][k].m[v] * sc;
+                else mo = qb[s][k][v] * sc;
+                const float d = d_of(ri, cj[k][v], gb[s][k][v], mo);
+                ps[s] = acc_fma(ps[s], d, d);
+                colR[k][v] = acc_fma(colR[k][v], d, d);
+              }
+            }
           }
+          // each wave's share of the row sums (rows past the band end go to the dummy row); the
+          // band's rows are combined after its last stage
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            const double wsum = wave_sum(ps[s]);
+            const int64_t slot = (r + s < r1) ? (r + s - r0) : int64_t(kMaxBandRows);
+            if (lane == 0) rowpart[bpar][slot][wid] = wsum;
+          }
+        };
+        // two register stages in flight; the prefetches are unconditional (rows past the band end
+        // reload its last row, from cache, and count for nothing)
+        wait_vm_all();
+        load_stage(gA, qA, aA, r0);
+        for (int64_t r = r0; r < r1; r += 2 * S) {
+          load_stage(gB, qB, aB, r + S);
+          process(gA, qA, aA, r);
+          load_stage(gA, qA, aA, r + 2 * S);
+          process(gB, qB, aB, r + S);
         }
       };
-      if (t.fp32st) run(std::false_type{}, std::true_type{});
+      if constexpr (F32ST) run(std::false_type{}, std::true_type{});
       else if (t.rowal) run(std::true_type{}, std::false_type{});
       else run(std::false_type{}, std::false_type{});
 #pragma unroll
       for (int k = 0; k < K; ++k) {
-        const int64_t c0 = (int64_t(tid) + int64_t(k) * TPB) * V;
-        if (c0 < C) {
+        if (cok[k]) {
 #pragma unroll
-          for (int v = 0; v < V; ++v) pR[c0 + v] = float(colR[k][v]);
+          for (int v = 0; v < V; ++v) pR[coff[k] + v] = float(colR[k][v]) + band_eps;
         }
       }
-      general = __syncthreads_or(bad);  // rare: the general path rewrites this band's outputs
-      if (!general) {
-        // row totals over the waves in a fixed order; the new residual row states go through
-        // LDS so that one thread can add them up in row order
-        for (int rr = tid; rr < r1 - r0; rr += TPB) {
-          float tot = rowpart[bpar][rr][0];
+      __syncthreads();
+      // row totals over the waves in a fixed order; the new residual row states go through LDS so
+      // that one thread can add them up in row order
+      for (int rr = tid; rr < r1 - r0; rr += TPB) {
+        double tot = rowpart[bpar][rr][0];
 #pragma unroll
-          for (int w2 = 1; w2 < NW; ++w2) tot += rowpart[bpar][rr][w2];
-          rowval[rr] = row_state(b * R + r0 + rr, tot);
-        }
-        __syncthreads();
-        if (tid == 0) {
-          float sum = 0.0f;
-          for (int64_t rr = 0; rr < r1 - r0; ++rr) sum += rowval[rr];
-          t.rrsum[b * t.nbands + it.band] = sum;
-        }
+        for (int w2 = 1; w2 < NW; ++w2) tot += rowpart[bpar][rr][w2];
+        rowval[rr] = row_state(b * R + r0 + rr, tot);
       }
-      bpar ^= 1;  // the next band writes the other half (after this band's barrier above)
-    }
-    if (general) {
-      const CAME8_GLOBAL float* __restrict__ m32g = gbl(static_cast<const float*>(st_m(t)) + ebase);
-      float bandRR = 0.0f;  // sum of the band's new residual row states (thread 0, row order)
-      // general path (wide rows, or exact divisions needed): column partials, segment by segment
+      __syncthreads();
+      if (tid == 0) {
+        float sum = 0.0f;
+        for (int64_t rr = 0; rr < r1 - r0; ++rr) sum += rowval[rr];
+        t.rrsum[b * t.nbands + it.band] = sum;
+      }
+      bpar ^= 1;  // the next band writes the other half (after this band's barriers above)
+    } else {
+      // rows wider than one sweep of the workgroup: column partials segment by segment, then the
+      // row sums over whole rows (the gradient and codes are read twice)
+      auto e_at = [&](float ri, float cjv, float x, int64_t e) {
+        float mo;
+        if constexpr (F32ST) mo = m32[e];
+        else mo = float(mq[e]) * scale_s8(ma[blk_of(ebase + e, hp)]);
+        return d_of(ri, cjv, x, mo);
+      };
       for (int64_t seg = 0; seg < nseg; ++seg) {
         Acc colR[K][V];
 #pragma unroll
@@ -676,20 +720,17 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
 #pragma unroll
           for (int v = 0; v < V; ++v) colR[k][v] = Acc(0);
         for (int64_t r = r0; r < r1; ++r) {
-          const float ri = rfac[b * R + r];
+          const float ri = rowsc[r - r0];
 #pragma unroll
           for (int k = 0; k < K; ++k) {
             const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
             if (c0 < C) {
-              const int64_t e = r * C + c0;
               Chunk<TG, V> x;
-              CodeChunk<V> q;
-              x.load(g + e);
-              q.load(mq + e);
+              x.load(g + r * C + c0);
 #pragma unroll
               for (int v = 0; v < V; ++v) {
-                const float mold = t.fp32st ? m32g[e + v] : q[v] * scale_s8(ma[blk_of(ebase + e + v, hp)]);
-                colR[k][v] += Acc(res_of(ri, cf[c0 + v], x[v], mold));
+                const float e = e_at(ri, cf[c0 + v], x[v], r * C + c0 + v);
+                colR[k][v] = acc_fma(colR[k][v], e, e);
               }
             }
           }
@@ -699,39 +740,36 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
           const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
           if (c0 < C) {
 #pragma unroll
-            for (int v = 0; v < V; ++v) pR[c0 + v] = float(colR[k][v]);
+            for (int v = 0; v < V; ++v) pR[c0 + v] = float(colR[k][v]) + band_eps;
           }
         }
       }
-      // row sums over whole rows
+      float bandRR = 0.0f;  // sum of the band's new residual row states (thread 0, row order)
       for (int64_t r = r0; r < r1; r += S) {
-        float ps[S];
+        double ps[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           ps[s] = 0.0f;
           if (r + s < r1) {
-            const float ri = rfac[b * R + r + s];
+            const float ri = rowsc[r + s - r0];
             for (int64_t seg = 0; seg < nseg; ++seg) {
 #pragma unroll
               for (int k = 0; k < K; ++k) {
                 const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
                 if (c0 < C) {
-                  const int64_t e = (r + s) * C + c0;
                   Chunk<TG, V> x;
-                  CodeChunk<V> q;
-                  x.load(g + e);
-                  q.load(mq + e);
+                  x.load(g + (r + s) * C + c0);
 #pragma unroll
                   for (int v = 0; v < V; ++v) {
-                    const float mold = t.fp32st ? m32g[e + v] : q[v] * scale_s8(ma[blk_of(ebase + e + v, hp)]);
-                    ps[s] += res_of(ri, cf[c0 + v], x[v], mold);
+                    const float e = e_at(ri, cf[c0 + v], x[v], (r + s) * C + c0 + v);
+                    ps[s] = acc_fma(ps[s], e, e);
                   }
                 }
               }
             }
           }
         }
-        float tot[S];
+        double tot[S];
         block_row_sums<S, NW>(ps, red, par, tot);
         par ^= 1;
 #pragma unroll
@@ -740,6 +778,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
       }
       if (tid == 0) t.rrsum[b * t.nbands + it.band] = bandRR;
     }
+    __syncthreads();  // rowsc is rewritten by the next work item
   }
 }
 
