@@ -35,11 +35,11 @@ constexpr size_t kAlign = 256;
 size_t align_up(size_t x, size_t a = kAlign) { return (x + a - 1) / a * a; }
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Rows per band: about 512K elements per workgroup work item, whole rows, at most 256 rows (so a
-// column partial sums at most 256 values before the fp64 sum across bands).
-int64_t band_rows(int64_t R, int64_t C, bool multiseg) {
-  (void)multiseg;
-  int64_t rb = std::max<int64_t>(1, (int64_t(1) << 19) / std::max<int64_t>(C, 1));
+// Rows per band: about 1M elements per workgroup work item, whole rows, at most 256 rows.  Every
+// band writes one fp32 partial per column and statistic, which the factor kernels read back, so
+// the band size sets that traffic (8-12 bytes per column per band).
+int64_t band_rows(int64_t R, int64_t C) {
+  int64_t rb = std::max<int64_t>(1, (int64_t(1) << 20) / std::max<int64_t>(C, 1));
   rb = std::min<int64_t>(rb, kMaxBandRows);
   return std::min<int64_t>(rb, R);
 }
@@ -95,6 +95,7 @@ struct Plan {
   std::map<int, WorkList> param2d_v;     // 8bit2d parameter write, vector form, by param type
   std::map<int, WorkList> param2d;       // 8bit2d parameter write, scalar form, by param type
   size_t plan_bytes = 0;
+  size_t zero_off = 0;  // kZeroBytes of zeros inside the plan blob
   size_t total_bytes = 0;
   std::vector<uint8_t> blob;
 };
@@ -126,12 +127,13 @@ struct BandShapeSel {
   bool multiseg;
 };
 
-BandShapeSel band_variant(const came8_tensor& t, int64_t C, int32_t B) {
+BandShapeSel band_variant(const came8_tensor& t, int64_t C, int32_t B, int pass) {
   const int vw = t.grad_dtype == CAME8_F32 ? 4 : 8;
   const bool aligned = (C % vw == 0) && (B % vw == 0) && (reinterpret_cast<uintptr_t>(t.grad) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(t.exp_avg_q) % vw == 0);
   BandShapeSel sel{aligned ? vw : 1, 0, 256, false};
   const int64_t chunks = ceil_div(C, sel.V);
+  (void)pass;  // both passes take the same shapes (wider workgroups cost pass 1 more barrier time)
   static const int vec_k[][2] = {{1, 256}, {2, 256}, {2, 512}, {3, 512}, {4, 512}};
   static const int one_k[][2] = {{1, 256}, {2, 256}, {4, 256}, {8, 256}, {16, 256}, {32, 256}};
   const int (*cand)[2] = sel.V > 1 ? vec_k : one_k;
@@ -251,8 +253,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     magic_div(d.C, d.mC, d.sC);
     magic_div(d.R, d.mR, d.sR);
     if (t.factored) {
-      const BandShapeSel sel = band_variant(t, d.C, B);
-      d.rb = band_rows(d.R, d.C, sel.multiseg);
+      d.rb = band_rows(d.R, d.C);
       d.nbands = ceil_div(d.R, d.rb);
       d.nbr = std::max<int64_t>(1, ceil_div(d.P * d.R, B));
       d.nbc = std::max<int64_t>(1, ceil_div(d.P * d.C, B));
@@ -312,7 +313,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     const DevTensor& d = plan.dev[i];
     const TypeKey tk{t.param_dtype, t.grad_dtype, d.fp32st};
     if (d.mode2d) {
-      const BandShapeSel sel = band_variant(t, d.C, B);
+      const BandShapeSel sel = band_variant(t, d.C, B, 1);
       add_item(plan.band[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB}], i, d.nbands);
       add_item(plan.factor, i, d.nbr + d.nbc);
       if (d.v2d) {
@@ -326,9 +327,9 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       continue;  // the clip of this layout has no parity-mode variant (the reference sums it with float atomics)
     }
     if (t.factored) {
-      const BandShapeSel sel = band_variant(t, d.C, B);
-      add_item(plan.band[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB}], i, d.P * d.nbands);
-      add_item(plan.band2[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB, d.fp32st}], i, d.P * d.nbands);
+      const BandShapeSel sel1 = band_variant(t, d.C, B, 1), sel2 = band_variant(t, d.C, B, 2);
+      add_item(plan.band[BandKey{t.grad_dtype, sel1.V, sel1.K, sel1.TPB}], i, d.P * d.nbands);
+      add_item(plan.band2[BandKey{t.grad_dtype, sel2.V, sel2.K, sel2.TPB, d.fp32st}], i, d.P * d.nbands);
       add_item(plan.factor, i, d.nbr + d.nbc);
       if (fastB) {
         if (d.p3_nbands > 0) add_item(plan.updb[tk], i, d.P * d.p3_nbands * d.p3_nseg);
@@ -364,6 +365,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
   for (auto& kv : plan.generic) place(kv.second);
   for (auto& kv : plan.refnorm) place(kv.second);
   place(plan.factor);
+  plan.zero_off = align_up(off);
+  off = plan.zero_off + kZeroBytes;
   plan.plan_bytes = align_up(off);
   plan.total_bytes = plan.plan_bytes + scr;
 
@@ -720,8 +723,9 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       ce.bytes = ce.keep.size();
     }
   }
-  const Hp hp = make_hp(h);
+  Hp hp = make_hp(h);
   const char* base = static_cast<const char*>(workspace);
+  hp.zeros = base + plan.zero_off;
   const DevTensor* dT = reinterpret_cast<const DevTensor*>(base);
   auto tids = [&](const WorkList& wl) { return reinterpret_cast<const int32_t*>(base + wl.tids_off); };
   auto wst = [&](const WorkList& wl) { return reinterpret_cast<const int64_t*>(base + wl.wstart_off); };

@@ -112,7 +112,9 @@ struct Hp {
   uint64_t mB;     // block sizes that are not powers of two)
   float a1f, a2f, a3f;  // 8bit2d: 1 - beta computed in float
   float wdfac;          // 8bit2d: multiplicative weight decay 1 - lr * wd, computed in float
+  const void* zeros;    // kZeroBytes of zeros in the workspace (reads that must count for nothing)
 };
+constexpr int kZeroBytes = 32768;  // >= TPB*V*K elements of any band-pass shape
 
 __device__ __forceinline__ int64_t blk_of(int64_t e, const Hp& hp) {
   return hp.log2B >= 0 ? (e >> hp.log2B) : int64_t(udiv_magic(uint32_t(e), hp.mB, hp.sB));
@@ -339,10 +341,13 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
       rowold[rr] = t.fp32st ? st_sq_row(t)[row] : deq_u8(rq[row], ra[blk_of(row, hp)]);
     }
     __syncthreads();
+    // (the mean through 1/C: within 1 ulp of tot / C, and equal to it for power-of-two C)
+    const float invC = 1.0f / fC;
     auto row_state = [&](int64_t row, double sum_g2) {
       const float tot = float(sum_g2 + double(C) * double(hp.eps0));
       const float Rold = rowold[row - b * R - r0];
-      return t.mode2d ? (Rold * hp.b2) + (hp.a2f * (tot / fC)) : fmaf(tot / fC, hp.a2, Rold * hp.b2);
+      const float mean = tot * invC;
+      return t.mode2d ? (Rold * hp.b2) + (hp.a2f * mean) : fmaf(mean, hp.a2, Rold * hp.b2);
     };
 
     if (nseg == 1) {
@@ -350,11 +355,18 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
       // them unconditionally, so that the compiler waits for exactly one stage while the next is in
       // flight: a chunk past the row end (cok false) loads the row's first chunk and is skipped, a
       // row past the band end loads the band's last row and is ignored.
-      Acc colU[K][V], colW[K][V];
+      // column sums of g^2 in fp64 (the column second moment is held to 1e-6); of g^2/R_i in fp32 (it
+      // only enters the clip, and an outlier's g^2/R_i outweighs the rest of its column by about C/R,
+      // not by orders of magnitude, since the outlier's row sum R_i holds it too)
+      Acc colU[K][V];
+      float colW[K][V];
 #pragma unroll
       for (int k = 0; k < K; ++k)
 #pragma unroll
-        for (int v = 0; v < V; ++v) colU[k][v] = colW[k][v] = Acc(0);
+        for (int v = 0; v < V; ++v) {
+          colU[k][v] = Acc(0);
+          colW[k][v] = 0.0f;
+        }
       Chunk<TG, V> A[S][K], Bf[S][K];
       int32_t coff[K];
       bool cok[K];
@@ -364,27 +376,32 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
         cok[k] = c < C;  // V > 1: C % V == 0, so a chunk that starts inside the row ends inside it
         coff[k] = cok[k] ? c : 0;
       }
+      // rows past the band end read the workspace's zero block (at least TPB*V*K elements long)
+      const CAME8_GLOBAL GS* __restrict__ zrow = gbl(static_cast<const GS*>(hp.zeros));
       auto load_stage = [&](Chunk<TG, V> (&buf)[S][K], int64_t r) __attribute__((always_inline)) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-          const int64_t rs = (r + s < r1) ? (r + s) : (r1 - 1);
-          const CAME8_GLOBAL GS* __restrict__ grow = g + rs * C;
+          const CAME8_GLOBAL GS* __restrict__ grow = (r + s < r1) ? g + (r + s) * C : zrow;
 #pragma unroll
           for (int k = 0; k < K; ++k) buf[s][k].load(grow + coff[k]);
         }
       };
       auto process = [&](const Chunk<TG, V> (&buf)[S][K], int64_t r) __attribute__((always_inline)) {
+        // row partials and the column sums of g^2 (neither needs the row sums), then the row sums
+        // over the workgroup, then the column sums of g^2/R_i.  A row past the band end holds zeros
+        // and adds nothing anywhere.
         double ps[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-          ps[s] = 0.0f;
+          ps[s] = 0.0;
 #pragma unroll
           for (int k = 0; k < K; ++k) {
             if (cok[k]) {
 #pragma unroll
               for (int v = 0; v < V; ++v) {
-                const float x = buf[s][k][v];
-                ps[s] = acc_fma(ps[s], x, x);
+                const double x = double(buf[s][k][v]);
+                ps[s] = fma(x, x, ps[s]);
+                colU[k][v] = fma(x, x, colU[k][v]);
               }
             }
           }
@@ -394,20 +411,22 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
         par ^= 1;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-          if (r + s < r1) {
+          const bool rok = r + s < r1;
+          float invR = 0.0f;
+          if (rok) {
             const float Rnew = row_state(b * R + r + s, tot[s]);
             if (tid == 0) rowR[r + s - r0] = Rnew;
             bandR += Rnew;
-            const float invR = 1.0f / Rnew;
+            // 1/R_i only weighs the clip's column sums: the hardware reciprocal (within 1 ulp) will do
+            invR = __builtin_amdgcn_rcpf(Rnew);
+          }
 #pragma unroll
-            for (int k = 0; k < K; ++k) {
-              if (cok[k]) {
+          for (int k = 0; k < K; ++k) {
+            if (cok[k]) {
 #pragma unroll
-                for (int v = 0; v < V; ++v) {
-                  const float x = buf[s][k][v];
-                  colU[k][v] = acc_fma(colU[k][v], x, x);
-                  colW[k][v] = acc_fma_w(colW[k][v], x, invR);
-                }
+              for (int v = 0; v < V; ++v) {
+                const float x = buf[s][k][v];
+                colW[k][v] = fmaf(x * invR, x, colW[k][v]);
               }
             }
           }
@@ -427,7 +446,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
 #pragma unroll
           for (int v = 0; v < V; ++v) {
             pU[coff[k] + v] = float(colU[k][v]) + band_eps;
-            pW[coff[k] + v] = float(colW[k][v]);
+            pW[coff[k] + v] = colW[k][v];
           }
         }
       }
