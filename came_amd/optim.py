@@ -33,21 +33,11 @@ import torch
 import torch.optim
 
 from . import _lib
+from . import state_layout
 from .blockwise_quantization import init_batched_qstate, init_qstate, num_blocks
 
 _DTYPE_CODE = {torch.float32: _lib.CAME8_F32, torch.bfloat16: _lib.CAME8_BF16, torch.float16: _lib.CAME8_F16}
 
-# state keys whose dtype is not the parameter's (torch's load_state_dict would cast them)
-_STATE_DTYPES = {
-    "exp_avg_q": torch.int8,
-    "exp_avg_absmax": torch.float32,
-    "factored_row_q": torch.uint8,
-    "factored_row_absmax": torch.float32,
-    "factored_col_q": torch.uint8,
-    "factored_col_absmax": torch.float32,
-    "exp_avg_sq_q": torch.uint8,
-    "exp_avg_sq_absmax": torch.float32,
-}
 _VIEW_KEYS = (
     "exp_avg_sq_row_q", "exp_avg_res_row_q", "exp_avg_sq_col_q", "exp_avg_res_col_q",
     "exp_avg_sq_row_absmax", "exp_avg_res_row_absmax", "exp_avg_sq_col_absmax", "exp_avg_res_col_absmax",
@@ -66,7 +56,6 @@ class _Came8Base(torch.optim.Optimizer):
 
     _MODE = "full8bit"                 # state["_mode"] of this optimizer's layout
     _STATE_KIND = _lib.CAME8_STATE_Q8  # how the library reads the state pointers
-    _KEEP_DTYPES = _STATE_DTYPES       # state tensors whose dtype a checkpoint load must keep
 
     def _validate_and_defaults(self, lr, eps, clip_threshold, betas, weight_decay, block_size):
         # came_pytorch/CAME8bitFull.py:73-91
@@ -132,9 +121,17 @@ class _Came8Base(torch.optim.Optimizer):
             raise RuntimeError("optimizer state lives on a different device than its parameter")
 
     # -------------------------------------------------------------- checkpoint
-    def load_state_dict(self, state_dict: dict) -> None:
-        """torch's loader casts every floating state tensor to the parameter dtype; the 8-bit codes and
-        the fp32 block scales must keep their own dtypes, so the originals are put back afterwards."""
+    def load_state_dict(self, state_dict: dict, convert_layouts: bool = True) -> None:
+        """torch's loader casts every floating state tensor to the parameter dtype.  Every state tensor of
+        these optimizers has a dtype of its own (int8/uint8 codes, fp32 scales and fp32 states, whatever
+        the parameter dtype), so each is put back as saved, on the parameter's device.
+
+        A state saved in another of the reference's layouts (the 8bit2d tiles its CUDA path keeps for
+        2-D parameters, the per-matrix blocks of its CUDA N-D path, fp32 CAMECUDA states, or full8bit
+        states under CAME8bit2D / CAMECUDA) is converted into this optimizer's layout
+        (``state_layout.convert_state``), so the momentum and second moments carry over.  With
+        ``convert_layouts=False`` such a state is left as loaded, and, as in the reference
+        (CAME8bit.py:757-759), re-initialised by the next step."""
         saved_groups = state_dict["param_groups"]
         saved_state = state_dict["state"]
         super().load_state_dict(state_dict)
@@ -145,17 +142,40 @@ class _Came8Base(torch.optim.Optimizer):
             if p is None or p not in self.state:
                 continue
             live = self.state[p]
-            for key, dt in self._KEEP_DTYPES.items():
-                v = st.get(key)
-                if isinstance(v, torch.Tensor):
-                    live[key] = v.detach().to(device=p.device, dtype=dt).clone()
-            # torch's loader rebuilds iterables element-wise, which turns the string "_mode" into a
-            # generator (and a mode mismatch would reset the state on the next step): plain values
-            # are restored as saved
             for key, v in st.items():
-                if isinstance(v, (str, bool, int, float)):
+                if isinstance(v, torch.Tensor):
+                    live[key] = v.detach().to(device=p.device).clone()
+                # torch's loader rebuilds iterables element-wise, which turns the string "_mode" into a
+                # generator (and a mode mismatch would reset the state on the next step): plain values
+                # are restored as saved
+                elif isinstance(v, (str, bool, int, float)):
                     live[key] = v
             self._after_load(live)
+            if convert_layouts:
+                self._adopt_layout(p, live)
+
+    def _group_of(self, p: torch.Tensor) -> dict:
+        for g in self.param_groups:
+            if any(q is p for q in g["params"]):
+                return g
+        raise KeyError("parameter is in no param group")
+
+    def _adopt_layout(self, p: torch.Tensor, state: dict) -> None:
+        """Convert a loaded state of another layout into this optimizer's (see load_state_dict)."""
+        src = state_layout.layout_of(state)
+        if not src or src == self._MODE or (self._MODE == "8bit2d" and p.dim() != 2):
+            return
+        block_size = int(self._group_of(p).get("block_size", 256))
+        new = state_layout.convert_state(state, tuple(p.shape), self._MODE, block_size)
+        state.clear()
+        if self._MODE == "8bit2d":
+            init_8bit2d_state(state, p.data, block_size=256)
+            for key, v in new.items():
+                if isinstance(v, torch.Tensor):
+                    state[key].copy_(v.reshape(state[key].shape))
+        else:
+            state.update(new)
+        self._after_load(state)
 
     def _after_load(self, state: dict) -> None:
         if state.get("factored") and "factored_row_q" in state:
@@ -554,7 +574,6 @@ class CAMECUDA(_Came8Base):
 
     _MODE = "cudafp"
     _STATE_KIND = _lib.CAME8_STATE_FP32
-    _KEEP_DTYPES = {k: torch.float32 for k in _FP32_STATE_KEYS}
     _WORK_BLOCK = 256  # shapes the library's work decomposition only; fp32 states have no blocks
 
     def __init__(
@@ -650,16 +669,6 @@ class CAMECUDA(_Came8Base):
         pass
 
 
-# state tensors of the 8bit2d layout and their dtypes (came_pytorch/came8bit2d_state.py:40-68)
-_STATE_DTYPES_2D = {
-    "exp_avg_q": torch.int8,
-    "exp_avg_absmax": torch.float32,
-    **{f"exp_avg_{k}_q": torch.uint8 for k in ("sq_row", "sq_col", "res_row", "res_col")},
-    **{f"exp_avg_{k}_absmax": torch.float32 for k in ("sq_row", "sq_col", "res_row", "res_col")},
-    **{k: torch.float32 for k in ("r_factor", "c_factor", "r_res_factor", "c_res_factor", "res_row_sum",
-                                  "res_col_sum", "res_row_partial", "res_col_partial", "sum_sq_row", "sum_update",
-                                  "sum_update_partial", "sum_res_row")},
-}
 _TILE_2D = 16
 
 
@@ -711,7 +720,6 @@ class CAME8bit2D(_Came8Base):
 
     _MODE = "8bit2d"
     _STATE_KIND = _lib.CAME8_STATE_8BIT2D
-    _KEEP_DTYPES = _STATE_DTYPES_2D
 
     def __init__(
         self,
