@@ -35,13 +35,33 @@ constexpr size_t kAlign = 256;
 size_t align_up(size_t x, size_t a = kAlign) { return (x + a - 1) / a * a; }
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Rows per band: about 1M elements per workgroup work item, whole rows, at most 256 rows.  Every
-// band writes one fp32 partial per column and statistic, which the factor kernels read back, so
-// the band size sets that traffic (8-12 bytes per column per band).
-int64_t band_rows(int64_t R, int64_t C) {
+// A launch of few bands leaves most CUs idle (one 2048x2048 matrix is 8 bands): bands are halved
+// (down to kMinShrunkBandRows rows) until the band passes have about kMinLaunchBands work items.
+constexpr int64_t kMinShrunkBandRows = 8;
+constexpr int64_t kMinLaunchBands = 2048;
+
+// Rows per band: about 1M elements per workgroup work item, whole rows, at most 256 rows, divided by
+// 2^shrink.  Every band writes one fp32 partial per column and statistic, which the factor kernels
+// read back, so the band size sets that traffic (8-12 bytes per column per band).
+int64_t band_rows(int64_t R, int64_t C, int shrink = 0) {
   int64_t rb = std::max<int64_t>(1, (int64_t(1) << 20) / std::max<int64_t>(C, 1));
   rb = std::min<int64_t>(rb, kMaxBandRows);
+  rb = std::max<int64_t>(std::min<int64_t>(rb, kMinShrunkBandRows), rb >> shrink);
   return std::min<int64_t>(rb, R);
+}
+
+int band_shrink(const came8_tensor* ts, int32_t n) {  // the 2^shrink of band_rows for a launch
+  int shrink = 0;
+  for (; shrink < 6; ++shrink) {
+    int64_t bands = 0;
+    for (int i = 0; i < n; ++i) {
+      const came8_tensor& t = ts[i];
+      if (!t.factored || t.rows < 1 || t.cols < 1 || t.prefix < 1) continue;
+      bands += t.prefix * ceil_div(t.rows, band_rows(t.rows, t.cols, shrink));
+    }
+    if (bands >= kMinLaunchBands) break;
+  }
+  return shrink;
 }
 
 int elem_size(int dt) { return dt == CAME8_F32 ? 4 : 2; }
@@ -168,6 +188,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
   // --- scratch layout (after the plan blob; offsets relative to the scratch start) ---
   std::vector<size_t> scr_off(n, 0);
   size_t scr = 0;
+  const int shrink = band_shrink(ts, n);
   for (int i = 0; i < n; ++i) {
     const came8_tensor& t = ts[i];
     const std::string who = "came8: tensor " + std::to_string(i) + ": ";
@@ -253,7 +274,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     magic_div(d.C, d.mC, d.sC);
     magic_div(d.R, d.mR, d.sR);
     if (t.factored) {
-      d.rb = band_rows(d.R, d.C);
+      d.rb = band_rows(d.R, d.C, shrink);
       d.nbands = ceil_div(d.R, d.rb);
       d.nbr = std::max<int64_t>(1, ceil_div(d.P * d.R, B));
       d.nbc = std::max<int64_t>(1, ceil_div(d.P * d.C, B));

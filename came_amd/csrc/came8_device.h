@@ -66,6 +66,18 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// the same with the alignment of their elements only: gfx9 loads vectors from any address (the
+// compiler emits one global_load_dwordx4 for these as well)
+typedef float f32x4u __attribute__((ext_vector_type(4), aligned(4)));
+
+// 8 consecutive floats from a 4-byte aligned address
+__device__ __forceinline__ void load8u_f32(const CAME8_GLOBAL float* __restrict__ p, float (&out)[8]) {
+  const f32x4u a = *(const CAME8_GLOBAL f32x4u*)p;
+  const f32x4u b = *(const CAME8_GLOBAL f32x4u*)(p + 4);
+  out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+  out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+}
+
 // Load / store 8 consecutive elements (16 or 32 bytes, aligned) of any element type.
 template <typename T>
 __device__ __forceinline__ void load8(const CAME8_GLOBAL typename T::storage* __restrict__ p, float (&out)[8]) {

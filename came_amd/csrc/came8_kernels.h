@@ -331,7 +331,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
     const int64_t nseg = (C + segw - 1) / segw;
     CAME8_GLOBAL float* __restrict__ pU = gbl(t.partU + (b * t.nbands + it.band) * C);
     CAME8_GLOBAL float* __restrict__ pW = gbl(t.partW + (b * t.nbands + it.band) * C);
-    float bandR = 0.0f;  // sum of this band's new row states, in row order (every thread alike)
+    double bandR = 0.0;  // sum of this band's new row states, in row order (every thread alike)
     const float band_eps = float(r1 - r0) * hp.eps0;  // eps0 of each element of a column partial
     // new row state from the row's sum of g^2 (eps0 added once per element count)
     // the old row states go through LDS: a per-row global load inside the stage loop would wait for
@@ -527,7 +527,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
       }
       __syncthreads();  // rowR is reused by the next work item
     }
-    if (tid == 0) t.rsum[b * t.nbands + it.band] = bandR;
+    if (tid == 0) t.rsum[b * t.nbands + it.band] = float(bandR);
     __syncthreads();  // rowold is rewritten by the next work item
   }
 }
@@ -718,9 +718,9 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
       }
       __syncthreads();
       if (tid == 0) {
-        float sum = 0.0f;
+        double sum = 0.0;
         for (int64_t rr = 0; rr < r1 - r0; ++rr) sum += rowval[rr];
-        t.rrsum[b * t.nbands + it.band] = sum;
+        t.rrsum[b * t.nbands + it.band] = float(sum);
       }
       bpar ^= 1;  // the next band writes the other half (after this band's barriers above)
     } else {
@@ -763,7 +763,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
           }
         }
       }
-      float bandRR = 0.0f;  // sum of the band's new residual row states (thread 0, row order)
+      double bandRR = 0.0;  // sum of the band's new residual row states (thread 0, row order)
       for (int64_t r = r0; r < r1; r += S) {
         double ps[S];
 #pragma unroll
@@ -795,7 +795,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
         for (int s = 0; s < S; ++s)
           if (r + s < r1 && tid == 0) bandRR += row_state(b * R + r + s, tot[s]);
       }
-      if (tid == 0) t.rrsum[b * t.nbands + it.band] = bandRR;
+      if (tid == 0) t.rrsum[b * t.nbands + it.band] = float(bandRR);
     }
     __syncthreads();  // rowsc is rewritten by the next work item
   }
@@ -807,14 +807,15 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
 // Work item = one quantisation block of the row state (first nbr items of a
 // tensor) or of the column state (next nbc items).
 
-// Mean row state of matrix b, max(mean, 1e-30): the per-band sums the band pass wrote, added in band
-// order (the reference: R.mean(dim=-1, keepdim=True).clamp_min(1e-30), CAME8bitFull.py:1021,1044).
+// Mean row state of matrix b, max(mean, 1e-30): the per-band sums the band pass wrote (each an fp64
+// sum rounded once), added in band order in fp64 (the reference: R.mean(dim=-1,
+// keepdim=True).clamp_min(1e-30), CAME8bitFull.py:1021,1044).
 __device__ __forceinline__ float matrix_row_mean(const DevTensor& t, const float* __restrict__ bandsum, int64_t b,
                                                  int64_t nb) {
   const float* __restrict__ src = bandsum + b * nb;
-  float s = 0.0f;
-  for (int64_t k = 0; k < nb; ++k) s += src[k];
-  const float m = s / float(t.R);
+  double s = 0.0;
+  for (int64_t k = 0; k < nb; ++k) s += double(src[k]);
+  const float m = float(s) / float(t.R);
   if (t.mode2d) return m > 0.0f ? m : 1.0f;  // 8bit2d: a mean that is not positive counts as 1
   return clamp_min_tiny(m);
 }
@@ -1169,6 +1170,36 @@ __device__ __forceinline__ void p3_math8(const float (&gv)[8], const float (&q)[
   for (int v = 0; v < 8; ++v) pv[v] = param_update<TP>(pv[v], (rri * crj[v]) * m[v], hp);
 }
 
+// p3_math8 for 8 elements that may lie on two rows: a row factor per element
+template <typename TP, bool F32ST>
+__device__ __forceinline__ void p3_math8r(const float (&gv)[8], const float (&q)[8], float (&pv)[8], float (&m)[8],
+                                          float amax_old, const float (&ri)[8], const float (&rri)[8],
+                                          const float (&cj)[8], const float (&crj)[8], float clip, float crcp,
+                                          bool clip_fast, const Hp& hp) {
+  float a[8];
+  DivGuard gd;
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    a[v] = (ri[v] * cj[v]) * gv[v];
+    gd.add(a[v]);
+  }
+  if (__builtin_expect(clip_fast && gd.fast() && (F32ST || fabsf(amax_old) <= 0x1.fffffep127f), 1)) {
+    const float scale = F32ST ? 0.0f : div_fast(amax_old, kSignedQ, kRcpSignedQ);
+#pragma unroll
+    for (int v = 0; v < 8; ++v)
+      m[v] = fmaf(div_fast(a[v], clip, crcp), hp.a1, (F32ST ? q[v] : q[v] * scale) * hp.b1);
+  } else {
+    const float scale = F32ST ? 0.0f : amax_old / kSignedQ;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const float u = (clip_fast && !div_exact_needed(a[v])) ? div_fast(a[v], clip, crcp) : a[v] / clip;
+      m[v] = fmaf(u, hp.a1, (F32ST ? q[v] : q[v] * scale) * hp.b1);
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < 8; ++v) pv[v] = param_update<TP>(pv[v], (rri[v] * crj[v]) * m[v], hp);
+}
+
 // int8 codes of 8 values of a block whose absmax is amax (abits: the block maximum of |m| as bits)
 __device__ __forceinline__ u32x2 p3_quant8(const float (&m)[8], float amax, uint32_t abits) {
   const float arcp = rcp_for_div(amax);
@@ -1222,18 +1253,45 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
     }
     int64_t j = e0 - row * C;
 
-    if (t.vec_ok && t.c8 && base + kTile <= N) {
-      // ---- fast tile: the 8 elements share a row; their column factors are contiguous ----
-      float gv[8], pv[8], q[8], cj[8], crj[8], m[8];
+    if (t.vec_ok && (t.c8 || C >= 8) && base + kTile <= N) {
+      // ---- fast tile: vector access to 8 elements of one quantisation block ----
+      float gv[8], pv[8], q[8], m[8];
       load8<TG>(g + e0, gv);
       load8<TP>(p + e0, pv);
       if constexpr (F32ST) load8<F32>(gbl(st_m(t)) + e0, q);
       else load_codes<8>(mq + e0, q);
       const float amax_old = F32ST ? 0.0f : ma[blk];
-      const float ri = rfac[row], rri = rrfac[row];
-      load8<F32>(cfac + bb * C + j, cj);
-      load8<F32>(crfac + bb * C + j, crj);
-      p3_math8<TP, F32ST>(gv, q, pv, m, amax_old, ri, rri, cj, crj, clip, crcp, clip_fast, hp);
+      if (t.c8) {
+        // the 8 elements share a row; their column factors are contiguous and aligned
+        float cj[8], crj[8];
+        const float ri = rfac[row], rri = rrfac[row];
+        load8<F32>(cfac + bb * C + j, cj);
+        load8<F32>(crfac + bb * C + j, crj);
+        p3_math8<TP, F32ST>(gv, q, pv, m, amax_old, ri, rri, cj, crj, clip, crcp, clip_fast, hp);
+      } else {
+        // rows of C >= 8 elements that are not a whole number of 8-element groups: the 8 elements
+        // lie on at most two rows.  Element v is column j + v of `row`, or, past the row's end,
+        // column j + v - C of row + 1 (which may begin the next matrix).  The factors come as two
+        // unaligned 8-column loads, C apart, and a select per element; the lanes a select drops
+        // read workspace memory next to the factor arrays (each array is padded to 256 bytes and
+        // the column state arrays precede the column factors), never outside the workspace.
+        const int64_t bb1 = (row + 1 - bb * R == R) ? bb + 1 : bb;
+        const float r0 = rfac[row], rr0 = rrfac[row], r1 = rfac[row + 1], rr1 = rrfac[row + 1];
+        float c0[8], cr0[8], c1[8], cr1[8], ri[8], rri[8], cj[8], crj[8];
+        load8u_f32(cfac + bb * C + j, c0);
+        load8u_f32(crfac + bb * C + j, cr0);
+        load8u_f32(cfac + bb1 * C + j - C, c1);
+        load8u_f32(crfac + bb1 * C + j - C, cr1);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const bool wrap = j + v >= C;
+          ri[v] = wrap ? r1 : r0;
+          rri[v] = wrap ? rr1 : rr0;
+          cj[v] = wrap ? c1[v] : c0[v];
+          crj[v] = wrap ? cr1[v] : cr0[v];
+        }
+        p3_math8r<TP, F32ST>(gv, q, pv, m, amax_old, ri, rri, cj, crj, clip, crcp, clip_fast, hp);
+      }
       store8<TP>(p + e0, pv);
       if constexpr (F32ST) {
         store8<F32>(gbl(st_m(t)) + e0, m);
@@ -1733,9 +1791,9 @@ __global__ __launch_bounds__(kThreads) void k_2d_rows(const DevTensor* __restric
     }
     __syncthreads();
     if (tid == 0) {
-      float sum = 0.0f;
+      double sum = 0.0;
       for (int k = 0; k < nrows; ++k) sum += racc[k];
-      t.rrsum[ty] = sum;
+      t.rrsum[ty] = float(sum);
     }
     __syncthreads();  // racc / LDS reused by the next item
   }
@@ -1837,9 +1895,9 @@ __global__ __launch_bounds__(kThreads) void k_2d_res_rows(const DevTensor* __res
     }
     __syncthreads();
     if (tid == 0) {
-      float s = 0.0f;
+      double s = 0.0;
       for (int k = 0; k < nrows; ++k) s += rowval[k];
-      t.rrsum[ty] = s;
+      t.rrsum[ty] = float(s);
     }
     __syncthreads();
   }
