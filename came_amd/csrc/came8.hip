@@ -81,9 +81,9 @@ float round_to_f16(float f) { return float(_Float16(f)); }
 
 // Kernel-variant keys.
 struct BandKey {
-  int gdt, V, K, TPB, st = 0;  // st: fp32 states (pass 2 only)
+  int gdt, V, K, TPB, st = 0, ua = 0;  // st: fp32 states (pass 2 only); ua: rows of any length/alignment
   bool operator<(const BandKey& o) const {
-    return std::tie(gdt, V, K, TPB, st) < std::tie(o.gdt, o.V, o.K, o.TPB, o.st);
+    return std::tie(gdt, V, K, TPB, st, ua) < std::tie(o.gdt, o.V, o.K, o.TPB, o.st, o.ua);
   }
 };
 struct TypeKey {
@@ -145,13 +145,21 @@ int log2_or_minus1(int B) {
 struct BandShapeSel {
   int V, K, TPB;
   bool multiseg;
+  bool ua;  // vector chunks over rows that are not whole chunks or not aligned (V > 1, one sweep)
 };
 
 BandShapeSel band_variant(const came8_tensor& t, int64_t C, int32_t B, int pass) {
   const int vw = t.grad_dtype == CAME8_F32 ? 4 : 8;
   const bool aligned = (C % vw == 0) && (B % vw == 0) && (reinterpret_cast<uintptr_t>(t.grad) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(t.exp_avg_q) % vw == 0);
-  BandShapeSel sel{aligned ? vw : 1, 0, 256, false};
+  BandShapeSel sel{aligned ? vw : 1, 0, 256, false, false};
+  // other rows of at least vw elements take vector chunks with unaligned loads (a partial last chunk
+  // re-reads the row's last vw elements), when one sweep of the widest shape covers them and a chunk
+  // can straddle at most two quantisation blocks
+  if (!aligned && C >= vw && B >= vw && C <= int64_t(512) * 4 * vw) {
+    sel.V = vw;
+    sel.ua = true;
+  }
   const int64_t chunks = ceil_div(C, sel.V);
   (void)pass;  // both passes take the same shapes (wider workgroups cost pass 1 more barrier time)
   static const int vec_k[][2] = {{1, 256}, {2, 256}, {2, 512}, {3, 512}, {4, 512}};
@@ -335,7 +343,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     const TypeKey tk{t.param_dtype, t.grad_dtype, d.fp32st};
     if (d.mode2d) {
       const BandShapeSel sel = band_variant(t, d.C, B, 1);
-      add_item(plan.band[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB}], i, d.nbands);
+      add_item(plan.band[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB, 0, sel.ua}], i, d.nbands);
       add_item(plan.factor, i, d.nbr + d.nbc);
       if (d.v2d) {
         add_item(plan.tiles2d_v[t.grad_dtype], i, d.tr);
@@ -349,8 +357,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     }
     if (t.factored) {
       const BandShapeSel sel1 = band_variant(t, d.C, B, 1), sel2 = band_variant(t, d.C, B, 2);
-      add_item(plan.band[BandKey{t.grad_dtype, sel1.V, sel1.K, sel1.TPB}], i, d.P * d.nbands);
-      add_item(plan.band2[BandKey{t.grad_dtype, sel2.V, sel2.K, sel2.TPB, d.fp32st}], i, d.P * d.nbands);
+      add_item(plan.band[BandKey{t.grad_dtype, sel1.V, sel1.K, sel1.TPB, 0, sel1.ua}], i, d.P * d.nbands);
+      add_item(plan.band2[BandKey{t.grad_dtype, sel2.V, sel2.K, sel2.TPB, d.fp32st, sel2.ua}], i, d.P * d.nbands);
       add_item(plan.factor, i, d.nbr + d.nbc);
       if (fastB) {
         if (d.p3_nbands > 0) add_item(plan.updb[tk], i, d.P * d.p3_nbands * d.p3_nseg);
@@ -508,11 +516,11 @@ Hp make_hp(const came8_hparams& h) {
 // kernel-variant dispatch
 // ---------------------------------------------------------------------------
 // band-pass kernels are instantiated in came8_band.hip (one translation unit per family)
-BandFn band_fn(int gdt, bool pass2, int V, int K, int TPB, int st) {
+BandFn band_fn(int gdt, bool pass2, int V, int K, int TPB, int st, int ua) {
   switch (gdt) {
-    case CAME8_F32: return pass2 ? band_fn_F32_p2(V, K, TPB, st) : band_fn_F32_p1(V, K, TPB, st);
-    case CAME8_BF16: return pass2 ? band_fn_BF16_p2(V, K, TPB, st) : band_fn_BF16_p1(V, K, TPB, st);
-    case CAME8_F16: return pass2 ? band_fn_F16_p2(V, K, TPB, st) : band_fn_F16_p1(V, K, TPB, st);
+    case CAME8_F32: return pass2 ? band_fn_F32_p2(V, K, TPB, st, ua) : band_fn_F32_p1(V, K, TPB, st, ua);
+    case CAME8_BF16: return pass2 ? band_fn_BF16_p2(V, K, TPB, st, ua) : band_fn_BF16_p1(V, K, TPB, st, ua);
+    case CAME8_F16: return pass2 ? band_fn_F16_p2(V, K, TPB, st, ua) : band_fn_F16_p1(V, K, TPB, st, ua);
     default: return nullptr;
   }
 }
@@ -759,7 +767,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     const BandKey& k = kv.first;
     const WorkList& wl = kv.second;
     BandFn fn = nullptr;
-    fn = band_fn(k.gdt, false, k.V, k.K, k.TPB, 0);
+    fn = band_fn(k.gdt, false, k.V, k.K, k.TPB, 0, k.ua);
     if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
     { PhaseTimer pt(PH_PASS1, alg_bytes(plan, wl, tensors, PH_PASS1), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
@@ -804,7 +812,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       const BandKey& k = kv.first;
       const WorkList& wl = kv.second;
       BandFn fn = nullptr;
-      fn = band_fn(k.gdt, true, k.V, k.K, k.TPB, k.st);
+      fn = band_fn(k.gdt, true, k.V, k.K, k.TPB, k.st, k.ua);
       if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
       { PhaseTimer pt(PH_PASS2, alg_bytes(plan, wl, tensors, PH_PASS2), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);

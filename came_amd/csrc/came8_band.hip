@@ -15,16 +15,22 @@ namespace {
 using TG = CAME8_BAND_TYPE;
 constexpr int kVW = 16 / int(sizeof(TG::storage));  // elements per 16-byte chunk
 
-template <int V, int K, int TPB>
+template <int V, int K, int TPB, bool UA = false>
 BandFn pick(int st) {
-  if constexpr (CAME8_BAND_PASS == 2) return st ? k_fact_pass2<TG, V, K, TPB, true> : k_fact_pass2<TG, V, K, TPB, false>;
-  else return (void)st, k_fact_pass1<TG, V, K, TPB>;
+  if constexpr (CAME8_BAND_PASS == 2)
+    return st ? k_fact_pass2<TG, V, K, TPB, true, UA> : k_fact_pass2<TG, V, K, TPB, false, UA>;
+  else return (void)st, k_fact_pass1<TG, V, K, TPB, UA>;
+}
+template <int V, int K, int TPB>
+BandFn pick_ua(int st, int ua) {
+  return ua ? pick<V, K, TPB, true>(st) : pick<V, K, TPB, false>(st);
 }
 }  // namespace
 
-// the (V, K, TPB) variants the host's band_variant() can choose; st selects fp32 states (pass 2)
-BandFn CAME8_BAND_SELECTOR(CAME8_BAND_TYPE, CAME8_BAND_PASS)(int V, int K, int TPB, int st) {
-  if (V == 1 && TPB == 256) {
+// the (V, K, TPB) variants the host's band_variant() can choose; st selects fp32 states (pass 2), ua the
+// variants for rows of any length and alignment
+BandFn CAME8_BAND_SELECTOR(CAME8_BAND_TYPE, CAME8_BAND_PASS)(int V, int K, int TPB, int st, int ua) {
+  if (V == 1 && TPB == 256 && !ua) {
     switch (K) {
       case 1: return pick<1, 1, 256>(st);
       case 2: return pick<1, 2, 256>(st);
@@ -36,11 +42,11 @@ BandFn CAME8_BAND_SELECTOR(CAME8_BAND_TYPE, CAME8_BAND_PASS)(int V, int K, int T
     }
   }
   if (V == kVW) {
-    if (TPB == 256 && K == 1) return pick<kVW, 1, 256>(st);
-    if (TPB == 256 && K == 2) return pick<kVW, 2, 256>(st);
-    if (TPB == 512 && K == 2) return pick<kVW, 2, 512>(st);
-    if (TPB == 512 && K == 3) return pick<kVW, 3, 512>(st);
-    if (TPB == 512 && K == 4) return pick<kVW, 4, 512>(st);
+    if (TPB == 256 && K == 1) return pick_ua<kVW, 1, 256>(st, ua);
+    if (TPB == 256 && K == 2) return pick_ua<kVW, 2, 256>(st, ua);
+    if (TPB == 512 && K == 2) return pick_ua<kVW, 2, 512>(st, ua);
+    if (TPB == 512 && K == 3) return pick_ua<kVW, 3, 512>(st, ua);
+    if (TPB == 512 && K == 4) return pick_ua<kVW, 4, 512>(st, ua);
   }
   return nullptr;
 }

@@ -69,6 +69,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // the same with the alignment of their elements only: gfx9 loads vectors from any address (the
 // compiler emits one global_load_dwordx4 for these as well)
 typedef float f32x4u __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x4u __attribute__((ext_vector_type(4), aligned(2)));
+typedef uint32_t u32x2u __attribute__((ext_vector_type(2), aligned(1)));
+typedef uint32_t u32u __attribute__((aligned(1)));
 
 // 8 consecutive floats from a 4-byte aligned address
 __device__ __forceinline__ void load8u_f32(const CAME8_GLOBAL float* __restrict__ p, float (&out)[8]) {

@@ -164,8 +164,9 @@ constexpr int kMaxBandRows = 256;
 // register buffers).  Wider rows are handled in column segments after a first
 // sweep that forms the row sums.
 
-// V consecutive gradient elements, kept as raw 32-bit words until used (V = 1, or 16 bytes).
-template <typename TG, int V>
+// V consecutive gradient elements, kept as raw 32-bit words until used (V = 1, or 16 bytes; U: the
+// 16 bytes need only the element's alignment).
+template <typename TG, int V, bool U = false>
 struct Chunk {
   static constexpr int NWD = V == 1 ? 1 : 4;
   uint32_t w[NWD];
@@ -175,24 +176,32 @@ struct Chunk {
       else w[0] = uint32_t(p[0]);
     } else {
       static_assert(V * sizeof(typename TG::storage) == 16, "vector chunk must be 16 bytes");
-      const u32x4 r = *(const CAME8_GLOBAL u32x4*)p;
+      using VT = typename std::conditional<U, u32x4u, u32x4>::type;
+      const VT r = *(const CAME8_GLOBAL VT*)p;
       w[0] = r.x; w[1] = r.y; w[2] = r.z; w[3] = r.w;
     }
+  }
+  // elements v < skip read as zero: word i keeps the halves (or the word) at or past `skip`
+  __device__ __forceinline__ void mask(const uint32_t (&m)[NWD]) {
+#pragma unroll
+    for (int i = 0; i < NWD; ++i) w[i] &= m[i];
   }
   __device__ __forceinline__ float operator[](int v) const { return TG::elem(w, v); }
 };
 
-// V consecutive int8 codes (V-byte aligned for V = 4, 8), as raw words.
-template <int V>
+// V consecutive int8 codes (V-byte aligned for V = 4, 8, unless U), as raw words.
+template <int V, bool U = false>
 struct CodeChunk {
   static constexpr int NWD = (V + 3) / 4;
   uint32_t w[NWD];
   __device__ __forceinline__ void load(const CAME8_GLOBAL int8_t* __restrict__ p) {
     if constexpr (V == 8) {
-      const u32x2 r = *(const CAME8_GLOBAL u32x2*)p;
+      using VT = typename std::conditional<U, u32x2u, u32x2>::type;
+      const VT r = *(const CAME8_GLOBAL VT*)p;
       w[0] = r.x; w[1] = r.y;
     } else if constexpr (V == 4) {
-      w[0] = *(const CAME8_GLOBAL uint32_t*)p;
+      using WT = typename std::conditional<U, u32u, uint32_t>::type;
+      w[0] = *(const CAME8_GLOBAL WT*)p;
     } else {
 #pragma unroll
       for (int i = 0; i < NWD; ++i) w[i] = 0;
@@ -205,15 +214,16 @@ struct CodeChunk {
   __device__ __forceinline__ float mold(int v, float scale) const { return code_elem(w, v) * scale; }
 };
 
-// V consecutive fp32 momentum values (fp32-state layout), V-element aligned for V = 4, 8
-template <int V>
+// V consecutive fp32 momentum values (fp32-state layout), V-element aligned for V = 4, 8 unless U
+template <int V, bool U = false>
 struct M32Chunk {
   float m[V];
   __device__ __forceinline__ void load(const CAME8_GLOBAL float* __restrict__ p) {
     if constexpr (V % 4 == 0) {
+      using VT = typename std::conditional<U, f32x4u, f32x4>::type;
 #pragma unroll
       for (int i = 0; i < V / 4; ++i) {
-        const f32x4 r = ((const CAME8_GLOBAL f32x4*)p)[i];
+        const VT r = ((const CAME8_GLOBAL VT*)p)[i];
         m[4 * i] = r.x; m[4 * i + 1] = r.y; m[4 * i + 2] = r.z; m[4 * i + 3] = r.w;
       }
     } else {
@@ -231,6 +241,18 @@ __device__ __forceinline__ void load_codes(const CAME8_GLOBAL int8_t* __restrict
   c.load(q);
 #pragma unroll
   for (int v = 0; v < V; ++v) out[v] = c[v];
+}
+
+// Rows whose length is not a multiple of V (UA variants of the band passes): every chunk is read with
+// unaligned vector loads, and the row's last, partial chunk instead reads the row's last V elements;
+// its first `skip` elements belong to the chunk before it and are masked out.  Word masks for
+// element size es bytes: element v of word i is kept when v >= skip.
+__device__ __forceinline__ uint32_t keep_mask(int i, int skip, int es) {
+  const int lo = i * (4 / es);             // first element of word i
+  const int n = skip - lo;                 // elements of word i to drop
+  if (n <= 0) return 0xffffffffu;
+  if (n >= 4 / es) return 0u;
+  return 0xffffffffu << (8 * es * n);      // little-endian: the low elements go first
 }
 
 // Rows per register stage: about 64 bytes of gradient per thread, 1..16 rows.
@@ -305,7 +327,7 @@ __device__ __forceinline__ Acc acc_fma_w(Acc a, float x, float w) {
 // band, the column partial sums of g^2 + eps0 and of g^2/R_i.  These sums feed the factors, which
 // are held to a relative tolerance rather than a bit pattern: each element costs one fused
 // multiply-add per sum, and eps0 is added once per summed element count instead of per element.
-template <typename TG, int V, int K, int TPB>
+template <typename TG, int V, int K, int TPB, bool UA = false>
 __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                     const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using GS = typename TG::storage;
@@ -367,18 +389,29 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
           colU[k][v] = Acc(0);
           colW[k][v] = 0.0f;
         }
-      Chunk<TG, V> A[S][K], Bf[S][K];
-      int32_t coff[K];
+      using CK = Chunk<TG, V, UA>;
+      CK A[S][K], Bf[S][K];
+      int32_t coff[K], cskip[K];
       bool cok[K];
+      uint32_t gmask[UA ? K : 1][CK::NWD];
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         const int32_t c = (tid + k * TPB) * V;
-        cok[k] = c < C;  // V > 1: C % V == 0, so a chunk that starts inside the row ends inside it
+        cok[k] = c < C;  // without UA, C % V == 0: a chunk that starts inside the row ends inside it
         coff[k] = cok[k] ? c : 0;
+        cskip[k] = 0;
+        if constexpr (UA) {  // the row's partial last chunk reads the row's last V elements
+          if (cok[k] && c + V > C) {
+            coff[k] = int32_t(C) - V;
+            cskip[k] = c - coff[k];
+          }
+#pragma unroll
+          for (int i = 0; i < CK::NWD; ++i) gmask[k][i] = keep_mask(i, cskip[k], int(sizeof(GS)));
+        }
       }
       // rows past the band end read the workspace's zero block (at least TPB*V*K elements long)
       const CAME8_GLOBAL GS* __restrict__ zrow = gbl(static_cast<const GS*>(hp.zeros));
-      auto load_stage = [&](Chunk<TG, V> (&buf)[S][K], int64_t r) __attribute__((always_inline)) {
+      auto load_stage = [&](CK (&buf)[S][K], int64_t r) __attribute__((always_inline)) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           const CAME8_GLOBAL GS* __restrict__ grow = (r + s < r1) ? g + (r + s) * C : zrow;
@@ -386,10 +419,16 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
           for (int k = 0; k < K; ++k) buf[s][k].load(grow + coff[k]);
         }
       };
-      auto process = [&](const Chunk<TG, V> (&buf)[S][K], int64_t r) __attribute__((always_inline)) {
+      auto process = [&](CK (&buf)[S][K], int64_t r) __attribute__((always_inline)) {
         // row partials and the column sums of g^2 (neither needs the row sums), then the row sums
         // over the workgroup, then the column sums of g^2/R_i.  A row past the band end holds zeros
-        // and adds nothing anywhere.
+        // and adds nothing anywhere; so do the masked leading elements of a partial last chunk.
+        if constexpr (UA) {
+#pragma unroll
+          for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int k = 0; k < K; ++k) buf[s][k].mask(gmask[k]);
+        }
         double ps[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
@@ -445,6 +484,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
         if (cok[k]) {
 #pragma unroll
           for (int v = 0; v < V; ++v) {
+            if (UA && v < cskip[k]) continue;
             pU[coff[k] + v] = float(colU[k][v]) + band_eps;
             pW[coff[k] + v] = colW[k][v];
           }
@@ -452,7 +492,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
       }
       __syncthreads();
       for (int64_t rr = tid; rr < r1 - r0; rr += TPB) Rn[b * R + r0 + rr] = rowR[rr];
-    } else {
+    } else if constexpr (!UA) {  // (the host gives UA variants single-sweep rows only)
       // phase A: row sums over all segments
       for (int64_t r = r0; r < r1; r += S) {
         double ps[S];
@@ -541,7 +581,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
 // so d = u - m is the reference's; it then sums d*d with fused multiply-adds and adds eps1 once per
 // summed element count.  The sums differ from the reference's only in the order of addition and the
 // rounding of d*d: a few 1e-8 relative even where one element dominates a short column.
-template <typename TG, int V, int K, int TPB, bool F32ST>
+template <typename TG, int V, int K, int TPB, bool F32ST, bool UA = false>
 __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                     const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using GS = typename TG::storage;
@@ -603,15 +643,26 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
       // first chunk instead, and a row past the band end loads the band's last row; both contribute
       // zero (their r_i, c_j and momentum scale are zero) and their sums are never stored.
       float cj[K][V];
-      int32_t coff[K];
+      int32_t coff[K], cskip[K];
       bool cok[K];
+      uint32_t cmask[UA ? K : 1][CodeChunk<V>::NWD];
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         const int32_t c = (tid + k * TPB) * V;
-        cok[k] = c < C;  // V > 1: C % V == 0, so a chunk that starts inside the row ends inside it
+        cok[k] = c < C;  // without UA, C % V == 0: a chunk that starts inside the row ends inside it
         coff[k] = cok[k] ? c : 0;
+        cskip[k] = 0;
+        if constexpr (UA) {  // the row's partial last chunk reads the row's last V elements
+          if (cok[k] && c + V > C) {
+            coff[k] = int32_t(C) - V;
+            cskip[k] = c - coff[k];
+          }
 #pragma unroll
-        for (int v = 0; v < V; ++v) cj[k][v] = cok[k] ? cf[c + v] : 0.0f;
+          for (int i = 0; i < CodeChunk<V>::NWD; ++i) cmask[k][i] = keep_mask(i, cskip[k], 1);
+        }
+        // a masked leading element has c_j = 0 (so u = 0) and a zeroed code (so m = 0)
+#pragma unroll
+        for (int v = 0; v < V; ++v) cj[k][v] = (cok[k] && v >= cskip[k]) ? cf[coff[k] + v] : 0.0f;
       }
       Acc colR[K][V];
 #pragma unroll
@@ -627,13 +678,20 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
       auto run = [&](auto AL, auto ST) __attribute__((always_inline)) {
         constexpr bool kF32 = decltype(ST)::value;
         constexpr bool kAligned = decltype(AL)::value && !kF32;
-        using MB = typename std::conditional<kF32, M32Chunk<V>, CodeChunk<V>>::type;
+        using MB = typename std::conditional<kF32, M32Chunk<V, UA>, CodeChunk<V, UA>>::type;
         // a stage: S rows of gradient chunks, momentum chunks and (8-bit states) the chunks' block
-        // absmax, all issued together so that waiting for one stage never waits for the next
-        Chunk<TG, V> gA[S][K], gB[S][K];
-        MB qA[S][K], qB[S][K];
-        float aA[S][K], aB[S][K];
-        auto load_stage = [&](Chunk<TG, V> (&gb)[S][K], MB (&qb)[S][K], float (&ab)[S][K], int64_t r) __attribute__((always_inline)) {
+        // absmax, all issued together so that waiting for one stage never waits for the next.
+        // UA: a chunk may straddle two quantisation blocks; it holds both scales and the number of
+        // its elements in the first block.
+        struct StageBuf {
+          Chunk<TG, V, UA> g[S][K];
+          MB q[S][K];
+          float a[S][K];
+          float a2[UA ? S : 1][UA ? K : 1];
+          int32_t split[UA ? S : 1][UA ? K : 1];
+        };
+        StageBuf A, Bs;
+        auto load_stage = [&](StageBuf& sb, int64_t r) __attribute__((always_inline)) {
 #pragma unroll
           for (int s = 0; s < S; ++s) {
             const int64_t rs = (r + s < r1) ? (r + s) : (r1 - 1);
@@ -641,17 +699,27 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
             const CAME8_GLOBAL float* __restrict__ marow = kAligned ? ma + blk_of_nb(erow, hp) : ma;
 #pragma unroll
             for (int k = 0; k < K; ++k) {
-              gb[s][k].load(g + rs * C + coff[k]);
+              sb.g[s][k].load(g + rs * C + coff[k]);
               if constexpr (kF32) {
-                qb[s][k].load(m32 + rs * C + coff[k]);
+                sb.q[s][k].load(m32 + rs * C + coff[k]);
+              } else if constexpr (UA) {
+                sb.q[s][k].load(mq + rs * C + coff[k]);
+                const int64_t e0 = erow + coff[k];
+                const int64_t b0 = blk_of_nb(e0, hp), b1 = blk_of_nb(e0 + V - 1, hp);
+                sb.a[s][k] = ma[b0];
+                sb.a2[s][k] = ma[b1];
+                sb.split[s][k] = int32_t((b0 + 1) * int64_t(hp.B) - e0);
               } else {
-                qb[s][k].load(mq + rs * C + coff[k]);
-                ab[s][k] = kAligned ? marow[cbk[k]] : ma[blk_of_nb(erow + coff[k], hp)];
+                sb.q[s][k].load(mq + rs * C + coff[k]);
+                sb.a[s][k] = kAligned ? marow[cbk[k]] : ma[blk_of_nb(erow + coff[k], hp)];
               }
             }
           }
         };
-        auto process = [&](const Chunk<TG, V> (&gb)[S][K], const MB (&qb)[S][K], const float (&ab)[S][K], int64_t r) __attribute__((always_inline)) {
+        auto process = [&](StageBuf& sb, int64_t r) __attribute__((always_inline)) {
+          auto& gb = sb.g;
+          auto& qb = sb.q;
+          auto& ab = sb.a;
           double ps[S];
 #pragma unroll
           for (int s = 0; s < S; ++s) {
@@ -663,13 +731,19 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
             for (int k = 0; k < K; ++k) {
               const bool ok = rok && cok[k];
               // momentum scale absmax/127 (fp32 states: 1), zero for a chunk that counts for nothing
-              float sc;
+              float sc, sc2 = 0.0f;
               if constexpr (kF32) sc = ok ? 1.0f : 0.0f;
               else sc = ok ? div_fast(ab[s][k], kSignedQ, kRcpSignedQ) : 0.0f;
+              if constexpr (UA && !kF32) {
+                sc2 = ok ? div_fast(sb.a2[s][k], kSignedQ, kRcpSignedQ) : 0.0f;
+                qb[s][k].w[0] &= cmask[k][0];
+                if constexpr (CodeChunk<V>::NWD > 1) qb[s][k].w[1] &= cmask[k][1];
+              }
 #pragma unroll
               for (int v = 0; v < V; ++v) {
                 float mo;
-                if constexpr (kF32) mo = qb[s][k].m[v] * sc;
+                if constexpr (kF32) mo = (UA && v < cskip[k]) ? 0.0f : qb[s][k].m[v] * sc;
+                else if constexpr (UA) mo = qb[s][k][v] * (v < sb.split[s][k] ? sc : sc2);
                 else mo = qb[s][k][v] * sc;
                 const float d = d_of(ri, cj[k][v], gb[s][k][v], mo);
                 ps[s] = acc_fma(ps[s], d, d);
@@ -689,22 +763,24 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
         // two register stages in flight; the prefetches are unconditional (rows past the band end
         // reload its last row, from cache, and count for nothing)
         wait_vm_all();
-        load_stage(gA, qA, aA, r0);
+        load_stage(A, r0);
         for (int64_t r = r0; r < r1; r += 2 * S) {
-          load_stage(gB, qB, aB, r + S);
-          process(gA, qA, aA, r);
-          load_stage(gA, qA, aA, r + 2 * S);
-          process(gB, qB, aB, r + S);
+          load_stage(Bs, r + S);
+          process(A, r);
+          load_stage(A, r + 2 * S);
+          process(Bs, r + S);
         }
       };
       if constexpr (F32ST) run(std::false_type{}, std::true_type{});
+      else if constexpr (UA) run(std::false_type{}, std::false_type{});
       else if (t.rowal) run(std::true_type{}, std::false_type{});
       else run(std::false_type{}, std::false_type{});
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         if (cok[k]) {
 #pragma unroll
-          for (int v = 0; v < V; ++v) pR[coff[k] + v] = float(colR[k][v]) + band_eps;
+          for (int v = 0; v < V; ++v)
+            if (!UA || v >= cskip[k]) pR[coff[k] + v] = float(colR[k][v]) + band_eps;
         }
       }
       __syncthreads();
@@ -723,7 +799,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
         t.rrsum[b * t.nbands + it.band] = float(sum);
       }
       bpar ^= 1;  // the next band writes the other half (after this band's barriers above)
-    } else {
+    } else if constexpr (!UA) {  // (the host gives UA variants single-sweep rows only)
       // rows wider than one sweep of the workgroup: column partials segment by segment, then the
       // row sums over whole rows (the gradient and codes are read twice)
       auto e_at = [&](float ri, float cjv, float x, int64_t e) {
