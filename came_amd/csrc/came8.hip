@@ -35,8 +35,9 @@ constexpr size_t kAlign = 256;
 size_t align_up(size_t x, size_t a = kAlign) { return (x + a - 1) / a * a; }
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// A launch of few bands leaves most CUs idle (one 2048x2048 matrix is 8 bands): bands are halved
-// (down to kMinShrunkBandRows rows) until the band passes have about kMinLaunchBands work items.
+// A launch of few bands leaves most CUs idle (one 2048x2048 matrix is 8 bands): the bands of the
+// tensors one band launch steps together are halved (down to kMinShrunkBandRows rows) until that
+// launch has about kMinLaunchBands work items.
 constexpr int64_t kMinShrunkBandRows = 8;
 constexpr int64_t kMinLaunchBands = 2048;
 
@@ -50,19 +51,6 @@ int64_t band_rows(int64_t R, int64_t C, int shrink = 0) {
   return std::min<int64_t>(rb, R);
 }
 
-int band_shrink(const came8_tensor* ts, int32_t n) {  // the 2^shrink of band_rows for a launch
-  int shrink = 0;
-  for (; shrink < 6; ++shrink) {
-    int64_t bands = 0;
-    for (int i = 0; i < n; ++i) {
-      const came8_tensor& t = ts[i];
-      if (!t.factored || t.rows < 1 || t.cols < 1 || t.prefix < 1) continue;
-      bands += t.prefix * ceil_div(t.rows, band_rows(t.rows, t.cols, shrink));
-    }
-    if (bands >= kMinLaunchBands) break;
-  }
-  return shrink;
-}
 
 int elem_size(int dt) { return dt == CAME8_F32 ? 4 : 2; }
 
@@ -187,6 +175,29 @@ void magic_div(int64_t d, uint64_t& m, uint32_t& s) {
   m = uint64_t(((__uint128_t(1) << s) / uint64_t(d)) + 1);
 }
 
+// The 2^shrink of band_rows for every tensor: tensors that share a band-pass kernel variant (one
+// launch) share a shrink, the least that gives their launch kMinLaunchBands work items (at most 6).
+std::vector<int> band_shrinks(const came8_tensor* ts, int32_t n, int32_t B) {
+  std::vector<int> out(n, 0);
+  std::map<BandKey, std::vector<int>> groups;
+  for (int i = 0; i < n; ++i) {
+    const came8_tensor& t = ts[i];
+    if (!t.factored || t.rows < 1 || t.cols < 1 || t.prefix < 1) continue;
+    const BandShapeSel sel = band_variant(t, t.cols, B, 1);
+    groups[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB, 0, sel.ua}].push_back(i);
+  }
+  for (auto& kv : groups) {
+    int shrink = 0;
+    for (; shrink < 6; ++shrink) {
+      int64_t bands = 0;
+      for (int i : kv.second) bands += ts[i].prefix * ceil_div(ts[i].rows, band_rows(ts[i].rows, ts[i].cols, shrink));
+      if (bands >= kMinLaunchBands) break;
+    }
+    for (int i : kv.second) out[i] = shrink;
+  }
+  return out;
+}
+
 int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refnorm, char* ws_base, Plan& plan) {
   (void)flags_refnorm;
   if (n < 0) return fail(CAME8_EINVAL, "came8: n_tensors must be >= 0");
@@ -196,7 +207,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
   // --- scratch layout (after the plan blob; offsets relative to the scratch start) ---
   std::vector<size_t> scr_off(n, 0);
   size_t scr = 0;
-  const int shrink = band_shrink(ts, n);
+  const std::vector<int> shrink = (B > 0 && n > 0) ? band_shrinks(ts, n, B) : std::vector<int>(std::max(n, 0), 0);
   for (int i = 0; i < n; ++i) {
     const came8_tensor& t = ts[i];
     const std::string who = "came8: tensor " + std::to_string(i) + ": ";
@@ -282,7 +293,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     magic_div(d.C, d.mC, d.sC);
     magic_div(d.R, d.mR, d.sR);
     if (t.factored) {
-      d.rb = band_rows(d.R, d.C, shrink);
+      d.rb = band_rows(d.R, d.C, shrink[i]);
       d.nbands = ceil_div(d.R, d.rb);
       d.nbr = std::max<int64_t>(1, ceil_div(d.P * d.R, B));
       d.nbc = std::max<int64_t>(1, ceil_div(d.P * d.C, B));
