@@ -883,31 +883,76 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
 // Work item = one quantisation block of the row state (first nbr items of a
 // tensor) or of the column state (next nbc items).
 
+// Loads per batch of the strided sums below: a batch is issued before its first add, so a column
+// sum over n partials waits for n / kSumBatch memory round trips instead of n.
+constexpr int kSumBatch = 16;
+
+// sum of n floats at stride s in fp64, in index order
+__device__ __forceinline__ double ordered_sum_f64(const float* __restrict__ p, int64_t n, int64_t s) {
+  double acc = 0.0;
+  int64_t k = 0;
+  for (; k + kSumBatch <= n; k += kSumBatch) {
+    float v[kSumBatch];
+#pragma unroll
+    for (int u = 0; u < kSumBatch; ++u) v[u] = p[(k + u) * s];
+#pragma unroll
+    for (int u = 0; u < kSumBatch; ++u) acc += double(v[u]);
+  }
+  for (; k < n; ++k) acc += double(p[k * s]);
+  return acc;
+}
+
+// sum of n floats at stride s in fp32, in index order from 0.0f (a running sum, as a sequential loop)
+__device__ __forceinline__ float ordered_sum_f32(const float* __restrict__ p, int64_t n, int64_t s) {
+  float acc = 0.0f;
+  int64_t k = 0;
+  for (; k + kSumBatch <= n; k += kSumBatch) {
+    float v[kSumBatch];
+#pragma unroll
+    for (int u = 0; u < kSumBatch; ++u) v[u] = p[(k + u) * s];
+#pragma unroll
+    for (int u = 0; u < kSumBatch; ++u) acc += v[u];
+  }
+  for (; k < n; ++k) acc += p[k * s];
+  return acc;
+}
+
 // Mean row state of matrix b, max(mean, 1e-30): the per-band sums the band pass wrote (each an fp64
 // sum rounded once), added in band order in fp64 (the reference: R.mean(dim=-1,
 // keepdim=True).clamp_min(1e-30), CAME8bitFull.py:1021,1044).
 __device__ __forceinline__ float matrix_row_mean(const DevTensor& t, const float* __restrict__ bandsum, int64_t b,
                                                  int64_t nb) {
-  const float* __restrict__ src = bandsum + b * nb;
-  double s = 0.0;
-  for (int64_t k = 0; k < nb; ++k) s += double(src[k]);
+  const double s = ordered_sum_f64(bandsum + b * nb, nb, 1);
   const float m = float(s) / float(t.R);
   if (t.mode2d) return m > 0.0f ? m : 1.0f;  // 8bit2d: a mean that is not positive counts as 1
   return clamp_min_tiny(m);
 }
 
-// sum over the nbands band partials of one column (stride C), four interleaved accumulators
-__device__ __forceinline__ double band_column_sum(const float* __restrict__ pp, int64_t nbands, int64_t C) {
-  double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+// Sums over the nbands band partials of one column (stride C) of one or two partial arrays: four
+// interleaved fp64 accumulators (band k into accumulator k % 4), combined as (a0 + a1) + (a2 + a3).
+template <int NA>
+__device__ __forceinline__ void band_column_sums(const float* __restrict__ p0, const float* __restrict__ p1,
+                                                 int64_t nbands, int64_t C, double* out) {
+  double a[NA][4] = {};
   int64_t k = 0;
-  for (; k + 4 <= nbands; k += 4) {
-    a0 += double(pp[k * C]);
-    a1 += double(pp[(k + 1) * C]);
-    a2 += double(pp[(k + 2) * C]);
-    a3 += double(pp[(k + 3) * C]);
+  for (; k + kSumBatch <= nbands; k += kSumBatch) {
+    float v[NA][kSumBatch];
+#pragma unroll
+    for (int u = 0; u < kSumBatch; ++u) {
+      v[0][u] = p0[(k + u) * C];
+      if constexpr (NA > 1) v[NA - 1][u] = p1[(k + u) * C];
+    }
+#pragma unroll
+    for (int x = 0; x < NA; ++x)
+#pragma unroll
+      for (int u = 0; u < kSumBatch; ++u) a[x][u & 3] += double(v[x][u]);
   }
-  for (; k < nbands; ++k) a0 += double(pp[k * C]);
-  return (a0 + a1) + (a2 + a3);
+  for (; k < nbands; ++k) {
+    a[0][0] += double(p0[k * C]);
+    if constexpr (NA > 1) a[NA - 1][0] += double(p1[k * C]);
+  }
+#pragma unroll
+  for (int x = 0; x < NA; ++x) out[x] = (a[x][0] + a[x][1]) + (a[x][2] + a[x][3]);
 }
 template <bool RES>
 __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
@@ -964,19 +1009,27 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
         const int64_t j = i - b * t.C;
         float* __restrict__ cst = RES ? t.ca : st_sq_col(t);  // fp32 column state
         float Cold, Cv;
+        double W = 0.0;  // column sum of the clip weights (!RES)
         if (t.mode2d) {
           // 8bit2d: residual column sums come from the tile partials (tiles in order); no clamp
           float s2 = 0.0f;
           if (RES) {
-            for (int64_t ty = 0; ty < t.tr; ++ty) s2 += t.t2col[ty * t.C + i];
+            s2 = ordered_sum_f32(t.t2col + i, t.tr, t.C);
           } else {
-            s2 = float(band_column_sum(part + (b * t.nbands) * t.C + j, t.nbands, t.C));
+            double sw[2];
+            band_column_sums<2>(part + (b * t.nbands) * t.C + j, t.partW + (b * t.nbands) * t.C + j, t.nbands, t.C, sw);
+            s2 = float(sw[0]);
+            W = sw[1];
           }
           Cold = RES ? deq_u8(t.rcq[i], t.rca[blk_of(i, hp)]) : deq_u8(t.cq[i], t.ca[blk_of(i, hp)]);
           Cv = (Cold * beta) + (alpha_f * (s2 / fR));
         } else {
           const float* __restrict__ pp = part + (b * t.nbands) * t.C + j;
-          const double s = band_column_sum(pp, t.nbands, t.C);
+          double sw[2] = {0.0, 0.0};  // column sums of the partials, and for !RES of the clip weights
+          if (RES) band_column_sums<1>(pp, nullptr, t.nbands, t.C, sw);
+          else band_column_sums<2>(pp, t.partW + (b * t.nbands) * t.C + j, t.nbands, t.C, sw);
+          const double s = sw[0];
+          W = sw[1];
           Cold = t.fp32st ? cst[i] : deq_u8(t.cq[off + i], t.ca[aoff + blk_of(i, hp)]);
           Cv = clamp_min_tiny(fmaf(float(s) / fR, alpha, Cold * beta));
         }
@@ -986,8 +1039,6 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
         if (t.fp32st) cst[i] = Cv;
         vmax = nan_max(vmax, Cv);
         if (!RES) {
-          const float* __restrict__ pw = t.partW + (b * t.nbands) * t.C + j;
-          const double W = band_column_sum(pw, t.nbands, t.C);
           if (b != cmb) {
             cmb = b;
             crm = matrix_row_mean(t, t.rsum, b, t.nbands);
