@@ -1791,9 +1791,17 @@ __global__ __launch_bounds__(kThreads) void k_generic_update(const DevTensor* __
 // came_kernels.cu:2584-2684, 2685-2780, 3333-3367)
 // ===========================================================================
 constexpr int kTile2 = 16;
-constexpr int kParam2Items = 4096;  // elements per work item of the vector parameter write
+constexpr int kParam2Groups = 4;                    // 8-element groups per thread of the vector parameter write
+constexpr int kParam2Items = kParam2Groups * kTile;  // elements per work item of the vector parameter write
 
-// one element of the momentum pass: u = (g*r)*c / clip; m = m_old*b1 + u*(1-b1); res = (u - m)^2 + eps1
+// one element of the momentum pass from its clipped update u = (g*r)*c / clip:
+// m = m_old*b1 + u*(1-b1); res = (u - m)^2 + eps1
+__device__ __forceinline__ void m2d_from_u(float u, float mold, const Hp& hp, float& m, float& res) {
+  const float mn = (mold * hp.b1) + (u * hp.a1f);
+  const float d = u - mn;
+  m = mn;
+  res = (d * d) + hp.eps1;
+}
 __device__ __forceinline__ void m2d_elem(float gv, float ri, float cj, float clip, float mold, const Hp& hp, float& m,
                                          float& res) {
   const float u = ((gv * ri) * cj) / clip;
@@ -1805,7 +1813,7 @@ __device__ __forceinline__ void m2d_elem(float gv, float ri, float cj, float cli
 
 // residual row state of one row from its sum over the tiles: RR_old*b3 + (1-b3)*(sum/C)
 __device__ __forceinline__ float rr2d_new(const DevTensor& t, int64_t row, float sum, const Hp& hp) {
-  const float old = deq_u8(t.rrq[row], t.rra[blk_of(row, hp)]);
+  const float old = deq_u8(gbl(t.rrq)[row], gbl(t.rra)[blk_of(row, hp)]);
   return (old * hp.b3) + (hp.a3f * (sum / float(t.C)));
 }
 
@@ -1840,8 +1848,12 @@ __global__ __launch_bounds__(kThreads) void k_2d_rows(const DevTensor* __restric
     CAME8_GLOBAL int8_t* __restrict__ qrow = gbl(t.mq + row * C);
     const CAME8_GLOBAL float* __restrict__ cf = gbl(static_cast<const float*>(t.cfac));
     CAME8_GLOBAL float* __restrict__ ma = gbl(t.ma + ty * tc);
-    const float clip = uniform_f32(t.clip[0]);
-    const float ri = t.rfac[row];
+    // global (not generic) stores: a generic store also counts in the LDS counter, and the wait for
+    // the LDS writes before each barrier would then wait for the store to reach memory
+    CAME8_GLOBAL float* __restrict__ t2col = gbl(t.t2col + ty * C);
+    const float clip = uniform_f32(t.clip[0]), crcp = uniform_f32(t.clip[1]);
+    const bool clip_fast = crcp == crcp;  // the reciprocal division serves this divisor
+    const float ri = gbl(t.rfac)[row];
     if (tid < kTile2) racc[tid] = 0.0f;
     for (int64_t tx0 = 0; tx0 < tc; tx0 += kTile2) {
       const int64_t tx = tx0 + wid * 4 + s;
@@ -1858,8 +1870,10 @@ __global__ __launch_bounds__(kThreads) void k_2d_rows(const DevTensor* __restric
         const u32x4 q = *(const CAME8_GLOBAL u32x4*)(qrow + c0);
         const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
         const float am_old = ma[tx];
-        const float sc_old = am_old / kSignedQ;
-        const bool have_m = am_old > 0.0f;
+        // u = (g*r)*c / clip: the reciprocal division where it gives the quotient exactly (every
+        // numerator of the chunk zero or in its range), else the IEEE division element by element
+        float u[kTile2];
+        DivGuard gd;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const f32x4 c4 = *(const CAME8_GLOBAL f32x4*)(cf + c0 + 4 * k);
@@ -1867,12 +1881,26 @@ __global__ __launch_bounds__(kThreads) void k_2d_rows(const DevTensor* __restric
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int j = 4 * k + v;
-            const float gv = j < 8 ? ga[j] : gb[j - 8];
-            const float mold = have_m ? code_elem(qw, j) * sc_old : 0.0f;
-            m2d_elem(gv, ri, cv[v], clip, mold, hp, m[j], res[j]);
-            abits = max(abits, abs_bits(m[j]));
-            rsum += res[j];
+            u[j] = ((j < 8 ? ga[j] : gb[j - 8]) * ri) * cv[v];
+            gd.add(u[j]);
           }
+        }
+        if (__builtin_expect(clip_fast && gd.fast(), 1)) {
+#pragma unroll
+          for (int j = 0; j < kTile2; ++j) u[j] = div_fast(u[j], clip, crcp);
+        } else {
+#pragma unroll
+          for (int j = 0; j < kTile2; ++j)
+            u[j] = (clip_fast && !div_exact_needed(u[j])) ? div_fast(u[j], clip, crcp) : u[j] / clip;
+        }
+        const float sc_old = scale_s8(am_old);  // after the loads: its rare branch would wait for am_old
+        const bool have_m = am_old > 0.0f;
+#pragma unroll
+        for (int j = 0; j < kTile2; ++j) {
+          const float mold = have_m ? code_elem(qw, j) * sc_old : 0.0f;
+          m2d_from_u(u[j], mold, hp, m[j], res[j]);
+          abits = max(abits, abs_bits(m[j]));
+          rsum += res[j];
         }
       } else {
 #pragma unroll
@@ -1901,7 +1929,7 @@ __global__ __launch_bounds__(kThreads) void k_2d_rows(const DevTensor* __restric
         float cs = 0.0f;
 #pragma unroll
         for (int k = 0; k < kTile2; ++k) cs += xres[wid][s * kTile2 + k][i];
-        t.t2col[ty * C + c0 + i] = cs;
+        t2col[c0 + i] = cs;
       }
       if (tid < nrows) {
         float a = racc[tid];
@@ -1913,14 +1941,14 @@ __global__ __launch_bounds__(kThreads) void k_2d_rows(const DevTensor* __restric
     }
     if (tid < nrows) {
       const float v = rr2d_new(t, r0 + tid, racc[tid], hp);
-      t.RRn[r0 + tid] = v;
+      gbl(t.RRn)[r0 + tid] = v;
       racc[tid] = v;
     }
     __syncthreads();
     if (tid == 0) {
       double sum = 0.0;
       for (int k = 0; k < nrows; ++k) sum += racc[k];
-      t.rrsum[ty] = float(sum);
+      gbl(t.rrsum)[ty] = float(sum);
     }
     __syncthreads();  // racc / LDS reused by the next item
   }
@@ -2040,37 +2068,54 @@ __device__ __forceinline__ float p2d_new(float pv, float code, float sc, float r
   return fmaf(step, hp.alr, pv);
 }
 
-// Parameter write, vector form (C a multiple of 16; parameter and codes 16-byte aligned): a thread
-// takes one tile row of 16 elements, 4096 elements per work item.
+// Parameter write, vector form (C a multiple of 16; parameter and codes 16-byte aligned).  A thread
+// takes kParam2Groups groups of 8 consecutive elements (half a tile row each), kTile elements apart,
+// and issues the loads of all its groups before the first arithmetic, so that one memory round
+// trip serves kParam2Items elements per workgroup.  A group past the end loads the tensor's last
+// group instead and stores nothing.
 template <typename TP>
 __global__ __launch_bounds__(kThreads) void k_2d_param_v(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                          const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using PS = typename TP::storage;
+  constexpr int G = kParam2Groups;
   const int tid = threadIdx.x;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
     const int slot = find_slot(wstart, ntens, w);
     const DevTensor& t = T[tids[slot]];
-    const int64_t e0 = (w - wstart[slot]) * kParam2Items + int64_t(tid) * kTile2;
-    if (e0 >= t.N) continue;
-    const int64_t row = t.idx32 ? int64_t(udiv_magic(uint32_t(e0), t.mC, t.sC)) : e0 / t.C;
-    const int64_t c0 = e0 - row * t.C;
-    CAME8_GLOBAL PS* __restrict__ p = gbl(static_cast<PS*>(t.p) + e0);
-    const u32x4 q = *(const CAME8_GLOBAL u32x4*)gbl(t.mq + e0);
-    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-    const float sc = t.ma[(row >> 4) * t.tc + (c0 >> 4)] / kSignedQ;
-    const float rr = t.rrfac[row];
-    const CAME8_GLOBAL float* __restrict__ crp = gbl(static_cast<const float*>(t.crfac) + c0);
+    const int64_t base = (w - wstart[slot]) * kParam2Items + int64_t(tid) * 8;
+    CAME8_GLOBAL PS* __restrict__ p = gbl(static_cast<PS*>(t.p));
+    const CAME8_GLOBAL int8_t* __restrict__ mq = gbl(t.mq);
+    const CAME8_GLOBAL float* __restrict__ ma = gbl(t.ma);
+    const CAME8_GLOBAL float* __restrict__ rrfac = gbl(t.rrfac);
+    const CAME8_GLOBAL float* __restrict__ crfac = gbl(static_cast<const float*>(t.crfac));
+    Raw8<TP> praw[G];
+    u32x2 q[G];
+    float am[G], rr[G], cr[G][8];
+    bool ok[G];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int gi = 0; gi < G; ++gi) {
+      const int64_t e = base + int64_t(gi) * kTile;
+      ok[gi] = e < t.N;
+      const int64_t el = ok[gi] ? e : t.N - 8;
+      const int64_t row = t.idx32 ? int64_t(udiv_magic(uint32_t(el), t.mC, t.sC)) : el / t.C;
+      const int64_t c0 = el - row * t.C;
+      praw[gi].load(p + el);
+      q[gi] = *(const CAME8_GLOBAL u32x2*)(mq + el);
+      am[gi] = ma[(row >> 4) * t.tc + (c0 >> 4)];
+      rr[gi] = rrfac[row];
+      load8<F32>(crfac + c0, cr[gi]);
+    }
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      if (!ok[gi]) continue;
+      const int64_t e = base + int64_t(gi) * kTile;
+      const uint32_t qw[2] = {q[gi].x, q[gi].y};
+      const float sc = am[gi] / kSignedQ;
       float pv[8];
-      load8<TP>(p + 8 * h, pv);
-      const f32x4 ca = *(const CAME8_GLOBAL f32x4*)(crp + 8 * h);
-      const f32x4 cb = *(const CAME8_GLOBAL f32x4*)(crp + 8 * h + 4);
-      const float cr[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
 #pragma unroll
-      for (int v = 0; v < 8; ++v) pv[v] = p2d_new<TP>(pv[v], code_elem(qw, 8 * h + v), sc, rr, cr[v], hp);
-      store8<TP>(p + 8 * h, pv);
+      for (int v = 0; v < 8; ++v) pv[v] = p2d_new<TP>(praw[gi][v], code_elem(qw, v), sc, rr[gi], cr[gi][v], hp);
+      store8<TP>(p + e, pv);
     }
   }
 }
