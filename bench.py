@@ -65,8 +65,38 @@ def gpt2_medium_shapes():
     return shapes
 
 
+def ragged_shapes(seed=0):
+    """500 tensors -- 250 1-D lengths U{1..4097}; the 2-D shapes 1000x3, 3x50257 and
+    4097x129; conv weights 320x320x3x3 and 1280x640x1x1; 245 2-D shapes with rows and columns drawn from
+    [1, 5000] outside multiples of 64."""
+    gen = torch.Generator().manual_seed(seed)
+    shapes = [(int(n),) for n in torch.randint(1, 4098, (250,), generator=gen)]
+    shapes += [(1000, 3), (3, 50257), (4097, 129), (320, 320, 3, 3), (1280, 640, 1, 1)]
+    while len(shapes) < 500:
+        r, c = (int(x) for x in torch.randint(1, 5001, (2,), generator=gen))
+        if r % 64 and c % 64:
+            shapes.append((r, c))
+    return shapes
+
+
+def heavy_grad(shape, gen, dtype, device="cuda"):
+    """1e-3 * Student-t(nu=2) (a normal over sqrt(Exp(1)), i.e. over sqrt(chi2_2 / 2)), 10% exact zeros,
+    and in each flat block of 256 elements, with probability 1/2, one element set to +-1e3."""
+    n = math.prod(shape)
+    z = torch.randn(n, device=device, generator=gen)
+    e = torch.rand(n, device=device, generator=gen).clamp_min_(1e-30).log_().neg_()
+    g = z.div_(e.sqrt_()).mul_(1e-3)
+    g.masked_fill_(torch.rand(n, device=device, generator=gen) < 0.1, 0.0)
+    nb = (n + 255) // 256
+    pos = torch.arange(nb, device=device) * 256 + torch.randint(0, 256, (nb,), device=device, generator=gen)
+    pick = (torch.rand(nb, device=device, generator=gen) < 0.5) & (pos < n)
+    sign = torch.where(torch.rand(nb, device=device, generator=gen) < 0.5, -1e3, 1e3)
+    g[pos[pick]] = sign[pick]
+    return g.reshape(shape).to(dtype)
+
+
 CONFIGS = {
-    # name: (workload label, shapes, param dtype, grad dtype, grad std, optimizer, hparams)
+    # name: (workload label, shapes, param dtype, grad dtype, grad std (None: heavy_grad), optimizer, hparams)
     "c4": ("llama7b-shape/CAME8bit/bf16", lambda: llama_shapes(32, 4096, 11008, 32000), torch.bfloat16,
            torch.bfloat16, 2e-4, "CAME8bit", dict(lr=2e-4, weight_decay=1e-2, betas=(0.9, 0.999, 0.9999))),
     "c3": ("llama1b-style/CAME8bitMemory/bf16", lambda: llama_shapes(24, 2048, 5461, 32000), torch.bfloat16,
@@ -82,6 +112,9 @@ CONFIGS = {
     # the same Llama-7B set stepped by CAMECUDA (fp32 optimizer states)
     "c4fp": ("llama7b-shape/CAMECUDA/bf16", lambda: llama_shapes(32, 4096, 11008, 32000), torch.bfloat16,
              torch.bfloat16, 2e-4, "CAMECUDA", dict(lr=2e-4, weight_decay=1e-2, betas=(0.9, 0.999, 0.9999))),
+    # the ragged stress set, heavy-tailed gradients, CAME8bitFull
+    "c5": ("ragged-500/CAME8bitFull/fp32", ragged_shapes, torch.float32, torch.float32, None, "CAME8bitFull",
+           dict(lr=2e-4, weight_decay=1e-2)),
 }
 
 
@@ -129,7 +162,7 @@ def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False, tiles=F
     sample = [distinct[0]] + ([distinct[-1]] if len(distinct) > 1 else []) + vec[:1]
     gen = torch.Generator().manual_seed(123)
     params = [(torch.randn(s, generator=gen) * 0.02).to(pdt) for s in sample]
-    grads = [(torch.randn(s, generator=gen) * gstd).to(gdt) for s in sample]
+    grads = [(torch.randn(s, generator=gen) * (gstd or 1e-3)).to(gdt) for s in sample]
     b1, b2, b3 = hp.get("betas", (0.9, 0.999, 0.9999))
     ohp = dict(beta1=b1, beta2=b2, beta3=b3, eps0=1e-30, eps1=1e-16, lr=hp["lr"], clip_threshold=1.0,
                weight_decay=hp.get("weight_decay", 0.0), block_size=256)
@@ -211,7 +244,10 @@ def main():
     params, grads = [], []
     for s in shapes:
         p = torch.randn(s, device=dev, dtype=torch.float32, generator=gen).mul_(0.02).to(pdt)
-        g = torch.randn(s, device=dev, dtype=torch.float32, generator=gen).mul_(gstd).to(gdt)
+        if gstd is None:
+            g = heavy_grad(s, gen, gdt, device=dev)
+        else:
+            g = torch.randn(s, device=dev, dtype=torch.float32, generator=gen).mul_(gstd).to(gdt)
         params.append(torch.nn.Parameter(p))
         params[-1].grad = g
         grads.append(g)
@@ -263,7 +299,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded N(0,0.02^2) params, N(0,std^2) grads, resident in HBM)",
+        "data": "synthetic (seeded N(0,0.02^2) params, " + ("N(0,std^2)" if gstd else "heavy-tailed Student-t(2)")
+                + " grads, resident in HBM)",
         "config": {
             "workload": label,
             "tensors": len(shapes),

@@ -90,6 +90,8 @@ struct Plan {
   std::vector<DevTensor> dev;
   std::map<BandKey, WorkList> band;      // P1 (every factored tensor)
   std::map<BandKey, WorkList> band2;     // P2 (factored tensors of the full8bit / fp32 layouts)
+  std::map<int, WorkList> tiny1;         // P1 of tensors of tiny matrices (per 256 matrices), by grad type
+  std::map<int, WorkList> tiny2;         // P2 of tensors of tiny matrices, by grad type
   std::map<TypeKey, WorkList> upd;       // P3, tile form (fast block sizes)
   std::map<TypeKey, WorkList> updb;      // P3, band form
   std::map<TypeKey, WorkList> vecB;      // 1-D pass B (fast block sizes)
@@ -175,6 +177,12 @@ void magic_div(int64_t d, uint64_t& m, uint32_t& s) {
   m = uint64_t(((__uint128_t(1) << s) / uint64_t(d)) + 1);
 }
 
+// A factored tensor of the full8bit / fp32 layouts whose matrices are at most kTinyElems elements
+// takes the thread-per-matrix passes.
+bool tiny_matrix(const came8_tensor& t, bool s2d) {
+  return t.factored && !s2d && t.rows >= 1 && t.cols >= 1 && t.rows * t.cols <= kTinyElems;
+}
+
 // The 2^shrink of band_rows for every tensor: tensors that share a band-pass kernel variant (one
 // launch) share a shrink, the least that gives their launch kMinLaunchBands work items (at most 6).
 std::vector<int> band_shrinks(const came8_tensor* ts, int32_t n, int32_t B) {
@@ -183,6 +191,7 @@ std::vector<int> band_shrinks(const came8_tensor* ts, int32_t n, int32_t B) {
   for (int i = 0; i < n; ++i) {
     const came8_tensor& t = ts[i];
     if (!t.factored || t.rows < 1 || t.cols < 1 || t.prefix < 1) continue;
+    if (tiny_matrix(t, t.state_kind == CAME8_STATE_8BIT2D)) continue;
     const BandShapeSel sel = band_variant(t, t.cols, B, 1);
     groups[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB, 0, sel.ua}].push_back(i);
   }
@@ -293,7 +302,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     magic_div(d.C, d.mC, d.sC);
     magic_div(d.R, d.mR, d.sR);
     if (t.factored) {
-      d.rb = band_rows(d.R, d.C, shrink[i]);
+      d.rb = tiny_matrix(t, s2d) ? d.R : band_rows(d.R, d.C, shrink[i]);
       d.nbands = ceil_div(d.R, d.rb);
       d.nbr = std::max<int64_t>(1, ceil_div(d.P * d.R, B));
       d.nbc = std::max<int64_t>(1, ceil_div(d.P * d.C, B));
@@ -367,9 +376,14 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       continue;  // the clip of this layout has no parity-mode variant (the reference sums it with float atomics)
     }
     if (t.factored) {
-      const BandShapeSel sel1 = band_variant(t, d.C, B, 1), sel2 = band_variant(t, d.C, B, 2);
-      add_item(plan.band[BandKey{t.grad_dtype, sel1.V, sel1.K, sel1.TPB, 0, sel1.ua}], i, d.P * d.nbands);
-      add_item(plan.band2[BandKey{t.grad_dtype, sel2.V, sel2.K, sel2.TPB, d.fp32st, sel2.ua}], i, d.P * d.nbands);
+      if (tiny_matrix(t, false)) {
+        add_item(plan.tiny1[t.grad_dtype], i, ceil_div(d.P, int64_t(kThreads)));
+        add_item(plan.tiny2[t.grad_dtype], i, ceil_div(d.P, int64_t(kThreads)));
+      } else {
+        const BandShapeSel sel1 = band_variant(t, d.C, B, 1), sel2 = band_variant(t, d.C, B, 2);
+        add_item(plan.band[BandKey{t.grad_dtype, sel1.V, sel1.K, sel1.TPB, 0, sel1.ua}], i, d.P * d.nbands);
+        add_item(plan.band2[BandKey{t.grad_dtype, sel2.V, sel2.K, sel2.TPB, d.fp32st, sel2.ua}], i, d.P * d.nbands);
+      }
       add_item(plan.factor, i, d.nbr + d.nbc);
       if (fastB) {
         if (d.p3_nbands > 0) add_item(plan.updb[tk], i, d.P * d.p3_nbands * d.p3_nseg);
@@ -393,6 +407,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
   };
   for (auto& kv : plan.band) place(kv.second);
   for (auto& kv : plan.band2) place(kv.second);
+  for (auto& kv : plan.tiny1) place(kv.second);
+  for (auto& kv : plan.tiny2) place(kv.second);
   for (auto& kv : plan.tiles2d_v) place(kv.second);
   for (auto& kv : plan.tiles2d) place(kv.second);
   for (auto& kv : plan.param2d_v) place(kv.second);
@@ -443,6 +459,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     };
     for (auto& kv : plan.band) put(kv.second);
     for (auto& kv : plan.band2) put(kv.second);
+    for (auto& kv : plan.tiny1) put(kv.second);
+    for (auto& kv : plan.tiny2) put(kv.second);
     for (auto& kv : plan.tiles2d_v) put(kv.second);
     for (auto& kv : plan.tiles2d) put(kv.second);
     for (auto& kv : plan.param2d_v) put(kv.second);
@@ -784,6 +802,14 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
     if ((rc = check_launch("pass1")) != CAME8_OK) return rc; }
   }
+  for (auto& kv : plan.tiny1) {
+    const WorkList& wl = kv.second;
+    GenFn fn;
+    CAME8_TYPE_SWITCH1(k_tiny_pass1, kv.first, fn);
+    { PhaseTimer pt(PH_PASS1, alg_bytes(plan, wl, tensors, PH_PASS1), stream);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+    if ((rc = check_launch("tiny_pass1")) != CAME8_OK) return rc; }
+  }
   for (auto& kv : plan.vecA) {
     const WorkList& wl = kv.second;
     GenFn fn;
@@ -828,6 +854,14 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       { PhaseTimer pt(PH_PASS2, alg_bytes(plan, wl, tensors, PH_PASS2), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("pass2")) != CAME8_OK) return rc; }
+    }
+    for (auto& kv : plan.tiny2) {
+      const WorkList& wl = kv.second;
+      GenFn fn;
+      CAME8_TYPE_SWITCH1(k_tiny_pass2, kv.first, fn);
+      { PhaseTimer pt(PH_PASS2, alg_bytes(plan, wl, tensors, PH_PASS2), stream);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      if ((rc = check_launch("tiny_pass2")) != CAME8_OK) return rc; }
     }
     for (auto& kv : plan.tiles2d_v) {
       const WorkList& wl = kv.second;

@@ -572,6 +572,111 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
   }
 }
 
+// ---------------- P1 / P2 for tiny matrices ----------------
+// Tensors whose matrices hold at most kTinyElems elements (conv kernels such as 320x320x3x3 are
+// 102400 matrices of 3x3; 1280x640x1x1 is 819200 matrices of one element) take one thread per
+// matrix instead of a workgroup per band: the matrix is its own band (nbands = 1), and the thread
+// writes what the band passes write -- new row states, the band's row-state sum, the column partial
+// sums -- with the same per-element arithmetic, its sums in fp64 in index order.
+constexpr int kTinyElems = 64;
+
+template <typename TG>
+__global__ __launch_bounds__(kThreads) void k_tiny_pass1(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                         const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using GS = typename TG::storage;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t b = (w - wstart[slot]) * kThreads + threadIdx.x;  // the matrix
+    if (b >= t.P) continue;
+    const int64_t R = t.R, C = t.C;
+    const CAME8_GLOBAL GS* __restrict__ g = gbl(static_cast<const GS*>(t.g) + b * R * C);
+    CAME8_GLOBAL float* __restrict__ Rn = gbl(t.Rn + b * R);
+    const float invC = 1.0f / float(C);
+    double bandR = 0.0;
+    for (int64_t i = 0; i < R; ++i) {
+      double s = 0.0;
+      for (int64_t j = 0; j < C; ++j) {
+        const double x = double(TG::load(g[i * C + j]));
+        s = fma(x, x, s);
+      }
+      const int64_t row = b * R + i;
+      const float Rold = t.fp32st ? st_sq_row(t)[row] : deq_u8(t.rq[row], t.ra[blk_of(row, hp)]);
+      const float mean = float(s + double(C) * double(hp.eps0)) * invC;
+      const float Rnew = fmaf(mean, hp.a2, Rold * hp.b2);
+      Rn[i] = Rnew;
+      bandR += Rnew;
+    }
+    const float band_eps = float(R) * hp.eps0;
+    for (int64_t j = 0; j < C; ++j) {
+      double u = 0.0;
+      float wsum = 0.0f;
+      for (int64_t i = 0; i < R; ++i) {
+        const float x = TG::load(g[i * C + j]);
+        u = fma(double(x), double(x), u);
+        wsum = fmaf(x * __builtin_amdgcn_rcpf(Rn[i]), x, wsum);
+      }
+      gbl(t.partU)[b * C + j] = float(u) + band_eps;
+      gbl(t.partW)[b * C + j] = wsum;
+    }
+    gbl(t.rsum)[b] = float(bandR);
+  }
+}
+
+template <typename TG>
+__global__ __launch_bounds__(kThreads) void k_tiny_pass2(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                         const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using GS = typename TG::storage;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t b = (w - wstart[slot]) * kThreads + threadIdx.x;
+    if (b >= t.P) continue;
+    const int64_t R = t.R, C = t.C, e0 = b * R * C;
+    const CAME8_GLOBAL GS* __restrict__ g = gbl(static_cast<const GS*>(t.g) + e0);
+    const CAME8_GLOBAL float* __restrict__ rf = gbl(t.rfac + b * R);
+    const CAME8_GLOBAL float* __restrict__ cf = gbl(t.cfac + b * C);
+    const float clip = t.clip[0];
+    const float crcp = 1.0f / clip;  // as the band pass: the divisor is >= 1
+    const int64_t PR = t.P * R;
+    // d = u - m of element (i, j), as the band pass forms it
+    auto d_at = [&](int64_t i, int64_t j) {
+      const int64_t e = e0 + i * C + j;
+      const float mo = t.fp32st ? st_m(t)[e]
+                                : float(t.mq[e]) * div_fast(t.ma[blk_of_nb(e, hp)], kSignedQ, kRcpSignedQ);
+      const float u = div_fast((rf[i] * cf[j]) * TG::load(g[i * C + j]), clip, crcp);
+      const float m = fmaf(u, hp.a1, mo * hp.b1);
+      return u - m;
+    };
+    double bandRR = 0.0;
+    for (int64_t i = 0; i < R; ++i) {
+      double s = 0.0;
+      for (int64_t j = 0; j < C; ++j) {
+        const float d = d_at(i, j);
+        s = fma(double(d), double(d), s);
+      }
+      const int64_t row = b * R + i;
+      const float tot = float(s + double(C) * double(hp.eps1));
+      const float RRold = t.fp32st ? t.ra[row] : deq_u8(t.rq[PR + row], t.ra[t.nbr + blk_of(row, hp)]);
+      const float RRnew = fmaf(tot / float(C), hp.a3, RRold * hp.b3);
+      gbl(t.RRn)[row] = RRnew;
+      bandRR += RRnew;
+    }
+    const float band_eps = float(R) * hp.eps1;
+    for (int64_t j = 0; j < C; ++j) {
+      double s = 0.0;
+      for (int64_t i = 0; i < R; ++i) {
+        const float d = d_at(i, j);
+        s = fma(double(d), double(d), s);
+      }
+      gbl(t.partRes)[b * C + j] = float(s) + band_eps;
+    }
+    gbl(t.rrsum)[b] = float(bandRR);
+  }
+}
+
 // ---------------- P2 ----------------
 // Residual row and column sums of a band.  Per element the reference forms u = (r_i*c_j)*g / clip,
 // m = fma(u, 1-b1, m_old*b1) and res = (u - m)^2 + eps1 (CAME8bitFull.py:1032-1036) and keeps only
