@@ -493,40 +493,39 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
       __syncthreads();
       for (int64_t rr = tid; rr < r1 - r0; rr += TPB) Rn[b * R + r0 + rr] = rowR[rr];
     } else if constexpr (!UA) {  // (the host gives UA variants single-sweep rows only)
+      // Rows wider than one sweep of the workgroup: the row sums first, row by row, then the column
+      // partials segment by segment (the band is read twice).  A row's K chunks of a segment are
+      // loaded together, before any is used: a chunk past the row end loads the row's first chunk
+      // and is skipped; in phase B two rows' loads are in flight.
+      using CK = Chunk<TG, V>;
+      auto seg_col = [&](int64_t seg, int k) { return seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V; };
       // phase A: row sums over all segments
-      for (int64_t r = r0; r < r1; r += S) {
-        double ps[S];
-#pragma unroll
-        for (int s = 0; s < S; ++s) ps[s] = 0.0f;
+      for (int64_t r = r0; r < r1; ++r) {
+        double ps[1] = {0.0};
         for (int64_t seg = 0; seg < nseg; ++seg) {
+          CK x[K];
 #pragma unroll
-          for (int s = 0; s < S; ++s) {
+          for (int k = 0; k < K; ++k) {
+            const int64_t c0 = seg_col(seg, k);
+            x[k].load(g + r * C + (c0 < C ? c0 : 0));
+          }
 #pragma unroll
-            for (int k = 0; k < K; ++k) {
-              const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
-              if (r + s < r1 && c0 < C) {
-                Chunk<TG, V> x;
-                x.load(g + (r + s) * C + c0);
+          for (int k = 0; k < K; ++k) {
+            if (seg_col(seg, k) < C) {
 #pragma unroll
-                for (int v = 0; v < V; ++v) ps[s] = acc_fma(ps[s], x[v], x[v]);
-              }
+              for (int v = 0; v < V; ++v) ps[0] = acc_fma(ps[0], x[k][v], x[k][v]);
             }
           }
         }
-        double tot[S];
-        block_row_sums<S, NW>(ps, red, par, tot);
+        double tot[1];
+        block_row_sums<1, NW>(ps, red, par, tot);
         par ^= 1;
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          if (r + s < r1) {
-            const int64_t row = b * R + r + s;
-            const float Rnew = row_state(row, tot[s]);
-            bandR += Rnew;
-            if (tid == 0) {
-              Rn[row] = Rnew;
-              rowR[r + s - r0] = Rnew;
-            }
-          }
+        const int64_t row = b * R + r;
+        const float Rnew = row_state(row, tot[0]);
+        bandR += Rnew;
+        if (tid == 0) {
+          Rn[row] = Rnew;
+          rowR[r - r0] = Rnew;
         }
       }
       __syncthreads();
@@ -537,25 +536,39 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
         for (int k = 0; k < K; ++k)
 #pragma unroll
           for (int v = 0; v < V; ++v) colU[k][v] = colW[k][v] = Acc(0);
-        for (int64_t r = r0; r < r1; ++r) {
-          const float invR = 1.0f / rowR[r - r0];
+        for (int64_t r = r0; r < r1; r += 2) {
+          const bool two = r + 1 < r1;
+          CK x0[K], x1[K];
 #pragma unroll
           for (int k = 0; k < K; ++k) {
-            const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
-            if (c0 < C) {
-              Chunk<TG, V> x;
-              x.load(g + r * C + c0);
+            const int64_t c0 = seg_col(seg, k);
+            const int64_t cc = c0 < C ? c0 : 0;
+            x0[k].load(g + r * C + cc);
+            x1[k].load(g + (two ? r + 1 : r) * C + cc);
+          }
+          const float invR0 = 1.0f / rowR[r - r0];
+          const float invR1 = two ? 1.0f / rowR[r + 1 - r0] : 0.0f;
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            if (seg_col(seg, k) < C) {
 #pragma unroll
               for (int v = 0; v < V; ++v) {
-                colU[k][v] = acc_fma(colU[k][v], x[v], x[v]);
-                colW[k][v] = acc_fma_w(colW[k][v], x[v], invR);
+                colU[k][v] = acc_fma(colU[k][v], x0[k][v], x0[k][v]);
+                colW[k][v] = acc_fma_w(colW[k][v], x0[k][v], invR0);
+              }
+              if (two) {
+#pragma unroll
+                for (int v = 0; v < V; ++v) {
+                  colU[k][v] = acc_fma(colU[k][v], x1[k][v], x1[k][v]);
+                  colW[k][v] = acc_fma_w(colW[k][v], x1[k][v], invR1);
+                }
               }
             }
           }
         }
 #pragma unroll
         for (int k = 0; k < K; ++k) {
-          const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
+          const int64_t c0 = seg_col(seg, k);
           if (c0 < C) {
 #pragma unroll
             for (int v = 0; v < V; ++v) {
@@ -905,13 +918,43 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
       }
       bpar ^= 1;  // the next band writes the other half (after this band's barriers above)
     } else if constexpr (!UA) {  // (the host gives UA variants single-sweep rows only)
-      // rows wider than one sweep of the workgroup: column partials segment by segment, then the
-      // row sums over whole rows (the gradient and codes are read twice)
-      auto e_at = [&](float ri, float cjv, float x, int64_t e) {
+      // Rows wider than one sweep of the workgroup: column partials segment by segment, then the row
+      // sums over whole rows (the gradient and momentum are read twice).  A row's K chunks of a
+      // segment are loaded together with their momentum, block scales and column factors, before
+      // any is used; a chunk past the row end loads the row's first chunk and is skipped.  (Without
+      // UA, B is a multiple of V and a chunk starts at a multiple of V: it lies in one block.)
+      using CK = Chunk<TG, V>;
+      using MB = typename std::conditional<F32ST, M32Chunk<V>, CodeChunk<V>>::type;
+      auto seg_col = [&](int64_t seg, int k) { return seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V; };
+      struct SegBuf {
+        CK g[K];
+        MB q[K];
+        float a[K];
+        float c[K][V];
+      };
+      auto load_seg = [&](SegBuf& sb, int64_t r, int64_t seg) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const int64_t c0 = seg_col(seg, k);
+          const int64_t cc = c0 < C ? c0 : 0;
+          const int64_t e = r * C + cc;
+          sb.g[k].load(g + e);
+          if constexpr (F32ST) {
+            sb.q[k].load(m32 + e);
+          } else {
+            sb.q[k].load(mq + e);
+            sb.a[k] = ma[blk_of(ebase + e, hp)];
+          }
+#pragma unroll
+          for (int v = 0; v < V; ++v) sb.c[k][v] = cf[cc + v];
+        }
+      };
+      // d of element v of chunk k, the row factor ri
+      auto d_seg = [&](const SegBuf& sb, int k, int v, float ri) __attribute__((always_inline)) {
         float mo;
-        if constexpr (F32ST) mo = m32[e];
-        else mo = float(mq[e]) * scale_s8(ma[blk_of(ebase + e, hp)]);
-        return d_of(ri, cjv, x, mo);
+        if constexpr (F32ST) mo = sb.q[k].m[v];
+        else mo = sb.q[k][v] * scale_s8(sb.a[k]);
+        return d_of(ri, sb.c[k][v], sb.g[k][v], mo);
       };
       for (int64_t seg = 0; seg < nseg; ++seg) {
         Acc colR[K][V];
@@ -920,16 +963,15 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
 #pragma unroll
           for (int v = 0; v < V; ++v) colR[k][v] = Acc(0);
         for (int64_t r = r0; r < r1; ++r) {
+          SegBuf sb;
+          load_seg(sb, r, seg);
           const float ri = rowsc[r - r0];
 #pragma unroll
           for (int k = 0; k < K; ++k) {
-            const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
-            if (c0 < C) {
-              Chunk<TG, V> x;
-              x.load(g + r * C + c0);
+            if (seg_col(seg, k) < C) {
 #pragma unroll
               for (int v = 0; v < V; ++v) {
-                const float e = e_at(ri, cf[c0 + v], x[v], r * C + c0 + v);
+                const float e = d_seg(sb, k, v, ri);
                 colR[k][v] = acc_fma(colR[k][v], e, e);
               }
             }
@@ -937,7 +979,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
         }
 #pragma unroll
         for (int k = 0; k < K; ++k) {
-          const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
+          const int64_t c0 = seg_col(seg, k);
           if (c0 < C) {
 #pragma unroll
             for (int v = 0; v < V; ++v) pR[c0 + v] = float(colR[k][v]) + band_eps;
@@ -945,36 +987,27 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
         }
       }
       double bandRR = 0.0;  // sum of the band's new residual row states (thread 0, row order)
-      for (int64_t r = r0; r < r1; r += S) {
-        double ps[S];
+      for (int64_t r = r0; r < r1; ++r) {
+        double ps[1] = {0.0};
+        const float ri = rowsc[r - r0];
+        for (int64_t seg = 0; seg < nseg; ++seg) {
+          SegBuf sb;
+          load_seg(sb, r, seg);
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-          ps[s] = 0.0f;
-          if (r + s < r1) {
-            const float ri = rowsc[r + s - r0];
-            for (int64_t seg = 0; seg < nseg; ++seg) {
+          for (int k = 0; k < K; ++k) {
+            if (seg_col(seg, k) < C) {
 #pragma unroll
-              for (int k = 0; k < K; ++k) {
-                const int64_t c0 = seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V;
-                if (c0 < C) {
-                  Chunk<TG, V> x;
-                  x.load(g + (r + s) * C + c0);
-#pragma unroll
-                  for (int v = 0; v < V; ++v) {
-                    const float e = e_at(ri, cf[c0 + v], x[v], (r + s) * C + c0 + v);
-                    ps[s] = acc_fma(ps[s], e, e);
-                  }
-                }
+              for (int v = 0; v < V; ++v) {
+                const float e = d_seg(sb, k, v, ri);
+                ps[0] = acc_fma(ps[0], e, e);
               }
             }
           }
         }
-        double tot[S];
-        block_row_sums<S, NW>(ps, red, par, tot);
+        double tot[1];
+        block_row_sums<1, NW>(ps, red, par, tot);
         par ^= 1;
-#pragma unroll
-        for (int s = 0; s < S; ++s)
-          if (r + s < r1 && tid == 0) bandRR += row_state(b * R + r + s, tot[s]);
+        if (tid == 0) bandRR += row_state(b * R + r, tot[0]);
       }
       if (tid == 0) t.rrsum[b * t.nbands + it.band] = float(bandRR);
     }
