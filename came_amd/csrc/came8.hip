@@ -39,6 +39,12 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // tensors one band launch steps together are halved (down to kMinShrunkBandRows rows) until that
 // launch has about kMinLaunchBands work items.
 constexpr int64_t kMinShrunkBandRows = 8;
+#ifndef CAME8_LB256
+#define CAME8_LB256 2048
+#endif
+#ifndef CAME8_LB512
+#define CAME8_LB512 2048
+#endif
 constexpr int64_t kMinLaunchBands = 2048;
 
 // Rows per band: about 1M elements per workgroup work item, whole rows, at most 256 rows, divided by
@@ -152,10 +158,11 @@ BandShapeSel band_variant(const came8_tensor& t, int64_t C, int32_t B, int pass)
   }
   const int64_t chunks = ceil_div(C, sel.V);
   (void)pass;  // both passes take the same shapes (wider workgroups cost pass 1 more barrier time)
-  static const int vec_k[][2] = {{1, 256}, {2, 256}, {2, 512}, {3, 512}, {4, 512}};
+  // 256-thread workgroups first: two of them per CU keep one's barriers off the other's loads
+  static const int vec_k[][2] = {{1, 256}, {2, 256}, {3, 256}, {2, 512}, {3, 512}, {4, 512}};
   static const int one_k[][2] = {{1, 256}, {2, 256}, {4, 256}, {8, 256}, {16, 256}, {32, 256}};
   const int (*cand)[2] = sel.V > 1 ? vec_k : one_k;
-  const int nc = sel.V > 1 ? 5 : 6;
+  const int nc = sel.V > 1 ? 6 : 6;
   for (int i = 0; i < nc; ++i) {
     if (int64_t(cand[i][0]) * cand[i][1] >= chunks) {
       sel.K = cand[i][0];
@@ -200,7 +207,7 @@ std::vector<int> band_shrinks(const came8_tensor* ts, int32_t n, int32_t B) {
     for (; shrink < 6; ++shrink) {
       int64_t bands = 0;
       for (int i : kv.second) bands += ts[i].prefix * ceil_div(ts[i].rows, band_rows(ts[i].rows, ts[i].cols, shrink));
-      if (bands >= kMinLaunchBands) break;
+      if (bands >= (kv.first.TPB >= 512 ? CAME8_LB512 : CAME8_LB256)) break;
     }
     for (int i : kv.second) out[i] = shrink;
   }

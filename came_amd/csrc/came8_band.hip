@@ -44,6 +44,7 @@ BandFn CAME8_BAND_SELECTOR(CAME8_BAND_TYPE, CAME8_BAND_PASS)(int V, int K, int T
   if (V == kVW) {
     if (TPB == 256 && K == 1) return pick_ua<kVW, 1, 256>(st, ua);
     if (TPB == 256 && K == 2) return pick_ua<kVW, 2, 256>(st, ua);
+    if (TPB == 256 && K == 3) return pick_ua<kVW, 3, 256>(st, ua);
     if (TPB == 512 && K == 2) return pick_ua<kVW, 2, 512>(st, ua);
     if (TPB == 512 && K == 3) return pick_ua<kVW, 3, 512>(st, ua);
     if (TPB == 512 && K == 4) return pick_ua<kVW, 4, 512>(st, ua);

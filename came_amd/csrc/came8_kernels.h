@@ -355,14 +355,18 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
     CAME8_GLOBAL float* __restrict__ pW = gbl(t.partW + (b * t.nbands + it.band) * C);
     double bandR = 0.0;  // sum of this band's new row states, in row order (every thread alike)
     const float band_eps = float(r1 - r0) * hp.eps0;  // eps0 of each element of a column partial
+    // The old row states go through LDS: a per-row global load inside the stage loop would wait for
+    // the next stage's loads as well.  The caller issues the band's first loads before this, so that
+    // their latencies overlap.
+    auto stage_rows = [&]() __attribute__((always_inline)) {
+      for (int64_t rr = tid; rr < r1 - r0; rr += TPB) {
+        const int64_t row = b * R + r0 + rr;
+        rowold[rr] = t.fp32st ? gbl(st_sq_row(t))[row] : deq_u8(rq[row], ra[blk_of(row, hp)]);
+      }
+      wait_vm_all();  // on every path: the stage loop's waits then count only its own loads
+      __syncthreads();
+    };
     // new row state from the row's sum of g^2 (eps0 added once per element count)
-    // the old row states go through LDS: a per-row global load inside the stage loop would wait for
-    // the next stage's loads as well
-    for (int64_t rr = tid; rr < r1 - r0; rr += TPB) {
-      const int64_t row = b * R + r0 + rr;
-      rowold[rr] = t.fp32st ? st_sq_row(t)[row] : deq_u8(rq[row], ra[blk_of(row, hp)]);
-    }
-    __syncthreads();
     // (the mean through 1/C: within 1 ulp of tot / C, and equal to it for power-of-two C)
     const float invC = 1.0f / fC;
     auto row_state = [&](int64_t row, double sum_g2) {
@@ -471,8 +475,10 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
           }
         }
       };
-      wait_vm_all();
+      // the row staging waits for every load issued so far, which also retires the previous band's
+      // stores
       load_stage(A, r0);
+      stage_rows();
       for (int64_t r = r0; r < r1; r += 2 * S) {
         load_stage(Bf, r + S);
         process(A, r);
@@ -497,6 +503,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
       // partials segment by segment (the band is read twice).  A row's K chunks of a segment are
       // loaded together, before any is used: a chunk past the row end loads the row's first chunk
       // and is skipped; in phase B two rows' loads are in flight.
+      stage_rows();
       using CK = Chunk<TG, V>;
       auto seg_col = [&](int64_t seg, int k) { return seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V; };
       // phase A: row sums over all segments
@@ -711,6 +718,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
   __shared__ double rowpart[2][kMaxBandRows + 1][NW];  // per-wave row sums of a band (+1: a dummy row)
   __shared__ float rowval[kMaxBandRows];           // the band's new residual row states
   __shared__ float rowsc[kMaxBandRows];            // the band's row factors r_i
+  __shared__ float rowold[kMaxBandRows];           // the band's old residual row states
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   int par = 0, bpar = 0;
   const int64_t total = wstart[ntens];
@@ -743,18 +751,25 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
       const float m = fmaf(u, hp.a1, mo * hp.b1);
       return u - m;
     };
-    auto row_state = [&](int64_t row, double sum_e2) {
+    // new residual row state of band row rr from its sum of d^2
+    auto row_state = [&](int64_t rr, double sum_e2) {
       const float tot = float(sum_e2 + double(C) * double(hp.eps1));
-      const float RRold = f32st ? t.ra[row] : deq_u8(rq[PR + row], ra[t.nbr + blk_of(row, hp)]);
-      const float RRnew = fmaf(tot / fC, hp.a3, RRold * hp.b3);
-      RRn[row] = RRnew;
+      const float RRnew = fmaf(tot / fC, hp.a3, rowold[rr] * hp.b3);
+      RRn[b * R + r0 + rr] = RRnew;
       return RRnew;
     };
-
-    // the row scalars go through LDS: a per-row global load inside the stage loop would wait for the
-    // next stage's loads as well
-    for (int64_t rr = tid; rr < r1 - r0; rr += TPB) rowsc[rr] = rfac[b * R + r0 + rr];
-    __syncthreads();
+    // The band's row scalars (r_i, old residual states) go through LDS: a per-row global load inside
+    // the stage loop, or at the band's end, would wait for the next stage's loads as well.  The
+    // caller issues the band's first loads before this, so that their latencies overlap.
+    auto stage_rows = [&]() __attribute__((always_inline)) {
+      for (int64_t rr = tid; rr < r1 - r0; rr += TPB) {
+        const int64_t row = b * R + r0 + rr;
+        rowsc[rr] = rfac[row];
+        rowold[rr] = f32st ? gbl(t.ra)[row] : deq_u8(rq[PR + row], ra[t.nbr + blk_of(row, hp)]);
+      }
+      wait_vm_all();  // on every path: the stage loop's waits then count only its own loads
+      __syncthreads();
+    };
     if (nseg == 1) {
       // The stage loop is branch-free, so that the compiler can wait for exactly one stage's loads
       // while the next stage's are in flight: a chunk past the row end (cok false) loads the row's
@@ -879,8 +894,11 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
           }
         };
         // two register stages in flight; the prefetches are unconditional (rows past the band end
-        // reload its last row, from cache, and count for nothing)
-        wait_vm_all();
+        // reload its last row, from cache, and count for nothing).  The row staging waits for every
+        // load issued so far, which also retires the previous band's stores.  (Issuing the first
+        // stage before it keeps that stage's registers live across the staging and the barrier,
+        // which costs this kernel more than the overlapped latency gains.)
+        stage_rows();
         load_stage(A, r0);
         for (int64_t r = r0; r < r1; r += 2 * S) {
           load_stage(Bs, r + S);
@@ -903,18 +921,20 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
       }
       __syncthreads();
       // row totals over the waves in a fixed order; the new residual row states go through LDS so
-      // that one thread can add them up in row order
+      // that the first wave can add them up: lane l over rows l, l+64, ..., then the lanes in the
+      // fixed order of the wave sum
       for (int rr = tid; rr < r1 - r0; rr += TPB) {
         double tot = rowpart[bpar][rr][0];
 #pragma unroll
         for (int w2 = 1; w2 < NW; ++w2) tot += rowpart[bpar][rr][w2];
-        rowval[rr] = row_state(b * R + r0 + rr, tot);
+        rowval[rr] = row_state(rr, tot);
       }
       __syncthreads();
-      if (tid == 0) {
+      if (wid == 0) {
         double sum = 0.0;
-        for (int64_t rr = 0; rr < r1 - r0; ++rr) sum += rowval[rr];
-        t.rrsum[b * t.nbands + it.band] = float(sum);
+        for (int64_t rr = lane; rr < r1 - r0; rr += kWave) sum += rowval[rr];
+        sum = wave_sum(sum);
+        if (lane == 0) t.rrsum[b * t.nbands + it.band] = float(sum);
       }
       bpar ^= 1;  // the next band writes the other half (after this band's barriers above)
     } else if constexpr (!UA) {  // (the host gives UA variants single-sweep rows only)
@@ -923,6 +943,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
       // segment are loaded together with their momentum, block scales and column factors, before
       // any is used; a chunk past the row end loads the row's first chunk and is skipped.  (Without
       // UA, B is a multiple of V and a chunk starts at a multiple of V: it lies in one block.)
+      stage_rows();
       using CK = Chunk<TG, V>;
       using MB = typename std::conditional<F32ST, M32Chunk<V>, CodeChunk<V>>::type;
       auto seg_col = [&](int64_t seg, int k) { return seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V; };
@@ -1007,7 +1028,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict_
         double tot[1];
         block_row_sums<1, NW>(ps, red, par, tot);
         par ^= 1;
-        if (tid == 0) bandRR += row_state(b * R + r, tot[0]);
+        if (tid == 0) bandRR += row_state(r - r0, tot[0]);
       }
       if (tid == 0) t.rrsum[b * t.nbands + it.band] = float(bandRR);
     }
