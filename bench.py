@@ -3,7 +3,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4] [--no-cpu-baseline]
 
-Workload (default): a Llama-7B-shape parameter set -- 32 layers, d=4096,
+Workload (default, the headline config c4): a Llama-7B-shape parameter set -- 32 layers, d=4096,
 SwiGLU FFN 11008, vocab 32000 embedding and lm_head, RMSNorm weights; 291 tensors, 6,738,415,616
 bf16 parameters with bf16 gradients ~ N(0, 2e-4^2) -- stepped by ``came_amd.CAME8bit``
 (lr 2e-4, weight decay 1e-2, betas (0.9, 0.999, 0.9999), int8 blockwise momentum, block 256).
@@ -66,7 +66,7 @@ def gpt2_medium_shapes():
 
 
 def ragged_shapes(seed=0):
-    """500 tensors -- 250 1-D lengths U{1..4097}; the 2-D shapes 1000x3, 3x50257 and
+    """The ragged stress set (config c5): 500 tensors -- 250 1-D lengths U{1..4097}; the 2-D shapes 1000x3, 3x50257 and
     4097x129; conv weights 320x320x3x3 and 1280x640x1x1; 245 2-D shapes with rows and columns drawn from
     [1, 5000] outside multiples of 64."""
     gen = torch.Generator().manual_seed(seed)
@@ -112,7 +112,7 @@ CONFIGS = {
     # the same Llama-7B set stepped by CAMECUDA (fp32 optimizer states)
     "c4fp": ("llama7b-shape/CAMECUDA/bf16", lambda: llama_shapes(32, 4096, 11008, 32000), torch.bfloat16,
              torch.bfloat16, 2e-4, "CAMECUDA", dict(lr=2e-4, weight_decay=1e-2, betas=(0.9, 0.999, 0.9999))),
-    # BASELINE config 5: the ragged stress set, heavy-tailed gradients, CAME8bitFull
+    # the ragged stress set, heavy-tailed gradients, CAME8bitFull
     "c5": ("ragged-500/CAME8bitFull/fp32", ragged_shapes, torch.float32, torch.float32, None, "CAME8bitFull",
            dict(lr=2e-4, weight_decay=1e-2)),
 }
@@ -212,8 +212,9 @@ def main():
                          "kernel of known bytes, to scale the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the optimizer step "
-              "is sharded by tensor across GPUs, see DESIGN.md", file=sys.stderr)
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); across GPUs the "
+              "optimizer step shards by tensor (each GPU steps its own tensors, no exchange during the step)",
+              file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)

@@ -1,4 +1,4 @@
-"""BASELINE config 5 at full size on the GPU: the ragged stress set of 500 tensors
+"""The ragged stress configuration (c5) at full size on the GPU: 500 tensors
 (bench.ragged_shapes: 1-D lengths 1..4097, 1000x3, 3x50257, 4097x129, conv weights 320x320x3x3 and
 1280x640x1x1, 245 matrices up to 5000x5000 with no dimension a multiple of 64; 1.52 G elements),
 heavy-tailed gradients with 10% exact zeros and +-1e3 outliers (bench.heavy_grad), stepped by
