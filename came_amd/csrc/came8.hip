@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <map>
 #include <mutex>
 #include <string>
@@ -35,17 +36,18 @@ constexpr size_t kAlign = 256;
 size_t align_up(size_t x, size_t a = kAlign) { return (x + a - 1) / a * a; }
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// A launch of few bands leaves most CUs idle (one 2048x2048 matrix is 8 bands): the bands of the
-// tensors one band launch steps together are halved (down to kMinShrunkBandRows rows) until that
-// launch has about kMinLaunchBands work items.
+// A launch of few bands leaves most CUs idle (one 2048x2048 matrix is 8 bands), and a launch whose
+// bands fill the resident workgroups a little more than k times runs a (k+1)-th round almost empty.
+// The bands of the tensors one band launch steps together are halved together (down to
+// kMinShrunkBandRows rows, at most kMaxShrink times), to the size that minimises a schedule
+// estimate of the launch (band_shrinks).
 constexpr int64_t kMinShrunkBandRows = 8;
-#ifndef CAME8_LB256
-#define CAME8_LB256 2048
-#endif
-#ifndef CAME8_LB512
-#define CAME8_LB512 2048
-#endif
-constexpr int64_t kMinLaunchBands = 2048;
+constexpr int kMaxShrink = 6;
+constexpr int64_t kMinLaunchBands = 2048;  // without a device to ask: the least work items per launch
+// Fixed time of a band (its start, its row sums, its partial stores), about 5 us, in elements the
+// whole GPU streams meanwhile: a workgroup among `slots` spends it as kBandFixedElems / slots.
+// (2e6 and 3.2e7 pick other shrinks on C2, C3 and C5 and measure within 1% of this value.)
+constexpr double kBandFixedElems = 8.4e6;
 
 // Rows per band: about 1M elements per workgroup work item, whole rows, at most 256 rows, divided by
 // 2^shrink.  Every band writes one fp32 partial per column and statistic, which the factor kernels
@@ -190,27 +192,130 @@ bool tiny_matrix(const came8_tensor& t, bool s2d) {
   return t.factored && !s2d && t.rows >= 1 && t.cols >= 1 && t.rows * t.cols <= kTinyElems;
 }
 
-// The 2^shrink of band_rows for every tensor: tensors that share a band-pass kernel variant (one
-// launch) share a shrink, the least that gives their launch kMinLaunchBands work items (at most 6).
+BandFn band_fn(int gdt, bool pass2, int V, int K, int TPB, int st, int ua);
+
+// Workgroups of kernel fn (tpb threads) resident on the current device at once: CUs times the
+// workgroups one CU holds (registers, LDS).  0 when no device answers (sizing on a host without a
+// GPU).  Cached per kernel.
+int64_t resident_slots(const void* fn, int tpb) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, int64_t> cache;
+  if (fn == nullptr) return 0;
+  std::lock_guard<std::mutex> lk(mu);
+  const auto key = std::make_pair(fn, tpb);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int dev = 0, cus = 0, per_cu = 0;
+  int64_t slots = 0;
+  if (hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, tpb, 0) == hipSuccess)
+    slots = int64_t(cus) * std::max(per_cu, 1);
+  else
+    (void)hipGetLastError();  // leave no sticky error behind for the caller's next HIP call
+  cache[key] = slots;
+  return slots;
+}
+
+// Finish time of work items of the given costs, started in order on `slots` workgroups, each item
+// on the workgroup that frees first (how the hardware dispatches a grid of one item per workgroup).
+double schedule_makespan(const std::vector<double>& cost, int64_t slots) {
+  std::vector<double> heap;  // finish times, a min-heap
+  heap.reserve(size_t(std::min<int64_t>(slots, int64_t(cost.size()))));
+  double end = 0.0;
+  for (const double c : cost) {
+    double t0 = 0.0;
+    if (int64_t(heap.size()) < slots) {
+      heap.push_back(t0 + c);
+      std::push_heap(heap.begin(), heap.end(), std::greater<double>());
+    } else {
+      std::pop_heap(heap.begin(), heap.end(), std::greater<double>());
+      t0 = heap.back();
+      heap.back() = t0 + c;
+      std::push_heap(heap.begin(), heap.end(), std::greater<double>());
+    }
+    end = std::max(end, t0 + c);
+  }
+  return end;
+}
+
+// The 2^shrink of band_rows for every tensor.  Tensors that share a band-pass kernel variant (one
+// launch) share a shrink: the one that minimises the estimated time of the launch's two passes --
+// each band costs its elements plus its fixed time, scheduled on the workgroups that pass 1 and pass 2
+// keep resident (a workgroup streams 1/slots of the GPU's rate) -- plus the factor kernels' reads of
+// the per-band column partials (three fp32 arrays).  Without a device to ask, the least shrink that gives
+// the launch kMinLaunchBands work items.
 std::vector<int> band_shrinks(const came8_tensor* ts, int32_t n, int32_t B) {
   std::vector<int> out(n, 0);
   std::map<BandKey, std::vector<int>> groups;
+  std::vector<int64_t> sig{B, n};  // what the result depends on (the plan is built on every step)
   for (int i = 0; i < n; ++i) {
     const came8_tensor& t = ts[i];
     if (!t.factored || t.rows < 1 || t.cols < 1 || t.prefix < 1) continue;
     if (tiny_matrix(t, t.state_kind == CAME8_STATE_8BIT2D)) continue;
     const BandShapeSel sel = band_variant(t, t.cols, B, 1);
     groups[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB, 0, sel.ua}].push_back(i);
+    sig.insert(sig.end(), {i, t.rows, t.cols, t.prefix, t.grad_dtype, t.state_kind, sel.V, sel.K, sel.TPB, sel.ua});
+  }
+  static std::mutex memo_mu;
+  static std::map<std::vector<int64_t>, std::vector<int>> memo;
+  {
+    std::lock_guard<std::mutex> lk(memo_mu);
+    auto it = memo.find(sig);
+    if (it != memo.end()) return it->second;
   }
   for (auto& kv : groups) {
-    int shrink = 0;
-    for (; shrink < 6; ++shrink) {
-      int64_t bands = 0;
-      for (int i : kv.second) bands += ts[i].prefix * ceil_div(ts[i].rows, band_rows(ts[i].rows, ts[i].cols, shrink));
-      if (bands >= (kv.first.TPB >= 512 ? CAME8_LB512 : CAME8_LB256)) break;
+    const BandKey& k = kv.first;
+    const came8_tensor& t0 = ts[kv.second.front()];
+    const bool s2d = t0.state_kind == CAME8_STATE_8BIT2D;
+    const int st = t0.state_kind == CAME8_STATE_FP32 ? 1 : 0;
+    const int64_t slots1 = resident_slots(reinterpret_cast<const void*>(band_fn(k.gdt, false, k.V, k.K, k.TPB, 0, k.ua)), k.TPB);
+    const int64_t slots2 = s2d ? 0 : resident_slots(reinterpret_cast<const void*>(band_fn(k.gdt, true, k.V, k.K, k.TPB, st, k.ua)), k.TPB);
+    int best = 0;
+    if (slots1 <= 0) {
+      for (; best < kMaxShrink; ++best) {
+        int64_t bands = 0;
+        for (int i : kv.second) bands += ts[i].prefix * ceil_div(ts[i].rows, band_rows(ts[i].rows, ts[i].cols, best));
+        if (bands >= kMinLaunchBands) break;
+      }
+    } else {
+      double best_t = 0.0;
+      int64_t prev_rb_sum = -1;
+      for (int s = 0; s <= kMaxShrink; ++s) {
+        std::vector<double> elems;
+        double partial = 0.0;
+        int64_t rb_sum = 0;
+        for (int i : kv.second) {
+          const came8_tensor& t = ts[i];
+          const int64_t rb = band_rows(t.rows, t.cols, s);
+          rb_sum += rb;
+          const int64_t nb = ceil_div(t.rows, rb);
+          for (int64_t m = 0; m < t.prefix; ++m)
+            for (int64_t bnd = 0; bnd < nb; ++bnd)
+              elems.push_back(double(std::min(rb, t.rows - bnd * rb)) * double(t.cols));
+          partial += 3.0 * double(t.prefix * nb) * double(t.cols);
+        }
+        if (rb_sum == prev_rb_sum) break;  // every band is at its least height already
+        prev_rb_sum = rb_sum;
+        // one pass: the busiest workgroup's elements, at 1/slots of the GPU's rate
+        auto pass_time = [&](int64_t slots) {
+          std::vector<double> cost(elems);
+          for (double& c : cost) c += kBandFixedElems / double(slots);
+          return schedule_makespan(cost, slots) * double(slots);
+        };
+        double est = pass_time(slots1) + 2.0 * partial;
+        if (slots2 > 0) est += 1.5 * pass_time(slots2);
+        if (s == 0 || est < best_t) {
+          best_t = est;
+          best = s;
+        }
+      }
     }
-    for (int i : kv.second) out[i] = shrink;
+    for (int i : kv.second) out[i] = best;
   }
+  std::lock_guard<std::mutex> lk(memo_mu);
+  if (memo.size() >= 64) memo.clear();
+  memo[sig] = out;
   return out;
 }
 
