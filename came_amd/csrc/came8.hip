@@ -13,6 +13,7 @@
 #include <cstring>
 #include <functional>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -606,7 +607,23 @@ struct CacheEntry {
   size_t bytes = 0;
   std::vector<uint8_t> keep;  // source of the last upload, alive until `done` has fired
   hipEvent_t done = nullptr;
+  // the launch plan last built for this workspace and the inputs it was built from: a call with the
+  // same descriptors, block size and workspace reuses it without planning again
+  std::vector<uint8_t> inputs;
+  std::shared_ptr<const Plan> plan;
 };
+
+// The inputs a plan depends on, as bytes: the descriptor count, the block size, the workspace
+// address (the plan holds pointers into the workspace) and the descriptors themselves.
+std::vector<uint8_t> plan_inputs(const came8_tensor* ts, int32_t n, int32_t B, const void* ws) {
+  const size_t nb = size_t(std::max(n, 0)) * sizeof(came8_tensor);
+  std::vector<uint8_t> v(16 + sizeof(void*) + nb);
+  const int64_t head[2] = {n, B};
+  std::memcpy(v.data(), head, 16);
+  std::memcpy(v.data() + 16, &ws, sizeof(void*));
+  if (nb) std::memcpy(v.data() + 16 + sizeof(void*), ts, nb);
+  return v;
+}
 std::mutex g_cache_mu;
 std::map<std::pair<const void*, uint64_t>, CacheEntry> g_cache;
 
@@ -838,10 +855,25 @@ const char* came8_last_error(void) { return g_last_error.c_str(); }
 
 int came8_workspace_size(const came8_tensor* tensors, int32_t n_tensors, int32_t block_size, size_t* bytes) {
   if (!bytes) return fail(CAME8_EINVAL, "came8_workspace_size: bytes is NULL");
+  // the size of a descriptor set already sized is remembered (callers ask on every step)
+  static std::mutex mu;
+  static std::map<std::vector<uint8_t>, size_t> sized;
+  const std::vector<uint8_t> k = plan_inputs(tensors, n_tensors, block_size, nullptr);
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = sized.find(k);
+    if (it != sized.end()) {
+      *bytes = it->second;
+      return CAME8_OK;
+    }
+  }
   Plan plan;
   const int rc = build_plan(tensors, n_tensors, block_size, 0, nullptr, plan);
   if (rc != CAME8_OK) return rc;
   *bytes = plan.total_bytes;
+  std::lock_guard<std::mutex> lk(mu);
+  if (sized.size() >= 64) sized.clear();
+  sized[k] = plan.total_bytes;
   return CAME8_OK;
 }
 
@@ -867,20 +899,35 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
   if (!(h.clip_threshold > 0.0)) return fail(CAME8_EINVAL, "came8_step: clip_threshold must be > 0");
   if (!workspace) return fail(CAME8_EINVAL, "came8_step: workspace is NULL");
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-  Plan plan;
-  int rc = build_plan(tensors, n_tensors, h.block_size, 0, static_cast<char*>(workspace), plan);
-  if (rc != CAME8_OK) return rc;
+  int rc = CAME8_OK;
+  const auto key = std::make_pair(static_cast<const void*>(workspace), workspace_tag);
+  std::vector<uint8_t> inputs;
+  if (workspace_tag) inputs = plan_inputs(tensors, n_tensors, h.block_size, workspace);
+  std::shared_ptr<const Plan> cached;
+  if (workspace_tag) {
+    std::lock_guard<std::mutex> lk(g_cache_mu);
+    auto it = g_cache.find(key);
+    if (it != g_cache.end() && it->second.plan && it->second.inputs == inputs) cached = it->second.plan;
+  }
+  std::shared_ptr<Plan> built;
+  if (!cached) {
+    built = std::make_shared<Plan>();
+    rc = build_plan(tensors, n_tensors, h.block_size, 0, static_cast<char*>(workspace), *built);
+    if (rc != CAME8_OK) return rc;
+  }
+  const Plan& plan = cached ? *cached : *built;
   if (workspace_bytes < plan.total_bytes)
     return fail(CAME8_ESPACE, "came8_step: workspace has " + std::to_string(workspace_bytes) + " bytes, needs " +
                                   std::to_string(plan.total_bytes));
-  {
-    const uint64_t hsh = fnv1a(plan.blob.data(), plan.blob.size());
+  if (built) {
+    const uint64_t hsh = fnv1a(built->blob.data(), built->blob.size());
     std::lock_guard<std::mutex> lk(g_cache_mu);
-    const auto key = std::make_pair(static_cast<const void*>(workspace), workspace_tag);
     CacheEntry& ce = g_cache[key];
-    if (workspace_tag == 0 || ce.hash != hsh || ce.bytes != plan.blob.size()) {
+    ce.inputs.clear();  // set again below once this plan is the one uploaded
+    ce.plan.reset();
+    if (workspace_tag == 0 || ce.hash != hsh || ce.bytes != built->blob.size()) {
       drop_entry(ce);  // the previous upload from this entry has completed before its source is replaced
-      ce.keep = std::move(plan.blob);
+      ce.keep = std::move(built->blob);
       hipError_t e = hipMemcpyAsync(workspace, ce.keep.data(), ce.keep.size(), hipMemcpyHostToDevice, stream);
       if (e == hipSuccess) e = hipEventCreateWithFlags(&ce.done, hipEventDisableTiming);
       if (e == hipSuccess) e = hipEventRecord(ce.done, stream);
@@ -891,6 +938,12 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       }
       ce.hash = hsh;
       ce.bytes = ce.keep.size();
+    }
+    built->blob.clear();  // uploaded (or already on the device): the launches need only the offsets
+    built->blob.shrink_to_fit();
+    if (workspace_tag) {
+      ce.inputs = std::move(inputs);
+      ce.plan = built;
     }
   }
   Hp hp = make_hp(h);
