@@ -190,24 +190,32 @@ class _Came8Base(torch.optim.Optimizer):
                                  float(group["clip_threshold"]), float(group["weight_decay"]),
                                  int(group["block_size"]), flags)
 
-    def _workspace(self, device: torch.device, descs, n: int, block_size: int):
-        """(workspace tensor, tag) for `device`, grown when the tensor list needs more.
+    def _workspace(self, group: dict, device: torch.device, descs, n: int, block_size: int):
+        """(workspace tensor, tag) for one param group on `device`, grown when its tensor list needs
+        more.
 
-        The workspace holds the launch plan between steps and nothing else writes to it; each
-        allocation gets a fresh tag, so the library never trusts a plan left in reused memory.
+        The workspace holds the group's launch plan between steps and nothing else writes to it; each
+        allocation gets a fresh tag, so the library never trusts a plan left in reused memory.  Each
+        param group has a workspace of its own: groups that shared one would replace each other's
+        plan on every step (an upload, and a wait for the previous one, per group and step).
         """
         lib = _lib.load()
         need = ctypes.c_size_t(0)
         _lib.check(lib.came8_workspace_size(descs, n, block_size, ctypes.byref(need)), "came8_workspace_size")
         cache = self.__dict__.setdefault("_came8_workspaces", {})
-        ent = cache.get(device)
+        key = (device, id(group))
+        ent = cache.get(key)
+        if ent is None:  # a new group (or groups replaced by load_state_dict): drop workspaces of gone groups
+            live = {id(g) for g in self.param_groups}
+            for k in [k for k in cache if k[1] not in live]:
+                lib.came8_release_workspace(cache.pop(k)[0].data_ptr())
         if ent is None or ent[0].numel() < need.value:
             if ent is not None:
                 lib.came8_release_workspace(ent[0].data_ptr())
             ws = torch.empty(max(int(need.value), 256), dtype=torch.uint8, device=device)
             weakref.finalize(ws, _release_workspace, ws.data_ptr())
             ent = (ws, _lib.new_workspace_tag())
-            cache[device] = ent
+            cache[key] = ent
         return ent
 
     def _prepare_param(self, p: torch.Tensor, block_size: int):
@@ -296,7 +304,7 @@ class _Came8Base(torch.optim.Optimizer):
                     d.prefix, d.rows, d.cols = 1, 1, p.numel()
                     d.factored = 0
                 self._fill_desc(d, p, state)
-            ws, tag = self._workspace(device, descs, n, block_size)
+            ws, tag = self._workspace(group, device, descs, n, block_size)
             with torch.cuda.device(device):
                 stream = torch.cuda.current_stream(device).cuda_stream
                 _lib.check(lib.came8_step(descs, n, ctypes.byref(hp), ws.data_ptr(), ws.numel(), tag, stream),
