@@ -2052,11 +2052,13 @@ __global__ __launch_bounds__(kThreads) void k_2d_rows(const DevTensor* __restric
           for (int j = 0; j < kTile2; ++j)
             u[j] = (clip_fast && !div_exact_needed(u[j])) ? div_fast(u[j], clip, crcp) : u[j] / clip;
         }
-        const float sc_old = scale_s8(am_old);  // after the loads: its rare branch would wait for am_old
-        const bool have_m = am_old > 0.0f;
+        // the guard `am_old > 0 ? code*scale : 0` folded into the scale: code*0 is a zero too (its sign
+        // can differ, which changes no code, sum or parameter)
+        // (after the loads: scale_s8's rare branch would make the column-factor loads wait for am_old)
+        const float sc_old = am_old > 0.0f ? scale_s8(am_old) : 0.0f;
 #pragma unroll
         for (int j = 0; j < kTile2; ++j) {
-          const float mold = have_m ? code_elem(qw, j) * sc_old : 0.0f;
+          const float mold = code_elem(qw, j) * sc_old;
           m2d_from_u(u[j], mold, hp, m[j], res[j]);
           abits = max(abits, abs_bits(m[j]));
           rsum += res[j];
