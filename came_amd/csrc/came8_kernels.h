@@ -706,8 +706,10 @@ __global__ __launch_bounds__(kThreads) void k_tiny_pass2(const DevTensor* __rest
 // so d = u - m is the reference's; it then sums d*d with fused multiply-adds and adds eps1 once per
 // summed element count.  The sums differ from the reference's only in the order of addition and the
 // rounding of d*d: a few 1e-8 relative even where one element dominates a short column.
+// The 16-bit-gradient UA variants of 256 threads are held to two resident workgroups per CU: left
+// free, the compiler spills a few registers to AGPRs and the total leaves room for one only.
 template <typename TG, int V, int K, int TPB, bool F32ST, bool UA = false>
-__global__ __launch_bounds__(TPB) void k_fact_pass2(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+__global__ __launch_bounds__(TPB, (UA && sizeof(typename TG::storage) == 2 && TPB == 256) ? 2 : 1) void k_fact_pass2(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                     const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using GS = typename TG::storage;
   using Acc = ColAcc<V, K>;
