@@ -112,6 +112,7 @@ struct Plan {
   std::map<int, WorkList> tiles2d;       // 8bit2d momentum pass, scalar form (per 16 rows x 256 columns)
   WorkList res2d;                        // 8bit2d residual row states after the scalar form (per tile row)
   std::map<int, WorkList> param2d_v;     // 8bit2d parameter write, vector form, by param type
+  std::map<int, WorkList> param2d_b;     // 8bit2d parameter write, band form (rows >= 1024 wide)
   std::map<int, WorkList> param2d;       // 8bit2d parameter write, scalar form, by param type
   size_t plan_bytes = 0;
   size_t zero_off = 0;  // kZeroBytes of zeros inside the plan blob
@@ -484,7 +485,10 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
         add_item(plan.tiles2d[t.grad_dtype], i, int64_t(d.tr) * ceil_div(d.C, 256));
         add_item(plan.res2d, i, d.tr);
       }
-      if (d.v2dp) add_item(plan.param2d_v[t.param_dtype], i, ceil_div(d.N, kParam2Items));
+      if (d.v2dp && d.C >= kP3BandMinCols)
+        add_item(plan.param2d_b[t.param_dtype], i, ceil_div(d.R, int64_t(kParam2BandRows)) * ceil_div(d.C, int64_t(kTile)));
+      else if (d.v2dp)
+        add_item(plan.param2d_v[t.param_dtype], i, ceil_div(d.N, kParam2Items));
       else add_item(plan.param2d[t.param_dtype], i, ceil_div(d.N, kTile));
       continue;  // the clip of this layout has no parity-mode variant (the reference sums it with float atomics)
     }
@@ -525,6 +529,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
   for (auto& kv : plan.tiles2d_v) place(kv.second);
   for (auto& kv : plan.tiles2d) place(kv.second);
   for (auto& kv : plan.param2d_v) place(kv.second);
+  for (auto& kv : plan.param2d_b) place(kv.second);
   for (auto& kv : plan.param2d) place(kv.second);
   place(plan.res2d);
   for (auto& kv : plan.upd) place(kv.second);
@@ -577,6 +582,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     for (auto& kv : plan.tiles2d_v) put(kv.second);
     for (auto& kv : plan.tiles2d) put(kv.second);
     for (auto& kv : plan.param2d_v) put(kv.second);
+    for (auto& kv : plan.param2d_b) put(kv.second);
     for (auto& kv : plan.param2d) put(kv.second);
     put(plan.res2d);
     for (auto& kv : plan.upd) put(kv.second);
@@ -1062,6 +1068,14 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     const WorkList& wl = kv.second;
     GenFn fn;
     CAME8_TYPE_SWITCH1(k_2d_param_v, kv.first, fn);
+    { PhaseTimer pt(PH_PARAM2D, alg_bytes(plan, wl, tensors, PH_PARAM2D, h.weight_decay != 0.0), stream);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+    if ((rc = check_launch("param2d")) != CAME8_OK) return rc; }
+  }
+  for (auto& kv : plan.param2d_b) {
+    const WorkList& wl = kv.second;
+    GenFn fn;
+    CAME8_TYPE_SWITCH1(k_2d_param_b, kv.first, fn);
     { PhaseTimer pt(PH_PARAM2D, alg_bytes(plan, wl, tensors, PH_PARAM2D, h.weight_decay != 0.0), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
     if ((rc = check_launch("param2d")) != CAME8_OK) return rc; }

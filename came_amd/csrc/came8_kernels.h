@@ -1954,6 +1954,7 @@ __global__ __launch_bounds__(kThreads) void k_generic_update(const DevTensor* __
 constexpr int kTile2 = 16;
 constexpr int kParam2Groups = 4;                    // 8-element groups per thread of the vector parameter write
 constexpr int kParam2Items = kParam2Groups * kTile;  // elements per work item of the vector parameter write
+constexpr int kParam2BandRows = 32;  // rows per work item of the band form of the parameter write
 
 // one element of the momentum pass from its clipped update u = (g*r)*c / clip:
 // m = m_old*b1 + u*(1-b1); res = (u - m)^2 + eps1
@@ -2279,6 +2280,63 @@ __global__ __launch_bounds__(kThreads) void k_2d_param_v(const DevTensor* __rest
 #pragma unroll
       for (int v = 0; v < 8; ++v) pv[v] = p2d_new<TP>(praw[gi][v], code_elem(qw, v), sc, rr[gi], cr[gi][v], hp);
       store8<TP>(p + e, pv);
+    }
+  }
+}
+
+// Parameter write, band form (C a multiple of 16; parameter and codes 16-byte aligned).  A work item
+// is (kParam2BandRows rows, a segment of at most kTile columns); thread t owns 8 columns (half a
+// tile row), loads their residual column factors once and streams the rows with the next row's
+// loads in flight.  The same arithmetic as k_2d_param_v.
+template <typename TP>
+__global__ __launch_bounds__(kThreads) void k_2d_param_b(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                         const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using PS = typename TP::storage;
+  const int tid = threadIdx.x;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t R = t.R, C = t.C, tc = t.tc;
+    const int64_t nseg = (C + kTile - 1) / kTile;
+    const int64_t local = w - wstart[slot];
+    const int64_t band = local / nseg, seg = local - band * nseg;
+    const int64_t r0 = band * kParam2BandRows;
+    const int64_t r1 = (r0 + kParam2BandRows < R) ? (r0 + kParam2BandRows) : R;
+    const int64_t col = seg * kTile + int64_t(tid) * 8;
+    if (col >= C) continue;  // no barrier below: idle lanes may leave the item
+    CAME8_GLOBAL PS* __restrict__ p = gbl(static_cast<PS*>(t.p));
+    const CAME8_GLOBAL int8_t* __restrict__ mq = gbl(t.mq);
+    const CAME8_GLOBAL float* __restrict__ ma = gbl(t.ma) + (col >> 4);
+    const CAME8_GLOBAL float* __restrict__ rrfac = gbl(t.rrfac);
+    float cr[8];
+    load8<F32>(gbl(static_cast<const float*>(t.crfac)) + col, cr);
+    Raw8<TP> pA, pB;
+    u32x2 qA, qB;
+    float aA = 0.0f, aB = 0.0f, rA = 0.0f, rB = 0.0f;
+    auto load_row = [&](int64_t r, Raw8<TP>& pr, u32x2& q, float& am, float& rr) {
+      const int64_t e = r * C + col;
+      pr.load(p + e);
+      q = *(const CAME8_GLOBAL u32x2*)(mq + e);
+      am = ma[(r >> 4) * tc];
+      rr = rrfac[r];
+    };
+    auto do_row = [&](int64_t r, const Raw8<TP>& pr, const u32x2& q, float am, float rr) {
+      const uint32_t qw[2] = {q.x, q.y};
+      const float sc = am / kSignedQ;
+      float pv[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) pv[v] = p2d_new<TP>(pr[v], code_elem(qw, v), sc, rr, cr[v], hp);
+      store8<TP>(p + r * C + col, pv);
+    };
+    load_row(r0, pA, qA, aA, rA);
+    for (int64_t r = r0; r < r1; r += 2) {
+      if (r + 1 < r1) load_row(r + 1, pB, qB, aB, rB);
+      do_row(r, pA, qA, aA, rA);
+      if (r + 1 < r1) {
+        if (r + 2 < r1) load_row(r + 2, pA, qA, aA, rA);
+        do_row(r + 1, pB, qB, aB, rB);
+      }
     }
   }
 }

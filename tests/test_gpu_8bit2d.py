@@ -33,7 +33,7 @@ TIE_TOL = 1e-3
 EXACT_TIE = 1e-4
 CODE_FRAC = 2e-2
 SHAPES = [(64, 2048), (1000, 3), (3, 5000), (33, 5461), (130, 1024), (17, 17), (1, 1), (16, 16), (257, 129),
-          (4097, 129), (48, 4100), (37, 400), (5, 48)]
+          (4097, 129), (48, 4100), (37, 400), (5, 48), (40, 3072)]
 
 
 def _ohp(hp):
@@ -235,7 +235,7 @@ def test_8bit2d_vector_and_scalar_forms_agree_bitwise(dtype):
     which needs only 8-byte aligned codes, stays the same).  Both forms run the same arithmetic in
     the same order, so three steps must agree bit for bit."""
     dt = getattr(torch, dtype)
-    shapes = [(64, 2048), (37, 400), (5, 48), (130, 1024)]
+    shapes = [(64, 2048), (37, 400), (5, 48), (130, 1024), (40, 3072)]
     refs = P.make_params(shapes, dt, seed=81)
     gen = torch.Generator().manual_seed(82)
     grads = [[P.heavy_grad(gen, s, dt) for s in shapes] for _ in range(3)]
