@@ -13,6 +13,7 @@
 #include <cstring>
 #include <functional>
 #include <map>
+#include <tuple>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -196,21 +197,31 @@ bool tiny_matrix(const came8_tensor& t, bool s2d) {
 
 BandFn band_fn(int gdt, bool pass2, int V, int K, int TPB, int st, int ua);
 
+// The calling thread's current device, or -1 when no device answers (a host without a GPU).
+int current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();  // leave no sticky error behind for the caller's next HIP call
+    dev = -1;
+  }
+  return dev;
+}
+
 // Workgroups of kernel fn (tpb threads) resident on the current device at once: CUs times the
 // workgroups one CU holds (registers, LDS).  0 when no device answers (sizing on a host without a
-// GPU).  Cached per kernel.
+// GPU).  Cached per kernel and device.
 int64_t resident_slots(const void* fn, int tpb) {
   static std::mutex mu;
-  static std::map<std::pair<const void*, int>, int64_t> cache;
+  static std::map<std::tuple<const void*, int, int>, int64_t> cache;
   if (fn == nullptr) return 0;
+  const int dev = current_device();
   std::lock_guard<std::mutex> lk(mu);
-  const auto key = std::make_pair(fn, tpb);
+  const auto key = std::make_tuple(fn, tpb, dev);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
-  int dev = 0, cus = 0, per_cu = 0;
+  int cus = 0, per_cu = 0;
   int64_t slots = 0;
-  if (hipGetDevice(&dev) == hipSuccess &&
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+  if (dev >= 0 && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, tpb, 0) == hipSuccess)
     slots = int64_t(cus) * std::max(per_cu, 1);
   else
@@ -250,7 +261,8 @@ double schedule_makespan(const std::vector<double>& cost, int64_t slots) {
 std::vector<int> band_shrinks(const came8_tensor* ts, int32_t n, int32_t B) {
   std::vector<int> out(n, 0);
   std::map<BandKey, std::vector<int>> groups;
-  std::vector<int64_t> sig{B, n};  // what the result depends on (the plan is built on every step)
+  // what the result depends on (the plan is built on every step); slots differ between device kinds
+  std::vector<int64_t> sig{B, n, current_device()};
   for (int i = 0; i < n; ++i) {
     const came8_tensor& t = ts[i];
     if (!t.factored || t.rows < 1 || t.cols < 1 || t.prefix < 1) continue;
@@ -623,11 +635,11 @@ struct CacheEntry {
 // address (the plan holds pointers into the workspace) and the descriptors themselves.
 std::vector<uint8_t> plan_inputs(const came8_tensor* ts, int32_t n, int32_t B, const void* ws) {
   const size_t nb = size_t(std::max(n, 0)) * sizeof(came8_tensor);
-  std::vector<uint8_t> v(16 + sizeof(void*) + nb);
-  const int64_t head[2] = {n, B};
-  std::memcpy(v.data(), head, 16);
-  std::memcpy(v.data() + 16, &ws, sizeof(void*));
-  if (nb) std::memcpy(v.data() + 16 + sizeof(void*), ts, nb);
+  std::vector<uint8_t> v(24 + sizeof(void*) + nb);
+  const int64_t head[3] = {n, B, current_device()};  // band sizes depend on the device
+  std::memcpy(v.data(), head, 24);
+  std::memcpy(v.data() + 24, &ws, sizeof(void*));
+  if (nb) std::memcpy(v.data() + 24 + sizeof(void*), ts, nb);
   return v;
 }
 std::mutex g_cache_mu;
