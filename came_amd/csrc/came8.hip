@@ -129,7 +129,8 @@ void add_item(WorkList& wl, int32_t tid, int64_t count) {
 
 bool fast_block(int B) { return B >= 8 && B <= kTile && (B & (B - 1)) == 0; }
 
-constexpr int kP3BandRows = 32;       // rows per work item of the band form of P3
+constexpr int kP3BandRows = 32;       // rows per work item of the band form of P3 (at most)
+constexpr int64_t kP3MinItems = 1024;  // band-form P3 work items wanted per launch (4 per CU)
 constexpr int64_t kP3BandMinCols = 1024;  // narrower rows leave too many of a workgroup's lanes idle
 
 int log2_or_minus1(int B) {
@@ -479,6 +480,18 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     d.clip_part = reinterpret_cast<double*>(scr + o.clipp);
     d.clip = at(o.clip);
     scr += off;
+  }
+  // Few band-form P3 work items (small matrices) would leave most CUs idle: lower every band's
+  // height until the launch has kP3MinItems items or the bands are one row high.
+  for (int32_t rb = kP3BandRows; rb > 1; rb >>= 1) {
+    int64_t items = 0;
+    for (const DevTensor& d : plan.dev) items += d.p3_nbands > 0 ? d.P * d.p3_nbands * d.p3_nseg : 0;
+    if (items == 0 || items >= kP3MinItems) break;
+    for (DevTensor& d : plan.dev)
+      if (d.p3_nbands > 0) {
+        d.p3_rb = rb >> 1;
+        d.p3_nbands = ceil_div(d.R, int64_t(d.p3_rb));
+      }
   }
 
   // --- work lists ---
