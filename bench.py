@@ -176,6 +176,17 @@ def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False, tiles=F
     else:
         states = [orc.init_full8bit_state(s) for s in sample]
         step_fn = orc.full8bit_step
+    # every core this process may run on (the box's share), capped by OMP_NUM_THREADS where the host sets it
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
+    torch.set_num_threads(max(1, cores))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), model)
+    except OSError:
+        pass
     times = []
     for it in range(3):
         t0 = time.perf_counter()
@@ -190,6 +201,7 @@ def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False, tiles=F
         "value": round(nbytes / t / 1e9, 4),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
+        "cpu_model": model,
         "kind": "port",
         "sample": f"{len(sample)} tensors {sample} ({n_sample} elements) of {cfg_name}, oracle step after one "
                   f"warm-up, best of 2: {t * 1e3:.1f} ms; whole workload extrapolated by element count: "
@@ -207,6 +219,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--exact-norm", action="store_true",
+                    help="the opt-in clip norm (exactly rounded fp64 sum) instead of the reference's fp32 order")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the step, copy a MIB-sized device buffer --steps times (a plain copy "
                          "kernel of known bytes, to scale the FETCH_SIZE / WRITE_SIZE counters)")
@@ -253,6 +267,7 @@ def main():
         params[-1].grad = g
         grads.append(g)
     opt = getattr(came_amd, cls_name)(params, **hp)
+    opt.exact_norm = bool(args.exact_norm)
     print(f"[bench] {label}: {len(shapes)} tensors, {sum(math.prod(s) for s in shapes)} params; warmup {args.warmup}",
           file=sys.stderr, flush=True)
     for _ in range(args.warmup):
@@ -311,6 +326,7 @@ def main():
             "state": "fp32 momentum + fp32 row/col factors" if fp32_state
             else "int8 momentum in 16x16 tiles + uint8 row/col factors, block 256" if tiles
             else "int8 momentum + uint8 row/col factors, block 256",
+            "clip_norm": "exact fp64 (opt-in)" if args.exact_norm else "reference fp32 order (default)",
             "compulsory_bytes_per_step": nbytes,
             "step_roofline_frac": round(value / HBM_PEAK_GBS, 4),
         },

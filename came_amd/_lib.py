@@ -15,8 +15,9 @@ LIB_PATH = os.path.join(HERE, "lib", "libcame8.so")
 
 CAME8_F32, CAME8_BF16, CAME8_F16 = 0, 1, 2
 CAME8_OK, CAME8_EINVAL, CAME8_ESPACE, CAME8_EHIP = 0, -1, -2, -3
-ABI_VERSION = 3  # include/came8.h: CAME8_ABI_VERSION
-CAME8_FLAG_REFERENCE_NORM = 1
+ABI_VERSION = 4  # include/came8.h: CAME8_ABI_VERSION
+CAME8_FLAG_REFERENCE_NORM = 1  # the default (accepted for callers of ABI 3)
+CAME8_FLAG_EXACT_NORM = 2
 CAME8_STATE_Q8 = 0
 CAME8_STATE_FP32 = 1
 CAME8_STATE_8BIT2D = 2
@@ -31,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "came8_step",
     "came8_profile_enable",
     "came8_profile_read",
+    "came8_read_clip",
     "came8_quantize_blockwise",
     "came8_dequantize_blockwise",
 )
@@ -141,6 +143,8 @@ def load(path: str | None = None) -> ctypes.CDLL:
         lib.came8_profile_enable.argtypes = [i32]
         lib.came8_profile_read.restype = ctypes.c_int
         lib.came8_profile_read.argtypes = [ctypes.POINTER(Came8PhaseStat), i32, ctypes.POINTER(i32), i32]
+        lib.came8_read_clip.restype = ctypes.c_int
+        lib.came8_read_clip.argtypes = [vp, ctypes.c_uint64, i32, ctypes.POINTER(ctypes.c_float), vp]
         lib.came8_quantize_blockwise.restype = ctypes.c_int
         lib.came8_quantize_blockwise.argtypes = [vp, i64, i32, i32, vp, vp, vp]
         lib.came8_dequantize_blockwise.restype = ctypes.c_int

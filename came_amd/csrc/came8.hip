@@ -22,6 +22,7 @@
 #include "../../include/came8.h"
 #include "came8_dispatch.h"
 #include "came8_kernels.h"
+#include "came8_norm.h"
 
 using namespace came8;
 
@@ -107,7 +108,14 @@ struct Plan {
   std::map<TypeKey, WorkList> vecB;      // 1-D pass B (fast block sizes)
   std::map<int, WorkList> vecA;          // 1-D pass A, by grad type
   std::map<TypeKey, WorkList> generic;   // P3 / B for other block sizes (per quantisation block)
-  std::map<int, WorkList> refnorm;       // parity-mode clip, by grad type
+  // the clip's norm in the reference's order (came8_norm.h)
+  WorkList nest_w;                       // unit estimates, a workgroup per row band (matrices >= 256 wide)
+  WorkList nest_n;                       // unit estimates, a thread per unit (per 256 units)
+  WorkList nscan;                        // prefix of the estimates (one item per tensor)
+  std::map<int, WorkList> nseg2d;        // segment records of matrices, runs of kNormRunSegs, by grad type
+  std::map<int, WorkList> nseg;          // the other segments' records, by 2 * grad type + vector form
+  std::map<int, WorkList> nwalk;         // chain walks (8 items per tensor), by grad type
+  std::map<int, WorkList> nfinal;        // accumulators + tail + clip (one item per tensor), by grad type
   WorkList factor;                       // F1b / F2b (per state block)
   std::map<int, WorkList> tiles2d_v;     // 8bit2d momentum pass, vector form (per tile row), by grad type
   std::map<int, WorkList> tiles2d;       // 8bit2d momentum pass, scalar form (per 16 rows x 256 columns)
@@ -334,8 +342,7 @@ std::vector<int> band_shrinks(const came8_tensor* ts, int32_t n, int32_t B) {
   return out;
 }
 
-int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refnorm, char* ws_base, Plan& plan) {
-  (void)flags_refnorm;
+int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan& plan) {
   if (n < 0) return fail(CAME8_EINVAL, "came8: n_tensors must be >= 0");
   if (n > 0 && ts == nullptr) return fail(CAME8_EINVAL, "came8: tensors is NULL");
   if (B <= 0) return fail(CAME8_EINVAL, "came8: block_size must be > 0, got " + std::to_string(B));
@@ -411,7 +418,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       return o;
     };
     struct Offs {
-      size_t Rn, rfac, RRn, rrfac, Cn, cfac, CRn, crfac, pU, pW, pR, rm, rmr, clipp, clip, t2r, t2c;
+      size_t Rn, rfac, RRn, rrfac, Cn, cfac, CRn, crfac, pU, pW, pR, rm, rmr, clipp, clip, t2r, t2c, nest, nrec, nch;
     } o{};
     d.idx32 = d.N < (int64_t(1) << 31) ? 1 : 0;
     d.rowal = (d.C % B) == 0 ? 1 : 0;
@@ -460,6 +467,21 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       o.clipp = take(size_t(d.nclip) * 8);
       o.clip = take(8);
     }
+    // reference-order norm: unit estimates, segment records, chain accumulators (not for 8bit2d,
+    // whose clip is the reference's float sum)
+    d.nseg = 0;
+    d.nseg0 = 0;
+    d.nunit = 0;
+    if (!s2d) {
+      d.nseg = ceil_div(d.N - (d.N & 7), kNormSegElems);
+      const bool lds = t.factored && d.c8 && d.idx32 && reinterpret_cast<uintptr_t>(t.grad) % 16 == 0 && d.P == 1 &&
+                       !tiny_matrix(t, false) && d.C <= kNormLdsCols;
+      d.nseg0 = lds ? (d.N - (d.N & 7)) / kNormSegElems : 0;
+      d.nunit = t.factored ? d.P * d.nbands : d.nclip;
+      o.nest = take(size_t(d.nunit + 1) * 4);
+      o.nrec = take(size_t(d.nseg) * 3 * 8 * 4);
+      o.nch = take(8 * 4);
+    }
     scr_off[i] = scr;
     // store offsets temporarily as integers in the pointer fields (rebased below)
     auto at = [&](size_t x) { return reinterpret_cast<float*>(scr + x); };
@@ -479,6 +501,11 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     }
     d.clip_part = reinterpret_cast<double*>(scr + o.clipp);
     d.clip = at(o.clip);
+    if (!s2d) {
+      d.nest = at(o.nest);
+      d.nrec = reinterpret_cast<uint32_t*>(scr + o.nrec);
+      d.nchain = at(o.nch);
+    }
     scr += off;
   }
   // Few band-form P3 work items (small matrices) would leave most CUs idle: lower every band's
@@ -536,7 +563,18 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       if (fastB) add_item(plan.vecB[tk], i, ceil_div(d.N, kTile));
     }
     if (!fastB) add_item(plan.generic[tk], i, d.nbm);
-    add_item(plan.refnorm[t.grad_dtype], i, 1);
+    if (t.factored && !tiny_matrix(t, false) && d.C >= kThreads) add_item(plan.nest_w, i, d.nunit);
+    else add_item(plan.nest_n, i, ceil_div(d.nunit, int64_t(kThreads)));
+    add_item(plan.nscan, i, 1);
+    if (d.nseg > 0) {
+      // the vector forms need rows of whole aligned 8-element chunks and 32-bit flat indices; matrices
+      // (prefix 1) up to kNormLdsCols wide take runs of segments with their column factors in LDS
+      const bool fast = t.factored && d.c8 && d.idx32 && reinterpret_cast<uintptr_t>(t.grad) % 16 == 0;
+      if (d.nseg0 > 0) add_item(plan.nseg2d[t.grad_dtype], i, ceil_div(d.nseg0, int64_t(kNormRunSegs)));
+      if (d.nseg > d.nseg0) add_item(plan.nseg[t.grad_dtype * 2 + (fast ? 1 : 0)], i, ceil_div(d.nseg - d.nseg0, int64_t(4)));
+    }
+    add_item(plan.nwalk[t.grad_dtype], i, 8);
+    add_item(plan.nfinal[t.grad_dtype], i, 1);
   }
 
   // --- blob: DevTensor[n] then every work list (tids, wstart) ---
@@ -562,7 +600,13 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
   for (auto& kv : plan.vecB) place(kv.second);
   for (auto& kv : plan.vecA) place(kv.second);
   for (auto& kv : plan.generic) place(kv.second);
-  for (auto& kv : plan.refnorm) place(kv.second);
+  place(plan.nest_w);
+  place(plan.nest_n);
+  place(plan.nscan);
+  for (auto& kv : plan.nseg2d) place(kv.second);
+  for (auto& kv : plan.nseg) place(kv.second);
+  for (auto& kv : plan.nwalk) place(kv.second);
+  for (auto& kv : plan.nfinal) place(kv.second);
   place(plan.factor);
   plan.zero_off = align_up(off);
   off = plan.zero_off + kZeroBytes;
@@ -593,6 +637,11 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
       }
       rebase(d.clip_part);
       rebase(d.clip);
+      if (!d.mode2d) {
+        rebase(d.nest);
+        rebase(d.nrec);
+        rebase(d.nchain);
+      }
     }
     plan.blob.assign(plan.plan_bytes, 0);
     std::memcpy(plan.blob.data(), plan.dev.data(), sizeof(DevTensor) * size_t(n));
@@ -615,7 +664,13 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, uint8_t flags_refno
     for (auto& kv : plan.vecB) put(kv.second);
     for (auto& kv : plan.vecA) put(kv.second);
     for (auto& kv : plan.generic) put(kv.second);
-    for (auto& kv : plan.refnorm) put(kv.second);
+    put(plan.nest_w);
+    put(plan.nest_n);
+    put(plan.nscan);
+    for (auto& kv : plan.nseg2d) put(kv.second);
+    for (auto& kv : plan.nseg) put(kv.second);
+    for (auto& kv : plan.nwalk) put(kv.second);
+    for (auto& kv : plan.nfinal) put(kv.second);
     put(plan.factor);
   }
   return CAME8_OK;
@@ -773,12 +828,14 @@ int check_launch(const char* what) {
 // ---------------------------------------------------------------------------
 // optional per-launch device timing (HIP events on the launch stream)
 // ---------------------------------------------------------------------------
-const char* const kPhaseNames[] = {"pass1", "vec_passA", "row_mean", "factor_blocks", "clip", "clip_refnorm",
+const char* const kPhaseNames[] = {"pass1", "vec_passA", "row_mean", "factor_blocks", "clip", "norm_est",
                                    "pass2", "row_mean_res", "factor_blocks_res", "pass3", "vec_passB",
-                                   "generic_update", "tiles2d", "res_rows2d", "param2d"};
+                                   "generic_update", "tiles2d", "res_rows2d", "param2d", "norm_scan",
+                                   "norm_seg", "norm_walk", "norm_final"};
 constexpr int kNumPhases = sizeof(kPhaseNames) / sizeof(kPhaseNames[0]);
-enum Phase { PH_PASS1, PH_VECA, PH_ROWMEAN, PH_FACTOR, PH_CLIP, PH_CLIP_REF, PH_PASS2, PH_ROWMEAN_RES,
-             PH_FACTOR_RES, PH_PASS3, PH_VECB, PH_GENERIC, PH_TILES2D, PH_RES2D, PH_PARAM2D };
+enum Phase { PH_PASS1, PH_VECA, PH_ROWMEAN, PH_FACTOR, PH_CLIP, PH_NORM_EST, PH_PASS2, PH_ROWMEAN_RES,
+             PH_FACTOR_RES, PH_PASS3, PH_VECB, PH_GENERIC, PH_TILES2D, PH_RES2D, PH_PARAM2D, PH_NORM_SCAN,
+             PH_NORM_SEG, PH_NORM_WALK, PH_NORM_FINAL };
 
 struct Pending {
   int phase;
@@ -864,6 +921,7 @@ double alg_bytes(const Plan& plan, const WorkList& wl, const came8_tensor* ts, i
         tot += N * (1.0 + 2.0 * sp) + 4.0 * double(d.tr) * double(d.tc);
         (void)wd;
         break;
+      case PH_NORM_SEG: tot += N * sg; break;  // g (the factors come from cache)
       case PH_FACTOR: case PH_FACTOR_RES:  // one row + one column state: codes rw, scales rw
         tot += 2.0 * double(d.P * d.R + d.P * d.C) + 8.0 * double(d.nbr + d.nbc);
         break;
@@ -899,7 +957,7 @@ int came8_workspace_size(const came8_tensor* tensors, int32_t n_tensors, int32_t
     }
   }
   Plan plan;
-  const int rc = build_plan(tensors, n_tensors, block_size, 0, nullptr, plan);
+  const int rc = build_plan(tensors, n_tensors, block_size, nullptr, plan);
   if (rc != CAME8_OK) return rc;
   *bytes = plan.total_bytes;
   std::lock_guard<std::mutex> lk(mu);
@@ -943,7 +1001,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
   std::shared_ptr<Plan> built;
   if (!cached) {
     built = std::make_shared<Plan>();
-    rc = build_plan(tensors, n_tensors, h.block_size, 0, static_cast<char*>(workspace), *built);
+    rc = build_plan(tensors, n_tensors, h.block_size, static_cast<char*>(workspace), *built);
     if (rc != CAME8_OK) return rc;
   }
   const Plan& plan = cached ? *cached : *built;
@@ -984,7 +1042,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
   auto tids = [&](const WorkList& wl) { return reinterpret_cast<const int32_t*>(base + wl.tids_off); };
   auto wst = [&](const WorkList& wl) { return reinterpret_cast<const int64_t*>(base + wl.wstart_off); };
   const dim3 blk(kThreads);
-  const bool refnorm = (h.flags & CAME8_FLAG_REFERENCE_NORM) != 0;
+  const bool exact_norm = (h.flags & CAME8_FLAG_EXACT_NORM) != 0;
   const bool fastB = fast_block(h.block_size);
 
   // ---- P1 and 1-D pass A ----
@@ -1023,20 +1081,80 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     if ((rc = check_launch("factor_blocks")) != CAME8_OK) return rc; }
   }
   // ---- clip divisor ----
-  if (refnorm) {
-    for (auto& kv : plan.refnorm) {
+  if (!exact_norm) {  // the update norm in the reference's order (came8_norm.h)
+    using EstFn = void (*)(const DevTensor*, const int32_t*, const int64_t*, int, Hp);
+    using FinFn = void (*)(const DevTensor*, const int32_t*, int, Hp);
+    if (!plan.nest_w.tids.empty()) {
+      const WorkList& wl = plan.nest_w;
+      PhaseTimer pt(PH_NORM_EST, 0.0, stream);
+      hipLaunchKernelGGL(k_norm_est<true>, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl),
+                         int(wl.tids.size()), hp);
+      if ((rc = check_launch("norm_est")) != CAME8_OK) return rc;
+    }
+    if (!plan.nest_n.tids.empty()) {
+      const WorkList& wl = plan.nest_n;
+      PhaseTimer pt(PH_NORM_EST, 0.0, stream);
+      EstFn fn = k_norm_est<false>;
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      if ((rc = check_launch("norm_est")) != CAME8_OK) return rc;
+    }
+    if (!plan.nscan.tids.empty()) {
+      const WorkList& wl = plan.nscan;
+      PhaseTimer pt(PH_NORM_SCAN, 0.0, stream);
+      hipLaunchKernelGGL(k_norm_scan<>, dim3(grid_for(int64_t(wl.tids.size()))), blk, 0, stream, dT, tids(wl),
+                         int(wl.tids.size()));
+      if ((rc = check_launch("norm_scan")) != CAME8_OK) return rc;
+    }
+    for (auto& kv : plan.nseg2d) {
       const WorkList& wl = kv.second;
-      void (*fn)(const DevTensor*, const int32_t*, int, Hp) = nullptr;
-      CAME8_TYPE_SWITCH1(k_clip_refnorm, kv.first, fn);
-      { PhaseTimer pt(PH_CLIP_REF, alg_bytes(plan, wl, tensors, PH_CLIP_REF), stream);
-    hipLaunchKernelGGL(fn, dim3(grid_for(int64_t(wl.tids.size()))), blk, 0, stream, dT, tids(wl), int(wl.tids.size()), hp);
-      if ((rc = check_launch("clip_refnorm")) != CAME8_OK) return rc; }
+      GenFn fn;
+      CAME8_TYPE_SWITCH1(k_norm_seg2d, kv.first, fn);
+      int64_t cmax = 0;  // LDS for the widest matrix of the launch
+      for (int32_t ti : wl.tids) cmax = std::max(cmax, plan.dev[ti].C);
+      PhaseTimer pt(PH_NORM_SEG, alg_bytes(plan, wl, tensors, PH_NORM_SEG), stream);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, size_t(cmax) * 4, stream, dT, tids(wl), wst(wl),
+                         int(wl.tids.size()), hp);
+      if ((rc = check_launch("norm_seg2d")) != CAME8_OK) return rc;
+    }
+    for (auto& kv : plan.nseg) {
+      const WorkList& wl = kv.second;
+      GenFn fn = nullptr;
+      switch (kv.first) {
+        case 2 * CAME8_F32: fn = k_norm_seg<F32, false>; break;
+        case 2 * CAME8_F32 + 1: fn = k_norm_seg<F32, true>; break;
+        case 2 * CAME8_BF16: fn = k_norm_seg<BF16, false>; break;
+        case 2 * CAME8_BF16 + 1: fn = k_norm_seg<BF16, true>; break;
+        case 2 * CAME8_F16: fn = k_norm_seg<F16, false>; break;
+        case 2 * CAME8_F16 + 1: fn = k_norm_seg<F16, true>; break;
+        default: return fail(CAME8_EINVAL, "came8_step: no norm kernel for this variant");
+      }
+      PhaseTimer pt(PH_NORM_SEG, alg_bytes(plan, wl, tensors, PH_NORM_SEG), stream);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      if ((rc = check_launch("norm_seg")) != CAME8_OK) return rc;
+    }
+    for (auto& kv : plan.nwalk) {
+      const WorkList& wl = kv.second;
+      GenFn fn;
+      CAME8_TYPE_SWITCH1(k_norm_walk, kv.first, fn);
+      PhaseTimer pt(PH_NORM_WALK, 0.0, stream);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(kNormWalkThreads), 0, stream, dT, tids(wl), wst(wl),
+                         int(wl.tids.size()), hp);
+      if ((rc = check_launch("norm_walk")) != CAME8_OK) return rc;
+    }
+    for (auto& kv : plan.nfinal) {
+      const WorkList& wl = kv.second;
+      FinFn fn;
+      CAME8_TYPE_SWITCH1(k_norm_final, kv.first, fn);
+      PhaseTimer pt(PH_NORM_FINAL, 0.0, stream);
+      hipLaunchKernelGGL(fn, dim3(grid_for(int64_t(wl.tids.size()), kThreads)), blk, 0, stream, dT, tids(wl),
+                         int(wl.tids.size()), hp);
+      if ((rc = check_launch("norm_final")) != CAME8_OK) return rc;
     }
   }
   const bool any2d = !plan.tiles2d.empty() || !plan.tiles2d_v.empty();
-  if (!refnorm || any2d) {  // parity mode: only the 8bit2d tensors take this divisor
+  if (exact_norm || any2d) {  // reference order: only the 8bit2d tensors take this divisor
     PhaseTimer pt(PH_CLIP, 0.0, stream);
-    hipLaunchKernelGGL(k_clip<>, dim3(grid_for(n_tensors)), blk, 0, stream, dT, int(n_tensors), int(refnorm), hp);
+    hipLaunchKernelGGL(k_clip<>, dim3(grid_for(n_tensors)), blk, 0, stream, dT, int(n_tensors), int(!exact_norm), hp);
     if ((rc = check_launch("clip")) != CAME8_OK) return rc;
   }
   // ---- P2, residual factors ----
@@ -1194,6 +1312,25 @@ int came8_profile_read(came8_phase_stat* out, int32_t max_phases, int32_t* n_pha
       p.bytes[ph] = 0.0;
     }
   }
+  return CAME8_OK;
+}
+
+int came8_read_clip(const void* workspace, uint64_t workspace_tag, int32_t n_tensors, float* out, void* stream_ptr) {
+  if (!workspace || !out) return fail(CAME8_EINVAL, "came8_read_clip: null pointer");
+  std::shared_ptr<const Plan> plan;
+  {
+    std::lock_guard<std::mutex> lk(g_cache_mu);
+    auto it = g_cache.find(std::make_pair(workspace, workspace_tag));
+    if (it != g_cache.end()) plan = it->second.plan;
+  }
+  if (!plan) return fail(CAME8_EINVAL, "came8_read_clip: no step has run on this workspace and tag");
+  if (size_t(std::max(n_tensors, 0)) != plan->dev.size())
+    return fail(CAME8_EINVAL, "came8_read_clip: the last step had " + std::to_string(plan->dev.size()) + " tensors");
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  hipError_t e = hipStreamSynchronize(stream);
+  for (int32_t i = 0; i < n_tensors && e == hipSuccess; ++i)
+    e = hipMemcpy(out + i, plan->dev[i].clip, sizeof(float), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return fail(CAME8_EHIP, std::string("came8_read_clip: ") + hipGetErrorString(e));
   return CAME8_OK;
 }
 

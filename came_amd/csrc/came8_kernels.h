@@ -64,6 +64,13 @@ struct DevTensor {
   double* clip_part;  // clip numerator partials     [nclip]
   float* clip;        // clip divisor and rcp_for_div of it [2]
   int64_t nclip;
+  // reference-order norm (the clip's update norm replayed as the reference's eight fp32 chains)
+  int64_t nseg;       // chain segments of kNormSegElems flat elements over the first N - N % 8
+  int64_t nseg0;      // leading whole segments of the LDS-staged kernel (0: every segment is the other's)
+  int64_t nunit;      // estimate units: row bands of every matrix (factored), 2048-element tiles (1-D)
+  float* nest;        // estimated sum of u^2 per unit, then its exclusive prefix [nunit + 1]
+  uint32_t* nrec;     // per chain and segment: binade/flags, two integer sums [3][8][nseg]
+  float* nchain;      // the eight chain accumulators                           [8]
   uint64_t mC, mR;    // magic multipliers for n / C and n / R (n < 2^31)
   uint32_t sC, sR;    // and their shifts
   int32_t idx32;      // N < 2^31: flat indices fit the magic division
@@ -1301,8 +1308,8 @@ __device__ __forceinline__ float clip_from_norm(float norm, int64_t N, const Hp&
   return q < 1.0f ? 1.0f : q;
 }
 
-// only2d: leave every tensor but those of the 8bit2d layout alone (their divisor comes from the
-// parity-mode kernel)
+// only2d: leave every tensor but those of the 8bit2d layout alone (the others take the norm in the
+// reference's order, came8_norm.h)
 template <int = 0>  // a template only so that every translation unit may include this header
 __global__ __launch_bounds__(kThreads) void k_clip(const DevTensor* __restrict__ T, int ntens, int only2d, Hp hp) {
   __shared__ double ssum[4];
@@ -1342,49 +1349,6 @@ __device__ __forceinline__ float u_at(const DevTensor& t, int64_t e, const Hp& h
     return (t.rfac[row] * t.cfac[b * t.C + j]) * gv;
   }
   return rsqrt_ref(vec_v_new<TG>(t, e, gv, hp)) * gv;
-}
-
-// Parity mode: the norm summed in the order of the reference CPU kernel for
-// tensor.norm(2) on fp32 (8 interleaved fused-multiply-add accumulators over
-// the first N - N%8 elements, a left-to-right sum of the 8 accumulators, then
-// the remaining elements as separately rounded square-and-add), so the clip
-// divisor equals the reference's bit for bit.  One workgroup per tensor;
-// slow by design (serial in N/8).
-template <typename TG>
-__global__ __launch_bounds__(kThreads) void k_clip_refnorm(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
-                                                           int ntens, Hp hp) {
-  __shared__ float ubuf[kTile];
-  __shared__ float accs[8];
-  const int tid = threadIdx.x;
-  for (int k = blockIdx.x; k < ntens; k += gridDim.x) {
-    const DevTensor& t = T[tids[k]];
-    const int64_t N = t.N;
-    const int64_t main = N - (N % 8);
-    float acc = 0.0f;
-    for (int64_t base = 0; base < main; base += kTile) {
-      const int64_t cnt = (main - base < kTile) ? (main - base) : kTile;
-      for (int i = tid; i < cnt; i += kThreads) ubuf[i] = u_at<TG>(t, base + i, hp);
-      __syncthreads();
-      if (tid < 8)
-        for (int i = tid; i < cnt; i += 8) acc = fmaf(ubuf[i], ubuf[i], acc);
-      __syncthreads();
-    }
-    if (tid < 8) accs[tid] = acc;
-    __syncthreads();
-    if (tid == 0) {
-      float bsum = accs[0];
-      for (int j = 1; j < 8; ++j) bsum = bsum + accs[j];
-      for (int64_t d = main; d < N; ++d) {
-        const float u = u_at<TG>(t, d, hp);
-        const float uu = u * u;
-        bsum = bsum + uu;
-      }
-      const float c = clip_from_norm(sqrtf(bsum), N, hp);
-      t.clip[0] = c;
-      t.clip[1] = rcp_for_div(c);
-    }
-    __syncthreads();
-  }
 }
 
 // ===========================================================================

@@ -185,7 +185,7 @@ class _Came8Base(torch.optim.Optimizer):
     def _group_hparams(self, group: dict) -> _lib.Came8HParams:
         b1, b2, b3 = group["betas"]
         e0, e1 = group["eps"]
-        flags = _lib.CAME8_FLAG_REFERENCE_NORM if getattr(self, "reference_norm", False) else 0
+        flags = _lib.CAME8_FLAG_EXACT_NORM if getattr(self, "exact_norm", False) else 0
         return _lib.Came8HParams(float(group["lr"]), float(b1), float(b2), float(b3), float(e0), float(e1),
                                  float(group["clip_threshold"]), float(group["weight_decay"]),
                                  int(group["block_size"]), flags)
@@ -309,8 +309,26 @@ class _Came8Base(torch.optim.Optimizer):
                 stream = torch.cuda.current_stream(device).cuda_stream
                 _lib.check(lib.came8_step(descs, n, ctypes.byref(hp), ws.data_ptr(), ws.numel(), tag, stream),
                            "came8_step")
+            self.__dict__.setdefault("_came8_last_step", {})[(device, id(group))] = [p for p, _, _ in items]
             for p, pd in copyback:
                 p.data.copy_(pd)
+
+    def last_clip_divisors(self, group_index: int = 0) -> dict:
+        """{param: clip divisor max(rms(u) / clip_threshold, 1)} of the param group's last step, read
+        back from the device (came8_read_clip; synchronises with the current stream)."""
+        group = self.param_groups[group_index]
+        lib = _lib.load()
+        out = {}
+        for (device, gid), plist in self.__dict__.get("_came8_last_step", {}).items():
+            if gid != id(group):
+                continue
+            ws, tag = self.__dict__["_came8_workspaces"][(device, gid)]
+            vals = (ctypes.c_float * len(plist))()
+            with torch.cuda.device(device):
+                stream = torch.cuda.current_stream(device).cuda_stream
+                _lib.check(lib.came8_read_clip(ws.data_ptr(), tag, len(plist), vals, stream), "came8_read_clip")
+            out.update({p: float(v) for p, v in zip(plist, vals)})
+        return out
 
     @torch.no_grad()
     def step(self, closure=None):
@@ -381,7 +399,9 @@ class CAME8bitFull(_Came8Base):
             self.cuda_factored_nd_chunked_direct_row_sum_min_matrix_numel is None
             and self.cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel is None)
         self.track_cuda_rms_state = False
-        self.reference_norm = False
+        # the clip's update norm: the reference's own fp32 order (default), or with exact_norm = True
+        # the exactly rounded fp64 sum (one pass over the gradients less; not the reference's value)
+        self.exact_norm = False
 
 
 class CAME8bitMemory(CAME8bitFull):
@@ -612,7 +632,9 @@ class CAMECUDA(_Came8Base):
             weight_decay=float(weight_decay),
         )
         super().__init__(params, defaults)
-        self.reference_norm = False
+        # the clip's update norm: the reference's own fp32 order (default), or with exact_norm = True
+        # the exactly rounded fp64 sum (one pass over the gradients less; not the reference's value)
+        self.exact_norm = False
 
     @property
     def supports_memory_efficient_fp16(self):
@@ -628,7 +650,7 @@ class CAMECUDA(_Came8Base):
     def _group_hparams(self, group: dict) -> _lib.Came8HParams:
         b1, b2, b3 = group["betas"]
         e0, e1 = group["eps"]
-        flags = _lib.CAME8_FLAG_REFERENCE_NORM if getattr(self, "reference_norm", False) else 0
+        flags = _lib.CAME8_FLAG_EXACT_NORM if getattr(self, "exact_norm", False) else 0
         return _lib.Came8HParams(float(group["lr"]), float(b1), float(b2), float(b3), float(e0), float(e1),
                                  float(group["clip_threshold"]), float(group["weight_decay"]),
                                  self._WORK_BLOCK, flags)

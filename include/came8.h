@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define CAME8_ABI_VERSION 3
+#define CAME8_ABI_VERSION 4
 
 /* element types of parameters and gradients */
 #define CAME8_F32 0
@@ -63,8 +63,13 @@ extern "C" {
 #define CAME8_STATE_FP32 1 /* fp32 states, CAMECUDA layout */
 #define CAME8_STATE_8BIT2D 2 /* 8-bit states, 8bit2d layout (CAME8bit2D): momentum in 16x16 tiles */
 
-/* flags for came8_hparams.flags */
-#define CAME8_FLAG_REFERENCE_NORM 1u /* clip RMS summed in the reference CPU order (slow; parity runs) */
+/* flags for came8_hparams.flags.  By default the clip's update norm is the reference's own: torch's
+ * CPU norm(2) order (eight fp32 fused-multiply-add chains, came_pytorch/CAME8bitFull.py:121-122,1032),
+ * replayed bit for bit in parallel. */
+#define CAME8_FLAG_REFERENCE_NORM 1u /* the default; accepted for callers of ABI 3 */
+#define CAME8_FLAG_EXACT_NORM 2u     /* opt-in: the update norm as the exactly rounded fp64 sum instead
+                                        (one pass less; differs from the reference by the fp32 chains'
+                                        rounding error, ~1e-4 relative at 2^22 elements) */
 
 /*
  * One parameter tensor and its full8bit state, laid out exactly as the
@@ -210,6 +215,16 @@ typedef struct came8_phase_stat {
 
 int came8_profile_enable(int32_t on);
 int came8_profile_read(came8_phase_stat* out, int32_t max_phases, int32_t* n_phases, int32_t reset);
+
+/*
+ * Inspection: the clip divisor max(rms(u) / clip_threshold, 1) that the last came8_step on this
+ * workspace and tag computed for each of its n_tensors tensors, copied to out[] (host memory) after
+ * the stream has finished that step.  Synchronises the host with `stream`.  No reference
+ * counterpart (the reference keeps the value in a device scratch tensor); it lets a caller check
+ * the update norm, the one reduction whose rounding order the reference fixes
+ * (came_pytorch/CAME8bitFull.py:121-122,1032).
+ */
+int came8_read_clip(const void* workspace, uint64_t workspace_tag, int32_t n_tensors, float* out, void* stream);
 
 /*
  * Blockwise absmax quantisation of n fp32 values into int8 (is_signed, Q = 127)

@@ -231,8 +231,9 @@ def init_fp32_state(shape) -> Dict[str, object]:
 @torch.no_grad()
 def fp32_state_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *, beta1: float, beta2: float,
                     beta3: float, eps0: float, eps1: float, lr: float, clip_threshold: float,
-                    weight_decay: float) -> None:
-    """Reference CAMECUDA.py:275-326 (generic fp32-state step), same op order."""
+                    weight_decay: float, capture: Dict[str, torch.Tensor] | None = None) -> None:
+    """Reference CAMECUDA.py:275-326 (generic fp32-state step), same op order.  ``capture``, if a
+    dict, receives the clip divisor under "clip"."""
     st["step"] += 1
     if grad.dtype in (torch.float16, torch.bfloat16):
         grad = grad.float()
@@ -248,7 +249,10 @@ def fp32_state_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], 
         sq = st["exp_avg_sq"]
         sq.mul_(beta2).add_(upd, alpha=1.0 - beta2)
         upd = sq.clamp_min_(1e-30).rsqrt().mul_(grad)
-    upd.div_((_rms(upd) / clip_threshold).clamp_(min=1.0))
+    clipv = (_rms(upd) / clip_threshold).clamp_(min=1.0)
+    if capture is not None:
+        capture["clip"] = clipv.clone()
+    upd.div_(clipv)
     m.mul_(beta1).add_(upd, alpha=1.0 - beta1)
     if st["factored"]:
         rrow, rcol = st["exp_avg_res_row"], st["exp_avg_res_col"]

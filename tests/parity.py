@@ -190,11 +190,11 @@ def run_oracle(params, grads_per_step, hp: dict, steps: int):
     return ps, sts
 
 
-def run_gpu(cls, params, grads_per_step, hp: dict, steps: int, reference_norm=False, device="cuda"):
+def run_gpu(cls, params, grads_per_step, hp: dict, steps: int, exact_norm=False, device="cuda"):
     ps = [torch.nn.Parameter(p.clone().to(device)) for p in params]
     kw = {k: v for k, v in hp.items()}
     opt = cls(ps, **kw)
-    opt.reference_norm = reference_norm
+    opt.exact_norm = exact_norm
     for s in range(steps):
         for p, g in zip(ps, grads_per_step[s]):
             p.grad = g.to(device)
@@ -203,8 +203,7 @@ def run_gpu(cls, params, grads_per_step, hp: dict, steps: int, reference_norm=Fa
     return ps, opt
 
 
-def run_lockstep(cls, params, grads_per_step, hp: dict, steps: int, reference_norm=False, device="cuda",
-                 exact_norm=False):
+def run_lockstep(cls, params, grads_per_step, hp: dict, steps: int, exact_norm=False, device="cuda"):
     """GPU optimizer and CPU oracle side by side on the same inputs.
 
     Returns, per tensor: (gpu_param, ref_param, gpu_state, ref_state, tainted, flips) where
@@ -218,7 +217,7 @@ def run_lockstep(cls, params, grads_per_step, hp: dict, steps: int, reference_no
     ohp = oracle_hp(hp)
     ps = [torch.nn.Parameter(p.clone().to(device)) for p in params]
     opt = cls(ps, **hp)
-    opt.reference_norm = reference_norm
+    opt.exact_norm = exact_norm
     refs = [p.clone() for p in params]
     sts = [orc.init_full8bit_state(p.shape, ohp["block_size"]) for p in refs]
     tainted = [torch.zeros(p.shape, dtype=torch.bool) for p in params]
@@ -279,16 +278,17 @@ def check_untainted_params(gp: torch.Tensor, rp: torch.Tensor, tainted: torch.Te
     return float(tainted.float().mean())
 
 
-def run_teacher_forced(cls, params, grads_per_step, hp: dict, steps: int, reference_norm=False, device="cuda",
+def run_teacher_forced(cls, params, grads_per_step, hp: dict, steps: int, exact_norm=False, device="cuda",
                        check=None):
     """Every step starts the GPU from the oracle's state and parameters of the previous step, so each
     step's arithmetic is compared on identical inputs (no divergence carried from earlier code flips).
-    The oracle uses the reference's float32 norm in parity mode and the exactly rounded norm otherwise.
+    Both sides take the reference's float32 norm by default, and the exactly rounded norm with
+    exact_norm=True (the library's opt-in mode and the oracle's matching variant).
     `check(step, i, gpu_param, ref_param, gpu_state, ref_state, movement)` is called per tensor."""
     ohp = oracle_hp(hp)
     ps = [torch.nn.Parameter(p.clone().to(device)) for p in params]
     opt = cls(ps, **hp)
-    opt.reference_norm = reference_norm
+    opt.exact_norm = exact_norm
     refs = [p.clone() for p in params]
     sts = [orc.init_full8bit_state(p.shape, ohp["block_size"]) for p in refs]
     for s in range(steps):
@@ -307,7 +307,7 @@ def run_teacher_forced(cls, params, grads_per_step, hp: dict, steps: int, refere
         for i, (r, g, st) in enumerate(zip(refs, grads_per_step[s], sts)):
             before = r.double()
             cap = {}
-            orc.full8bit_step(r, g, st, capture=cap, exact_norm=not reference_norm, **ohp)
+            orc.full8bit_step(r, g, st, capture=cap, exact_norm=exact_norm, **ohp)
             mv = (r.double() - before).abs()
             if check is not None:
                 check(s + 1, i, ps[i].data, r, opt.state[ps[i]], st, mv, cap)

@@ -57,12 +57,11 @@ def test_ragged_500_full_size_vs_oracle():
     gen = torch.Generator(device=dev).manual_seed(5)
     ps = [torch.nn.Parameter(torch.randn(s, device=dev, generator=gen).mul_(0.02)) for s in shapes]
     opt = came_amd.CAME8bitFull(ps, **HP)
-    opt.reference_norm = True
     chk = _checked(shapes)
     refs = {i: ps[i].detach().cpu().clone() for i in chk}
     sts = {i: orc.init_full8bit_state(shapes[i], 256) for i in chk}
     ohp = P.oracle_hp(HP)
-    check = _tight_step_check(True, "C5 full size")
+    check = _tight_step_check("C5 full size")
     for step in range(2):
         grads = [bench.heavy_grad(s, gen, torch.float32, device=dev) for s in shapes]
         with torch.no_grad():

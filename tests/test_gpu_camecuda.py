@@ -45,7 +45,6 @@ def _run(shapes, dtype, steps, hp, seed):
     grads = [[P.heavy_grad(gen, s, dt) for s in shapes] for _ in range(steps)]
     gpu_p = [torch.nn.Parameter(p.clone().to("cuda")) for p in ref_p]
     opt = came_amd.CAMECUDA(gpu_p, **hp)
-    opt.reference_norm = True
     ohp = {k: v for k, v in P.oracle_hp(hp).items() if k != "block_size"}
     ref_st = [orc.init_fp32_state(s) for s in shapes]
     for step in range(steps):

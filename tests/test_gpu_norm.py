@@ -1,0 +1,164 @@
+"""GPU: the clip divisor of the default step against the reference's.
+
+The reference divides the update by max(u.norm(2) / sqrt(N) / clip_threshold, 1)
+(came_pytorch/CAME8bitFull.py:121-122,1032), where torch's CPU norm sums fp32 squares as eight
+serial fused-multiply-add chains; at these sizes the chains drift from the exact norm by up to ~1%
+(32000 x 4096), so only a replay of those chains gives the reference's value.  The library replays
+them in parallel (came_amd/csrc/came8_norm.h); these tests read its divisors back
+(came8_read_clip) and compare them with the oracle's, which calls torch.norm itself.
+
+Bit for bit wherever the update u itself is the reference's bit for bit: 1-D tensors (u is
+elementwise), and matrices whose gradients make the row and column factors exact in any summation
+order ("latin": magnitudes 2^-(10+l) with l = (a_i + b_j) mod 4 and a, b balanced, so every row and
+every column holds the same multiset of powers of two, and the row count is a power of two).  Other
+matrices: within 4 fp32 ulps, because the GPU forms the row/column means in fp64 rounded once while
+torch rounds along the way, so u can differ from the reference's by an ulp; the drift-regime test
+also checks that the exactly rounded norm misses the reference by far more than that.
+
+A clip threshold of 1e-6 keeps the divisor active (rms / threshold > 1), so that every bit of the
+norm reaches it.  Step 2 starts from the oracle's state (teacher-forced), so both sides norm the
+same update.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import came8_oracle as orc
+from tests import parity as P
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True, scope="module")
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import came_amd._lib as L
+    L.load()
+    torch.set_num_threads(8)
+    yield
+
+
+def _grad(gen, shape, kind, dtype):
+    n = math.prod(shape)
+    if kind == "normal":
+        g = torch.randn(n, generator=gen) * 1e-3
+    elif kind == "const":
+        g = torch.full((n,), 1e-3)
+    elif kind == "sparse":
+        g = torch.zeros(n)
+        k = max(1, n // 97)
+        g[torch.randint(0, n, (k,), generator=gen)] = torch.randn(k, generator=gen)
+    elif kind == "heavy":
+        return P.heavy_grad(gen, shape, dtype)
+    elif kind == "latin":
+        R, C = shape
+        a = torch.arange(R) % 4
+        b = torch.arange(C) % 4
+        a = a[torch.randperm(R, generator=gen)]
+        b = b[torch.randperm(C, generator=gen)]
+        l = (a.reshape(-1, 1) + b.reshape(1, -1)) % 4
+        sign = torch.where(torch.rand(R, C, generator=gen) < 0.5, -1.0, 1.0)
+        return (sign * torch.pow(2.0, -(10 + l).double()).float()).to(dtype)
+    elif kind == "scaled":  # rows of very different scales
+        g = torch.randn(shape, generator=gen) * torch.logspace(-6, 0, shape[0]).reshape(-1, *([1] * (len(shape) - 1)))
+    else:
+        raise ValueError(kind)
+    return g.reshape(shape).to(dtype)
+
+
+def _ulps(a: float, b: float) -> int:
+    ia = torch.tensor([a], dtype=torch.float32).view(torch.int32).item()
+    ib = torch.tensor([b], dtype=torch.float32).view(torch.int32).item()
+    return abs(ia - ib)
+
+
+def _run(cls_name, cases, steps=2, max_ulps=0, check_exact_gap=False, **hp_kw):
+    import came_amd
+    gen = torch.Generator().manual_seed(1234)
+    shapes = [c[0] for c in cases]
+    dts = [c[2] for c in cases]
+    params = [(torch.randn(s, generator=gen) * 0.02).to(dt) for s, dt in zip(shapes, dts)]
+    grads = [[_grad(gen, s, kind, dt) for s, kind, dt in cases] for _ in range(steps)]
+    hp = dict(lr=2e-4, weight_decay=1e-2, clip_threshold=1e-6)
+    hp.update(hp_kw)
+    ohp = P.oracle_hp(hp)
+    ps = [torch.nn.Parameter(p.clone().to(DEV)) for p in params]
+    opt = getattr(came_amd, cls_name)(ps, **hp)
+    fp32 = cls_name == "CAMECUDA"
+    refs = [p.clone() for p in params]
+    sts = [(orc.init_fp32_state(p.shape) if fp32 else orc.init_full8bit_state(p.shape, ohp["block_size"]))
+           for p in refs]
+    for s in range(steps):
+        with torch.no_grad():  # teacher forcing: the GPU starts from the oracle's state
+            for p, r, st in zip(ps, refs, sts):
+                p.data.copy_(r.to(DEV))
+                gst = opt.state[p]
+                for k, v in gst.items():
+                    if isinstance(v, torch.Tensor) and k in st and isinstance(st[k], torch.Tensor) and v.shape == st[k].shape:
+                        v.copy_(st[k].to(DEV))
+        for p, g in zip(ps, grads[s]):
+            p.grad = g.to(DEV)
+        opt.step()
+        got = opt.last_clip_divisors()
+        for i, (r, g, st) in enumerate(zip(refs, grads[s], sts)):
+            ex = None
+            if check_exact_gap:  # the exactly rounded norm on the same inputs (the oracle's opt-in branch)
+                cap2 = {}
+                st2 = {k: (v.clone() if isinstance(v, torch.Tensor) else v) for k, v in st.items()}
+                orc.full8bit_step(r.clone(), g, st2, capture=cap2, exact_norm=True, **ohp)
+                ex = float(cap2["clip"])
+            cap = {}
+            if fp32:
+                orc.fp32_state_step(r, g, st, capture=cap, **{k: v for k, v in ohp.items() if k != "block_size"})
+            else:
+                orc.full8bit_step(r, g, st, capture=cap, **ohp)
+            want = float(cap["clip"])
+            have = got[ps[i]]
+            assert want > 1.0, f"case {cases[i]}: the clip is not active"
+            exact = cases[i][1] == "latin" or len(cases[i][0]) == 1
+            tol = 0 if exact else max_ulps
+            d = _ulps(have, want)
+            print(f"[norm] {cls_name} step {s + 1} {cases[i]}: clip {have!r} vs {want!r}: {d} ulps"
+                  + ("" if ex is None else f"; exactly rounded norm: {_ulps(ex, want)} ulps"), flush=True)
+            assert d <= tol, (f"{cls_name} step {s + 1} case {cases[i]}: clip {have!r} != reference {want!r} "
+                              f"({d} ulps; {(have - want) / want:.3e} relative; allowed {tol})")
+            if ex is not None:
+                assert _ulps(ex, want) > 100, f"{cases[i]}: the exactly rounded norm is as close as the replay"
+
+
+F32, BF16 = torch.float32, torch.bfloat16
+
+ONE_D = [((n,), "normal", F32) for n in (1, 7, 8, 9, 63, 4095, 4096, 4097, 8193, 100003)] + [
+    ((1_000_000,), "const", F32), ((300_001,), "sparse", F32), ((250_000,), "heavy", BF16)]
+
+
+def test_norm_one_d():
+    _run("CAME8bit", ONE_D)
+
+
+MATRICES = [((2048, 2048), "latin", F32), ((256, 4096), "latin", BF16), ((64, 1000), "latin", F32),
+            ((2048, 2048), "normal", F32), ((64, 20000), "normal", BF16), ((1000, 3), "normal", F32),
+            ((3, 50257), "heavy", F32), ((4097, 129), "normal", BF16), ((777, 1024), "sparse", BF16),
+            ((512, 4096), "scaled", BF16), ((320, 320, 3, 3), "normal", F32), ((1280, 640, 1, 1), "heavy", F32),
+            ((5, 7, 1), "normal", F32)]
+
+
+def test_norm_matrices():
+    _run("CAME8bit", MATRICES, max_ulps=4)
+
+
+def test_norm_large_matrices_drift_regime():
+    """Chains of millions of elements, where the reference's norm is far from the exact one."""
+    _run("CAME8bit", [((8192, 4096), "latin", BF16), ((2048, 11008), "latin", BF16), ((4096, 11008), "normal", BF16)],
+         steps=1, max_ulps=4, check_exact_gap=True)
+
+
+def test_norm_memory_and_camecuda():
+    _run("CAME8bitMemory", [((256, 5460), "latin", BF16), ((300, 5461), "normal", BF16), ((2048,), "normal", BF16)],
+         max_ulps=4, betas=(0.9, 0.95, 0.995))
+    _run("CAMECUDA", [((256, 5460), "latin", BF16), ((300, 5461), "normal", BF16), ((2048,), "normal", F32),
+                      ((33, 4, 4), "heavy", F32)], max_ulps=4)

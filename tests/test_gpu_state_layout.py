@@ -71,7 +71,6 @@ def test_8bit2d_checkpoint_loads_into_came8bit(dtype):
     refs = [_cpu_state({"p": q.data})["p"] for q in ps]
     sts = [_cpu_state(opt2.state[q]) for q in ps]
     grads = _grads(shapes, dt, 20)
-    opt2.reference_norm = True
     _run(opt2, ps, grads)
     for i, (q, r, g, st) in enumerate(zip(ps, refs, grads, sts)):
         st["step"] = 0
@@ -176,7 +175,6 @@ def test_nd_per_matrix_checkpoint_loads_into_came8bitfull(shape, B):
     ref_state = _cpu_state(st)
     r = p.data.detach().cpu().clone()
     g = _grads([shape], torch.float32, 60)
-    opt.reference_norm = True
     _run(opt, [p], g)
     cap = {}
     before = r.double()
