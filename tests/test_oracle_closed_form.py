@@ -161,16 +161,49 @@ def test_reference_norm_order_replica(n):
 
 
 def test_reference_norm_error_on_c1_and_exact_norm_variant():
-    """The reference's float32 norm of a C1-sized update is off by ~1e-4 relative (why the GPU's default
-    mode, which rounds the exact value, differs from it), while exact_norm=True is the rounded fp64 value."""
+    """The reference's float32 norm of a C1-sized update is off the exact one by ~1e-4 relative (which is
+    why the library replays its order rather than computing the exact value)."""
     gen = torch.Generator().manual_seed(0)
     g = torch.randn(2048, 2048, generator=gen) * 1e-3
     u = g * 30.0
-    exact = math.sqrt(float((u.double() ** 2).sum()))
+    exact = math.sqrt(math.fsum(float(v) ** 2 for v in u.double().reshape(-1).tolist()))
     ref = u.norm(2).item()
     assert 1e-6 < abs(ref / exact - 1) < 5e-4
-    st = orc.init_full8bit_state((64, 64))
+
+
+def _exact_clip(u: torch.Tensor, thr: float) -> float:
+    """max(RN32(sqrt(sum u^2)) / RN32(sqrt(n)) / thr, 1) with the sum exactly rounded (math.fsum) and
+    each float32 operation rounded as torch rounds it."""
+    s = math.fsum(float(v) ** 2 for v in u.double().reshape(-1).tolist())
+    norm = np.float32(math.sqrt(s))
+    rms = np.float32(norm / np.float32(u.numel() ** 0.5))
+    q = np.float32(rms / np.float32(thr))
+    return float(max(q, np.float32(1.0)))
+
+
+@pytest.mark.parametrize("case", ["const4096", "const_ragged", "heavy", "rank_one"])
+def test_exact_norm_branch_clip(case):
+    """The oracle's exact_norm=True clip against math.fsum, bit for bit, on updates built so that the
+    oracle's step-1 update u is known: 1-D tensors at step 1 have u = g / sqrt((1-b2)(g^2+eps0)) elementwise
+    (recomputed here exactly as the oracle forms it), and for constant |g| every |u| is equal, so the
+    norm is |u| sqrt(n) (n = 4096: sqrt exact).  A dropped square, a wrong count or a float32 sum would
+    fail these (the C1-size test above shows the float32 sum is off by far more than an ulp)."""
+    gen = torch.Generator().manual_seed(7)
+    n = {"const4096": 4096, "const_ragged": 4099, "heavy": 200_003, "rank_one": 4096}[case]
+    if case.startswith("const") or case == "rank_one":
+        g = torch.full((n,), 3e-4) * torch.where(torch.rand(n, generator=gen) < 0.5, -1.0, 1.0)
+    else:
+        g = torch.randn(n, generator=gen) / torch.rand(n, generator=gen).clamp_min(1e-3) * 1e-3
+    hp = dict(HP, clip_threshold=1e-3)
+    st = orc.init_full8bit_state((n,))
     cap = {}
-    g2 = torch.randn(64, 64, generator=gen) * 1e-3
-    orc.full8bit_step(torch.zeros(64, 64), g2, st, capture=cap, exact_norm=True, **HP)
-    assert cap["clip"].item() > 1.0
+    orc.full8bit_step(torch.zeros(n), g.clone(), st, capture=cap, exact_norm=True, **hp)
+    # the update exactly as the oracle forms it at step 1 (zero state)
+    sq = (g * g + hp["eps0"]) * (1.0 - hp["beta2"])
+    u = sq.clamp_min(1e-30).rsqrt() * g
+    want = _exact_clip(u, hp["clip_threshold"])
+    assert float(cap["clip"]) == want, (case, float(cap["clip"]), want)
+    if case == "const4096":
+        absu = float(u.abs()[0])
+        assert float(np.float32(np.float32(absu * 64.0) / np.float32(64.0))) == float(np.float32(absu))
+        assert all(float(v) == absu for v in u.abs()[:50])
