@@ -1000,6 +1000,16 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
   }
   std::shared_ptr<Plan> built;
   if (!cached) {
+    // building and uploading a plan copies from host memory and synchronises on the previous upload:
+    // neither belongs in a graph
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess) {
+      (void)hipGetLastError();
+      cap = hipStreamCaptureStatusNone;
+    }
+    if (cap != hipStreamCaptureStatusNone)
+      return fail(CAME8_EINVAL, "came8_step: the stream is capturing and no launch plan exists for these tensors and "
+                                "this workspace; run one step (or a CAME8_FLAG_PLAN_ONLY call) before capture");
     built = std::make_shared<Plan>();
     rc = build_plan(tensors, n_tensors, h.block_size, static_cast<char*>(workspace), *built);
     if (rc != CAME8_OK) return rc;
@@ -1035,6 +1045,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       ce.plan = built;
     }
   }
+  if (h.flags & CAME8_FLAG_PLAN_ONLY) return CAME8_OK;
   Hp hp = make_hp(h);
   const char* base = static_cast<const char*>(workspace);
   hp.zeros = base + plan.zero_off;

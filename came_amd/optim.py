@@ -262,9 +262,13 @@ class _Came8Base(torch.optim.Optimizer):
             d.row_absmax = state["exp_avg_sq_absmax"].data_ptr()
 
     @torch.no_grad()
-    def _step_group(self, group: dict, params: list) -> None:
+    def _step_group(self, group: dict, params: list, plan_only: bool = False) -> None:
+        """One came8_step per device over the group's params; with plan_only the library builds and
+        uploads the launch plan and launches nothing (states are created, step counts not advanced)."""
         block_size = self._group_block_size(group)
         hp = self._group_hparams(group)
+        if plan_only:
+            hp.flags |= _lib.CAME8_FLAG_PLAN_ONLY
         by_device: dict = defaultdict(list)
         for p in params:
             by_device[p.device].append(p)
@@ -273,7 +277,8 @@ class _Came8Base(torch.optim.Optimizer):
             items = []
             for p in plist:
                 state, grad = self._prepare_param(p, block_size)
-                self._count_step(state)
+                if not plan_only:
+                    self._count_step(state)
                 if p.numel() == 0:
                     continue
                 items.append((p, state, grad))
@@ -309,6 +314,8 @@ class _Came8Base(torch.optim.Optimizer):
                 stream = torch.cuda.current_stream(device).cuda_stream
                 _lib.check(lib.came8_step(descs, n, ctypes.byref(hp), ws.data_ptr(), ws.numel(), tag, stream),
                            "came8_step")
+            if plan_only:
+                continue
             self.__dict__.setdefault("_came8_last_step", {})[(device, id(group))] = [p for p, _, _ in items]
             for p, pd in copyback:
                 p.data.copy_(pd)
@@ -569,9 +576,10 @@ class CAME8bit(CAME8bitFull):
 
     @torch.no_grad()
     def prime_for_cuda_graph(self) -> None:
-        """Create every state and the workspace before capture (CAME8bit.py:672-693)."""
+        """Create every state, the workspace and its uploaded launch plan before capture
+        (CAME8bit.py:672-693), so that a captured step only enqueues kernel launches."""
         for group in self.param_groups:
-            block_size = group["block_size"]
+            params = []
             for p in group["params"]:
                 if p.grad is None:
                     continue
@@ -579,7 +587,9 @@ class CAME8bit(CAME8bitFull):
                     raise RuntimeError("CAME does not support sparse gradients.")
                 if not (p.data.is_contiguous() and p.grad.is_contiguous()):
                     raise RuntimeError("CUDA graph capture requires contiguous parameter and gradient tensors.")
-                self._prepare_param(p, block_size)
+                params.append(p)
+            if params:
+                self._step_group(group, params, plan_only=True)
 
 
 # state tensors of the fp32-state layout (all fp32, whatever the parameter dtype)
@@ -864,9 +874,10 @@ class CAME8bit2D(_Came8Base):
 
     @torch.no_grad()
     def prime_for_cuda_graph(self) -> None:
-        """Create every state before capture (came_pytorch/CAME8bit2D.py:52-72, same messages)."""
+        """Create every state, the workspace and its uploaded launch plan before capture
+        (came_pytorch/CAME8bit2D.py:52-72, same messages)."""
         for group in self.param_groups:
-            block_size = group["block_size"]
+            params = []
             for p in group["params"]:
                 if p.grad is None:
                     continue
@@ -880,4 +891,6 @@ class CAME8bit2D(_Came8Base):
                     raise RuntimeError(f"Expected g.dtype == p.dtype, got {p.grad.dtype} vs {p.dtype}")
                 if not (p.data.is_contiguous() and p.grad.is_contiguous()):
                     raise RuntimeError("CUDA graph capture requires contiguous parameter and gradient tensors.")
-                self._prepare_param(p, block_size)
+                params.append(p)
+            if params:
+                self._step_group(group, params, plan_only=True)

@@ -70,6 +70,8 @@ extern "C" {
 #define CAME8_FLAG_EXACT_NORM 2u     /* opt-in: the update norm as the exactly rounded fp64 sum instead
                                         (one pass less; differs from the reference by the fp32 chains'
                                         rounding error, ~1e-4 relative at 2^22 elements) */
+#define CAME8_FLAG_PLAN_ONLY 4u      /* build and upload the launch plan for this workspace and tag, launch
+                                        nothing (prepares a later capture into a HIP graph) */
 
 /*
  * One parameter tensor and its full8bit state, laid out exactly as the
@@ -194,6 +196,10 @@ int came8_release_workspace(const void* workspace);
  * plan is re-uploaded only when the tensor list (pointers, shapes, dtypes) or
  * the block size changes, and the caller must not write to the workspace
  * between calls; tag 0 uploads on every call.
+ *
+ * Under HIP graph capture of `stream` the call only enqueues kernel launches, so the plan must exist
+ * already: a call that would have to build or upload it while the stream is capturing fails with
+ * CAME8_EINVAL.  Prepare with one eager call, or with CAME8_FLAG_PLAN_ONLY, before capture.
  */
 int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hparams* hp,
                void* workspace, size_t workspace_bytes, uint64_t workspace_tag, void* stream);
