@@ -116,12 +116,15 @@ def test_primed_capture_without_eager_step(cls_name, dtype):
 
 def test_capture_without_plan_fails_cleanly():
     """A capture that would have to build the launch plan (no eager step, no priming) fails with the
-    library's message instead of recording a host-to-device copy into the graph."""
+    library's message instead of recording a host-to-device copy into the graph.  (States created
+    inside a capture would be filled by captured kernels that never run: they are created first.)"""
     shapes = [(64, 96), (96,)]
     ps = [torch.nn.Parameter(p.cuda()) for p in P.make_params(shapes, torch.float32, seed=8)]
     opt = came_amd.CAME8bit(ps, lr=1e-3)
     for p in ps:
         p.grad = torch.randn_like(p) * 1e-3
+        opt._prepare_param(p, 256)  # the states exist (created and filled outside the capture); the plan does not
+    torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with pytest.raises(RuntimeError):
         with torch.cuda.graph(graph):
