@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "came8_workspace_size",
     "came8_release_workspace",
     "came8_step",
+    "came8_step_static",
     "came8_profile_enable",
     "came8_profile_read",
     "came8_read_clip",
@@ -140,6 +141,8 @@ def load(path: str | None = None) -> ctypes.CDLL:
         lib.came8_step.restype = ctypes.c_int
         lib.came8_step.argtypes = [ctypes.POINTER(Came8Tensor), i32, ctypes.POINTER(Came8HParams), vp, sz,
                                    ctypes.c_uint64, vp]
+        lib.came8_step_static.restype = ctypes.c_int
+        lib.came8_step_static.argtypes = [ctypes.POINTER(Came8Tensor), i32, ctypes.POINTER(Came8HParams), vp]
         lib.came8_profile_enable.restype = ctypes.c_int
         lib.came8_profile_enable.argtypes = [i32]
         lib.came8_profile_read.restype = ctypes.c_int

@@ -933,6 +933,38 @@ double alg_bytes(const Plan& plan, const WorkList& wl, const came8_tensor* ts, i
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// the static scratch of came8_step_static: a workspace that is part of the library's code object, so
+// that a step needs no allocation by anyone.  Each GPU the library runs on holds its own copy (at its
+// own address) until the process ends.  In host code `scratch` names a host-side stand-in; the device
+// address comes from hipGetSymbolAddress, once per device, and only that address is ever used.
+// ---------------------------------------------------------------------------
+constexpr size_t kStaticScratchBytes = size_t(32) << 20;
+constexpr uint64_t kStaticScratchTag = 0x5354415449435343ull;  // the plan-cache tag of the static scratch
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+std::map<int, void*> g_scratch_ptr;  // device -> address of that device's scratch
+
+int static_scratch(void** out) {
+  const int dev = current_device();
+  if (dev < 0) return fail(CAME8_EHIP, "came8_step_static: no current HIP device");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  auto it = g_scratch_ptr.find(dev);
+  if (it == g_scratch_ptr.end()) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(CAME8_EHIP, std::string("came8_step_static: hipGetSymbolAddress of the static scratch failed: ") +
+                                  hipGetErrorString(e));
+    it = g_scratch_ptr.emplace(dev, ptr).first;
+  }
+  *out = it->second;
+  return CAME8_OK;
+}
+}  // namespace
+
 // ===========================================================================
 // C ABI
 // ===========================================================================
@@ -1278,6 +1310,21 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     }
   }
   return CAME8_OK;
+}
+
+int came8_step_static(const came8_tensor* tensors, int32_t n_tensors, const came8_hparams* hp, void* stream) {
+  if (!hp) return fail(CAME8_EINVAL, "came8_step_static: hparams is NULL");
+  if (n_tensors == 0) return CAME8_OK;
+  void* ws = nullptr;
+  int rc = static_scratch(&ws);
+  if (rc != CAME8_OK) return rc;
+  size_t need = 0;
+  if ((rc = came8_workspace_size(tensors, n_tensors, hp->block_size, &need)) != CAME8_OK) return rc;
+  if (need > kStaticScratchBytes)
+    return fail(CAME8_ESPACE, "came8_step_static: these tensors need " + std::to_string(need) +
+                                  " bytes of scratch; the static scratch holds " + std::to_string(kStaticScratchBytes) +
+                                  " (use came8_step with a workspace of that size)");
+  return came8_step(tensors, n_tensors, hp, ws, kStaticScratchBytes, kStaticScratchTag, stream);
 }
 
 int came8_profile_enable(int32_t on) {

@@ -285,30 +285,7 @@ class _Came8Base(torch.optim.Optimizer):
             if not items:
                 continue
             n = len(items)
-            descs = (_lib.Came8Tensor * n)()
-            keep, copyback = [], []
-            for i, (p, state, grad) in enumerate(items):
-                pd = p.data
-                if not pd.is_contiguous():
-                    pd = pd.contiguous()
-                    copyback.append((p, pd))
-                g = grad if grad.is_contiguous() else grad.contiguous()
-                keep.append(g)
-                d = descs[i]
-                d.param = pd.data_ptr()
-                d.grad = g.data_ptr()
-                d.param_dtype = _DTYPE_CODE[p.dtype]
-                d.grad_dtype = _DTYPE_CODE[g.dtype]
-                d.state_kind = self._STATE_KIND
-                if self._is_factored(state):
-                    shape = tuple(p.shape)
-                    d.prefix = math.prod(shape[:-2])
-                    d.rows, d.cols = shape[-2], shape[-1]
-                    d.factored = 1
-                else:
-                    d.prefix, d.rows, d.cols = 1, 1, p.numel()
-                    d.factored = 0
-                self._fill_desc(d, p, state)
+            descs, keep, copyback = self._descriptors(items)
             ws, tag = self._workspace(group, device, descs, n, block_size)
             with torch.cuda.device(device):
                 stream = torch.cuda.current_stream(device).cuda_stream
@@ -319,6 +296,35 @@ class _Came8Base(torch.optim.Optimizer):
             self.__dict__.setdefault("_came8_last_step", {})[(device, id(group))] = [p for p, _, _ in items]
             for p, pd in copyback:
                 p.data.copy_(pd)
+
+    def _descriptors(self, items: list):
+        """came8_tensor descriptors of (param, state, grad) triples (include/came8.h), the contiguous
+        gradient copies they point to, and (param, contiguous copy) pairs to write back after the step."""
+        descs = (_lib.Came8Tensor * len(items))()
+        keep, copyback = [], []
+        for i, (p, state, grad) in enumerate(items):
+            pd = p.data
+            if not pd.is_contiguous():
+                pd = pd.contiguous()
+                copyback.append((p, pd))
+            g = grad if grad.is_contiguous() else grad.contiguous()
+            keep.append(g)
+            d = descs[i]
+            d.param = pd.data_ptr()
+            d.grad = g.data_ptr()
+            d.param_dtype = _DTYPE_CODE[p.dtype]
+            d.grad_dtype = _DTYPE_CODE[g.dtype]
+            d.state_kind = self._STATE_KIND
+            if self._is_factored(state):
+                shape = tuple(p.shape)
+                d.prefix = math.prod(shape[:-2])
+                d.rows, d.cols = shape[-2], shape[-1]
+                d.factored = 1
+            else:
+                d.prefix, d.rows, d.cols = 1, 1, p.numel()
+                d.factored = 0
+            self._fill_desc(d, p, state)
+        return descs, keep, copyback
 
     def last_clip_divisors(self, group_index: int = 0) -> dict:
         """{param: clip divisor max(rms(u) / clip_threshold, 1)} of the param group's last step, read

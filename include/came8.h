@@ -205,6 +205,18 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
                void* workspace, size_t workspace_bytes, uint64_t workspace_tag, void* stream);
 
 /*
+ * came8_step without a caller workspace, for callers that cannot allocate device memory (code under
+ * HIP graph capture that must not call hipMalloc, tight serving loops, harnesses that forbid
+ * allocation).  No counterpart in the reference.  The workspace is a static 32 MiB array in the
+ * library's code object (one per GPU, held until the process ends); the call allocates nothing.
+ * Tensor lists whose workspace (came8_workspace_size) exceeds 32 MiB fail with CAME8_ESPACE.  Every
+ * call on one GPU shares that GPU's array and its cached launch plan: calls that overlap on one GPU
+ * (other streams, other threads) race and must be serialised by the caller.  Otherwise as
+ * came8_step with a nonzero workspace tag (the plan is rebuilt when the tensor list changes).
+ */
+int came8_step_static(const came8_tensor* tensors, int32_t n_tensors, const came8_hparams* hp, void* stream);
+
+/*
  * Per-kernel device timing.  While enabled, every launch of came8_step is
  * bracketed by HIP events recorded on the launch stream; came8_profile_read
  * waits for the recorded events and returns, per kernel phase, the number of
