@@ -114,6 +114,8 @@ struct Plan {
   WorkList nscan;                        // prefix of the estimates (one item per tensor)
   std::map<int, WorkList> nseg2d;        // segment records of matrices, runs of kNormRunSegs, by grad type
   std::map<int, WorkList> nseg;          // the other segments' records, by 2 * grad type + vector form
+  WorkList ncscan;                       // each chain's prefix of its segment sums (8 items per tensor)
+  std::map<int, WorkList> nfix;          // records rebuilt under the chains' own estimates, by grad type * 2 + fast
   std::map<int, WorkList> nwalk;         // chain walks (8 items per tensor), by grad type
   std::map<int, WorkList> nfinal;        // accumulators + tail + clip (one item per tensor), by grad type
   WorkList factor;                       // F1b / F2b (per state block)
@@ -202,6 +204,12 @@ void magic_div(int64_t d, uint64_t& m, uint32_t& s) {
 // takes the thread-per-matrix passes.
 bool tiny_matrix(const came8_tensor& t, bool s2d) {
   return t.factored && !s2d && t.rows >= 1 && t.cols >= 1 && t.rows * t.cols <= kTinyElems;
+}
+
+// The clip-norm estimate of a tensor takes a workgroup per row band (matrices at least a workgroup
+// wide) rather than a thread per unit.
+bool norm_est_wide(const came8_tensor& t, const DevTensor& d) {
+  return t.factored && !tiny_matrix(t, false) && d.C >= kThreads;
 }
 
 BandFn band_fn(int gdt, bool pass2, int V, int K, int TPB, int st, int ua);
@@ -418,7 +426,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       return o;
     };
     struct Offs {
-      size_t Rn, rfac, RRn, rrfac, Cn, cfac, CRn, crfac, pU, pW, pR, rm, rmr, clipp, clip, t2r, t2c, nest, nrec, nch;
+      size_t Rn, rfac, RRn, rrfac, Cn, cfac, CRn, crfac, pU, pW, pR, rm, rmr, clipp, clip, t2r, t2c, nest, nrec, nsum,
+          nch;
     } o{};
     d.idx32 = d.N < (int64_t(1) << 31) ? 1 : 0;
     d.rowal = (d.C % B) == 0 ? 1 : 0;
@@ -472,14 +481,19 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     d.nseg = 0;
     d.nseg0 = 0;
     d.nunit = 0;
+    d.ngrp = 1;
     if (!s2d) {
       d.nseg = ceil_div(d.N - (d.N & 7), kNormSegElems);
       const bool lds = t.factored && d.c8 && d.idx32 && reinterpret_cast<uintptr_t>(t.grad) % 16 == 0 && d.P == 1 &&
                        !tiny_matrix(t, false) && d.C <= kNormLdsCols;
       d.nseg0 = lds ? (d.N - (d.N & 7)) / kNormSegElems : 0;
-      d.nunit = t.factored ? d.P * d.nbands : d.nclip;
+      const int64_t nbase = t.factored ? d.P * d.nbands : d.nclip;
+      // the thread-per-unit estimate groups single-band matrices and tiles into at most kNormMaxUnits units
+      if (!norm_est_wide(t, d) && (!t.factored || d.nbands == 1)) d.ngrp = ceil_div(nbase, kNormMaxUnits);
+      d.nunit = ceil_div(nbase, d.ngrp);
       o.nest = take(size_t(d.nunit + 1) * 4);
       o.nrec = take(size_t(d.nseg) * 3 * 8 * 4);
+      o.nsum = take(size_t(d.nseg) * 8 * 4);
       o.nch = take(8 * 4);
     }
     scr_off[i] = scr;
@@ -504,6 +518,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     if (!s2d) {
       d.nest = at(o.nest);
       d.nrec = reinterpret_cast<uint32_t*>(scr + o.nrec);
+      d.nsum = at(o.nsum);
       d.nchain = at(o.nch);
     }
     scr += off;
@@ -563,7 +578,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       if (fastB) add_item(plan.vecB[tk], i, ceil_div(d.N, kTile));
     }
     if (!fastB) add_item(plan.generic[tk], i, d.nbm);
-    if (t.factored && !tiny_matrix(t, false) && d.C >= kThreads) add_item(plan.nest_w, i, d.nunit);
+    if (norm_est_wide(t, d)) add_item(plan.nest_w, i, d.nunit);
     else add_item(plan.nest_n, i, ceil_div(d.nunit, int64_t(kThreads)));
     add_item(plan.nscan, i, 1);
     if (d.nseg > 0) {
@@ -572,6 +587,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       const bool fast = t.factored && d.c8 && d.idx32 && reinterpret_cast<uintptr_t>(t.grad) % 16 == 0;
       if (d.nseg0 > 0) add_item(plan.nseg2d[t.grad_dtype], i, ceil_div(d.nseg0, int64_t(kNormRunSegs)));
       if (d.nseg > d.nseg0) add_item(plan.nseg[t.grad_dtype * 2 + (fast ? 1 : 0)], i, ceil_div(d.nseg - d.nseg0, int64_t(4)));
+      add_item(plan.ncscan, i, 8);
+      add_item(plan.nfix[t.grad_dtype * 2 + (fast ? 1 : 0)], i, ceil_div(d.nseg, int64_t(kNormFixSegs)));
     }
     add_item(plan.nwalk[t.grad_dtype], i, 8);
     add_item(plan.nfinal[t.grad_dtype], i, 1);
@@ -605,6 +622,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
   place(plan.nscan);
   for (auto& kv : plan.nseg2d) place(kv.second);
   for (auto& kv : plan.nseg) place(kv.second);
+  place(plan.ncscan);
+  for (auto& kv : plan.nfix) place(kv.second);
   for (auto& kv : plan.nwalk) place(kv.second);
   for (auto& kv : plan.nfinal) place(kv.second);
   place(plan.factor);
@@ -640,6 +659,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       if (!d.mode2d) {
         rebase(d.nest);
         rebase(d.nrec);
+        rebase(d.nsum);
         rebase(d.nchain);
       }
     }
@@ -669,6 +689,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     put(plan.nscan);
     for (auto& kv : plan.nseg2d) put(kv.second);
     for (auto& kv : plan.nseg) put(kv.second);
+    put(plan.ncscan);
+    for (auto& kv : plan.nfix) put(kv.second);
     for (auto& kv : plan.nwalk) put(kv.second);
     for (auto& kv : plan.nfinal) put(kv.second);
     put(plan.factor);
@@ -831,11 +853,11 @@ int check_launch(const char* what) {
 const char* const kPhaseNames[] = {"pass1", "vec_passA", "row_mean", "factor_blocks", "clip", "norm_est",
                                    "pass2", "row_mean_res", "factor_blocks_res", "pass3", "vec_passB",
                                    "generic_update", "tiles2d", "res_rows2d", "param2d", "norm_scan",
-                                   "norm_seg", "norm_walk", "norm_final"};
+                                   "norm_seg", "norm_walk", "norm_final", "norm_fix"};
 constexpr int kNumPhases = sizeof(kPhaseNames) / sizeof(kPhaseNames[0]);
 enum Phase { PH_PASS1, PH_VECA, PH_ROWMEAN, PH_FACTOR, PH_CLIP, PH_NORM_EST, PH_PASS2, PH_ROWMEAN_RES,
              PH_FACTOR_RES, PH_PASS3, PH_VECB, PH_GENERIC, PH_TILES2D, PH_RES2D, PH_PARAM2D, PH_NORM_SCAN,
-             PH_NORM_SEG, PH_NORM_WALK, PH_NORM_FINAL };
+             PH_NORM_SEG, PH_NORM_WALK, PH_NORM_FINAL, PH_NORM_FIX };
 
 struct Pending {
   int phase;
@@ -1174,6 +1196,29 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       PhaseTimer pt(PH_NORM_SEG, alg_bytes(plan, wl, tensors, PH_NORM_SEG), stream);
       hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("norm_seg")) != CAME8_OK) return rc;
+    }
+    if (!plan.ncscan.tids.empty()) {
+      const WorkList& wl = plan.ncscan;
+      PhaseTimer pt(PH_NORM_SCAN, 0.0, stream);
+      hipLaunchKernelGGL(k_norm_cscan<>, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl),
+                         int(wl.tids.size()));
+      if ((rc = check_launch("norm_cscan")) != CAME8_OK) return rc;
+    }
+    for (auto& kv : plan.nfix) {
+      const WorkList& wl = kv.second;
+      GenFn fn = nullptr;
+      switch (kv.first) {
+        case 2 * CAME8_F32: fn = k_norm_fix<F32, false>; break;
+        case 2 * CAME8_F32 + 1: fn = k_norm_fix<F32, true>; break;
+        case 2 * CAME8_BF16: fn = k_norm_fix<BF16, false>; break;
+        case 2 * CAME8_BF16 + 1: fn = k_norm_fix<BF16, true>; break;
+        case 2 * CAME8_F16: fn = k_norm_fix<F16, false>; break;
+        case 2 * CAME8_F16 + 1: fn = k_norm_fix<F16, true>; break;
+        default: return fail(CAME8_EINVAL, "came8_step: no norm kernel for this variant");
+      }
+      PhaseTimer pt(PH_NORM_FIX, 0.0, stream);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      if ((rc = check_launch("norm_fix")) != CAME8_OK) return rc;
     }
     for (auto& kv : plan.nwalk) {
       const WorkList& wl = kv.second;

@@ -15,10 +15,11 @@
 // floats are exactly the multiples of 2^(E-23).  So inside a binade the chain is an integer sum of
 // per-element increments that do not depend on s.  Elements whose increment is not determined this
 // way are "special": the rounded square x*x is a half-integer after scaling (the true square may be
-// a tie, whose rounding depends on m's parity), the scaled square is 2^20 or more, or x*x is
-// subnormal, infinite or NaN.  (When the rounded square is not a half-integer, the true square
-// rounds the same way: its distance to hi = RN(x*x) is at most half an ulp of hi, less than the
-// distance from hi to any half-integer.)
+// a tie, whose rounding depends on m's parity), or x*x is infinite or NaN; an element whose increment
+// takes the chain out of the binade ends the run of known increments.  (When the rounded square is
+// not a half-integer, the true square rounds the same way: its distance to hi = RN(x*x) is at most
+// half an ulp of hi, less than the distance from hi to any half-integer, for every binade above the
+// subnormal one, whose half-integers lie on hi's grid.)
 //
 //   k_norm_est, k_norm_scan  an estimate of each chain's value along the tensor, from sums the step
 //                            has already formed (per row band: rm * sum_j c_j^2 * sum_i g_ij^2 / R_i;
@@ -26,18 +27,34 @@
 //   k_norm_seg               one wavefront per segment of kNormSegElems elements (512 per chain):
 //                            per chain, the candidate binade Ea of the estimate (and Ea + 1 near a
 //                            binade edge), the integer sums of the increments under each, whether
-//                            the segment holds special elements, and whether it holds a NaN.
-//   k_norm_walk              one workgroup per chain: from s = 0, skips every run of segments whose
+//                            the segment holds special elements, and whether it holds a NaN; and
+//                            the chain's fp32 sum of the segment's rounded squares.
+//   k_norm_cscan, k_norm_fix each chain's own estimate (the prefix of its segment sums), and records
+//                            rebuilt under that estimate's binades where the tensor-wide estimate
+//                            (an eighth of the prefix) named others.  The chains of heavy-tailed
+//                            updates drift far apart; without the rebuild most of their segments
+//                            would miss and be replayed.
+//   k_norm_walk              one wavefront per chain: from s = 0, skips every run of segments whose
 //                            record covers the chain's current binade without specials and without
-//                            leaving the binade (a block-wide scan of the integer sums), and replays
-//                            the segment where that fails element by element with fmaf: the chain's
-//                            start, binade crossings, specials, and estimates that missed.
+//                            leaving the binade (a wavefront scan of the integer sums), and replays
+//                            the segment where that fails: the chain's start, binade crossings,
+//                            specials, and estimates that missed.  A replay holds the segment's 512
+//                            elements in the wavefront and applies the increments of the chain's
+//                            binade with a saturating prefix sum up to the first element that leaves
+//                            the binade or is special, that element with fmaf, and so on: one round
+//                            per crossing or special element.
 //   k_norm_final             the eight accumulators and the tail in the reference's order, sqrt,
 //                            and the clip divisor.
 //
-// Only the replay uses floating-point addition on the chain; everything else is exact integer
-// arithmetic, so the result equals the serial chain bit for bit whatever the estimates were (they
-// only decide how many segments are replayed).
+// Only the replay's fmaf of an element that leaves the binade (or is special) uses floating-point
+// addition on the chain; everything else is exact integer arithmetic, so the result equals the
+// serial chain bit for bit whatever the estimates were (they only decide how many segments are
+// replayed).
+//
+// The subnormal binade E = -126 (unit 2^-149, which is also the spacing of subnormal squares) has
+// one more special element: |x| = 2^-75, whose square 2^-150 is half a unit (a tie) but rounds to 0
+// as x * x.  (For |x| = k * 2^-75 with odd k > 1 the square rounds to a nonzero multiple of the
+// unit, which is special there already.)
 #pragma once
 
 #include "came8_kernels.h"
@@ -49,7 +66,8 @@ constexpr int kNormChainSeg = kNormSegElems / 8;       // elements per chain per
 constexpr int kNormChunks = kNormSegElems / (8 * 64);  // 8-element chunks per lane of a segment's wavefront
 constexpr int kNormWalkSegs = 16;                      // segments per thread per batch of the walk
 constexpr int kNormGroup = 2;                          // chunks per lane loaded together
-constexpr float kNormIncrMax = 0x1p20f;                // scaled squares at or above this are special
+constexpr int64_t kNormMaxUnits = 4096;                // estimate units per tensor of single-band matrices
+                                                       // or tiles (more are grouped)
 
 // binade of a finite s >= 0: E with s in [2^E, 2^(E+1)), or -126 below 2^-125
 __device__ __forceinline__ int norm_binade(float s) {
@@ -76,7 +94,7 @@ __device__ __forceinline__ int norm_est_binade(float v) {
 //   * dh >= 2^23: in a normal binade (m >= 2^23) it takes the chain out of the binade by itself, so
 //     the segment's sum, at least 2^23, already fails the walk's test m + sum < 2^24;
 //   * the subnormal binade (E = -126, k = 149), where hi's own rounding may hide a tie: any nonzero
-//     increment there;
+//     increment there, and any |x| = 2^-75 (NormAcc's TINY form);
 //   * NaN or infinite squares: a NaN or infinite sum.
 // An exception saturates the segment's sum at kNormFull, which makes the walk replay the segment.
 constexpr float kNormSpecial = 0x1p24f;
@@ -134,56 +152,82 @@ __global__ __launch_bounds__(kThreads) void k_norm_est(const DevTensor* __restri
     } else {
       const int64_t u = (w - wstart[slot]) * kThreads + tid;
       if (u >= t.nunit) continue;
-      float e;
-      if (t.factored) {
-        const int64_t m = u / t.nbands;
-        const float* __restrict__ W = t.partW + u * t.C;
-        const float* __restrict__ cf = t.cfac + m * t.C;
-        float s = 0.0f;
-        for (int64_t j = 0; j < t.C; ++j) s = fmaf(cf[j] * cf[j], W[j], s);
-        e = norm_unit_rm(t, u) * s;
-      } else {
-        e = float(t.clip_part[u]);
+      // the unit's ngrp base units: row bands, or (ngrp > 1) whole single-band matrices, or tiles
+      const int64_t nbase = t.factored ? t.P * t.nbands : t.nclip;
+      const int64_t b0 = u * t.ngrp, b1 = min(nbase, b0 + t.ngrp);
+      float e = 0.0f;
+      for (int64_t b = b0; b < b1; ++b) {
+        if (t.factored) {
+          const int64_t m = b / t.nbands;
+          const float* __restrict__ W = t.partW + b * t.C;
+          const float* __restrict__ cf = t.cfac + m * t.C;
+          float s = 0.0f;
+          for (int64_t j = 0; j < t.C; ++j) s = fmaf(cf[j] * cf[j], W[j], s);
+          e += norm_unit_rm(t, b) * s;
+        } else {
+          e += float(t.clip_part[b]);
+        }
       }
       t.nest[u] = e;
     }
   }
 }
 
-// In-place exclusive prefix of the unit estimates of one tensor per workgroup; nest[nunit] = total.
-// Each thread sums a run of consecutive units, the runs' sums are scanned across the workgroup, and
-// each thread rewrites its run.
+constexpr int kScanBatch = 16;  // loads per thread in flight in block_excl_scan
+
+// In-place exclusive prefix sum of a[0, n) by one workgroup; returns the total to every thread.  Thread
+// i takes the i-th run of ceil(n / kThreads) consecutive values.  part: kThreads / kWave floats of LDS.
+__device__ float block_excl_scan(float* a, int64_t n, float* part) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t per = (n + kThreads - 1) / kThreads;
+  const int64_t u0 = min(n, int64_t(tid) * per), u1 = min(n, u0 + per);
+  float s = 0.0f;
+  for (int64_t u = u0; u < u1; u += kScanBatch) {
+    float v[kScanBatch];
+#pragma unroll
+    for (int q = 0; q < kScanBatch; ++q) v[q] = u + q < u1 ? a[u + q] : 0.0f;
+#pragma unroll
+    for (int q = 0; q < kScanBatch; ++q) s += v[q];
+  }
+  float incl = s;  // inclusive scan of the runs' sums over the wavefront, then over the wavefronts
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const float y = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += y;
+  }
+  if (lane == kWave - 1) part[wid] = incl;
+  __syncthreads();
+  float off = 0.0f, tot = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kThreads / kWave; ++k) {
+    off += k < wid ? part[k] : 0.0f;
+    tot += part[k];
+  }
+  float run = off + (incl - s);
+  for (int64_t u = u0; u < u1; u += kScanBatch) {
+    float v[kScanBatch];
+#pragma unroll
+    for (int q = 0; q < kScanBatch; ++q) v[q] = u + q < u1 ? a[u + q] : 0.0f;
+#pragma unroll
+    for (int q = 0; q < kScanBatch; ++q) {
+      if (u + q < u1) a[u + q] = run;
+      run += v[q];
+    }
+  }
+  __syncthreads();  // part is reused by the next call
+  return tot;
+}
+
+// In place: the unit estimates of one tensor per work item become their exclusive prefix; nest[nunit]
+// = total (block_excl_scan).
 template <int = 0>
 __global__ __launch_bounds__(kThreads) void k_norm_scan(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                         int ntens) {
-  __shared__ float part[kThreads];
-  const int tid = threadIdx.x;
+  __shared__ float part[kThreads / kWave];
   for (int k = blockIdx.x; k < ntens; k += gridDim.x) {
     const DevTensor& t = T[tids[k]];
-    const int64_t n = t.nunit;
-    const int64_t per = (n + kThreads - 1) / kThreads;
-    const int64_t u0 = min(n, int64_t(tid) * per), u1 = min(n, u0 + per);
-    float s = 0.0f;
-    for (int64_t u = u0; u < u1; ++u) s += t.nest[u];
-    part[tid] = s;
-    __syncthreads();
-    if (tid == 0) {
-      float run = 0.0f;
-      for (int i = 0; i < kThreads; ++i) {
-        const float v = part[i];
-        part[i] = run;
-        run += v;
-      }
-      t.nest[n] = run;
-    }
-    __syncthreads();
-    float run = part[tid];
-    for (int64_t u = u0; u < u1; ++u) {
-      const float v = t.nest[u];
-      t.nest[u] = run;
-      run += v;
-    }
-    __syncthreads();
+    const float tot = block_excl_scan(t.nest, t.nunit, part);
+    if (threadIdx.x == 0) t.nest[t.nunit] = tot;
   }
 }
 
@@ -195,15 +239,21 @@ __device__ __forceinline__ float norm_est_at(const DevTensor& t, int64_t f) {
     const int64_t m = t.idx32 ? int64_t(udiv_magic(uint32_t(row), t.mR, t.sR)) : row / t.R;
     if (m >= t.P) return t.nest[t.nunit];
     const int64_t i = row - m * t.R;
-    const int64_t b = int64_t(uint32_t(i) / uint32_t(t.rb));  // rows per band <= 256
-    u = m * t.nbands + b;
-    us = (m * t.R + b * t.rb) * t.C;
-    ue = (m * t.R + min((b + 1) * t.rb, t.R)) * t.C;
+    if (t.ngrp > 1) {  // groups of ngrp single-band matrices
+      u = m / t.ngrp;
+      us = u * t.ngrp * t.R * t.C;
+      ue = min(t.P, (u + 1) * t.ngrp) * t.R * t.C;
+    } else {
+      const int64_t b = int64_t(uint32_t(i) / uint32_t(t.rb));  // rows per band <= 256
+      u = m * t.nbands + b;
+      us = (m * t.R + b * t.rb) * t.C;
+      ue = (m * t.R + min((b + 1) * t.rb, t.R)) * t.C;
+    }
   } else {
-    u = f / kTile;
+    u = f / (kTile * t.ngrp);
     if (u >= t.nunit) return t.nest[t.nunit];
-    us = u * kTile;
-    ue = min(us + kTile, t.N);
+    us = u * kTile * t.ngrp;
+    ue = min(us + kTile * t.ngrp, t.N);
   }
   const float p0 = t.nest[u], p1 = t.nest[u + 1];
   return p0 + (p1 - p0) * (float(f - us) / float(ue - us));
@@ -214,14 +264,14 @@ __device__ __forceinline__ float norm_est_at(const DevTensor& t, int64_t f) {
 // ---------------------------------------------------------------------------
 // One halving step of norm_lane_sums: lanes with bit O set keep values [H, 2H) and send [0, H) to their
 // partner lane ^ O, which keeps [0, H); each adds what it receives (H, O compile-time constants).
-template <int H, int O>
-__device__ __forceinline__ void norm_halve(uint32_t (&v)[16], int lane) {
+template <int H, int O, typename T, int L>
+__device__ __forceinline__ void norm_halve(T (&v)[L], int lane) {
   const bool up = (lane & O) != 0;
 #pragma unroll
   for (int k = 0; k < H; ++k) {
-    const uint32_t mine = up ? v[H + k] : v[k];
-    const uint32_t other = up ? v[k] : v[H + k];
-    v[k] = mine + uint32_t(__shfl_xor(int(other), O, kWave));
+    const T mine = up ? v[H + k] : v[k];
+    const T other = up ? v[k] : v[H + k];
+    v[k] = mine + __shfl_xor(other, O, kWave);
   }
 }
 
@@ -229,8 +279,9 @@ __device__ __forceinline__ void norm_halve(uint32_t (&v)[16], int lane) {
 // partners lane ^ 32, ^ 16, ... leave each lane one value, value index (lane >> (6 - log2 NV)), summed
 // over the lanes that share those bits; butterfly sums over the remaining low lane bits complete it.
 // On return v[0] of lane l holds the total of value l >> 3 (NV = 8) or l >> 2 (NV = 16).
-template <int NV>
-__device__ __forceinline__ void norm_lane_sums(uint32_t (&v)[16], int lane) {
+template <int NV, typename T, int L>
+__device__ __forceinline__ void norm_lane_sums(T (&v)[L], int lane) {
+  static_assert(L >= NV, "too few values");
   if constexpr (NV == 16) {
     norm_halve<8, 32>(v, lane);
     norm_halve<4, 16>(v, lane);
@@ -240,10 +291,10 @@ __device__ __forceinline__ void norm_lane_sums(uint32_t (&v)[16], int lane) {
     norm_halve<4, 32>(v, lane);
     norm_halve<2, 16>(v, lane);
     norm_halve<1, 8>(v, lane);
-    v[0] += uint32_t(__shfl_xor(int(v[0]), 4, kWave));
+    v[0] += __shfl_xor(v[0], 4, kWave);
   }
-  v[0] += uint32_t(__shfl_xor(int(v[0]), 2, kWave));
-  v[0] += uint32_t(__shfl_xor(int(v[0]), 1, kWave));
+  v[0] += __shfl_xor(v[0], 2, kWave);
+  v[0] += __shfl_xor(v[0], 1, kWave);
 }
 
 // u at flat index e (u_at), with 32-bit index arithmetic where the flat indices fit.
@@ -275,20 +326,60 @@ struct NormChunk {
   }
 };
 
+// Per-lane, per-chain accumulators of one segment: the integer sums of the increments under the
+// candidate binades Ea (sa) and Ea + 1 (sb), their largest rounding distances (ra, rb), and the fp32
+// sum of the rounded squares (hs).
+struct NormAcc {
+  float sa[8], ra[8], sb[8], rb[8], hs[8];
+  __device__ __forceinline__ void clear() {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) sa[v] = ra[v] = sb[v] = rb[v] = hs[v] = 0.0f;
+  }
+  // element x of chain v under ka = 23 - Ea (TWO: and ka - 1).  TINY: Ea = -126, where |x| = 2^-75
+  // is a tie that x * x hides.
+  template <bool TWO, bool TINY>
+  __device__ __forceinline__ void add(int v, float x, int ka) {
+    const float hi = x * x;
+    hs[v] += hi;
+    norm_acc(hi, ka, sa[v], ra[v]);
+    if constexpr (TWO) norm_acc(hi, ka - 1, sb[v], rb[v]);
+    if constexpr (TINY) ra[v] = fabsf(x) == 0x1p-75f ? 0.5f : ra[v];
+  }
+  // both binades, with the TINY rule when tiny (the rebuild of k_norm_fix, a binade per chain)
+  __device__ __forceinline__ void add_both(int v, float x, int ka, bool tiny) {
+    const float hi = x * x;
+    norm_acc(hi, ka, sa[v], ra[v]);
+    norm_acc(hi, ka - 1, sb[v], rb[v]);
+    ra[v] = tiny && fabsf(x) == 0x1p-75f ? 0.5f : ra[v];
+  }
+};
+
+// The x of the 8 elements at flat index f (a multiple of 8): element v belongs to chain v.  Elements
+// at or past f1 (a multiple of 8) are 0.  FAST as for k_norm_seg.
+template <typename TG, bool FAST>
+__device__ __forceinline__ void norm_chunk_x(const DevTensor& t, int64_t f, int64_t f1, const Hp& hp,
+                                             float (&x)[8]) {
+  const bool in = f < f1;
+  if constexpr (FAST) {
+    NormChunk<TG> ch;
+    ch.load(t, uint32_t(in ? f : f1 - 8));
+#pragma unroll
+    for (int v = 0; v < 8; ++v) x[v] = in ? (ch.r * ch.cf[v]) * ch.g[v] : 0.0f;
+  } else {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) x[v] = in ? norm_x_at<TG>(t, f + v, hp) : 0.0f;
+  }
+}
+
 // The per-lane, per-chain sums of one segment's increments under the candidate binade (ka = 23 - Ea)
-// and, with TWO, under Ea + 1, with their largest rounding distances.  FULL: the segment holds all
-// kNormSegElems elements.
-template <typename TG, bool FAST, bool TWO, bool FULL>
+// and, with TWO, under Ea + 1, with their largest rounding distances and the sums of the squares.
+// FULL: the segment holds all kNormSegElems elements.
+template <typename TG, bool FAST, bool TWO, bool TINY, bool FULL>
 __device__ __forceinline__ void norm_seg_sums(const DevTensor& t, int64_t f0, int64_t f1, int ka, int lane,
-                                              const Hp& hp, float (&sa)[8], float (&ra)[8], float (&sb)[8],
-                                              float (&rb)[8]) {
+                                              const Hp& hp, NormAcc& a) {
   auto account = [&](const float (&x)[8]) {
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const float hi = x[v] * x[v];
-      norm_acc(hi, ka, sa[v], ra[v]);
-      if constexpr (TWO) norm_acc(hi, ka - 1, sb[v], rb[v]);
-    }
+    for (int v = 0; v < 8; ++v) a.add<TWO, TINY>(v, x[v], ka);
   };
   if constexpr (FAST) {
     // in a partial segment, chunks past its end load its last chunk and count for nothing
@@ -321,20 +412,23 @@ __device__ __forceinline__ void norm_seg_sums(const DevTensor& t, int64_t f0, in
   }
 }
 
-// Writes the records of one segment from the lanes' per-chain sums.
+// Writes the records of one segment from the lanes' per-chain sums, and the chains' sums of squares.
 __device__ __forceinline__ void norm_write_records(const DevTensor& t, int64_t seg, int Ea, bool two, int lane,
-                                                   const float (&sa)[8], const float (&ra)[8], const float (&sb)[8],
-                                                   const float (&rb)[8]) {
+                                                   const NormAcc& a) {
   uint32_t acc[16];
+  float hs[8];
 #pragma unroll
   for (int v = 0; v < 8; ++v) {
-    acc[v] = norm_lane_value(sa[v], ra[v], Ea);
-    acc[8 + v] = two ? norm_lane_value(sb[v], rb[v], Ea + 1) : 0u;
+    acc[v] = norm_lane_value(a.sa[v], a.ra[v], Ea);
+    acc[8 + v] = two ? norm_lane_value(a.sb[v], a.rb[v], Ea + 1) : 0u;
+    hs[v] = a.hs[v];
   }
   const int64_t nseg = t.nseg;
   uint32_t* __restrict__ W0 = t.nrec;
   uint32_t* __restrict__ WA = t.nrec + 8 * nseg;
   uint32_t* __restrict__ WB = t.nrec + 16 * nseg;
+  norm_lane_sums<8>(hs, lane);  // lane 8c: chain c
+  if ((lane & 7) == 0) t.nsum[(lane >> 3) * nseg + seg] = hs[0];
   if (two) {
     norm_lane_sums<16>(acc, lane);  // lane 4c: chain c under Ea; lane 32 + 4c: under Ea + 1
     const int c = (lane >> 2) & 7;
@@ -371,9 +465,9 @@ constexpr int kNormLdsCols = 16384;    // widest rows k_norm_seg2d stages in LDS
 // staged in LDS (cl), rows of whole 8-element chunks, 16-byte aligned, 32-bit flat indices.  Every
 // gradient chunk and row factor of the segment is loaded first; the column factors come from LDS
 // as each chunk is accounted.
-template <typename TG, bool TWO>
+template <typename TG, bool TWO, bool TINY>
 __device__ __forceinline__ void norm_seg_lds(const DevTensor& t, const float* cl, int64_t f0, int ka, int lane,
-                                             float (&sa)[8], float (&ra)[8], float (&sb)[8], float (&rb)[8]) {
+                                             NormAcc& a) {
   using GS = typename TG::storage;
   constexpr int Q = kNormChunks;
   const CAME8_GLOBAL GS* __restrict__ g = gbl(static_cast<const GS*>(t.g));
@@ -390,10 +484,10 @@ __device__ __forceinline__ void norm_seg_lds(const DevTensor& t, const float* cl
       const u32x4 v = *(const CAME8_GLOBAL u32x4*)(g + f);
       gw[q][0] = v.x; gw[q][1] = v.y; gw[q][2] = v.z; gw[q][3] = v.w;
     } else {
-      const u32x4 a = *(const CAME8_GLOBAL u32x4*)(g + f);
-      const u32x4 b = *(const CAME8_GLOBAL u32x4*)(g + f + 4);
-      gw[q][0] = a.x; gw[q][1] = a.y; gw[q][2] = a.z; gw[q][3] = a.w;
-      gw[q][4] = b.x; gw[q][5] = b.y; gw[q][6] = b.z; gw[q][7] = b.w;
+      const u32x4 b0 = *(const CAME8_GLOBAL u32x4*)(g + f);
+      const u32x4 b1 = *(const CAME8_GLOBAL u32x4*)(g + f + 4);
+      gw[q][0] = b0.x; gw[q][1] = b0.y; gw[q][2] = b0.z; gw[q][3] = b0.w;
+      gw[q][4] = b1.x; gw[q][5] = b1.y; gw[q][6] = b1.z; gw[q][7] = b1.w;
     }
   }
 #pragma unroll
@@ -402,12 +496,7 @@ __device__ __forceinline__ void norm_seg_lds(const DevTensor& t, const float* cl
     const f32x4 c1 = *reinterpret_cast<const f32x4*>(cl + col[q] + 4);
     const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const float x = (r[q] * cv[v]) * TG::elem(gw[q], v);
-      const float hi = x * x;
-      norm_acc(hi, ka, sa[v], ra[v]);
-      if constexpr (TWO) norm_acc(hi, ka - 1, sb[v], rb[v]);
-    }
+    for (int v = 0; v < 8; ++v) a.add<TWO, TINY>(v, (r[q] * cv[v]) * TG::elem(gw[q], v), ka);
   }
 }
 
@@ -448,12 +537,12 @@ __global__ __launch_bounds__(kThreads) void k_norm_seg2d(const DevTensor* __rest
       bool two;
       norm_candidates(e0 + (e1 - e0) * (float(k) / float(nrun)), Ea, two);
       const int ka = 23 - Ea;
-      float sa[8], sb[8], ra[8], rb[8];
-#pragma unroll
-      for (int v = 0; v < 8; ++v) sa[v] = sb[v] = ra[v] = rb[v] = 0.0f;
-      if (two) norm_seg_lds<TG, true>(t, cl, f0, ka, lane, sa, ra, sb, rb);
-      else norm_seg_lds<TG, false>(t, cl, f0, ka, lane, sa, ra, sb, rb);
-      norm_write_records(t, seg, Ea, two, lane, sa, ra, sb, rb);
+      NormAcc a;
+      a.clear();
+      if (Ea == -126) norm_seg_lds<TG, true, true>(t, cl, f0, ka, lane, a);
+      else if (two) norm_seg_lds<TG, true, false>(t, cl, f0, ka, lane, a);
+      else norm_seg_lds<TG, false, false>(t, cl, f0, ka, lane, a);
+      norm_write_records(t, seg, Ea, two, lane, a);
     }
   }
 }
@@ -481,58 +570,233 @@ __global__ __launch_bounds__(kThreads, 4) void k_norm_seg(const DevTensor* __res
     bool two;
     norm_candidates(uniform_f32(norm_est_at(t, f0)) * 0.125f, Ea, two);
     const int ka = 23 - Ea;
-    float sa[8], sb[8], ra[8], rb[8];
-#pragma unroll
-    for (int v = 0; v < 8; ++v) sa[v] = sb[v] = ra[v] = rb[v] = 0.0f;
+    NormAcc a;
+    a.clear();
     const bool full = f1 - f0 == kNormSegElems;
-    if (two) {
-      if (full) norm_seg_sums<TG, FAST, true, true>(t, f0, f1, ka, lane, hp, sa, ra, sb, rb);
-      else norm_seg_sums<TG, FAST, true, false>(t, f0, f1, ka, lane, hp, sa, ra, sb, rb);
+    if (Ea == -126) {
+      norm_seg_sums<TG, FAST, true, true, false>(t, f0, f1, ka, lane, hp, a);
+    } else if (two) {
+      if (full) norm_seg_sums<TG, FAST, true, false, true>(t, f0, f1, ka, lane, hp, a);
+      else norm_seg_sums<TG, FAST, true, false, false>(t, f0, f1, ka, lane, hp, a);
     } else {
-      if (full) norm_seg_sums<TG, FAST, false, true>(t, f0, f1, ka, lane, hp, sa, ra, sb, rb);
-      else norm_seg_sums<TG, FAST, false, false>(t, f0, f1, ka, lane, hp, sa, ra, sb, rb);
+      if (full) norm_seg_sums<TG, FAST, false, false, true>(t, f0, f1, ka, lane, hp, a);
+      else norm_seg_sums<TG, FAST, false, false, false>(t, f0, f1, ka, lane, hp, a);
     }
-    norm_write_records(t, seg, Ea, two, lane, sa, ra, sb, rb);
+    norm_write_records(t, seg, Ea, two, lane, a);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// each chain's own estimate, and records rebuilt under it
+// ---------------------------------------------------------------------------
+// In place: each chain's segment sums become their exclusive prefix, the chain's estimated value at
+// each segment's start.  One work item per tensor and chain.
+template <int = 0>
+__global__ __launch_bounds__(kThreads) void k_norm_cscan(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                         const int64_t* __restrict__ wstart, int ntens) {
+  __shared__ float part[kThreads / kWave];
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int c = int(w - wstart[slot]);
+    block_excl_scan(t.nsum + c * t.nseg, t.nseg, part);
+  }
+}
+
+constexpr int kNormFixSegs = kThreads;  // segments per work item of k_norm_fix (one per thread)
+
+// Writes the records of the chains in mask from a rebuild under a binade pair per chain (Ea[c], Ea[c] + 1).
+__device__ __forceinline__ void norm_write_records_pc(const DevTensor& t, int64_t seg, const int (&Ea)[8],
+                                                      uint32_t mask, int lane, const NormAcc& a) {
+  uint32_t acc[16];
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    acc[v] = norm_lane_value(a.sa[v], a.ra[v], Ea[v]);
+    acc[8 + v] = norm_lane_value(a.sb[v], a.rb[v], Ea[v] + 1);
+  }
+  norm_lane_sums<16>(acc, lane);  // lane 4c: chain c under Ea[c]; lane 32 + 4c: under Ea[c] + 1
+  const int c = (lane >> 2) & 7;
+  int Ec = Ea[0];
+#pragma unroll
+  for (int v = 1; v < 8; ++v) Ec = c == v ? Ea[v] : Ec;
+  if ((lane & 3) == 0 && ((mask >> c) & 1u)) {
+    const int64_t nseg = t.nseg;
+    const uint32_t sum = min(acc[0], kNormFull);
+    if (lane < 32) {
+      t.nrec[c * nseg + seg] = uint32_t(Ec + 256) | kRecTwo;
+      t.nrec[(8 + c) * nseg + seg] = sum;
+    } else {
+      t.nrec[(16 + c) * nseg + seg] = sum;
+    }
+  }
+}
+
+// Records rebuilt under each chain's own estimate.  A work item is kNormFixSegs consecutive segments
+// of one tensor, 64 per wavefront: each lane checks one segment's eight records against the chains'
+// estimates (k_norm_cscan), and the wavefront rebuilds, a segment at a time, the records whose
+// candidate binades do not cover a chain's own candidates, under that chain's Ea and Ea + 1 (both
+// sums always).  FAST as for k_norm_seg.
+template <typename TG, bool FAST>
+__global__ __launch_bounds__(kThreads) void k_norm_fix(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                       const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const int slot = find_slot(wstart, ntens, w);
+    const DevTensor& t = T[tids[slot]];
+    const int64_t nseg = t.nseg;
+    const int64_t base = (w - wstart[slot]) * kNormFixSegs + wid * kWave;
+    const int64_t seg = base + lane;
+    float est[8];
+    uint32_t need = 0;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      est[c] = 0.0f;
+      if (seg < nseg) {
+        est[c] = t.nsum[c * nseg + seg];
+        const uint32_t w0 = t.nrec[c * nseg + seg];
+        const int Ea = int(w0 & 511u) - 256;
+        const bool two = (w0 & kRecTwo) != 0;
+        int Ec;
+        bool twoc;
+        norm_candidates(est[c], Ec, twoc);
+        const bool lo = Ec == Ea || (two && Ec == Ea + 1);
+        const bool hi = !twoc || Ec + 1 == Ea || (two && Ec + 1 == Ea + 1);
+        need |= (lo && hi) ? 0u : (1u << c);
+      }
+    }
+    uint64_t bal = __ballot(need != 0);
+    const int64_t main = t.N - (t.N & 7);
+    while (bal != 0) {  // uniform
+      const int L = __builtin_ctzll(bal);
+      bal &= bal - 1;
+      const int64_t sf = base + L;
+      const uint32_t mask = __shfl(need, L, kWave);
+      int Ea[8], ka[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        bool two;
+        norm_candidates(__shfl(est[c], L, kWave), Ea[c], two);
+        ka[c] = 23 - Ea[c];
+      }
+      NormAcc a;
+      a.clear();
+      const int64_t f0 = sf * kNormSegElems, f1 = min(f0 + kNormSegElems, main);
+#pragma unroll 1
+      for (int q = 0; q < kNormChunks; ++q) {
+        float x[8];
+        norm_chunk_x<TG, FAST>(t, f0 + q * 512 + lane * 8, f1, hp, x);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) a.add_both(v, x[v], ka[v], Ea[v] == -126);
+      }
+      norm_write_records_pc(t, sf, Ea, mask, lane, a);
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
 // walk
 // ---------------------------------------------------------------------------
-// Replays chain c of segment seg from s with fmaf, element by element, as the reference does (one
-// wavefront; lane 0 runs the chain).
+constexpr uint32_t kNormSat = 1u << 25;  // saturating integer sums: anything >= 2^24 leaves the binade
+__device__ __forceinline__ uint32_t sat_add(uint32_t a, uint32_t b) { return min(a + b, kNormSat); }
+
+// Replays chain c over segment seg from s, equal to the reference's serial fmaf loop bit for bit (one
+// wavefront).  Lane l holds the chain's elements 8l .. 8l + 7 of the segment.  A round takes every
+// remaining element's increment under s's binade, a saturating prefix sum of them in element order,
+// and the first element that is special or whose prefix takes the chain out of the binade; the
+// elements before it are one integer add, that element is one fmaf, and the next round starts after
+// it.  A finite chain only grows, so the rounds are the segment's binade crossings and special
+// elements, plus one.  An infinite chain changes only at a NaN element; a NaN chain not at all.
 template <typename TG>
-__device__ float norm_replay(const DevTensor& t, int c, int64_t seg, float s, const Hp& hp, float* xs) {
-  const int lane = threadIdx.x;
+__device__ float norm_replay(const DevTensor& t, int c, int64_t seg, float s, const Hp& hp) {
+  const int lane = threadIdx.x & (kWave - 1);
   const int64_t main = t.N - (t.N & 7);
   const int64_t f0 = seg * kNormSegElems;
   const int cnt = int(min(int64_t(kNormChainSeg), (main - f0) / 8));
+  float x[8], h[8];
 #pragma unroll
-  for (int i = 0; i < kNormChainSeg / kWave; ++i) {
-    const int k = i * kWave + lane;
-    if (k < cnt) xs[k] = norm_x_at<TG>(t, f0 + 8 * int64_t(k) + c, hp);
+  for (int j = 0; j < 8; ++j) {
+    const int k = lane * 8 + j;
+    x[j] = k < cnt ? norm_x_at<TG>(t, f0 + 8 * int64_t(k) + c, hp) : 0.0f;
   }
-  __syncthreads();
-  if (lane == 0) {
-    int k = 0;
-    for (; k + 16 <= cnt; k += 16) {
-      float v[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) v[u] = xs[k + u];
+  for (int j = 0; j < 8; ++j) h[j] = x[j] * x[j];
+  int pos = 0;  // the elements before pos are applied
+  while (pos < cnt) {  // uniform
+    if (!(s <= 0x1.fffffep127f)) {
+      if (s != s) break;
+      uint32_t nanm = 0;
 #pragma unroll
-      for (int u = 0; u < 16; ++u) s = fmaf(v[u], v[u], s);
+      for (int j = 0; j < 8; ++j) {
+        const int k = lane * 8 + j;
+        nanm |= (k >= pos && k < cnt && x[j] != x[j]) ? (1u << j) : 0u;
+      }
+      const uint64_t bal = __ballot(nanm != 0);
+      if (bal != 0) {
+        const int fl = __builtin_ctzll(bal);
+        const int jj = __shfl(__builtin_ctz(nanm | 0x100u), fl, kWave);
+        float xe = x[0];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) xe = jj == j ? x[j] : xe;
+        xe = __shfl(xe, fl, kWave);
+        s = fmaf(xe, xe, s);
+      }
+      break;
     }
-    for (; k < cnt; ++k) s = fmaf(xs[k], xs[k], s);
-    xs[kNormChainSeg] = s;
+    const int E = norm_binade(s);
+    const uint32_t m = norm_mant(s, E);
+    const uint32_t room = kNormFull - m;  // an increment prefix that reaches this leaves the binade
+    const int kk = 23 - E;
+    uint32_t incl[8], spm = 0, run = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int k = lane * 8 + j;
+      const bool live = k >= pos && k < cnt;
+      const float dh = ldexpf(h[j], kk);
+      const float nf = rintf(dh);
+      const bool special = fabsf(dh - nf) == 0.5f || (E == -126 && (nf != 0.0f || fabsf(x[j]) == 0x1p-75f));
+      const uint32_t n = nf < 0x1p25f ? uint32_t(nf) : kNormSat;  // NaN and inf squares saturate
+      run = sat_add(run, live ? n : 0u);
+      incl[j] = run;
+      spm |= (live && special) ? (1u << j) : 0u;
+    }
+    uint32_t winc = run;  // inclusive scan of the lanes' runs
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const uint32_t y = __shfl_up(winc, o, kWave);
+      if (lane >= o) winc = sat_add(winc, y);
+    }
+    const uint32_t up1 = __shfl_up(winc, 1, kWave);  // every lane takes part in the shuffle
+    const uint32_t excl = lane == 0 ? 0u : up1;
+    uint32_t evm = spm;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int k = lane * 8 + j;
+      evm |= (k >= pos && k < cnt && sat_add(excl, incl[j]) >= room) ? (1u << j) : 0u;
+    }
+    const uint64_t bal = __ballot(evm != 0);
+    if (bal == 0) {
+      s = norm_value(m + __shfl(winc, kWave - 1, kWave), E);  // below room
+      break;
+    }
+    const int fl = __builtin_ctzll(bal);
+    const int j0 = __builtin_ctz(evm | 0x100u);  // this lane's first event (8: none)
+    uint32_t before = excl;                      // the increments before that event, on lane fl
+    float xe = x[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) {
+      before = j0 == j ? excl + incl[j - 1] : before;
+      xe = j0 == j ? x[j] : xe;
+    }
+    const int jj = __shfl(j0, fl, kWave);
+    before = __shfl(before, fl, kWave);
+    xe = __shfl(xe, fl, kWave);
+    s = fmaf(xe, xe, norm_value(m + before, E));
+    pos = fl * 8 + jj + 1;
   }
-  __syncthreads();
-  s = xs[kNormChainSeg];
-  __syncthreads();
   return s;
 }
-
-constexpr uint32_t kNormSat = 1u << 25;  // saturating integer sums: anything >= 2^24 leaves the binade
-__device__ __forceinline__ uint32_t sat_add(uint32_t a, uint32_t b) { return min(a + b, kNormSat); }
 
 // The increment of a segment's record for a chain in binade E, or kNormSat when the record does not
 // cover E.  With s = +inf (E = 128), a segment needs its replay only if it may hold a NaN: an
@@ -555,7 +819,6 @@ template <typename TG>
 __global__ __launch_bounds__(kNormWalkThreads) void k_norm_walk(const DevTensor* __restrict__ T,
                                                                 const int32_t* __restrict__ tids,
                                                                 const int64_t* __restrict__ wstart, int ntens, Hp hp) {
-  __shared__ float xs[kNormChainSeg + 1];
   const int lane = threadIdx.x;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
@@ -623,11 +886,10 @@ __global__ __launch_bounds__(kNormWalkThreads) void k_norm_walk(const DevTensor*
       }
       const uint32_t mm = m + uint32_t(__shfl(int(acc), first, kWave));
       const int64_t ks = __shfl(k, first, kWave);
-      s = norm_replay<TG>(t, c, ks, inf ? s : norm_value(mm, E), hp, xs);
+      s = norm_replay<TG>(t, c, ks, inf ? s : norm_value(mm, E), hp);
       seg = ks + 1;
     }
     if (lane == 0) t.nchain[c] = s;
-    __syncthreads();
   }
 }
 

@@ -1,13 +1,14 @@
 """CPU check of the parallel replay of torch's fp32 norm chains (came_amd/csrc/came8_norm.h): a C model of
-its rules (tests/native/norm_replay_model.c) must equal the serial chain s = fma(x, x, s) bit for bit on
-adversarial inputs (constant values that stall the chain, values with few significant bits that make
-rounding ties, zeros, outliers, squares that are subnormal or overflow, NaN, rows of very different
-scales), whatever the binade estimates (exact, 1% off, 50% off), and replay few segments when the
+its rules (tests/native/norm_replay_model.c), segment records and the wavefront replay of a segment, must
+equal the serial chain s = fma(x, x, s) bit for bit on adversarial inputs (constant values that stall the chain, values with few significant bits that make
+rounding ties, zeros, outliers, squares that are subnormal (some exact half-units of the subnormal grid)
+or overflow, NaN, rows of very different scales), whatever the binade estimates (exact, 1% off, 50% off), and replay few segments when the
 estimates are good."""
 import ctypes
 import os
 import shutil
 import subprocess
+import zlib
 
 import numpy as np
 import pytest
@@ -28,6 +29,10 @@ def lib(tmp_path_factory):
     so.chain_serial.argtypes = [ctypes.c_void_p, ctypes.c_int64]
     so.chain_replay.restype = ctypes.c_float
     so.chain_replay.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64)]
+    so.chain_serial_from.restype = ctypes.c_float
+    so.chain_serial_from.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_float]
+    so.segment_replay.restype = ctypes.c_float
+    so.segment_replay.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.POINTER(ctypes.c_int64)]
     return so
 
 
@@ -50,6 +55,12 @@ def _inputs(kind, n, rng):
     elif kind == "nan":
         x = rng.standard_normal(n)
         x[n // 2] = np.nan
+    elif kind == "subties":  # squares (2k+1)^2 * 2^-150: half-units of the subnormal grid, so every one a tie
+        x = np.ldexp(rng.choice([0.0, 1.0, 3.0, 5.0, 7.0], n), -75) * rng.choice([-1.0, 1.0], n)
+    elif kind == "halfunits":  # a chain of one unit (2^-149, odd), then only 0 and +-2^-75: squares of half a unit
+        x = np.ldexp(rng.choice([0.0, 1.0, -1.0], n), -75)
+        x[: min(n, 512)] = 0.0
+        x[min(n, 512) - 1] = np.ldexp(1.5, -75)  # (1.5 * 2^-75)^2 = 1.125 units: the chain becomes 1 unit
     elif kind == "blocks":
         x = np.where((np.arange(n) // 1000) % 2 == 0, 0.0, rng.standard_normal(n) * scale)
     else:
@@ -57,14 +68,16 @@ def _inputs(kind, n, rng):
     return x.astype(np.float32)
 
 
-KINDS = ["normal", "const", "fewbits", "zeros", "outliers", "subnormal", "overflow", "nan", "blocks"]
+KINDS = ["normal", "const", "fewbits", "zeros", "outliers", "subnormal", "subties", "halfunits", "overflow", "nan", "blocks"]
 
 
 @pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("noise", [0.0, 0.01, 0.5])
 def test_replay_equals_serial_chain(lib, kind, noise):
-    rng = np.random.default_rng(hash((kind, noise)) % 2**32)
+    rng = np.random.default_rng(zlib.crc32(f"{kind}/{noise}".encode()))
     for n in (1, 7, 511, 512, 513, 4097, int(rng.integers(10_000, 300_000)), 1_000_003):
+        if kind in ("subties", "halfunits") and n > 5000:  # a chain that stays subnormal replays every element alone
+            continue
         x = _inputs(kind, n, rng)
         nseg = (n + 511) // 512
         exact = np.concatenate([[0.0], np.cumsum(x.astype(np.float64) ** 2)])[::512][:nseg]
@@ -89,3 +102,41 @@ def test_replays_are_few_on_realistic_chains(lib):
     b = lib.chain_replay(x.ctypes.data, n, est.ctypes.data, ctypes.byref(rep))
     assert np.float32(a).tobytes() == np.float32(b).tobytes()
     assert rep.value < 60, rep.value
+
+
+def _starts(rng):
+    """Chain values a replay may start from: zero, subnormals, values at and next to binade edges,
+    random normals, the largest float, +inf and NaN."""
+    edges = [np.float32(2.0) ** int(e) for e in rng.integers(-126, 127, 12)]
+    near = [np.nextafter(e, np.float32(0)) for e in edges] + [np.nextafter(e, np.float32(np.inf)) for e in edges]
+    rand = list(np.exp(rng.uniform(-80, 80, 12)).astype(np.float32))
+    # the unit-2^-149 range [0, 2^-125): odd and even multiples of the unit, subnormal and normal
+    low = list(np.array([1, 2, 3, 0x7FFFFF, 0x800000, 0x800001, 0xFFFFFE, 0xFFFFFF], np.uint32).view(np.float32))
+    return ([np.float32(0.0), np.float32(3e-39), np.float32(3.4e38), np.float32(np.inf), np.float32(np.nan)]
+            + low + edges + near + rand)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_segment_replay_from_any_start(lib, kind):
+    """One segment (up to 512 chain elements) replayed in wavefront rounds from every kind of start value
+    equals the serial fmaf loop from that value.  For finite starts the elements are also rescaled so
+    that their squares are 2^-k of the start (k in [0, 12]): increments of a few units, where half-unit
+    ties and binade crossings concentrate."""
+    rng = np.random.default_rng(zlib.crc32(kind.encode()))
+    for s0 in _starts(rng):
+        for cnt in (1, 2, 8, 9, 63, 64, 65, 300, 511, 512):
+            for near in (False, True):
+                x = _inputs(kind, cnt, rng)
+                if near:
+                    if not (np.isfinite(s0) and s0 > 0):
+                        continue
+                    top = float(np.nanmax(np.abs(x))) if np.isfinite(x).any() else 0.0
+                    if not top > 0 or not np.isfinite(top):
+                        continue
+                    x = (x.astype(np.float64) / top * np.sqrt(float(s0)) * 2.0 ** -rng.uniform(0, 6)).astype(np.float32)
+                x = np.ascontiguousarray(x)
+                rounds = ctypes.c_int64(0)
+                want = lib.chain_serial_from(x.ctypes.data, cnt, float(s0))
+                got = lib.segment_replay(x.ctypes.data, cnt, float(s0), ctypes.byref(rounds))
+                same = np.float32(got).tobytes() == np.float32(want).tobytes() or (np.isnan(got) and np.isnan(want))
+                assert same, (kind, float(s0), cnt, near, got, want)
