@@ -113,9 +113,9 @@ struct Plan {
   WorkList nest_n;                       // unit estimates, a thread per unit (per 256 units)
   WorkList nscan;                        // prefix of the estimates (one item per tensor)
   std::map<int, WorkList> nseg2d;        // segment records of matrices, runs of kNormRunSegs, by grad type
-  std::map<int, WorkList> nseg;          // the other segments' records, by 2 * grad type + vector form
+  std::map<int, WorkList> nseg;          // the other segments' records, by 3 * grad type + chunk form
   WorkList ncscan;                       // each chain's prefix of its segment sums (8 items per tensor)
-  std::map<int, WorkList> nfix;          // records rebuilt under the chains' own estimates, by grad type * 2 + fast
+  std::map<int, WorkList> nfix;          // records rebuilt under the chains' own estimates, by 3 * grad type + form
   std::map<int, WorkList> nwalk;         // chain walks (8 items per tensor), by grad type
   std::map<int, WorkList> nfinal;        // accumulators + tail + clip (one item per tensor), by grad type
   WorkList factor;                       // F1b / F2b (per state block)
@@ -584,11 +584,12 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     if (d.nseg > 0) {
       // the vector forms need rows of whole aligned 8-element chunks and 32-bit flat indices; matrices
       // (prefix 1) up to kNormLdsCols wide take runs of segments with their column factors in LDS
-      const bool fast = t.factored && d.c8 && d.idx32 && reinterpret_cast<uintptr_t>(t.grad) % 16 == 0;
+      const bool vec = t.factored && d.idx32 && reinterpret_cast<uintptr_t>(t.grad) % 16 == 0;
+      const int form = vec && d.c8 ? kNormVec : (vec && d.C >= 8 ? kNormRows : kNormAny);
       if (d.nseg0 > 0) add_item(plan.nseg2d[t.grad_dtype], i, ceil_div(d.nseg0, int64_t(kNormRunSegs)));
-      if (d.nseg > d.nseg0) add_item(plan.nseg[t.grad_dtype * 2 + (fast ? 1 : 0)], i, ceil_div(d.nseg - d.nseg0, int64_t(4)));
+      if (d.nseg > d.nseg0) add_item(plan.nseg[t.grad_dtype * 3 + form], i, ceil_div(d.nseg - d.nseg0, int64_t(4)));
       add_item(plan.ncscan, i, 8);
-      add_item(plan.nfix[t.grad_dtype * 2 + (fast ? 1 : 0)], i, ceil_div(d.nseg, int64_t(kNormFixSegs)));
+      add_item(plan.nfix[t.grad_dtype * 3 + form], i, ceil_div(d.nseg, int64_t(kNormFixSegs)));
     }
     add_item(plan.nwalk[t.grad_dtype], i, 8);
     add_item(plan.nfinal[t.grad_dtype], i, 1);
@@ -833,6 +834,26 @@ constexpr GenFn k_fact_pass3b_f32st = k_fact_pass3b<TP, TG, true>;
     if (gdt == CAME8_BF16) out = KERNEL<BF16>;         \
     if (gdt == CAME8_F16) out = KERNEL<F16>;           \
   } while (0)
+
+// The segment-record and record-rebuild kernels of a work-list key 3 * grad type + chunk form.
+#define CAME8_NORM_FN(NAME, KERNEL)                                          \
+  GenFn NAME(int key) {                                                      \
+    switch (key) {                                                           \
+      case 3 * CAME8_F32 + kNormAny: return KERNEL<F32, kNormAny>;           \
+      case 3 * CAME8_F32 + kNormRows: return KERNEL<F32, kNormRows>;         \
+      case 3 * CAME8_F32 + kNormVec: return KERNEL<F32, kNormVec>;           \
+      case 3 * CAME8_BF16 + kNormAny: return KERNEL<BF16, kNormAny>;         \
+      case 3 * CAME8_BF16 + kNormRows: return KERNEL<BF16, kNormRows>;       \
+      case 3 * CAME8_BF16 + kNormVec: return KERNEL<BF16, kNormVec>;         \
+      case 3 * CAME8_F16 + kNormAny: return KERNEL<F16, kNormAny>;           \
+      case 3 * CAME8_F16 + kNormRows: return KERNEL<F16, kNormRows>;         \
+      case 3 * CAME8_F16 + kNormVec: return KERNEL<F16, kNormVec>;           \
+      default: return nullptr;                                               \
+    }                                                                        \
+  }
+CAME8_NORM_FN(norm_seg_fn, k_norm_seg)
+CAME8_NORM_FN(norm_fix_fn, k_norm_fix)
+#undef CAME8_NORM_FN
 
 constexpr int64_t kMaxGrid = 16384;
 
@@ -1183,16 +1204,8 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     }
     for (auto& kv : plan.nseg) {
       const WorkList& wl = kv.second;
-      GenFn fn = nullptr;
-      switch (kv.first) {
-        case 2 * CAME8_F32: fn = k_norm_seg<F32, false>; break;
-        case 2 * CAME8_F32 + 1: fn = k_norm_seg<F32, true>; break;
-        case 2 * CAME8_BF16: fn = k_norm_seg<BF16, false>; break;
-        case 2 * CAME8_BF16 + 1: fn = k_norm_seg<BF16, true>; break;
-        case 2 * CAME8_F16: fn = k_norm_seg<F16, false>; break;
-        case 2 * CAME8_F16 + 1: fn = k_norm_seg<F16, true>; break;
-        default: return fail(CAME8_EINVAL, "came8_step: no norm kernel for this variant");
-      }
+      const GenFn fn = norm_seg_fn(kv.first);
+      if (fn == nullptr) return fail(CAME8_EINVAL, "came8_step: no norm kernel for this variant");
       PhaseTimer pt(PH_NORM_SEG, alg_bytes(plan, wl, tensors, PH_NORM_SEG), stream);
       hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("norm_seg")) != CAME8_OK) return rc;
@@ -1200,22 +1213,14 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     if (!plan.ncscan.tids.empty()) {
       const WorkList& wl = plan.ncscan;
       PhaseTimer pt(PH_NORM_SCAN, 0.0, stream);
-      hipLaunchKernelGGL(k_norm_cscan<>, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl),
+      hipLaunchKernelGGL(k_norm_cscan<>, dim3(grid_for(wl.total())), dim3(kNormScanThreads), 0, stream, dT, tids(wl), wst(wl),
                          int(wl.tids.size()));
       if ((rc = check_launch("norm_cscan")) != CAME8_OK) return rc;
     }
     for (auto& kv : plan.nfix) {
       const WorkList& wl = kv.second;
-      GenFn fn = nullptr;
-      switch (kv.first) {
-        case 2 * CAME8_F32: fn = k_norm_fix<F32, false>; break;
-        case 2 * CAME8_F32 + 1: fn = k_norm_fix<F32, true>; break;
-        case 2 * CAME8_BF16: fn = k_norm_fix<BF16, false>; break;
-        case 2 * CAME8_BF16 + 1: fn = k_norm_fix<BF16, true>; break;
-        case 2 * CAME8_F16: fn = k_norm_fix<F16, false>; break;
-        case 2 * CAME8_F16 + 1: fn = k_norm_fix<F16, true>; break;
-        default: return fail(CAME8_EINVAL, "came8_step: no norm kernel for this variant");
-      }
+      const GenFn fn = norm_fix_fn(kv.first);
+      if (fn == nullptr) return fail(CAME8_EINVAL, "came8_step: no norm kernel for this variant");
       PhaseTimer pt(PH_NORM_FIX, 0.0, stream);
       hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("norm_fix")) != CAME8_OK) return rc;

@@ -175,11 +175,13 @@ __global__ __launch_bounds__(kThreads) void k_norm_est(const DevTensor* __restri
 
 constexpr int kScanBatch = 16;  // loads per thread in flight in block_excl_scan
 
-// In-place exclusive prefix sum of a[0, n) by one workgroup; returns the total to every thread.  Thread
-// i takes the i-th run of ceil(n / kThreads) consecutive values.  part: kThreads / kWave floats of LDS.
+// In-place exclusive prefix sum of a[0, n) by one workgroup of NT threads; returns the total to every
+// thread.  Thread i takes the i-th run of ceil(n / NT) consecutive values.  part: NT / kWave floats of
+// LDS.
+template <int NT>
 __device__ float block_excl_scan(float* a, int64_t n, float* part) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int64_t per = (n + kThreads - 1) / kThreads;
+  const int64_t per = (n + NT - 1) / NT;
   const int64_t u0 = min(n, int64_t(tid) * per), u1 = min(n, u0 + per);
   float s = 0.0f;
   for (int64_t u = u0; u < u1; u += kScanBatch) {
@@ -199,7 +201,7 @@ __device__ float block_excl_scan(float* a, int64_t n, float* part) {
   __syncthreads();
   float off = 0.0f, tot = 0.0f;
 #pragma unroll
-  for (int k = 0; k < kThreads / kWave; ++k) {
+  for (int k = 0; k < NT / kWave; ++k) {
     off += k < wid ? part[k] : 0.0f;
     tot += part[k];
   }
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(kThreads) void k_norm_scan(const DevTensor* __restr
   __shared__ float part[kThreads / kWave];
   for (int k = blockIdx.x; k < ntens; k += gridDim.x) {
     const DevTensor& t = T[tids[k]];
-    const float tot = block_excl_scan(t.nest, t.nunit, part);
+    const float tot = block_excl_scan<kThreads>(t.nest, t.nunit, part);
     if (threadIdx.x == 0) t.nest[t.nunit] = tot;
   }
 }
@@ -326,6 +328,36 @@ struct NormChunk {
   }
 };
 
+// The same for a factored tensor of at least 8 columns whose rows do not hold whole chunks: the chunk
+// may end in the next row (and the next matrix); its gradient is still 16-byte aligned.
+template <typename TG>
+__device__ __forceinline__ void norm_chunk_rows(const DevTensor& t, uint32_t f, float (&x)[8]) {
+  using GS = typename TG::storage;
+  const uint32_t C = uint32_t(t.C);
+  const uint32_t row = udiv_magic(f, t.mC, t.sC);
+  const uint32_t j = f - row * C;
+  const uint32_t m0 = udiv_magic(row, t.mR, t.sR);
+  float gv[8];
+  load8<TG>(gbl(static_cast<const GS*>(t.g) + f), gv);
+  const bool cross = j + 8 > C;  // the elements from C - j on are the next row's
+  const uint32_t m1 = cross ? udiv_magic(row + 1, t.mR, t.sR) : m0;
+  const float r0 = gbl(t.rfac)[row];
+  const float r1 = cross ? gbl(t.rfac)[row + 1] : r0;
+  const CAME8_GLOBAL float* __restrict__ cf = gbl(t.cfac);
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    const bool nx = j + v >= C;
+    const uint32_t col = nx ? j + v - C : j + v;
+    const float c = cf[int64_t(nx ? m1 : m0) * C + col];
+    x[v] = ((nx ? r1 : r0) * c) * gv[v];
+  }
+}
+
+// How a norm kernel loads the x of a tensor's 8-element chunks: kNormVec for factored tensors whose rows
+// hold whole chunks, kNormRows for other factored tensors of at least 8 columns (both: gradient 16-byte
+// aligned, N < 2^31; the host checks), kNormAny (u_at per element) for the rest.
+constexpr int kNormAny = 0, kNormRows = 1, kNormVec = 2;
+
 // Per-lane, per-chain accumulators of one segment: the integer sums of the increments under the
 // candidate binades Ea (sa) and Ea + 1 (sb), their largest rounding distances (ra, rb), and the fp32
 // sum of the rounded squares (hs).
@@ -355,16 +387,20 @@ struct NormAcc {
 };
 
 // The x of the 8 elements at flat index f (a multiple of 8): element v belongs to chain v.  Elements
-// at or past f1 (a multiple of 8) are 0.  FAST as for k_norm_seg.
-template <typename TG, bool FAST>
+// at or past f1 (a multiple of 8) are 0.
+template <typename TG, int FORM>
 __device__ __forceinline__ void norm_chunk_x(const DevTensor& t, int64_t f, int64_t f1, const Hp& hp,
                                              float (&x)[8]) {
   const bool in = f < f1;
-  if constexpr (FAST) {
+  if constexpr (FORM == kNormVec) {
     NormChunk<TG> ch;
     ch.load(t, uint32_t(in ? f : f1 - 8));
 #pragma unroll
     for (int v = 0; v < 8; ++v) x[v] = in ? (ch.r * ch.cf[v]) * ch.g[v] : 0.0f;
+  } else if constexpr (FORM == kNormRows) {
+    norm_chunk_rows<TG>(t, uint32_t(in ? f : f1 - 8), x);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) x[v] = in ? x[v] : 0.0f;
   } else {
 #pragma unroll
     for (int v = 0; v < 8; ++v) x[v] = in ? norm_x_at<TG>(t, f + v, hp) : 0.0f;
@@ -374,14 +410,24 @@ __device__ __forceinline__ void norm_chunk_x(const DevTensor& t, int64_t f, int6
 // The per-lane, per-chain sums of one segment's increments under the candidate binade (ka = 23 - Ea)
 // and, with TWO, under Ea + 1, with their largest rounding distances and the sums of the squares.
 // FULL: the segment holds all kNormSegElems elements.
-template <typename TG, bool FAST, bool TWO, bool TINY, bool FULL>
+template <typename TG, int FORM, bool TWO, bool TINY, bool FULL>
 __device__ __forceinline__ void norm_seg_sums(const DevTensor& t, int64_t f0, int64_t f1, int ka, int lane,
                                               const Hp& hp, NormAcc& a) {
   auto account = [&](const float (&x)[8]) {
 #pragma unroll
     for (int v = 0; v < 8; ++v) a.add<TWO, TINY>(v, x[v], ka);
   };
-  if constexpr (FAST) {
+  if constexpr (FORM == kNormRows) {
+#pragma unroll 1
+    for (int h = 0; h < kNormChunks; h += kNormGroup) {
+      float x[kNormGroup][8];
+#pragma unroll
+      for (int q = 0; q < kNormGroup; ++q)
+        norm_chunk_x<TG, kNormRows>(t, f0 + (h + q) * 512 + lane * 8, FULL ? f0 + kNormSegElems : f1, hp, x[q]);
+#pragma unroll
+      for (int q = 0; q < kNormGroup; ++q) account(x[q]);
+    }
+  } else if constexpr (FORM == kNormVec) {
     // in a partial segment, chunks past its end load its last chunk and count for nothing
 #pragma unroll 1
     for (int h = 0; h < kNormChunks; h += kNormGroup) {
@@ -548,11 +594,9 @@ __global__ __launch_bounds__(kThreads) void k_norm_seg2d(const DevTensor* __rest
 }
 
 // Records of the segments [nseg0, nseg).  One wavefront per segment (four per workgroup).  Lane l
-// takes the 8-element chunks at
-// 512q + 8l (q < kNormChunks) of the segment: element v of a chunk belongs to chain v.  FAST: the
-// tensor is factored, its rows hold whole 8-element chunks, the gradient is 16-byte aligned and
-// N < 2^31 (the host checks); otherwise every element goes through u_at.
-template <typename TG, bool FAST>
+// takes the 8-element chunks at 512q + 8l (q < kNormChunks) of the segment: element v of a chunk
+// belongs to chain v.  FORM: how the chunks are loaded (norm_chunk_x).
+template <typename TG, int FORM>
 __global__ __launch_bounds__(kThreads, 4) void k_norm_seg(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                           const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -574,13 +618,13 @@ __global__ __launch_bounds__(kThreads, 4) void k_norm_seg(const DevTensor* __res
     a.clear();
     const bool full = f1 - f0 == kNormSegElems;
     if (Ea == -126) {
-      norm_seg_sums<TG, FAST, true, true, false>(t, f0, f1, ka, lane, hp, a);
+      norm_seg_sums<TG, FORM, true, true, false>(t, f0, f1, ka, lane, hp, a);
     } else if (two) {
-      if (full) norm_seg_sums<TG, FAST, true, false, true>(t, f0, f1, ka, lane, hp, a);
-      else norm_seg_sums<TG, FAST, true, false, false>(t, f0, f1, ka, lane, hp, a);
+      if (full) norm_seg_sums<TG, FORM, true, false, true>(t, f0, f1, ka, lane, hp, a);
+      else norm_seg_sums<TG, FORM, true, false, false>(t, f0, f1, ka, lane, hp, a);
     } else {
-      if (full) norm_seg_sums<TG, FAST, false, false, true>(t, f0, f1, ka, lane, hp, a);
-      else norm_seg_sums<TG, FAST, false, false, false>(t, f0, f1, ka, lane, hp, a);
+      if (full) norm_seg_sums<TG, FORM, false, false, true>(t, f0, f1, ka, lane, hp, a);
+      else norm_seg_sums<TG, FORM, false, false, false>(t, f0, f1, ka, lane, hp, a);
     }
     norm_write_records(t, seg, Ea, two, lane, a);
   }
@@ -590,17 +634,20 @@ __global__ __launch_bounds__(kThreads, 4) void k_norm_seg(const DevTensor* __res
 // each chain's own estimate, and records rebuilt under it
 // ---------------------------------------------------------------------------
 // In place: each chain's segment sums become their exclusive prefix, the chain's estimated value at
-// each segment's start.  One work item per tensor and chain.
+// each segment's start.  One work item per tensor and chain, kNormScanThreads threads each (fewer
+// dependent loads per thread for the longest chains).
+constexpr int kNormScanThreads = 1024;
 template <int = 0>
-__global__ __launch_bounds__(kThreads) void k_norm_cscan(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
-                                                         const int64_t* __restrict__ wstart, int ntens) {
-  __shared__ float part[kThreads / kWave];
+__global__ __launch_bounds__(kNormScanThreads) void k_norm_cscan(const DevTensor* __restrict__ T,
+                                                                 const int32_t* __restrict__ tids,
+                                                                 const int64_t* __restrict__ wstart, int ntens) {
+  __shared__ float part[kNormScanThreads / kWave];
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
     const int slot = find_slot(wstart, ntens, w);
     const DevTensor& t = T[tids[slot]];
     const int c = int(w - wstart[slot]);
-    block_excl_scan(t.nsum + c * t.nseg, t.nseg, part);
+    block_excl_scan<kNormScanThreads>(t.nsum + c * t.nseg, t.nseg, part);
   }
 }
 
@@ -633,65 +680,69 @@ __device__ __forceinline__ void norm_write_records_pc(const DevTensor& t, int64_
 }
 
 // Records rebuilt under each chain's own estimate.  A work item is kNormFixSegs consecutive segments
-// of one tensor, 64 per wavefront: each lane checks one segment's eight records against the chains'
-// estimates (k_norm_cscan), and the wavefront rebuilds, a segment at a time, the records whose
-// candidate binades do not cover a chain's own candidates, under that chain's Ea and Ea + 1 (both
-// sums always).  FAST as for k_norm_seg.
-template <typename TG, bool FAST>
+// of one tensor, one per thread: each thread checks its segment's eight records against the chains'
+// estimates (k_norm_cscan, taken as within [-2%, +0.5%] of the chain), and the segments where a
+// record's binades do not cover a chain's are listed in LDS and shared out to the wavefronts, which
+// rebuild them a segment at a time under each chain's own candidates Ea and Ea + 1 (both sums always).
+// FORM as for k_norm_seg.
+template <typename TG, int FORM>
 __global__ __launch_bounds__(kThreads) void k_norm_fix(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                        const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  __shared__ uint32_t list[kNormFixSegs];  // (thread << 8) | mask of the chains to rebuild
+  __shared__ int nlist;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
     const int slot = find_slot(wstart, ntens, w);
     const DevTensor& t = T[tids[slot]];
     const int64_t nseg = t.nseg;
-    const int64_t base = (w - wstart[slot]) * kNormFixSegs + wid * kWave;
-    const int64_t seg = base + lane;
-    float est[8];
+    const int64_t base = (w - wstart[slot]) * kNormFixSegs;
+    const int64_t seg = base + tid;
+    if (tid == 0) nlist = 0;
+    __syncthreads();
     uint32_t need = 0;
+    if (seg < nseg) {
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      est[c] = 0.0f;
-      if (seg < nseg) {
-        est[c] = t.nsum[c * nseg + seg];
+      for (int c = 0; c < 8; ++c) {
+        const float est = t.nsum[c * nseg + seg];
         const uint32_t w0 = t.nrec[c * nseg + seg];
         const int Ea = int(w0 & 511u) - 256;
         const bool two = (w0 & kRecTwo) != 0;
-        int Ec;
-        bool twoc;
-        norm_candidates(est[c], Ec, twoc);
-        const bool lo = Ec == Ea || (two && Ec == Ea + 1);
-        const bool hi = !twoc || Ec + 1 == Ea || (two && Ec + 1 == Ea + 1);
-        need |= (lo && hi) ? 0u : (1u << c);
+        const int lo = norm_est_binade(est * 0.98f), hi = norm_est_binade(est * 1.005f);
+        const bool ok = (lo == Ea || (two && lo == Ea + 1)) && (hi == Ea || (two && hi == Ea + 1));
+        need |= ok ? 0u : (1u << c);
       }
     }
-    uint64_t bal = __ballot(need != 0);
+    if (need != 0) list[atomicAdd(&nlist, 1)] = (uint32_t(tid) << 8) | need;
+    __syncthreads();
+    const int n = nlist;
     const int64_t main = t.N - (t.N & 7);
-    while (bal != 0) {  // uniform
-      const int L = __builtin_ctzll(bal);
-      bal &= bal - 1;
-      const int64_t sf = base + L;
-      const uint32_t mask = __shfl(need, L, kWave);
+    for (int k = wid; k < n; k += kThreads / kWave) {  // uniform over the wavefront
+      const uint32_t e = list[k];
+      const int64_t sf = base + (e >> 8);
       int Ea[8], ka[8];
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
         bool two;
-        norm_candidates(__shfl(est[c], L, kWave), Ea[c], two);
+        norm_candidates(uniform_f32(t.nsum[c * nseg + sf]), Ea[c], two);
         ka[c] = 23 - Ea[c];
       }
       NormAcc a;
       a.clear();
       const int64_t f0 = sf * kNormSegElems, f1 = min(f0 + kNormSegElems, main);
 #pragma unroll 1
-      for (int q = 0; q < kNormChunks; ++q) {
-        float x[8];
-        norm_chunk_x<TG, FAST>(t, f0 + q * 512 + lane * 8, f1, hp, x);
+      for (int h = 0; h < kNormChunks; h += kNormGroup) {
+        float x[kNormGroup][8];
 #pragma unroll
-        for (int v = 0; v < 8; ++v) a.add_both(v, x[v], ka[v], Ea[v] == -126);
+        for (int q = 0; q < kNormGroup; ++q) norm_chunk_x<TG, FORM>(t, f0 + (h + q) * 512 + lane * 8, f1, hp, x[q]);
+#pragma unroll
+        for (int q = 0; q < kNormGroup; ++q)
+#pragma unroll
+          for (int v = 0; v < 8; ++v) a.add_both(v, x[q][v], ka[v], Ea[v] == -126);
       }
-      norm_write_records_pc(t, sf, Ea, mask, lane, a);
+      norm_write_records_pc(t, sf, Ea, e & 255u, lane, a);
     }
+    __syncthreads();  // the list is reused by the next item
   }
 }
 
@@ -811,10 +862,11 @@ __device__ __forceinline__ uint32_t norm_rec_add(uint32_t w0, uint32_t wa, uint3
 
 constexpr int kNormWalkThreads = kWave;  // one wavefront per chain
 
-// One wavefront per (tensor, chain).  Each batch: every lane sums the records of its run of
-// kNormWalkSegs segments under the chain's binade, a scan over the lanes finds the first segment
-// whose record does not cover the binade or takes the chain out of it, every segment before it is
-// skipped with its integer sum, and that segment is replayed.
+// One wavefront per (tensor, chain).  A batch loads the records of kWave * kNormWalkSegs segments, a
+// run of kNormWalkSegs per lane.  Then, from the chain's position: every lane sums its records under
+// the chain's binade, a scan over the lanes finds the first segment whose record does not cover the
+// binade or takes the chain out of it, every segment before it is skipped with its integer sum, that
+// segment is replayed, and the scan resumes after it with the records already loaded.
 template <typename TG>
 __global__ __launch_bounds__(kNormWalkThreads) void k_norm_walk(const DevTensor* __restrict__ T,
                                                                 const int32_t* __restrict__ tids,
@@ -832,62 +884,64 @@ __global__ __launch_bounds__(kNormWalkThreads) void k_norm_walk(const DevTensor*
     float s = 0.0f;
     int64_t seg = 0;
     while (seg < nseg && s == s) {  // a NaN chain stays NaN
-      const bool inf = !(s <= 0x1.fffffep127f);
-      const int E = inf ? 128 : norm_binade(s);
-      const uint32_t m = inf ? 0u : norm_mant(s, E);
-      const uint32_t room = kNormFull - m;  // the chain leaves its binade once its increments reach this
       const int64_t base = seg + int64_t(lane) * kNormWalkSegs;
-      uint32_t add[kNormWalkSegs], r0[kNormWalkSegs], ra[kNormWalkSegs], rb[kNormWalkSegs];
+      const int64_t bend = min(nseg, seg + int64_t(kWave) * kNormWalkSegs);
+      uint32_t r0[kNormWalkSegs], ra[kNormWalkSegs], rb[kNormWalkSegs];
 #pragma unroll
-      for (int j = 0; j < kNormWalkSegs; ++j) {  // every load first, then the decoding
+      for (int j = 0; j < kNormWalkSegs; ++j) {
         const int64_t k = min(base + j, nseg - 1);
         r0[j] = W0[k];
         ra[j] = WA[k];
         rb[j] = WB[k];
       }
+      while (seg < bend && s == s) {  // the segments [seg, bend) of this batch
+        const bool inf = !(s <= 0x1.fffffep127f);
+        const int E = inf ? 128 : norm_binade(s);
+        const uint32_t m = inf ? 0u : norm_mant(s, E);
+        const uint32_t room = kNormFull - m;  // the chain leaves its binade once its increments reach this
+        // this lane's run: the sum of its records from seg on, up to the first one that stops the chain
+        uint32_t add[kNormWalkSegs], run = 0;
+        bool stop = false;
 #pragma unroll
-      for (int j = 0; j < kNormWalkSegs; ++j) add[j] = norm_rec_add(r0[j], ra[j], rb[j], E);
-      // this lane's run: the sum of its records up to the first one that stops the chain
-      uint32_t run = 0;
-      bool stop = false;
-#pragma unroll
-      for (int j = 0; j < kNormWalkSegs; ++j) {
-        if (base + j < nseg && !stop) {
-          if (add[j] >= kNormSat) stop = true;
-          else run = sat_add(run, add[j]);
+        for (int j = 0; j < kNormWalkSegs; ++j) {
+          add[j] = norm_rec_add(r0[j], ra[j], rb[j], E);
+          if (base + j >= seg && base + j < bend && !stop) {
+            if (add[j] >= kNormSat) stop = true;
+            else run = sat_add(run, add[j]);
+          }
         }
-      }
-      // inclusive scan of the runs over the lanes (saturating sums, in lane order)
-      uint32_t incl = run;
+        // inclusive scan of the runs over the lanes (saturating sums, in lane order)
+        uint32_t incl = run;
 #pragma unroll
-      for (int o = 1; o < kWave; o <<= 1) {
-        const uint32_t y = uint32_t(__shfl_up(int(incl), o, kWave));
-        if (lane >= o) incl = sat_add(incl, y);
-      }
-      const uint32_t prev = uint32_t(__shfl_up(int(incl), 1, kWave));
-      const uint32_t excl = lane == 0 ? 0u : prev;  // exact while the chain has not left its binade
-      const uint32_t tot = uint32_t(__shfl(int(incl), kWave - 1, kWave));
-      // the first lane whose run is cut short or takes the chain out of its binade
-      const uint64_t bal = __ballot(base < nseg && (stop || sat_add(excl, run) >= room));
-      if (bal == 0) {
-        if (!inf) s = norm_value(m + tot, E);  // tot < room
-        seg = min(nseg, seg + int64_t(kNormWalkThreads) * kNormWalkSegs);
-        continue;
-      }
-      const int first = __builtin_ctzll(bal);
-      uint32_t acc = excl;
-      int64_t k = base;
-#pragma unroll
-      for (int j = 0; j < kNormWalkSegs; ++j) {
-        if (k == base + j && base + j < nseg && add[j] < kNormSat && acc + add[j] < room) {
-          acc += add[j];
-          k = base + j + 1;
+        for (int o = 1; o < kWave; o <<= 1) {
+          const uint32_t y = __shfl_up(incl, o, kWave);
+          if (lane >= o) incl = sat_add(incl, y);
         }
+        const uint32_t prev = __shfl_up(incl, 1, kWave);
+        const uint32_t excl = lane == 0 ? 0u : prev;  // exact while the chain has not left its binade
+        const uint32_t tot = __shfl(incl, kWave - 1, kWave);
+        // the first lane whose run is cut short or takes the chain out of its binade
+        const uint64_t bal = __ballot(stop || sat_add(excl, run) >= room);
+        if (bal == 0) {
+          if (!inf) s = norm_value(m + tot, E);  // tot < room
+          seg = bend;
+          break;
+        }
+        const int first = __builtin_ctzll(bal);
+        uint32_t acc = excl;
+        int64_t k = max(base, seg);
+#pragma unroll
+        for (int j = 0; j < kNormWalkSegs; ++j) {
+          if (k == base + j && k < bend && add[j] < kNormSat && acc + add[j] < room) {
+            acc += add[j];
+            k = base + j + 1;
+          }
+        }
+        const uint32_t mm = m + __shfl(acc, first, kWave);
+        const int64_t ks = __shfl(k, first, kWave);
+        s = norm_replay<TG>(t, c, ks, inf ? s : norm_value(mm, E), hp);
+        seg = ks + 1;
       }
-      const uint32_t mm = m + uint32_t(__shfl(int(acc), first, kWave));
-      const int64_t ks = __shfl(k, first, kWave);
-      s = norm_replay<TG>(t, c, ks, inf ? s : norm_value(mm, E), hp);
-      seg = ks + 1;
     }
     if (lane == 0) t.nchain[c] = s;
   }
