@@ -135,11 +135,14 @@ def full8bit_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *,
     (keys ``exp_avg``, ``sq_row``/``sq_col``/``res_row``/``res_col`` or ``sq``)
     and the clip divisor; capturing does not change any result.
 
+    ``capture`` also receives the clipped update (``update``) and, for factored
+    tensors, the residual factor the momentum is scaled by (``res_factor``).
+
     ``exact_norm=True`` replaces the reference's float32 ``norm(2)`` (whose
     accumulation error reaches ~1e-4 relative on multi-million-element
     tensors) by sqrt of the fp64 sum of squares rounded to float32: the
-    definition the GPU's default mode implements.  Every other operation is
-    unchanged.
+    library's opt-in exactly rounded clip (CAME8_FLAG_EXACT_NORM).  Every
+    other operation is unchanged.
     """
     st["step"] += 1
     st["RMS"] = _rms(p)
@@ -170,6 +173,8 @@ def full8bit_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *,
         rms = _rms(upd)
     clipv = (rms / clip_threshold).clamp_(min=1.0)
     upd.div_(clipv)
+    if capture is not None:
+        capture["update"] = upd.clone()
     m.mul_(beta1).add_(upd, alpha=1.0 - beta1)
     res = (upd - m) ** 2 + eps1
     if factored:
@@ -177,7 +182,10 @@ def full8bit_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *,
         res_col = dequantize_blockwise(cq[1], ca[1], signed=False, block_size=bs)
         res_row.mul_(beta3).add_(res.mean(dim=-1), alpha=1.0 - beta3)
         res_col.mul_(beta3).add_(res.mean(dim=-2), alpha=1.0 - beta3)
-        step_dir = _approx_sq_grad(res_row, res_col).mul_(m)
+        step_dir = _approx_sq_grad(res_row, res_col)
+        if capture is not None:
+            capture["res_factor"] = step_dir.clone()
+        step_dir.mul_(m)
     else:
         step_dir = m.clone()
 
@@ -435,4 +443,5 @@ def came8bit2d_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], 
     p.copy_(pf.to(p.dtype))
     if capture is not None:
         capture.update(clip=torch.tensor(float(clip)), exp_avg=m_new.clone(), sq_row=upd_r.clone(),
-                       sq_col=upd_c.clone(), res_row=upd_rr.clone(), res_col=upd_rc.clone(), update=upd.clone())
+                       sq_col=upd_c.clone(), res_row=upd_rr.clone(), res_col=upd_rc.clone(), update=upd.clone(),
+                       res_factor=rr[:, None] * cr[None, :])

@@ -11,7 +11,7 @@ from collections import namedtuple
 
 from oracle import came8_oracle as orc
 
-Lockstep = namedtuple("Lockstep", "gpu_param ref_param gpu_state ref_state tainted flips movement")
+Lockstep = namedtuple("Lockstep", "gpu_param ref_param gpu_state ref_state tainted flips movement bound")
 
 HP_DEFAULTS = dict(lr=None, eps=(1e-30, 1e-16), clip_threshold=1.0, betas=(0.9, 0.999, 0.9999),
                    weight_decay=0.0, block_size=256)
@@ -133,7 +133,7 @@ def tie_distance(k: str, ref_state: dict, ref_fp32: dict, block: int) -> torch.T
 def compare_states(gpu_state: dict, ref_state: dict, *, code_frac: float, abs_rel: float, where: str,
                    ref_fp32: dict | None = None, tie_tol: float | None = None, block: int = 256,
                    max_code_diff: int = 1):
-    """Codes: never more than 1 apart, at most max(2, code_frac * n) differ, and (given the oracle's
+    """Codes: never more than 1 apart, at most max(8, code_frac * n) differ, and (given the oracle's
     pre-quantisation values) every differing code sits within `tie_tol` of a rounding tie of the
     reference's scaled value; block scales within `abs_rel` relative."""
     report = {}
@@ -150,9 +150,12 @@ def compare_states(gpu_state: dict, ref_state: dict, *, code_frac: float, abs_re
                 dist = tie_distance(k, ref_state, ref_fp32, block)
                 diff = g.to(torch.int32) != r.to(torch.int32)
                 worst = dist[diff].max().item()
+                report[k] = (frac, mx, worst)
+                print(f"[ties] {where}/{k}: {int(diff.sum())} of {g.numel()} codes differ, worst distance from a "
+                      f"tie {worst:.2e}", flush=True)
                 assert worst <= tie_tol, f"{where}/{k}: a differing code is {worst:.2e} from a rounding tie (> {tie_tol})"
-            n = max(1, g.numel())
-            assert frac * n <= max(2.0, code_frac * n), f"{where}/{k}: {frac:.3e} of codes differ (bound {code_frac})"
+            n = max(1, g.numel())  # small state arrays: a handful of exact ties is not a fraction
+            assert frac * n <= max(8.0, code_frac * n), f"{where}/{k}: {frac:.3e} of codes differ (bound {code_frac})"
         else:
             m, _ = rel_err(g, r)
             report[k] = m
@@ -177,6 +180,84 @@ def heavy_grad(gen, shape, dtype):
         pick = torch.randint(0, n, (max(1, n // 256),), generator=gen)
         flat[pick] = torch.where(torch.rand(pick.shape, generator=gen) < 0.5, -1e3, 1e3)
     return g.to(dtype)
+
+
+class DriftBound:
+    """Per-element allowance for a free-running GPU trajectory that parts from the reference only
+    through 8-bit codes that came out one apart at rounding ties (each such code is checked to sit
+    at a tie by the teacher-forced tests).
+
+    After step t both sides' states are dequantised: the momentum difference |dm| (exact, from both
+    sides' codes and scales) enters step t + 1 as beta1 * |dm|; a second-moment state that differs
+    by a relative d perturbs the next update u by beta2 * d / 2 (through the rsqrt), and a residual
+    state by beta3 * d / 2 the residual factor rf.  Step t + 1 then moves the parameter by lr * rf * m,
+    so its difference grows by at most lr * (|rf| * E + |rf * m| * rho_res) with
+    E = beta1 * |dm| + (1 - beta1) * |u| * rho_u, and weight decay scales what is carried.  First
+    order: the caller allows twice the accumulated bound."""
+
+    def __init__(self, shape, factored, hp):
+        self.factored = factored
+        self.b1, self.b2 = hp["beta1"], hp["beta2"]
+        self.b3, self.lr, self.wd = hp["beta3"], hp["lr"], hp["weight_decay"]
+        self.bs = hp["block_size"]
+        z = lambda: torch.zeros(shape, dtype=torch.float64)  # noqa: E731
+        self.D, self.Em, self.rho_u, self.rho_res = z(), z(), z(), z()
+
+    def _deq(self, q, a, signed):
+        return orc.dequantize_blockwise(q.detach().cpu(), a.detach().cpu(), signed=signed, block_size=self.bs).double()
+
+    def _rel(self, gq, ga, rq, ra):
+        r = self._deq(rq, ra, False)
+        return (self._deq(gq, ga, False) - r).abs() / r.abs().clamp_min(1e-30)
+
+    def update(self, gpu_state, ref_state, cap):
+        """After both sides took step t (cap: the oracle's capture of step t)."""
+        u = cap["update"].double().abs()
+        em = self.Em + (1.0 - self.b1) * u * self.rho_u
+        if self.factored:
+            rf = cap["res_factor"].double().abs()
+            dstep = rf * em + rf * cap["exp_avg"].double().abs() * self.rho_res
+        else:
+            dstep = em
+        self.D = self.D * abs(1.0 - self.lr * self.wd) + self.lr * dstep
+        g, r = gpu_state, ref_state
+        self.Em = self.b1 * (self._deq(g["exp_avg_q"], g["exp_avg_absmax"], True)
+                             - self._deq(r["exp_avg_q"], r["exp_avg_absmax"], True)).abs()
+        if self.factored:
+            d = [self._rel(g[f"factored_{k}_q"][j], g[f"factored_{k}_absmax"][j], r[f"factored_{k}_q"][j],
+                           r[f"factored_{k}_absmax"][j]) for j in (0, 1) for k in ("row", "col")]
+            self.rho_u = 0.5 * self.b2 * (d[0].unsqueeze(-1) + d[1].unsqueeze(-2))
+            self.rho_res = 0.5 * self.b3 * (d[2].unsqueeze(-1) + d[3].unsqueeze(-2))
+        else:
+            self.rho_u = 0.5 * self.b2 * self._rel(g["exp_avg_sq_q"], g["exp_avg_sq_absmax"], r["exp_avg_sq_q"],
+                                                   r["exp_avg_sq_absmax"])
+
+
+def check_params_bound(gp: torch.Tensor, rp: torch.Tensor, bound: torch.Tensor, where: str,
+                       movement: torch.Tensor, tol: float = 1e-5, scale: float = 2.0) -> float:
+    """Every element: |dp| <= tol * (|p_ref| + movement + 1e-2 * rms(p_ref)) + scale * bound (DriftBound:
+    first order, hence twice); bf16/fp16: or within 1 ulp, and an element with an allowance also gets
+    the ulp its final rounding may add.  Returns the fraction of elements with a nonzero allowance."""
+    g = gp.detach().cpu().reshape(-1)
+    r = rp.detach().cpu().reshape(-1)
+    rd, gd = r.double(), g.double()
+    rms = rd.pow(2).mean().sqrt().item()
+    allow = tol * (rd.abs() + movement.reshape(-1) + 1e-2 * rms) + scale * bound.reshape(-1)
+    if r.dtype != torch.float32:
+        ulp = (torch.nextafter(r.abs(), torch.full_like(r, float("inf"))) - r.abs()).double()
+        allow = allow + torch.where(bound.reshape(-1) > 0, ulp, torch.zeros_like(ulp))
+    dp = (gd - rd).abs()
+    ok = dp <= allow
+    if r.dtype != torch.float32:
+        ai = g.contiguous().view(torch.int16).to(torch.int32)
+        bi = r.contiguous().view(torch.int16).to(torch.int32)
+        ordered = lambda x: torch.where(x < 0, -(x & 0x7FFF), x)  # noqa: E731
+        ok |= (ordered(ai) - ordered(bi)).abs() <= 1
+    if not bool(ok.all()):
+        k = int((~ok).nonzero()[0])
+        raise AssertionError(f"{where}: element {k}: |dp| {dp[k].item():.3e} > allowed {allow[k].item():.3e} "
+                             f"(drift allowance {bound.reshape(-1)[k].item():.3e}); {int((~ok).sum())} elements")
+    return float((bound > 0).double().mean())
 
 
 def run_oracle(params, grads_per_step, hp: dict, steps: int):
@@ -209,10 +290,8 @@ def run_lockstep(cls, params, grads_per_step, hp: dict, steps: int, exact_norm=F
     Returns, per tensor: (gpu_param, ref_param, gpu_state, ref_state, tainted, flips) where
     `tainted` marks elements whose inputs to a later step differed because an 8-bit code of
     theirs (momentum, or the row/column second-moment or residual state of their row/column)
-    came out one apart at an earlier step, and `flips` is the per-step fraction of differing
-    momentum codes.  A code flip moves the element's later updates by up to absmax/127 of the
-    momentum times the residual factor, so untainted elements are held to the tight bound and
-    tainted ones are only counted.
+    came out one apart at an earlier step, `flips` is the per-step fraction of differing
+    momentum codes, and `bound` the per-element drift allowance those differences add (DriftBound).
     """
     ohp = oracle_hp(hp)
     ps = [torch.nn.Parameter(p.clone().to(device)) for p in params]
@@ -222,6 +301,7 @@ def run_lockstep(cls, params, grads_per_step, hp: dict, steps: int, exact_norm=F
     sts = [orc.init_full8bit_state(p.shape, ohp["block_size"]) for p in refs]
     tainted = [torch.zeros(p.shape, dtype=torch.bool) for p in params]
     movement = [torch.zeros(p.shape, dtype=torch.float64) for p in params]
+    bounds = [DriftBound(p.shape, st["factored"], ohp) for p, st in zip(params, sts)]
     flips = [[] for _ in params]
     for s in range(steps):
         for p, g in zip(ps, grads_per_step[s]):
@@ -230,9 +310,11 @@ def run_lockstep(cls, params, grads_per_step, hp: dict, steps: int, exact_norm=F
         torch.cuda.synchronize()
         for i, (r, g, st) in enumerate(zip(refs, grads_per_step[s], sts)):
             before = r.double()
-            orc.full8bit_step(r, g, st, exact_norm=exact_norm, **ohp)
+            cap = {}
+            orc.full8bit_step(r, g, st, capture=cap, exact_norm=exact_norm, **ohp)
             movement[i] += (r.double() - before).abs()
             gs = opt.state[ps[i]]
+            bounds[i].update(gs, st, cap)
             dq = gs["exp_avg_q"].cpu() != st["exp_avg_q"]
             flips[i].append(float(dq.float().mean()))
             t = dq.clone()
@@ -245,7 +327,7 @@ def run_lockstep(cls, params, grads_per_step, hp: dict, steps: int, exact_norm=F
             else:
                 t |= gs["exp_avg_sq_q"].cpu() != st["exp_avg_sq_q"]
             tainted[i] |= t
-    return [Lockstep(ps[i].data, refs[i], opt.state[ps[i]], sts[i], tainted[i], flips[i], movement[i])
+    return [Lockstep(ps[i].data, refs[i], opt.state[ps[i]], sts[i], tainted[i], flips[i], movement[i], bounds[i].D)
             for i in range(len(ps))]
 
 

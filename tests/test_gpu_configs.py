@@ -1,0 +1,119 @@
+"""The BASELINE workloads C2, C3 and C4 at full size on the GPU, in the library's default mode (the
+reference's float32 clip norm).
+
+  c2  GPT-2 Medium shapes, fp32, CAME8bit (292 tensors, 355 M parameters)
+  c3  Llama-1B-style shapes, bf16, CAME8bitMemory, betas (0.9, 0.95, 0.995) (219 tensors, 1.34 G)
+  c4  Llama-7B shapes, bf16, CAME8bit (291 tensors, 6.74 G): the headline workload
+
+Each config takes bench.py's own construction (bench.CONFIGS: shapes, dtypes, hyperparameters and
+gradient scale) and two steps over all its tensors in one optimizer, so every launch variant the
+workload selects runs at its real size: the 32000 x 4096 embedding and lm_head bands, the 11008-wide
+512-thread pass variants, the 5461-wide rows, the norm's LDS-staged and row-crossing segment kernels.
+A representative subset is checked against the CPU oracle, teacher-forced (each checked tensor's
+parameter and state are set from the oracle before each step), with the tolerances of
+tests/test_gpu_parity.py.  Every tensor is held to what the blockwise quantiser fixes whatever the
+values (a full-scale code in every block, or an all-zero block under absmax 1) and to finiteness.
+"""
+import math
+
+import pytest
+import torch
+
+import bench
+from oracle import came8_oracle as orc
+from tests import parity as P
+from tests.test_gpu_c5 import _block_full_scale
+from tests.test_gpu_parity import _tight_step_check
+
+pytestmark = pytest.mark.gpu
+
+# the tensors checked against the oracle: the first occurrence of each named shape (and the last
+# one for the 32000-row embedding / lm_head pair)
+SUBSETS = {
+    "c2": [(50257, 1024), (1024, 1024), (3072, 1024), (1024, 4096), (3072,), (1024,)],
+    "c3": [(32000, 2048), (5461, 2048), (2048, 5461), (2048, 2048), (2048,)],
+    "c4": [(32000, 4096), (11008, 4096), (4096, 11008), (4096, 4096), (4096,)],
+}
+
+
+def _subset(name, shapes):
+    want = SUBSETS[name]
+    idx = [shapes.index(s) for s in want]
+    if name in ("c3", "c4"):  # the lm_head: the last 32000-row matrix
+        idx.append(len(shapes) - 1 - shapes[::-1].index(want[0]))
+    return sorted(set(idx))
+
+
+def _f32_bits(v: float) -> int:
+    return torch.tensor([v], dtype=torch.float32).view(torch.int32).item()
+
+
+def _full_scale_checks(opt, ps, shapes, block):
+    bad = []
+    for i, (p, s) in enumerate(zip(ps, shapes)):
+        st = opt.state[p]
+        assert torch.isfinite(p.data).all(), f"tensor {i} {s}: non-finite parameter"
+        assert torch.isfinite(st["exp_avg_absmax"]).all(), f"tensor {i} {s}: non-finite momentum scale"
+        ok, n = _block_full_scale(st["exp_avg_q"], st["exp_avg_absmax"], block, 127)
+        if not ok:
+            bad.append((i, s, "exp_avg", n))
+        pairs = ([("factored_row", 0), ("factored_row", 1), ("factored_col", 0), ("factored_col", 1)]
+                 if st["factored"] else [("exp_avg_sq", None)])
+        for key, j in pairs:
+            q = st[f"{key}_q"] if j is None else st[f"{key}_q"][j]
+            a = st[f"{key}_absmax"] if j is None else st[f"{key}_absmax"][j]
+            assert torch.isfinite(a).all(), f"tensor {i} {s}: non-finite {key} scale"
+            ok, n = _block_full_scale(q, a, block, 255)
+            if not ok:
+                bad.append((i, s, key, j, n))
+    assert not bad, f"blocks without a full-scale code: {bad[:5]}"
+
+
+@pytest.mark.parametrize("name", ["c2", "c3", "c4"])
+def test_baseline_config_full_size_vs_oracle(name):
+    import came_amd
+    from came_amd import _lib
+    _lib.load()
+    label, shapes_fn, pdt, gdt, gstd, cls_name, hp = bench.CONFIGS[name]
+    shapes = shapes_fn()
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(17)
+    ps = [torch.nn.Parameter(torch.randn(s, device=dev, generator=gen).mul_(0.02).to(pdt)) for s in shapes]
+    opt = getattr(came_amd, cls_name)(ps, **hp)
+    assert not opt.exact_norm, "the default mode is the reference's float32 clip norm"
+    chk = _subset(name, shapes)
+    block = opt.param_groups[0]["block_size"]
+    refs = {i: ps[i].detach().cpu().clone() for i in chk}
+    sts = {i: orc.init_full8bit_state(shapes[i], block) for i in chk}
+    ohp = P.oracle_hp(hp)
+    check = _tight_step_check(f"{name} full size")
+    n_el = sum(math.prod(s) for s in shapes)
+    print(f"[{name}] {label}: {len(shapes)} tensors, {n_el} elements; checked {[shapes[i] for i in chk]}", flush=True)
+    for step in range(2):
+        grads = [torch.randn(s, device=dev, generator=gen).mul_(gstd).to(gdt) for s in shapes]
+        with torch.no_grad():
+            for i in chk:
+                ps[i].data.copy_(refs[i].to(dev))
+                gst = opt.state[ps[i]]
+                for k in P.STATE_KEYS:
+                    if len(gst) and k in sts[i]:
+                        gst[k].copy_(sts[i][k].to(dev))
+        for p, g in zip(ps, grads):
+            p.grad = g
+        opt.step()
+        torch.cuda.synchronize()
+        print(f"[{name}] step {step + 1}: GPU step over {len(shapes)} tensors done", flush=True)
+        for i in chk:
+            g = grads[i].cpu()
+            before = refs[i].double()
+            cap = {}
+            orc.full8bit_step(refs[i], g, sts[i], capture=cap, **ohp)
+            check(step + 1, i, ps[i].data, refs[i], opt.state[ps[i]], sts[i], (refs[i].double() - before).abs(), cap)
+            # the clip divisor: the reference's float32 norm replayed; u itself may differ by an ulp
+            # where the row / column means round differently, hence a few ulps (tests/test_gpu_norm.py)
+            have, want = opt.last_clip_divisors()[ps[i]], float(cap["clip"])
+            d = abs(_f32_bits(have) - _f32_bits(want))
+            assert d <= 4, f"{name} step {step + 1} tensor {i}: clip {have!r} vs {want!r} ({d} ulps)"
+        print(f"[{name}] step {step + 1}: {len(chk)} tensors match the oracle", flush=True)
+        del grads
+        _full_scale_checks(opt, ps, shapes, block)

@@ -90,8 +90,9 @@ def golden(golden_dir):
 def test_gpu_matches_reference_golden(golden, case):
     """The default step against the reference's own outputs.  Step 1: every parameter element within
     the tight bound.  Step 10: state codes within 1, block scales within 1e-6, and every parameter
-    element that no earlier code flip touched within the tight bound (flips are tracked with the
-    oracle, which the CPU tests pin bit-exactly to the same golden vectors)."""
+    element within the tight bound plus the drift that codes one apart at earlier steps allow it
+    (parity.DriftBound, computed from both sides' states with the oracle, which the CPU tests pin
+    bit-exactly to the same golden vectors)."""
     z, meta = golden
     m = meta[case]
     dtype = getattr(torch, m["dtype"])
@@ -102,14 +103,12 @@ def test_gpu_matches_reference_golden(golden, case):
     out1 = P.run_lockstep(_cls(m["cls"]), params, grads, m["hp"], 1)
     outN = P.run_lockstep(_cls(m["cls"]), params, grads, m["hp"], steps)
     for step, out in ((1, out1), (steps, outN)):
-        for i, (gp, rp, gs, rs, tainted, flips, mv) in enumerate(out):
+        for i, (gp, rp, gs, rs, tainted, flips, mv, bound) in enumerate(out):
             where = f"{case} step {step} tensor {i} {shapes[i]}"
             ref_p = _to_torch(z[f"{case}/p{step}/{i}"], dtype)
             assert torch.equal(rp.view(torch.int16) if dtype == torch.bfloat16 else rp,
                                ref_p.view(torch.int16) if dtype == torch.bfloat16 else ref_p), where + " (oracle)"
-            frac = P.check_untainted_params(gp, ref_p, tainted, where, mv)
-            n = gp.numel()
-            assert frac * n <= max(2.0, 0.02 * n), f"{where}: {frac:.3e} of the elements saw a flipped code"
+            P.check_params_bound(gp, ref_p, bound, where, mv)
             ref_state = {k: torch.from_numpy(np.array(z[f"{case}/s{step}/{i}/{k}"])) for k in P.STATE_KEYS
                          if f"{case}/s{step}/{i}/{k}" in z}
             P.compare_states(gs, ref_state, code_frac=2e-3, abs_rel=1e-6, where=where)
@@ -131,13 +130,18 @@ def _c1_inputs():
 
 
 # Teacher-forced bounds, identical for both modes: the oracle of each mode is the reference's
-# arithmetic with the reference's float32 norm (parity mode) or with the exactly rounded norm (default
-# mode; the reference's float32 accumulation of the norm is itself off by up to ~1e-4 relative on
-# multi-million-element tensors, C1: -8.3e-5, see tests/test_oracle_closed_form.py).  What is left
-# is the row/column summation order: ulps.
+# arithmetic with the reference's float32 norm (the default) or with the exactly rounded norm (the
+# opt-in mode).  What is left is the order of the row and column sums (fp64 rounded once here,
+# torch's fp32 cascade there): a few ulps of each mean.
 #   (param tolerance, block-scale tolerance, distance of a differing code from a rounding tie,
 #    fraction of codes that may differ)
-TOL = (1e-5, 1e-6, 1e-3, 2e-2)
+# The tie distance: a state value and its block's absmax that each differ from the reference's by up
+# to ~4 ulps (2.4e-7 relative) move the scaled value x / absmax * Q (Q = 127 or 255) by at most
+# 2 * 2.4e-7 * 255 = 1.2e-4 code units; 2e-4 allows for that.  The most seen over the GPU suite and
+# the C2-C5 workloads is 7.6e-5 (5 fp32 ulps at 255).  The fraction: data with exactly tied values
+# (equal +-1e3 outliers, whose row means come out exactly 1/2 of each other) put up to 1.1e-2 of a
+# row state's codes at exact ties; elsewhere below 3e-3.
+TOL = (1e-5, 1e-6, 2e-4, 1.5e-2)
 
 
 def _tight_step_check(tag, block=256, code_frac=None):
@@ -168,8 +172,9 @@ def test_c1_ten_steps_vs_oracle(exact_norm):
     for i, o in enumerate(out):
         where = f"C1 free-running tensor {i} exact_norm={exact_norm}"
         assert max(o.flips) <= 1e-4, f"{where}: flips per step {o.flips}"
-        _, nr = P.rel_err(o.gpu_param, o.ref_param)
-        assert nr <= 1e-4, f"{where}: ||dp||/||p|| = {nr:.3e}"
+        # elementwise: 1e-5 relative, plus what codes one apart at ties allow each element
+        drifting = P.check_params_bound(o.gpu_param, o.ref_param, o.bound, where, o.movement)
+        print(f"[c1 free] {where}: {drifting:.2e} of the elements carry a drift allowance", flush=True)
         ga, ra = o.gpu_state["exp_avg_absmax"].cpu().double(), o.ref_state["exp_avg_absmax"].double()
         off = ((ga - ra).abs() / ra > 1e-5).double().mean().item()
         assert off <= 1e-2, f"{where}: {off:.3e} of the block scales differ by more than 1e-5"
@@ -189,7 +194,8 @@ def test_c1_default_free_running_vs_reference_digest(c1_digest):
     path) at steps 1 and 10: every momentum block scale and every factored / 1-D second-moment
     scale within 1e-6 relative; every factored / 1-D state code within 1 of the reference's, and a
     differing one only at a rounding tie of the reference's value; the sampled momentum codes within
-    1; the sampled parameters within 1e-5 relative (floor 1e-7 * rms).  The oracle runs alongside
+    1; the sampled parameters within 1e-5 relative (floor 1e-7 * rms) plus the drift that codes one
+    apart at ties allow each element (parity.DriftBound).  The oracle runs alongside
     (it reproduces this digest bit for bit, tests/test_oracle_golden.py) to give the reference's
     pre-quantisation values for the tie check."""
     z, digests = c1_digest
@@ -202,6 +208,7 @@ def test_c1_default_free_running_vs_reference_digest(c1_digest):
     sts = [orc.init_full8bit_state(p.shape) for p in refs]
     tainted = [torch.zeros(p.shape, dtype=torch.bool) for p in params]
     movement = [torch.zeros(p.shape, dtype=torch.float64) for p in params]
+    bounds = [P.DriftBound(p.shape, st["factored"], ohp) for p, st in zip(params, sts)]
     worst = {}
     for step in range(1, 11):
         for p, g in zip(ps, grads[step - 1]):
@@ -216,6 +223,7 @@ def test_c1_default_free_running_vs_reference_digest(c1_digest):
             movement[i] += (r.double() - before).abs()
             caps.append(cap)
             gst = opt.state[ps[i]]
+            bounds[i].update(gst, st, cap)
             t = gst["exp_avg_q"].cpu() != st["exp_avg_q"]
             if st["factored"]:
                 t |= (gst["factored_row_q"].cpu() != st["factored_row_q"]).any(dim=0).unsqueeze(-1).expand(t.shape)
@@ -252,13 +260,15 @@ def test_c1_default_free_running_vs_reference_digest(c1_digest):
             print(f"[c1 digest] {where}: worst sample {wi}: gpu {got[wi].item()!r} ref {ref_p[wi].item()!r} "
                   f"movement {mv[wi].item():.3e} tainted {bool(tainted[i].reshape(-1)[::997][wi])}", flush=True)
             # an element whose inputs differed at an earlier step (a code one apart at a tie, in its
-            # momentum or its row/column states) follows a neighbouring trajectory from then on
+            # momentum or its row/column states) follows a neighbouring trajectory from then on, within
+            # the drift those differences allow it (parity.DriftBound)
             t = tainted[i].reshape(-1)[::997]
+            allow = 1e-5 * (ref_p.double().abs() + mv + 1e-2 * rms) + 2.0 * bounds[i].D.reshape(-1)[::997]
+            over = (got.double() - ref_p.double()).abs() - allow
             worst[f"s{step}/p{i}/param_sample"] = (err[~t].max().item() if (~t).any() else 0.0, err.max().item(),
-                                                   float(t.float().mean()))
-            if (~t).any():
-                assert err[~t].max().item() <= 1e-5, f"{where}: sampled parameter error {err[~t].max().item():.3e}"
-            assert float(t.float().mean()) <= 2e-2, f"{where}: {float(t.float().mean()):.3e} of the samples saw a flip"
+                                                   float(t.float().mean()), over.max().item())
+            assert over.max().item() <= 0.0, (f"{where}: sample {int(over.argmax())} beyond its allowance by "
+                                              f"{over.max().item():.3e}")
     print("[c1 digest] worst per entry:", json.dumps(worst, sort_keys=True), flush=True)
 
 
@@ -296,11 +306,10 @@ def test_band_parameter_pass_vs_oracle(block, dtype):
     steps = 3
     grads = [[P.heavy_grad(gen, s, dt) for s in BAND] for _ in range(steps)]
     hp = dict(lr=1e-3, weight_decay=1e-2, block_size=block)
-    # The +-1e3 outliers are all the same magnitude, so with one 2048-wide block per column state
-    # many columns hold exactly tied scaled values; every differing code must still sit at a tie,
-    # only the share of such codes may exceed the usual bound.
+    # The +-1e3 outliers are all the same magnitude, so many rows and columns hold exactly tied
+    # scaled values (up to 8.3e-3 of a state's codes here); every differing code must sit at a tie.
     P.run_teacher_forced(_cls("CAME8bitFull"), params, grads, hp, steps,
-                         check=_tight_step_check(f"band {dtype} B={block}", block=block, code_frac=0.05))
+                         check=_tight_step_check(f"band {dtype} B={block}", block=block))
 
 
 def test_mixed_param_grad_dtypes_vs_oracle():
