@@ -151,15 +151,46 @@ def compulsory_bytes(shapes, pdt, gdt, block=256, fp32_state=False, tiles=False)
 
 
 # --------------------------------------------------------------------------------- CPU baseline
+CPU_SAMPLE_MAX = 400_000_000  # elements the CPU baseline steps (about 10-20 s of CPU work in all)
+
+
+def cpu_sample(cfg_name, shapes):
+    """The tensors the CPU baseline steps: the whole workload when it is small enough; for the
+    Llama-shaped sets the embedding, the first decoder layer, the final norm and the lm_head (the
+    other layers repeat the first); otherwise every k-th tensor."""
+    if sum(math.prod(s) for s in shapes) <= CPU_SAMPLE_MAX:
+        return list(shapes), "the whole workload"
+    if cfg_name in ("c3", "c4", "c4fp"):
+        return shapes[:10] + shapes[-2:], "embedding + decoder layer 0 + final norm + lm_head"
+    k = 1
+    while sum(math.prod(s) for s in shapes[::k]) > CPU_SAMPLE_MAX:
+        k += 1
+    return shapes[::k], f"every {k}-th tensor"
+
+
+def cpu_model_name() -> str:
+    """lscpu's model name (the host CPU), else /proc/cpuinfo's."""
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            return next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "unknown")
+    except OSError:
+        return "unknown"
+
+
 def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False, tiles=False):
-    """Time the CPU oracle on a bounded sample of the workload; returns the cpu_baseline object."""
+    """Time the CPU oracle on a bounded sample of the workload (cpu_sample): one warm-up step, then
+    the median of three; returns the cpu_baseline object."""
     from oracle import came8_oracle as orc
 
-    factored = [s for s in shapes if len(s) >= 2]
-    vec = [s for s in shapes if len(s) == 1]
-    # sample: the smallest and the largest distinct matrix shapes below 64M elements, plus one 1-D tensor
-    distinct = sorted({s for s in factored if math.prod(s) <= (1 << 26)}, key=math.prod)
-    sample = [distinct[0]] + ([distinct[-1]] if len(distinct) > 1 else []) + vec[:1]
+    sample, how = cpu_sample(cfg_name, shapes)
     gen = torch.Generator().manual_seed(123)
     params = [(torch.randn(s, generator=gen) * 0.02).to(pdt) for s in sample]
     grads = [(torch.randn(s, generator=gen) * (gstd or 1e-3)).to(gdt) for s in sample]
@@ -176,24 +207,21 @@ def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False, tiles=F
     else:
         states = [orc.init_full8bit_state(s) for s in sample]
         step_fn = orc.full8bit_step
-    # every core this process may run on (the box's share), capped by OMP_NUM_THREADS where the host sets it
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    # every core this process may run on: os.cpu_count(), within the affinity mask and the host's
+    # OMP_NUM_THREADS (the box's share of a shared host)
+    host = os.cpu_count() or 1
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else host
     if os.environ.get("OMP_NUM_THREADS", "").isdigit():
         cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
-    torch.set_num_threads(max(1, cores))
-    model = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), model)
-    except OSError:
-        pass
+    torch.set_num_threads(max(1, min(host, cores)))
     times = []
-    for it in range(3):
+    for it in range(4):
         t0 = time.perf_counter()
         for p, g, st in zip(params, grads, states):
             step_fn(p, g, st, **ohp)
         times.append(time.perf_counter() - t0)
-    t = sorted(times[1:])[0]  # first step allocates; best of the next two
+        print(f"[bench] cpu baseline step {it}: {times[-1] * 1e3:.0f} ms", file=sys.stderr, flush=True)
+    t = sorted(times[1:])[1]  # the first step allocates; the median of the next three
     nbytes = compulsory_bytes(sample, pdt, gdt, fp32_state=fp32_state, tiles=tiles)
     n_sample = sum(math.prod(s) for s in sample)
     n_total = sum(math.prod(s) for s in shapes)
@@ -201,13 +229,14 @@ def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False, tiles=F
         "value": round(nbytes / t / 1e9, 4),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
-        "cpu_model": model,
+        "cpu_model": cpu_model_name(),
         "kind": "port",
-        "sample": f"{len(sample)} tensors {sample} ({n_sample} elements) of {cfg_name}, oracle step after one "
-                  f"warm-up, best of 2: {t * 1e3:.1f} ms; whole workload extrapolated by element count: "
+        "sample": f"{how}: {len(sample)} tensors, {n_sample} elements of {cfg_name}; the oracle's step, one warm-up "
+                  f"then the median of 3: {t * 1e3:.1f} ms; the whole workload extrapolated by element count: "
                   f"{t * n_total / n_sample * 1e3:.0f} ms/step",
         "ms_per_step_extrapolated": round(t * n_total / n_sample * 1e3, 1),
-        "host_cpu_count": os.cpu_count(),
+        "os_cpu_count": host,
+        "torch_threads": torch.get_num_threads(),
     }
 
 
@@ -291,6 +320,19 @@ def main():
     torch.cuda.synchronize()
     phases = _lib.profile_read(reset=True)
     _lib.profile_enable(False)
+    # the other clip-norm mode on the same optimizer, for comparison (not the reported value)
+    other_ms = None
+    if cls_name != "CAME8bit2D":
+        opt.exact_norm = not bool(args.exact_norm)
+        for _ in range(2):
+            opt.step()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        for _ in range(args.steps):
+            opt.step()
+        torch.cuda.synchronize()
+        other_ms = (time.perf_counter() - t2) * 1e3 / args.steps
+        opt.exact_norm = bool(args.exact_norm)
 
     ms = (t1 - t0) * 1e3 / args.steps
     fp32_state = cls_name == "CAMECUDA"
@@ -345,6 +387,10 @@ def main():
         },
         "phases": phase_rep,
     }
+    if other_ms is not None:
+        out["other_clip_mode"] = {
+            "clip_norm": "reference fp32 order (default)" if args.exact_norm else "exact fp64 (opt-in)",
+            "ms_per_step": round(other_ms, 4)}
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle on a sample", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(args.config, shapes, pdt, gdt, gstd, hp, fp32_state=fp32_state,

@@ -19,6 +19,7 @@ ABI_VERSION = 4  # include/came8.h: CAME8_ABI_VERSION
 CAME8_FLAG_REFERENCE_NORM = 1  # the default (accepted for callers of ABI 3)
 CAME8_FLAG_EXACT_NORM = 2
 CAME8_FLAG_PLAN_ONLY = 4
+CAME8_FLAG_FP16_UPDATE = 8
 CAME8_STATE_Q8 = 0
 CAME8_STATE_FP32 = 1
 CAME8_STATE_8BIT2D = 2

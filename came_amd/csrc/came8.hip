@@ -768,6 +768,7 @@ Hp make_hp(const came8_hparams& h) {
   hp.a3f = 1.0f - float(h.beta3);
   const float lr_wd = float(h.lr) * float(h.weight_decay);
   hp.wdfac = 1.0f - lr_wd;
+  hp.fp16u = (h.flags & CAME8_FLAG_FP16_UPDATE) ? 1 : 0;
   hp.B = h.block_size;
   hp.log2B = log2_or_minus1(h.block_size);
   if (hp.log2B >= 0) {

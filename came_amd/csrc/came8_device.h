@@ -46,11 +46,27 @@ struct BF16 {
   }
 };
 
+// x rounded to fp16 (round to nearest even) and back.  Written with integer operations on x's bits: a
+// plain (_Float16) conversion of a product lets the compiler fuse the multiply and the conversion
+// into one mixed-precision fma, which rounds the exact product to fp16 once instead of the fp32
+// product (two roundings, as the reference computes it); the two differ where the fp32 product
+// lands on an fp16 rounding tie.
+__device__ __forceinline__ float round_f16(float x) {
+  const uint32_t b = __float_as_uint(x);
+  if ((b & 0x7f800000u) == 0x7f800000u) return x;  // inf, NaN
+  if ((b & 0x7fffffffu) < 0x38800000u)             // |x| < 2^-14: fp16's subnormal grid, 2^-24
+    return rintf(x * 0x1p24f) * 0x1p-24f;
+  const uint32_t r = (b + 0x0fffu + ((b >> 13) & 1u)) & ~0x1fffu;  // 10 fraction bits, ties to even
+  return (r & 0x7fffffffu) > 0x477fe000u ? __uint_as_float((b & 0x80000000u) | 0x7f800000u)  // > 65504
+                                         : __uint_as_float(r);
+}
+
 // IEEE half, round-to-nearest-even conversion.
 struct F16 {
   using storage = uint16_t;
   static __device__ __forceinline__ float load(storage v) { return float(__builtin_bit_cast(_Float16, v)); }
-  static __device__ __forceinline__ storage store(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+  // round_f16 first: the conversion then sees an fp16 value, never a product it could fuse with
+  static __device__ __forceinline__ storage store(float f) { return __builtin_bit_cast(uint16_t, (_Float16)round_f16(f)); }
   static __device__ __forceinline__ float elem(const uint32_t* w, int v) {
     return float(__builtin_bit_cast(_Float16, uint16_t(w[v >> 1] >> (16 * (v & 1)))));
   }

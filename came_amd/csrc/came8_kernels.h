@@ -123,6 +123,7 @@ struct Hp {
   float a1f, a2f, a3f;  // 8bit2d: 1 - beta computed in float
   float wdfac;          // 8bit2d: multiplicative weight decay 1 - lr * wd, computed in float
   const void* zeros;    // kZeroBytes of zeros in the workspace (reads that must count for nothing)
+  int32_t fp16u;        // 1-D tensors: the momentum takes the update rounded to fp16 (CAME8_FLAG_FP16_UPDATE)
 };
 constexpr int kZeroBytes = 32768;  // >= TPB*V*K elements of any band-pass shape
 
@@ -1783,7 +1784,9 @@ __global__ __launch_bounds__(kThreads) void k_vec_passB(const DevTensor* __restr
       if (e < N) {
         const float gv = TG::load(g[e]);
         vv[v] = vec_v_new<TG>(t, e, gv, hp);
-        const float u = (rsqrt_ref(vv[v]) * gv) / clip;
+        float uu = rsqrt_ref(vv[v]) * gv;
+        if (hp.fp16u && !t.fp32st) uu = round_f16(uu);
+        const float u = uu / clip;
         const float mold = t.fp32st ? st_m(t)[e] : deq_s8(t.mq[e], t.ma[blk_of(e, hp)]);
         m[v] = fmaf(u, hp.a1, mold * hp.b1);
         pv[v] = param_update<TP>(TP::load(p[e]), m[v], hp);
@@ -1857,7 +1860,9 @@ __global__ __launch_bounds__(kThreads) void k_vec_passB(const DevTensor* __restr
 // ===========================================================================
 template <typename TG>
 __device__ __forceinline__ float m_new_fact(const DevTensor& t, int64_t e, float clip, const Hp& hp) {
-  const float u = u_at<TG>(t, e, hp) / clip;
+  float uu = u_at<TG>(t, e, hp);
+  if (hp.fp16u && !t.factored) uu = round_f16(uu);
+  const float u = uu / clip;
   return fmaf(u, hp.a1, deq_s8(t.mq[e], t.ma[blk_of(e, hp)]) * hp.b1);
 }
 

@@ -186,6 +186,12 @@ class _Came8Base(torch.optim.Optimizer):
         b1, b2, b3 = group["betas"]
         e0, e1 = group["eps"]
         flags = _lib.CAME8_FLAG_EXACT_NORM if getattr(self, "exact_norm", False) else 0
+        # the reference's fp16-update kernels for unfactored tensors (CAME8bitFull.py:488-509; CAME8bit
+        # selects them with cuda_1d_batched_use_fp16_update or the repeated_fp16_pairmin runtime mode,
+        # CAME8bit.py:142-156); one launch steps every 1-D tensor here, so the flag covers all of them
+        if getattr(self, "cuda_nonfactored_use_fp16_update", False) or getattr(self, "cuda_1d_batched_use_fp16_update",
+                                                                               False):
+            flags |= _lib.CAME8_FLAG_FP16_UPDATE
         return _lib.Came8HParams(float(group["lr"]), float(b1), float(b2), float(b3), float(e0), float(e1),
                                  float(group["clip_threshold"]), float(group["weight_decay"]),
                                  int(group["block_size"]), flags)
@@ -394,8 +400,9 @@ class CAME8bitFull(_Came8Base):
     ):
         defaults = self._validate_and_defaults(lr, eps, clip_threshold, betas, weight_decay, block_size)
         super().__init__(params, defaults)
-        # Accepted for signature compatibility (CAME8bitFull.py:92-120); they tuned the reference's
-        # per-parameter CUDA chains and select nothing here, but their validation is kept.
+        # Accepted for signature compatibility (CAME8bitFull.py:92-120); apart from
+        # cuda_nonfactored_use_fp16_update they tuned the reference's per-parameter CUDA chains and
+        # select nothing here, but their validation is kept.
         self.prefer_factored_cuda_ext_path = bool(prefer_factored_cuda_ext_path)
         self.cuda_factored_nd_chunk_size_override = (
             None if cuda_factored_nd_chunk_size_override is None else int(cuda_factored_nd_chunk_size_override))
@@ -405,6 +412,8 @@ class CAME8bitFull(_Came8Base):
         self.cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel = (
             None if cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel is None
             else int(cuda_factored_nd_chunked_direct_row_sum_max_matrix_numel))
+        # the one that changes numerics: 1-D tensors take the reference's fp16-update variant
+        # (CAME8_FLAG_FP16_UPDATE); settable after construction as well
         self.cuda_nonfactored_use_fp16_update = bool(cuda_nonfactored_use_fp16_update)
         if self.cuda_factored_nd_chunk_size_override is not None and self.cuda_factored_nd_chunk_size_override <= 0:
             raise ValueError("cuda_factored_nd_chunk_size_override must be positive when set")
@@ -422,6 +431,10 @@ class CAME8bitMemory(CAME8bitFull):
 
     The reference shares scratch buffers per device between parameters; here every param group's
     step uses one workspace per optimizer and device, so the same holds by construction.
+
+    The reference's CUDA path steps 1-D tensors with its fp16-update kernels whatever the arguments
+    (CAME8bitMemory.py:524-557); its CPU path, which this class follows by default, does not.  Set
+    ``opt.cuda_nonfactored_use_fp16_update = True`` for the CUDA path's rounding.
     """
 
     def __init__(

@@ -72,6 +72,13 @@ extern "C" {
                                         rounding error, ~1e-4 relative at 2^22 elements) */
 #define CAME8_FLAG_PLAN_ONLY 4u      /* build and upload the launch plan for this workspace and tag, launch
                                         nothing (prepares a later capture into a HIP graph) */
+#define CAME8_FLAG_FP16_UPDATE 8u    /* unfactored (1-D) tensors of the 8-bit layout: the momentum takes the
+                                        update rsqrt(v) * g rounded to fp16 (round to nearest even), then
+                                        divided by the clip, as the reference's fp16-update CUDA kernels
+                                        store it (came_pytorch/came_cuda/csrc/came_kernels.cu:1068-1122,
+                                        1546-1601; selected by CAME8bitFull.py:488-509, and always by
+                                        CAME8bitMemory.py:524-557).  The clip's norm stays that of the fp32
+                                        update.  Lossy: the update moves by up to 2^-11 relative. */
 
 /*
  * One parameter tensor and its full8bit state, laid out exactly as the

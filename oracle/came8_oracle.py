@@ -126,7 +126,7 @@ def _rms(t: torch.Tensor) -> torch.Tensor:
 def full8bit_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *, beta1: float, beta2: float,
                   beta3: float, eps0: float, eps1: float, lr: float, clip_threshold: float,
                   weight_decay: float, block_size: int, capture: Dict[str, torch.Tensor] | None = None,
-                  exact_norm: bool = False) -> None:
+                  exact_norm: bool = False, fp16_update: bool = False) -> None:
     """One CPU full8bit step on parameter ``p`` (in place) and state ``st`` (in place).
 
     Follows reference CAME8bitFull.py:962-966 (step/RMS bookkeeping) and
@@ -143,6 +143,11 @@ def full8bit_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *,
     tensors) by sqrt of the fp64 sum of squares rounded to float32: the
     library's opt-in exactly rounded clip (CAME8_FLAG_EXACT_NORM).  Every
     other operation is unchanged.
+
+    ``fp16_update=True`` is the reference's fp16-update CUDA variant for
+    unfactored tensors (came_kernels.cu:1068-1122,1546-1601): the norm is that
+    of the fp32 update, and the momentum takes the update rounded to fp16 (round
+    to nearest even) before the clip division.
     """
     st["step"] += 1
     st["RMS"] = _rms(p)
@@ -172,6 +177,8 @@ def full8bit_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *,
     else:
         rms = _rms(upd)
     clipv = (rms / clip_threshold).clamp_(min=1.0)
+    if fp16_update and not factored:
+        upd = upd.half().float()
     upd.div_(clipv)
     if capture is not None:
         capture["update"] = upd.clone()

@@ -207,3 +207,36 @@ def test_exact_norm_branch_clip(case):
         absu = float(u.abs()[0])
         assert float(np.float32(np.float32(absu * 64.0) / np.float32(64.0))) == float(np.float32(absu))
         assert all(float(v) == absu for v in u.abs()[:50])
+
+
+def test_first_step_fp16_update_closed_form():
+    """Step 1, 1-D, the fp16-update branch: v = (1-b2)(g^2+eps0), u = g/sqrt(v) (eps0 = 1e-6, about g^2,
+    so that |u| varies); the clip is the RMS of the fp32 u (threshold 0.5, so active and not a power
+    of two); the momentum takes u rounded to fp16 before the division: m = (1-b1) * fp16(u) / clip.
+    Computed here in fp64 with numpy's fp16 rounding; elements whose u lies within 1e-6 of an fp16
+    rounding tie are left out.  Rounding after the division, rounding the norm's input, or not
+    rounding at all each miss by up to 2^-11."""
+    gen = torch.Generator().manual_seed(7)
+    n = 4096
+    g = torch.randn(n, generator=gen) * 1e-3 * torch.exp(torch.randn(n, generator=gen))
+    hp = dict(HP, clip_threshold=0.5, eps0=1e-6)
+    p = torch.zeros(n)
+    st = orc.init_full8bit_state((n,))
+    cap = {}
+    orc.full8bit_step(p, g, st, capture=cap, fp16_update=True, **hp)
+    g64 = g.double().numpy()
+    v = (1 - 0.999) * (g64 ** 2 + 1e-6)
+    u = g64 / np.sqrt(v)
+    clip = max(np.sqrt(np.mean(u ** 2)) / 0.5, 1.0)
+    assert abs(cap["clip"].item() / clip - 1) < 1e-6
+    u16 = u.astype(np.float16).astype(np.float64)
+    # distance of u from an fp16 rounding tie, relative
+    ulp = np.abs(np.spacing(u.astype(np.float16)).astype(np.float64))
+    frac = np.abs(u - u16) / ulp
+    keep = np.abs(frac - 0.5) > 1e-6 * np.abs(u) / ulp + 1e-3
+    m = (1 - 0.9) * u16 / clip
+    got = cap["exp_avg"].double().numpy()
+    assert keep.mean() > 0.99
+    assert np.allclose(got[keep], m[keep], rtol=2e-6, atol=0), np.abs(got[keep] / m[keep] - 1).max()
+    m32 = (1 - 0.9) * u / clip  # without the rounding: visibly different
+    assert np.abs(got / m32 - 1).max() > 1e-4
