@@ -16,7 +16,12 @@ Outputs (numpy ``.npz``, no pickles):
   * ``golden_small.npz``  -- inputs and full outputs after step 1 and step 10
     for a set of small and ragged shapes;
   * ``golden_c1_digest.npz`` -- SHA-256 digests plus a strided sample of the
-    config-1 run (2048x2048 fp32 weight + 2048 bias, 10 steps).
+    config-1 run (2048x2048 fp32 weight + 2048 bias, 10 steps);
+  * ``golden_camecuda.npz`` -- the same as ``golden_small.npz`` for the
+    reference's ``CAMECUDA`` on CPU tensors, whose fp32-state step is its
+    pure-torch ``_step_param_generic`` (``came_pytorch/CAMECUDA.py:275-326``).
+
+``--camecuda`` writes only ``golden_camecuda.npz``.
 All runs use ``torch.set_num_threads(4)`` so that torch's parallel reductions
 split the same way when the oracle replays them.
 """
@@ -53,6 +58,16 @@ SMALL_CASES = [
      "float32", "normal", dict(lr=5e-4, weight_decay=1e-2, block_size=64, clip_threshold=0.5)),
 ]
 NSTEPS = 10
+
+# CAMECUDA (fp32 states) on CPU tensors: (name, shapes, p dtype, grad kind, hyper-parameters)
+CAMECUDA_CASES = [
+    ("cudafp_ragged_fp32", [(1,), (3,), (255,), (257,), (1000, 3), (3, 517), (129, 257), (2, 3, 5, 7), (4, 1, 1)],
+     "float32", "normal", dict(lr=2e-4, weight_decay=1e-2)),
+    ("cudafp_heavy_bf16", [(5,), (300,), (17, 300), (260, 9), (3, 3, 4, 4), (1, 1)],
+     "bfloat16", "heavy", dict(lr=1e-3, weight_decay=1e-2, betas=(0.9, 0.95, 0.995))),
+    ("cudafp_clip_fp32", [(100,), (70, 130)],
+     "float32", "normal", dict(lr=5e-4, weight_decay=0.0, clip_threshold=0.5)),
+]
 
 
 def make_grad(gen: torch.Generator, shape, kind: str, dtype: torch.dtype) -> torch.Tensor:
@@ -122,6 +137,28 @@ def run_small(mod, out: dict, meta: dict) -> None:
                           steps=NSTEPS)
 
 
+def run_camecuda(mod, out: dict, meta: dict) -> None:
+    for ci, (name, shapes, pdt, kind, hp) in enumerate(CAMECUDA_CASES):
+        dtype = getattr(torch, pdt)
+        gen = torch.Generator().manual_seed(2000 + ci)
+        params = [torch.nn.Parameter((torch.randn(s, generator=gen) * 0.02).to(dtype)) for s in shapes]
+        for i, p in enumerate(params):
+            out[f"{name}/p0/{i}"] = p_array(p)
+        opt = mod.CAMECUDA(params, **hp)
+        for step in range(1, NSTEPS + 1):
+            for i, (p, s) in enumerate(zip(params, shapes)):
+                g = make_grad(gen, s, kind, dtype)
+                out[f"{name}/g{step}/{i}"] = p_array(g)
+                p.grad = g
+            opt.step()
+            if step in (1, NSTEPS):
+                for i, p in enumerate(params):
+                    out[f"{name}/p{step}/{i}"] = p_array(p)
+                    state_arrays(f"{name}/s{step}/{i}", opt.state[p], out)
+        meta[name] = dict(cls="CAMECUDA", shapes=[list(s) for s in shapes], dtype=pdt, grad=kind, hp=hp,
+                          steps=NSTEPS)
+
+
 def digest(t: torch.Tensor) -> str:
     return hashlib.sha256(t.detach().cpu().contiguous().view(torch.uint8).numpy().tobytes()).hexdigest()
 
@@ -176,6 +213,12 @@ def main() -> None:
 
     meta = {"torch": torch.__version__, "threads": THREADS, "reference": REF}
     out: dict = {}
+    if "--camecuda" in sys.argv[1:]:
+        run_camecuda(mod, out, meta)
+        out["meta_json"] = np.array(json.dumps(meta, sort_keys=True))
+        np.savez_compressed(os.path.join(HERE, "golden_camecuda.npz"), **out)
+        print("wrote", os.path.join(HERE, "golden_camecuda.npz"))
+        return
     run_small(mod, out, meta)
     out["meta_json"] = np.array(json.dumps(meta, sort_keys=True))
     np.savez_compressed(os.path.join(HERE, "golden_small.npz"), **out)

@@ -109,3 +109,37 @@ def test_oracle_c1_digest(golden_dir):
                     if key in digests:
                         hv = hashlib.sha256(v.contiguous().view(torch.uint8).numpy().tobytes()).hexdigest()
                         assert hv == digests[key], key
+
+
+CAMECUDA_CASES = ["cudafp_ragged_fp32", "cudafp_heavy_bf16", "cudafp_clip_fp32"]
+
+
+@pytest.mark.parametrize("case", CAMECUDA_CASES)
+def test_fp32_state_oracle_matches_reference_camecuda(golden_dir, case):
+    """oracle.fp32_state_step against the reference's CAMECUDA on CPU tensors (its fp32-state
+    _step_param_generic, CAMECUDA.py:275-326; golden_camecuda.npz from make_golden.py --camecuda):
+    parameters and every fp32 state bit-exact after steps 1 and 10, ragged shapes, fp32 and bf16."""
+    z = np.load(os.path.join(golden_dir, "golden_camecuda.npz"))
+    m = json.loads(str(z["meta_json"]))[case]
+    dtype = getattr(torch, m["dtype"])
+    hp = _hp(m["hp"])
+    hp.pop("block_size")
+    shapes = [tuple(s) for s in m["shapes"]]
+    params = [_to_torch(z[f"{case}/p0/{i}"], dtype).clone() for i in range(len(shapes))]
+    states = [orc.init_fp32_state(s) for s in shapes]
+    for step in range(1, m["steps"] + 1):
+        for i in range(len(shapes)):
+            g = _to_torch(z[f"{case}/g{step}/{i}"], dtype)
+            orc.fp32_state_step(params[i], g, states[i], **hp)
+        if step in (1, m["steps"]):
+            for i in range(len(shapes)):
+                np.testing.assert_array_equal(_as_np(params[i]), z[f"{case}/p{step}/{i}"],
+                                              err_msg=f"{case} step {step} param {i} {shapes[i]}")
+                n = 0
+                for k, v in states[i].items():
+                    key = f"{case}/s{step}/{i}/{k}"
+                    if isinstance(v, torch.Tensor) and key in z:
+                        np.testing.assert_array_equal(_as_np(v), z[key], err_msg=key)
+                        n += 1
+                assert n == (5 if states[i]["factored"] else 2), f"{case} {shapes[i]}: {n} states compared"
+                assert int(z[f"{case}/s{step}/{i}/step"]) == states[i]["step"]
