@@ -119,6 +119,15 @@ class _Came8Base(torch.optim.Optimizer):
             raise RuntimeError("block_size changed after the 8-bit state was created; the state layout is fixed.")
         if state["exp_avg_q"].device != p.device:
             raise RuntimeError("optimizer state lives on a different device than its parameter")
+        if state.get("factored") and "factored_row_absmax" in state:
+            # the flat layout: [2][blocks of the P*R row states] and [2][blocks of the P*C column states]
+            # (a per-matrix layout with as many codes has [2*P][blocks per matrix] scales instead)
+            rows = math.prod(p.shape[:-1])
+            cols = math.prod(p.shape[:-2]) * p.shape[-1]
+            for key, n in (("factored_row", rows), ("factored_col", cols)):
+                if (state[f"{key}_q"].numel() != 2 * n
+                        or state[f"{key}_absmax"].numel() != 2 * num_blocks(n, block_size)):
+                    raise RuntimeError(f"{key} state does not have the flat full8bit layout of this parameter")
 
     # -------------------------------------------------------------- checkpoint
     def load_state_dict(self, state_dict: dict, convert_layouts: bool = True) -> None:
@@ -131,7 +140,9 @@ class _Came8Base(torch.optim.Optimizer):
         states under CAME8bit2D / CAMECUDA) is converted into this optimizer's layout
         (``state_layout.convert_state``), so the momentum and second moments carry over.  With
         ``convert_layouts=False`` such a state is left as loaded, and, as in the reference
-        (CAME8bit.py:757-759), re-initialised by the next step."""
+        (CAME8bit.py:757-759), re-initialised by the next step; that includes the reference CUDA N-D
+        path's per-matrix blocks (``_mode`` "full8bit" with ``_cuda_factored_nd_ext_path``), which no
+        kernel here steps in place."""
         saved_groups = state_dict["param_groups"]
         saved_state = state_dict["state"]
         super().load_state_dict(state_dict)
@@ -237,7 +248,9 @@ class _Came8Base(torch.optim.Optimizer):
         if grad.shape != p.shape:
             raise RuntimeError(f"grad shape {tuple(grad.shape)} does not match param shape {tuple(p.shape)}")
         state = self.state[p]
-        if len(state) == 0 or state.get("_mode") != self._MODE:
+        # another layout (a different _mode, or the reference CUDA N-D path's per-matrix blocks under
+        # _mode "full8bit") starts over, as the reference does (CAME8bit.py:757-759)
+        if len(state) == 0 or state_layout.layout_of(state) != self._MODE:
             state.clear()
             self._init_state(state, grad, block_size)
         self._check_state(p, state, block_size)

@@ -185,3 +185,26 @@ def test_nd_per_matrix_checkpoint_loads_into_came8bitfull(shape, B):
     tainted = opt.state[p]["exp_avg_q"].cpu() != ref_state["exp_avg_q"]
     P.check_untainted_params(p.data, r, tainted, where, (r.double() - before).abs())
     assert opt.state[p]["step"] == 6
+
+
+@pytest.mark.parametrize("shape,B", [((4, 16, 256), 256), ((3, 40, 24), 64)])
+def test_nd_per_matrix_checkpoint_without_conversion_resets(shape, B):
+    """convert_layouts=False with the reference CUDA N-D path's per-matrix state (_mode "full8bit" plus
+    _cuda_factored_nd_ext_path): the next step starts the state over, as the reference does for a
+    layout it does not step (CAME8bit.py:757-759), rather than reading the per-matrix scales as flat
+    ones.  (4, 16, 256) at block 256 is a shape whose per-matrix codes have the flat layout's element
+    count, so only the layout check tells the two apart."""
+    sd = _nd_checkpoint(shape, B, seed=6)
+    p = torch.nn.Parameter(P.make_params([shape], torch.float32, seed=7)[0].cuda())
+    q = torch.nn.Parameter(p.detach().clone())
+    opt = came_amd.CAME8bitFull([p], lr=1e-3, weight_decay=1e-2, block_size=B)
+    opt.load_state_dict(sd, convert_layouts=False)
+    assert SL.layout_of(opt.state[p]) == "full8bit-nd"
+    fresh = came_amd.CAME8bitFull([q], lr=1e-3, weight_decay=1e-2, block_size=B)
+    g = _grads([shape], torch.float32, 61)
+    _run(opt, [p], g)
+    _run(fresh, [q], g)
+    assert opt.state[p]["step"] == 1 and SL.layout_of(opt.state[p]) == "full8bit"
+    assert torch.equal(p.data, q.data)
+    for k in Q8_KEYS:
+        assert torch.equal(opt.state[p][k], fresh.state[q][k]), k
