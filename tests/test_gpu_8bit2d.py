@@ -29,9 +29,13 @@ PERSIST = ("exp_avg_q", "exp_avg_absmax") + tuple(
     f"exp_avg_{k}_{s}" for k in ("sq_row", "sq_col", "res_row", "res_col") for s in ("q", "absmax"))
 CAPTURED = {"exp_avg_q": "exp_avg", "exp_avg_sq_row_q": "sq_row", "exp_avg_sq_col_q": "sq_col",
             "exp_avg_res_row_q": "res_row", "exp_avg_res_col_q": "res_col"}
-TIE_TOL = 1e-3
+# A differing code must sit within TIE_TOL code units of a rounding tie of the oracle's value: the
+# reference's float sums (atomics of unfixed order on the GPU) and the oracle's differ by a few ulps,
+# which moves a scaled value by ~1e-4 at most (the most seen here: 1.07e-4); codes off an exact tie
+# (EXACT_TIE) may be at most CODE_FRAC of a state (the most seen: 1.0%).
+TIE_TOL = 2e-4
 EXACT_TIE = 1e-4
-CODE_FRAC = 2e-2
+CODE_FRAC = 1.5e-2
 SHAPES = [(64, 2048), (1000, 3), (3, 5000), (33, 5461), (130, 1024), (17, 17), (1, 1), (16, 16), (257, 129),
           (4097, 129), (48, 4100), (37, 400), (5, 48), (40, 3072)]
 
