@@ -114,7 +114,7 @@ struct Plan {
   WorkList nscan;                        // prefix of the estimates (one item per tensor)
   std::map<int, WorkList> nseg2d;        // segment records of matrices, runs of kNormRunSegs, by grad type
   std::map<int, WorkList> nseg;          // the other segments' records, by 3 * grad type + chunk form
-  WorkList ncscan;                       // each chain's prefix of its segment sums (8 items per tensor)
+  WorkList nbsum;                        // the chains' sums per block of segments (one item per block)
   std::map<int, WorkList> nfix;          // records rebuilt under the chains' own estimates, by 3 * grad type + form
   std::map<int, WorkList> nwalk;         // chain walks (8 items per tensor), by grad type
   std::map<int, WorkList> nfinal;        // accumulators + tail + clip (one item per tensor), by grad type
@@ -427,7 +427,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     };
     struct Offs {
       size_t Rn, rfac, RRn, rrfac, Cn, cfac, CRn, crfac, pU, pW, pR, rm, rmr, clipp, clip, t2r, t2c, nest, nrec, nsum,
-          nch;
+          nbsum, nch;
     } o{};
     d.idx32 = d.N < (int64_t(1) << 31) ? 1 : 0;
     d.rowal = (d.C % B) == 0 ? 1 : 0;
@@ -494,6 +494,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       o.nest = take(size_t(d.nunit + 1) * 4);
       o.nrec = take(size_t(d.nseg) * 3 * 8 * 4);
       o.nsum = take(size_t(d.nseg) * 8 * 4);
+      d.nblk = ceil_div(d.nseg, int64_t(kNormFixSegs));
+      o.nbsum = take(size_t(d.nblk) * 8 * 4);
       o.nch = take(8 * 4);
     }
     scr_off[i] = scr;
@@ -519,6 +521,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       d.nest = at(o.nest);
       d.nrec = reinterpret_cast<uint32_t*>(scr + o.nrec);
       d.nsum = at(o.nsum);
+      d.nbsum = at(o.nbsum);
       d.nchain = at(o.nch);
     }
     scr += off;
@@ -588,7 +591,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       const int form = vec && d.c8 ? kNormVec : (vec && d.C >= 8 ? kNormRows : kNormAny);
       if (d.nseg0 > 0) add_item(plan.nseg2d[t.grad_dtype], i, ceil_div(d.nseg0, int64_t(kNormRunSegs)));
       if (d.nseg > d.nseg0) add_item(plan.nseg[t.grad_dtype * 3 + form], i, ceil_div(d.nseg - d.nseg0, int64_t(4)));
-      add_item(plan.ncscan, i, 8);
+      add_item(plan.nbsum, i, d.nblk);
       add_item(plan.nfix[t.grad_dtype * 3 + form], i, ceil_div(d.nseg, int64_t(kNormFixSegs)));
     }
     add_item(plan.nwalk[t.grad_dtype], i, 8);
@@ -623,7 +626,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
   place(plan.nscan);
   for (auto& kv : plan.nseg2d) place(kv.second);
   for (auto& kv : plan.nseg) place(kv.second);
-  place(plan.ncscan);
+  place(plan.nbsum);
   for (auto& kv : plan.nfix) place(kv.second);
   for (auto& kv : plan.nwalk) place(kv.second);
   for (auto& kv : plan.nfinal) place(kv.second);
@@ -661,6 +664,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
         rebase(d.nest);
         rebase(d.nrec);
         rebase(d.nsum);
+        rebase(d.nbsum);
         rebase(d.nchain);
       }
     }
@@ -690,7 +694,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     put(plan.nscan);
     for (auto& kv : plan.nseg2d) put(kv.second);
     for (auto& kv : plan.nseg) put(kv.second);
-    put(plan.ncscan);
+    put(plan.nbsum);
     for (auto& kv : plan.nfix) put(kv.second);
     for (auto& kv : plan.nwalk) put(kv.second);
     for (auto& kv : plan.nfinal) put(kv.second);
@@ -1211,12 +1215,12 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("norm_seg")) != CAME8_OK) return rc;
     }
-    if (!plan.ncscan.tids.empty()) {
-      const WorkList& wl = plan.ncscan;
+    if (!plan.nbsum.tids.empty()) {
+      const WorkList& wl = plan.nbsum;
       PhaseTimer pt(PH_NORM_SCAN, 0.0, stream);
-      hipLaunchKernelGGL(k_norm_cscan<>, dim3(grid_for(wl.total())), dim3(kNormScanThreads), 0, stream, dT, tids(wl), wst(wl),
+      hipLaunchKernelGGL(k_norm_bsum<>, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl),
                          int(wl.tids.size()));
-      if ((rc = check_launch("norm_cscan")) != CAME8_OK) return rc;
+      if ((rc = check_launch("norm_bsum")) != CAME8_OK) return rc;
     }
     for (auto& kv : plan.nfix) {
       const WorkList& wl = kv.second;

@@ -71,8 +71,9 @@ struct DevTensor {
   int64_t ngrp;       //   or groups of ngrp single-band matrices / tiles (ngrp > 1 bounds nunit)
   float* nest;        // estimated sum of u^2 per unit, then its exclusive prefix [nunit + 1]
   uint32_t* nrec;     // per chain and segment: binade/flags, two integer sums [3][8][nseg]
-  float* nsum;        // per chain and segment: fp32 sum of the rounded squares, then its
-                      // exclusive prefix per chain (the chain's estimated value) [8][nseg]
+  float* nsum;        // per chain and segment: fp32 sum of the rounded squares      [8][nseg]
+  float* nbsum;       // their sums per block of 256 segments                        [8][nblk]
+  int64_t nblk;
   float* nchain;      // the eight chain accumulators                           [8]
   uint64_t mC, mR;    // magic multipliers for n / C and n / R (n < 2^31)
   uint32_t sC, sR;    // and their shifts

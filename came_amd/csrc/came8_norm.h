@@ -29,7 +29,7 @@
 //                            binade edge), the integer sums of the increments under each, whether
 //                            the segment holds special elements, and whether it holds a NaN; and
 //                            the chain's fp32 sum of the segment's rounded squares.
-//   k_norm_cscan, k_norm_fix each chain's own estimate (the prefix of its segment sums), and records
+//   k_norm_bsum, k_norm_fix  each chain's own estimate (the prefix of its segment sums), and records
 //                            rebuilt under that estimate's binades where the tensor-wide estimate
 //                            (an eighth of the prefix) named others.  The chains of heavy-tailed
 //                            updates drift far apart; without the rebuild most of their segments
@@ -633,25 +633,83 @@ __global__ __launch_bounds__(kThreads, 4) void k_norm_seg(const DevTensor* __res
 // ---------------------------------------------------------------------------
 // each chain's own estimate, and records rebuilt under it
 // ---------------------------------------------------------------------------
-// In place: each chain's segment sums become their exclusive prefix, the chain's estimated value at
-// each segment's start.  One work item per tensor and chain, kNormScanThreads threads each (fewer
-// dependent loads per thread for the longest chains).
-constexpr int kNormScanThreads = 1024;
+constexpr int kNormFixSegs = kThreads;  // segments per block of the chains' estimates and per work item of k_norm_fix
+
+// Each chain's sum of squares over a block of kNormFixSegs segments (nbsum[c][block]), for the prefix
+// k_norm_fix forms.  One work item per block; thread i takes segment i of the block.
 template <int = 0>
-__global__ __launch_bounds__(kNormScanThreads) void k_norm_cscan(const DevTensor* __restrict__ T,
-                                                                 const int32_t* __restrict__ tids,
-                                                                 const int64_t* __restrict__ wstart, int ntens) {
-  __shared__ float part[kNormScanThreads / kWave];
+__global__ __launch_bounds__(kThreads) void k_norm_bsum(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                        const int64_t* __restrict__ wstart, int ntens) {
+  __shared__ float part[kThreads / kWave][8];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
     const int slot = find_slot(wstart, ntens, w);
     const DevTensor& t = T[tids[slot]];
-    const int c = int(w - wstart[slot]);
-    block_excl_scan<kNormScanThreads>(t.nsum + c * t.nseg, t.nseg, part);
+    const int64_t nseg = t.nseg;
+    const int64_t blk = w - wstart[slot];
+    const int64_t seg = blk * kNormFixSegs + tid;
+    float v[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) v[c] = seg < nseg ? t.nsum[c * nseg + seg] : 0.0f;
+    norm_lane_sums<8>(v, lane);  // lane 8c: chain c over the wavefront
+    if ((lane & 7) == 0) part[wid][lane >> 3] = v[0];
+    __syncthreads();
+    if (tid < 8) t.nbsum[tid * t.nblk + blk] = (part[0][tid] + part[1][tid]) + (part[2][tid] + part[3][tid]);
+    __syncthreads();
   }
 }
 
-constexpr int kNormFixSegs = kThreads;  // segments per work item of k_norm_fix (one per thread)
+// The chains' estimates at the segments of one work item of k_norm_fix, into est[c][thread]: the sums of
+// the blocks before it (k_norm_bsum) plus an exclusive scan of the item's own segment sums.
+__device__ __forceinline__ void norm_item_estimates(const DevTensor& t, int64_t blk, float (&est)[8][kNormFixSegs],
+                                                    float (&part)[kThreads / kWave][8], float (&base)[8]) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t nseg = t.nseg;
+  // the blocks before this one: thread i adds chain i % 8's blocks i / 8, i / 8 + 32, ...
+  {
+    float acc = 0.0f;
+    const int c = tid & 7;
+    for (int64_t b = tid >> 3; b < blk; b += kThreads / 8) acc += t.nbsum[c * t.nblk + b];
+    est[c][tid >> 3] = acc;  // scratch: 32 partials per chain
+  }
+  __syncthreads();
+  if (tid < 8) {
+    float acc = 0.0f;
+    for (int k = 0; k < kThreads / 8; ++k) acc += est[tid][k];
+    base[tid] = acc;
+  }
+  __syncthreads();
+  // this item's segments: an exclusive scan over the threads, per chain
+  const int64_t seg = blk * kNormFixSegs + tid;
+  float v[8], incl[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    v[c] = seg < nseg ? t.nsum[c * nseg + seg] : 0.0f;
+    incl[c] = v[c];
+  }
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const float y = __shfl_up(incl[c], o, kWave);
+      incl[c] += lane >= o ? y : 0.0f;
+    }
+  }
+  if (lane == kWave - 1) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) part[wid][c] = incl[c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    float off = base[c];
+    for (int k = 0; k < kThreads / kWave; ++k) off += k < wid ? part[k][c] : 0.0f;
+    est[c][tid] = off + (incl[c] - v[c]);
+  }
+  __syncthreads();
+}
+
 
 // Writes the records of the chains in mask from a rebuild under a binade pair per chain (Ea[c], Ea[c] + 1).
 __device__ __forceinline__ void norm_write_records_pc(const DevTensor& t, int64_t seg, const int (&Ea)[8],
@@ -680,31 +738,35 @@ __device__ __forceinline__ void norm_write_records_pc(const DevTensor& t, int64_
 }
 
 // Records rebuilt under each chain's own estimate.  A work item is kNormFixSegs consecutive segments
-// of one tensor, one per thread: each thread checks its segment's eight records against the chains'
-// estimates (k_norm_cscan, taken as within [-2%, +0.5%] of the chain), and the segments where a
-// record's binades do not cover a chain's are listed in LDS and shared out to the wavefronts, which
-// rebuild them a segment at a time under each chain's own candidates Ea and Ea + 1 (both sums always).
-// FORM as for k_norm_seg.
+// of one tensor, one per thread: the chains' estimates at each segment (norm_item_estimates, taken as
+// within [-2%, +0.5%] of the chain) are checked against the segment's eight records, and the segments
+// where a record's binades do not cover a chain's are listed in LDS and shared out to the wavefronts,
+// which rebuild them a segment at a time under each chain's own candidates Ea and Ea + 1 (both sums
+// always).  FORM as for k_norm_seg.
 template <typename TG, int FORM>
 __global__ __launch_bounds__(kThreads) void k_norm_fix(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                        const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   __shared__ uint32_t list[kNormFixSegs];  // (thread << 8) | mask of the chains to rebuild
   __shared__ int nlist;
+  __shared__ float est_l[8][kNormFixSegs];
+  __shared__ float part[kThreads / kWave][8];
+  __shared__ float base_l[8];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
     const int slot = find_slot(wstart, ntens, w);
     const DevTensor& t = T[tids[slot]];
     const int64_t nseg = t.nseg;
-    const int64_t base = (w - wstart[slot]) * kNormFixSegs;
+    const int64_t blk = w - wstart[slot];
+    const int64_t base = blk * kNormFixSegs;
     const int64_t seg = base + tid;
     if (tid == 0) nlist = 0;
-    __syncthreads();
+    norm_item_estimates(t, blk, est_l, part, base_l);  // synchronises the workgroup
     uint32_t need = 0;
     if (seg < nseg) {
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        const float est = t.nsum[c * nseg + seg];
+        const float est = est_l[c][tid];
         const uint32_t w0 = t.nrec[c * nseg + seg];
         const int Ea = int(w0 & 511u) - 256;
         const bool two = (w0 & kRecTwo) != 0;
@@ -724,7 +786,7 @@ __global__ __launch_bounds__(kThreads) void k_norm_fix(const DevTensor* __restri
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
         bool two;
-        norm_candidates(uniform_f32(t.nsum[c * nseg + sf]), Ea[c], two);
+        norm_candidates(est_l[c][e >> 8], Ea[c], two);
         ka[c] = 23 - Ea[c];
       }
       NormAcc a;
