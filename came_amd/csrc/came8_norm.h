@@ -814,6 +814,29 @@ __global__ __launch_bounds__(kThreads) void k_norm_fix(const DevTensor* __restri
 constexpr uint32_t kNormSat = 1u << 25;  // saturating integer sums: anything >= 2^24 leaves the binade
 __device__ __forceinline__ uint32_t sat_add(uint32_t a, uint32_t b) { return min(a + b, kNormSat); }
 
+// Cross-lane steps of the walk, all 64 lanes active.  DPP: row_shr:n (0x110 + n; lanes shifted in from
+// before their row's start read 0), row_bcast:15 (0x142) and row_bcast:31 (0x143) with row masks
+// (rows outside them add 0), wave_shr:1 (0x138).
+template <int CTRL, int ROWS, bool BOUND>
+__device__ __forceinline__ uint32_t norm_dpp(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, ROWS, 0xf, BOUND));
+}
+// inclusive scan of saturating sums over the wavefront, in lane order
+__device__ __forceinline__ uint32_t norm_wave_scan(uint32_t v) {
+  v = sat_add(v, norm_dpp<0x111, 0xf, true>(v));
+  v = sat_add(v, norm_dpp<0x112, 0xf, true>(v));
+  v = sat_add(v, norm_dpp<0x114, 0xf, true>(v));
+  v = sat_add(v, norm_dpp<0x118, 0xf, true>(v));  // each row of 16 scanned
+  v = sat_add(v, norm_dpp<0x142, 0xa, false>(v));  // rows 1 and 3 add the totals of rows 0 and 2
+  v = sat_add(v, norm_dpp<0x143, 0xc, false>(v));  // rows 2 and 3 add the total of rows 0 and 1
+  return v;
+}
+// the inclusive value of the previous lane (0 for lane 0)
+__device__ __forceinline__ uint32_t norm_wave_prev(uint32_t incl) { return norm_dpp<0x138, 0xf, true>(incl); }
+// lane `src`'s value (src uniform)
+__device__ __forceinline__ uint32_t norm_lane(uint32_t v, int src) { return uint32_t(__builtin_amdgcn_readlane(int(v), src)); }
+__device__ __forceinline__ float norm_lane(float v, int src) { return __uint_as_float(norm_lane(__float_as_uint(v), src)); }
+
 // Replays chain c over segment seg from s, equal to the reference's serial fmaf loop bit for bit (one
 // wavefront).  Lane l holds the chain's elements 8l .. 8l + 7 of the segment.  A round takes every
 // remaining element's increment under s's binade, a saturating prefix sum of them in element order,
@@ -836,6 +859,16 @@ __device__ float norm_replay(const DevTensor& t, int c, int64_t seg, float s, co
 #pragma unroll
   for (int j = 0; j < 8; ++j) h[j] = x[j] * x[j];
   int pos = 0;  // the elements before pos are applied
+  if (s == 0.0f) {  // a chain's start crosses a binade every few elements: the first 64 one by one
+#pragma unroll
+    for (int k = 0; k < 64; ++k) {
+      if (k < cnt) {  // uniform
+        const float xk = norm_lane(x[k & 7], k >> 3);
+        s = fmaf(xk, xk, s);
+      }
+    }
+    pos = min(cnt, 64);
+  }
   while (pos < cnt) {  // uniform
     if (!(s <= 0x1.fffffep127f)) {
       if (s != s) break;
@@ -848,11 +881,11 @@ __device__ float norm_replay(const DevTensor& t, int c, int64_t seg, float s, co
       const uint64_t bal = __ballot(nanm != 0);
       if (bal != 0) {
         const int fl = __builtin_ctzll(bal);
-        const int jj = __shfl(__builtin_ctz(nanm | 0x100u), fl, kWave);
+        const int jj = int(norm_lane(uint32_t(__builtin_ctz(nanm | 0x100u)), fl));
         float xe = x[0];
 #pragma unroll
         for (int j = 1; j < 8; ++j) xe = jj == j ? x[j] : xe;
-        xe = __shfl(xe, fl, kWave);
+        xe = norm_lane(xe, fl);
         s = fmaf(xe, xe, s);
       }
       break;
@@ -874,14 +907,8 @@ __device__ float norm_replay(const DevTensor& t, int c, int64_t seg, float s, co
       incl[j] = run;
       spm |= (live && special) ? (1u << j) : 0u;
     }
-    uint32_t winc = run;  // inclusive scan of the lanes' runs
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      const uint32_t y = __shfl_up(winc, o, kWave);
-      if (lane >= o) winc = sat_add(winc, y);
-    }
-    const uint32_t up1 = __shfl_up(winc, 1, kWave);  // every lane takes part in the shuffle
-    const uint32_t excl = lane == 0 ? 0u : up1;
+    const uint32_t winc = norm_wave_scan(run);  // inclusive scan of the lanes' runs
+    const uint32_t excl = norm_wave_prev(winc);
     uint32_t evm = spm;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -890,7 +917,7 @@ __device__ float norm_replay(const DevTensor& t, int c, int64_t seg, float s, co
     }
     const uint64_t bal = __ballot(evm != 0);
     if (bal == 0) {
-      s = norm_value(m + __shfl(winc, kWave - 1, kWave), E);  // below room
+      s = norm_value(m + norm_lane(winc, kWave - 1), E);  // below room
       break;
     }
     const int fl = __builtin_ctzll(bal);
@@ -902,9 +929,9 @@ __device__ float norm_replay(const DevTensor& t, int c, int64_t seg, float s, co
       before = j0 == j ? excl + incl[j - 1] : before;
       xe = j0 == j ? x[j] : xe;
     }
-    const int jj = __shfl(j0, fl, kWave);
-    before = __shfl(before, fl, kWave);
-    xe = __shfl(xe, fl, kWave);
+    const int jj = int(norm_lane(uint32_t(j0), fl));
+    before = norm_lane(before, fl);
+    xe = norm_lane(xe, fl);
     s = fmaf(xe, xe, norm_value(m + before, E));
     pos = fl * 8 + jj + 1;
   }
@@ -946,15 +973,29 @@ __global__ __launch_bounds__(kNormWalkThreads) void k_norm_walk(const DevTensor*
     float s = 0.0f;
     int64_t seg = 0;
     while (seg < nseg && s == s) {  // a NaN chain stays NaN
-      const int64_t base = seg + int64_t(lane) * kNormWalkSegs;
-      const int64_t bend = min(nseg, seg + int64_t(kWave) * kNormWalkSegs);
+      // the batch starts at a multiple of kNormWalkSegs; its segments before seg count for nothing
+      const int64_t bstart = seg & ~int64_t(kNormWalkSegs - 1);
+      const int64_t base = bstart + int64_t(lane) * kNormWalkSegs;
+      const int64_t bend = min(nseg, bstart + int64_t(kWave) * kNormWalkSegs);
       uint32_t r0[kNormWalkSegs], ra[kNormWalkSegs], rb[kNormWalkSegs];
+      if (base + kNormWalkSegs <= nseg) {  // 16 consecutive records of each array: 4-dword loads
 #pragma unroll
-      for (int j = 0; j < kNormWalkSegs; ++j) {
-        const int64_t k = min(base + j, nseg - 1);
-        r0[j] = W0[k];
-        ra[j] = WA[k];
-        rb[j] = WB[k];
+        for (int q = 0; q < kNormWalkSegs / 4; ++q) {
+          const u32x4u a0 = *reinterpret_cast<const CAME8_GLOBAL u32x4u*>(W0 + base + 4 * q);
+          const u32x4u aa = *reinterpret_cast<const CAME8_GLOBAL u32x4u*>(WA + base + 4 * q);
+          const u32x4u ab = *reinterpret_cast<const CAME8_GLOBAL u32x4u*>(WB + base + 4 * q);
+          r0[4 * q] = a0.x; r0[4 * q + 1] = a0.y; r0[4 * q + 2] = a0.z; r0[4 * q + 3] = a0.w;
+          ra[4 * q] = aa.x; ra[4 * q + 1] = aa.y; ra[4 * q + 2] = aa.z; ra[4 * q + 3] = aa.w;
+          rb[4 * q] = ab.x; rb[4 * q + 1] = ab.y; rb[4 * q + 2] = ab.z; rb[4 * q + 3] = ab.w;
+        }
+      } else {  // the array's end: clamped loads (the records past it count for nothing)
+#pragma unroll
+        for (int j = 0; j < kNormWalkSegs; ++j) {
+          const int64_t k = min(base + j, nseg - 1);
+          r0[j] = W0[k];
+          ra[j] = WA[k];
+          rb[j] = WB[k];
+        }
       }
       while (seg < bend && s == s) {  // the segments [seg, bend) of this batch
         const bool inf = !(s <= 0x1.fffffep127f);
@@ -973,15 +1014,9 @@ __global__ __launch_bounds__(kNormWalkThreads) void k_norm_walk(const DevTensor*
           }
         }
         // inclusive scan of the runs over the lanes (saturating sums, in lane order)
-        uint32_t incl = run;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-          const uint32_t y = __shfl_up(incl, o, kWave);
-          if (lane >= o) incl = sat_add(incl, y);
-        }
-        const uint32_t prev = __shfl_up(incl, 1, kWave);
-        const uint32_t excl = lane == 0 ? 0u : prev;  // exact while the chain has not left its binade
-        const uint32_t tot = __shfl(incl, kWave - 1, kWave);
+        const uint32_t incl = norm_wave_scan(run);
+        const uint32_t excl = norm_wave_prev(incl);  // exact while the chain has not left its binade
+        const uint32_t tot = norm_lane(incl, kWave - 1);
         // the first lane whose run is cut short or takes the chain out of its binade
         const uint64_t bal = __ballot(stop || sat_add(excl, run) >= room);
         if (bal == 0) {
@@ -999,8 +1034,8 @@ __global__ __launch_bounds__(kNormWalkThreads) void k_norm_walk(const DevTensor*
             k = base + j + 1;
           }
         }
-        const uint32_t mm = m + __shfl(acc, first, kWave);
-        const int64_t ks = __shfl(k, first, kWave);
+        const uint32_t mm = m + norm_lane(acc, first);
+        const int64_t ks = int64_t(norm_lane(uint32_t(k), first)) | (int64_t(norm_lane(uint32_t(uint64_t(k) >> 32), first)) << 32);
         s = norm_replay<TG>(t, c, ks, inf ? s : norm_value(mm, E), hp);
         seg = ks + 1;
       }
