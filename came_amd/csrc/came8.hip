@@ -485,7 +485,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     if (!s2d) {
       d.nseg = ceil_div(d.N - (d.N & 7), kNormSegElems);
       const bool lds = t.factored && d.c8 && d.idx32 && reinterpret_cast<uintptr_t>(t.grad) % 16 == 0 && d.P == 1 &&
-                       !tiny_matrix(t, false) && d.C <= kNormLdsCols;
+                       !tiny_matrix(t, false) && d.C >= 8 * kNormSegLanes && d.C <= kNormLdsCols;
       d.nseg0 = lds ? (d.N - (d.N & 7)) / kNormSegElems : 0;
       const int64_t nbase = t.factored ? d.P * d.nbands : d.nclip;
       // the thread-per-unit estimate groups single-band matrices and tiles into at most kNormMaxUnits units

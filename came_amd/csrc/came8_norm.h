@@ -264,7 +264,7 @@ __device__ __forceinline__ float norm_est_at(const DevTensor& t, int64_t f) {
 // ---------------------------------------------------------------------------
 // segment records
 // ---------------------------------------------------------------------------
-// One halving step of norm_lane_sums: lanes with bit O set keep values [H, 2H) and send [0, H) to their
+// One halving step of norm_group_sums: lanes with bit O set keep values [H, 2H) and send [0, H) to their
 // partner lane ^ O, which keeps [0, H); each adds what it receives (H, O compile-time constants).
 template <int H, int O, typename T, int L>
 __device__ __forceinline__ void norm_halve(T (&v)[L], int lane) {
@@ -277,26 +277,33 @@ __device__ __forceinline__ void norm_halve(T (&v)[L], int lane) {
   }
 }
 
-// Per-chain sums over the 64 lanes of NV values per lane (NV = 8 or 16).  Halving steps with the
-// partners lane ^ 32, ^ 16, ... leave each lane one value, value index (lane >> (6 - log2 NV)), summed
-// over the lanes that share those bits; butterfly sums over the remaining low lane bits complete it.
-// On return v[0] of lane l holds the total of value l >> 3 (NV = 8) or l >> 2 (NV = 16).
+// Per-value sums over groups of G lanes (G a power of two up to 64) of NV values per lane (NV = 8 or
+// 16).  Halving steps with the partners lane ^ G/2, ^ G/4, ... leave each lane NV / G values (NV > G)
+// or one, summed over the lanes that share the lane bits halved so far; butterfly sums over the
+// remaining low lane bits complete it (NV < G).  On return, lane i of a group (i = lane % G) holds
+// the totals of values i * NV / G + k in v[k], k < NV / G (NV >= G), or of value i / (G / NV) in v[0]
+// (NV < G).
+template <int O, int H, typename T, int L>
+__device__ __forceinline__ void norm_group_steps(T (&v)[L], int lane) {
+  if constexpr (O >= 1) {
+    if constexpr (H >= 1) {
+      norm_halve<H, O>(v, lane);
+    } else {
+      v[0] += __shfl_xor(v[0], O, kWave);
+    }
+    norm_group_steps<O / 2, H / 2>(v, lane);
+  }
+}
+template <int G, int NV, typename T, int L>
+__device__ __forceinline__ void norm_group_sums(T (&v)[L], int lane) {
+  static_assert(L >= NV && G >= 2 && G <= kWave && (G & (G - 1)) == 0, "bad group");
+  norm_group_steps<G / 2, NV / 2>(v, lane);
+}
+// The same over the whole wavefront: v[0] of lane l holds the total of value l >> 3 (NV = 8) or l >> 2
+// (NV = 16).
 template <int NV, typename T, int L>
 __device__ __forceinline__ void norm_lane_sums(T (&v)[L], int lane) {
-  static_assert(L >= NV, "too few values");
-  if constexpr (NV == 16) {
-    norm_halve<8, 32>(v, lane);
-    norm_halve<4, 16>(v, lane);
-    norm_halve<2, 8>(v, lane);
-    norm_halve<1, 4>(v, lane);
-  } else {
-    norm_halve<4, 32>(v, lane);
-    norm_halve<2, 16>(v, lane);
-    norm_halve<1, 8>(v, lane);
-    v[0] += __shfl_xor(v[0], 4, kWave);
-  }
-  v[0] += __shfl_xor(v[0], 2, kWave);
-  v[0] += __shfl_xor(v[0], 1, kWave);
+  norm_group_sums<kWave, NV>(v, lane);
 }
 
 // u at flat index e (u_at), with 32-bit index arithmetic where the flat indices fit.
@@ -376,6 +383,17 @@ struct NormAcc {
     norm_acc(hi, ka, sa[v], ra[v]);
     if constexpr (TWO) norm_acc(hi, ka - 1, sb[v], rb[v]);
     if constexpr (TINY) ra[v] = fabsf(x) == 0x1p-75f ? 0.5f : ra[v];
+  }
+  // An empty asm that reads and writes the sums: in a fully unrolled segment the code generator would
+  // otherwise defer the roundings to the segment's end (their results are read only there) and hold
+  // every square until then.
+  template <bool TWO>
+  __device__ __forceinline__ void pin() {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      asm volatile("" : "+v"(sa[v]), "+v"(ra[v]), "+v"(hs[v]));
+      if constexpr (TWO) asm volatile("" : "+v"(sb[v]), "+v"(rb[v]));
+    }
   }
   // both binades, with the TINY rule when tiny (the rebuild of k_norm_fix, a binade per chain)
   __device__ __forceinline__ void add_both(int v, float x, int ka, bool tiny) {
@@ -506,54 +524,166 @@ __device__ __forceinline__ void norm_candidates(float est, int& Ea, bool& two) {
 
 constexpr int kNormRunSegs = 64;       // segments per work item of k_norm_seg2d
 constexpr int kNormLdsCols = 16384;    // widest rows k_norm_seg2d stages in LDS (64 KB of column factors)
+constexpr int kNormSegLanes = 16;      // lanes per segment in k_norm_seg2d (narrowest rows: 8 * this)
+constexpr int kNormSegAhead = 8;       // chunks per lane in flight there
 
-// The per-lane, per-chain sums of one whole segment of a matrix (prefix 1) whose column factors are
-// staged in LDS (cl), rows of whole 8-element chunks, 16-byte aligned, 32-bit flat indices.  Every
-// gradient chunk and row factor of the segment is loaded first; the column factors come from LDS
-// as each chunk is accounted.
-template <typename TG, bool TWO, bool TINY>
-__device__ __forceinline__ void norm_seg_lds(const DevTensor& t, const float* cl, int64_t f0, int ka, int lane,
+// The per-lane, per-chain sums of one whole segment per group of G lanes (lane i = lane % G of the
+// group takes the 8-element chunks at f0 + 8 * G * q + 8 * i) of a matrix (prefix 1) whose column
+// factors are staged in LDS (cl), rows of whole 8-element chunks at least 8 * G wide, 16-byte aligned,
+// 32-bit flat indices.  A chunk's row and column follow from the previous chunk's by one wrap, as the
+// rows are at least 8 * G wide.  The schedule is fixed by hand, a step per chunk: the column factors
+// of the next chunk are read from LDS, this chunk is accounted, and the gradient and row factor of
+// the chunk kNormSegAhead on are loaded into the registers this one frees.  Scheduling barriers keep
+// the compiler from hoisting the loads further, and NormAcc::pin keeps each chunk's roundings in its
+// step (either would cost registers, not time).
+template <typename TG, int G, bool TWO, bool TINY>
+__device__ __forceinline__ void norm_seg_lds(const DevTensor& t, const float* cl, uint32_t f0, int ka, int li,
                                              NormAcc& a) {
   using GS = typename TG::storage;
-  constexpr int Q = kNormChunks;
+  constexpr int Q = kNormSegElems / (8 * G), D = kNormSegAhead, NW = int(sizeof(GS)) * 2;
+  static_assert(Q >= D, "segment chunks");
   const CAME8_GLOBAL GS* __restrict__ g = gbl(static_cast<const GS*>(t.g));
-  uint32_t gw[Q][sizeof(GS) * 2];  // 16 or 32 bytes of gradient per chunk
-  float r[Q];
-  uint32_t col[Q];
-#pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    const uint32_t f = uint32_t(f0) + uint32_t(q * 512 + lane * 8);
-    const uint32_t row = udiv_magic(f, t.mC, t.sC);
-    col[q] = f - row * uint32_t(t.C);
-    r[q] = gbl(t.rfac)[row];
+  const CAME8_GLOBAL float* __restrict__ rf = gbl(t.rfac);
+  const uint32_t C = uint32_t(t.C);
+  uint32_t f = f0 + uint32_t(li * 8);
+  uint32_t row = udiv_magic(f, t.mC, t.sC);
+  uint32_t col = f - row * C;
+  uint32_t gw[D][NW];  // 16 or 32 bytes of gradient per chunk
+  float r[D];
+  uint32_t cc[D];
+  auto issue = [&](int s) __attribute__((always_inline)) {
+    cc[s] = col;
+    r[s] = rf[row];
     if constexpr (sizeof(GS) == 2) {
       const u32x4 v = *(const CAME8_GLOBAL u32x4*)(g + f);
-      gw[q][0] = v.x; gw[q][1] = v.y; gw[q][2] = v.z; gw[q][3] = v.w;
+      gw[s][0] = v.x; gw[s][1] = v.y; gw[s][2] = v.z; gw[s][3] = v.w;
     } else {
       const u32x4 b0 = *(const CAME8_GLOBAL u32x4*)(g + f);
       const u32x4 b1 = *(const CAME8_GLOBAL u32x4*)(g + f + 4);
-      gw[q][0] = b0.x; gw[q][1] = b0.y; gw[q][2] = b0.z; gw[q][3] = b0.w;
-      gw[q][4] = b1.x; gw[q][5] = b1.y; gw[q][6] = b1.z; gw[q][7] = b1.w;
+      gw[s][0] = b0.x; gw[s][1] = b0.y; gw[s][2] = b0.z; gw[s][3] = b0.w;
+      gw[s][4] = b1.x; gw[s][5] = b1.y; gw[s][6] = b1.z; gw[s][7] = b1.w;
     }
-  }
+    f += 8 * G;
+    col += 8 * G;
+    const bool wrap = col >= C;
+    col = wrap ? col - C : col;
+    row += wrap ? 1u : 0u;
+  };
+#pragma unroll
+  for (int q = 0; q < D; ++q) issue(q);
+  f32x4 c0 = *reinterpret_cast<const f32x4*>(cl + cc[0]);
+  f32x4 c1 = *reinterpret_cast<const f32x4*>(cl + cc[0] + 4);
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
-    const f32x4 c0 = *reinterpret_cast<const f32x4*>(cl + col[q]);
-    const f32x4 c1 = *reinterpret_cast<const f32x4*>(cl + col[q] + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    const int s = q % D;
     const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    if (q + 1 < Q) {
+      c0 = *reinterpret_cast<const f32x4*>(cl + cc[(q + 1) % D]);
+      c1 = *reinterpret_cast<const f32x4*>(cl + cc[(q + 1) % D] + 4);
+    }
 #pragma unroll
-    for (int v = 0; v < 8; ++v) a.add<TWO, TINY>(v, (r[q] * cv[v]) * TG::elem(gw[q], v), ka);
+    for (int v = 0; v < 8; ++v) a.add<TWO, TINY>(v, (r[s] * cv[v]) * TG::elem(gw[s], v), ka);
+    a.template pin<TWO>();
+    if (q + D < Q) issue(s);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Writes the records of the segment of each active group of G lanes (li = lane % G) from the lanes'
+// per-chain sums, and the chains' sums of squares.  Ea: the group's binade; two: sums under Ea + 1
+// were formed (uniform over the wavefront).
+template <int G>
+__device__ __forceinline__ void norm_write_records_g(const DevTensor& t, int64_t seg, int Ea, bool two, bool act,
+                                                     int lane, const NormAcc& a) {
+  const int li = lane & (G - 1);
+  uint32_t acc[16];
+  float hs[8];
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    acc[v] = norm_lane_value(a.sa[v], a.ra[v], Ea);
+    acc[8 + v] = two ? norm_lane_value(a.sb[v], a.rb[v], Ea + 1) : 0u;
+    hs[v] = a.hs[v];
+  }
+  const int64_t nseg = t.nseg;
+  uint32_t* __restrict__ W0 = t.nrec;
+  uint32_t* __restrict__ WA = t.nrec + 8 * nseg;
+  uint32_t* __restrict__ WB = t.nrec + 16 * nseg;
+  // value index i / (G / NV) (NV < G) or i * NV / G + k (NV >= G) after norm_group_sums
+  norm_group_sums<G, 8>(hs, lane);
+  constexpr int H8 = G > 8 ? G / 8 : 1, K8 = G < 8 ? 8 / G : 1;
+#pragma unroll
+  for (int k = 0; k < K8; ++k) {
+    const int c = G >= 8 ? li / H8 : li * K8 + k;
+    if (act && li % H8 == 0) t.nsum[c * nseg + seg] = hs[k];
+  }
+  if (two) {
+    norm_group_sums<G, 16>(acc, lane);
+    constexpr int H16 = G > 16 ? G / 16 : 1, K16 = G < 16 ? 16 / G : 1;
+#pragma unroll
+    for (int k = 0; k < K16; ++k) {
+      const int i = G >= 16 ? li / H16 : li * K16 + k;  // i < 8: chain i under Ea; else chain i - 8 under Ea + 1
+      if (act && li % H16 == 0) {
+        const uint32_t sum = min(acc[k], kNormFull);
+        if (i < 8) {
+          W0[i * nseg + seg] = uint32_t(Ea + 256) | kRecTwo;
+          WA[i * nseg + seg] = sum;
+        } else {
+          WB[(i - 8) * nseg + seg] = sum;
+        }
+      }
+    }
+  } else {
+    norm_group_sums<G, 8>(acc, lane);
+#pragma unroll
+    for (int k = 0; k < K8; ++k) {
+      const int c = G >= 8 ? li / H8 : li * K8 + k;
+      if (act && li % H8 == 0) {
+        W0[c * nseg + seg] = uint32_t(Ea + 256);
+        WA[c * nseg + seg] = min(acc[k], kNormFull);
+        WB[c * nseg + seg] = kNormFull;
+      }
+    }
+  }
+}
+
+// The segments of one wavefront in a run of k_norm_seg2d: segments k0 + sub for k0 = wid * SPW,
+// wid * SPW + 4 * SPW, ... below nrun, sub = lane / G.  TWO and TINY hold for all of them.
+template <typename TG, int G, bool TWO, bool TINY>
+__device__ __forceinline__ void norm_seg2d_wave(const DevTensor& t, const float* cl, int64_t run0, int64_t nrun,
+                                                float e0, float e1, int wid, int lane) {
+  constexpr int SPW = kWave / G;
+  const int li = lane & (G - 1), sub = lane / G;
+#pragma unroll 1
+  for (int64_t k0 = int64_t(wid) * SPW; k0 < nrun; k0 += (kThreads / kWave) * SPW) {
+    // a group past the run's end takes its last segment again and writes nothing
+    const bool act = k0 + sub < nrun;
+    const int64_t k = act ? k0 + sub : nrun - 1;
+    const int64_t seg = run0 + k;
+    int Ea;
+    bool two;
+    norm_candidates(e0 + (e1 - e0) * (float(k) / float(nrun)), Ea, two);
+    NormAcc a;
+    a.clear();
+    wait_vm_all();  // the previous records' stores: the chunk loads' waits then count only loads
+    norm_seg_lds<TG, G, TWO, TINY>(t, cl, uint32_t(seg * kNormSegElems), 23 - Ea, li, a);
+    norm_write_records_g<G>(t, seg, Ea, TWO, act, lane, a);
   }
 }
 
 // Records of the whole segments [0, nseg0) of 2-D factored tensors whose rows hold whole 8-element
-// chunks (at most kNormLdsCols), 16-byte aligned, with 32-bit flat indices (the host checks); the last,
-// partial segment is k_norm_seg's.  A work item is a run of
-// kNormRunSegs segments: the workgroup stages the matrix's column factors in LDS once, and its four
-// wavefronts take every fourth segment of the run.
+// chunks (at least 8 * kNormSegLanes, at most kNormLdsCols), 16-byte aligned, with 32-bit flat indices
+// (the host checks); the last, partial segment is k_norm_seg's.  A work item is a run of kNormRunSegs
+// segments: the workgroup stages the matrix's column factors in LDS once, and each wavefront takes
+// kWave / kNormSegLanes consecutive segments at a time, a group of kNormSegLanes lanes per segment.
+// A wavefront forms the sums under Ea + 1 for all its segments of the run when one of them needs them
+// (a record with both sums is never wrong), and the subnormal rule when one of them is in that binade;
+// the choice is made once per run, so that no code is shared between the forms' segment loops (the
+// compiler would hoist a shared start, and the registers it holds, above the branch).
 template <typename TG>
 __global__ __launch_bounds__(kThreads) void k_norm_seg2d(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                          const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  constexpr int G = kNormSegLanes, SPW = kWave / G;  // lanes per segment, segments per wavefront
   extern __shared__ float cl[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t total = wstart[ntens];
@@ -575,21 +705,18 @@ __global__ __launch_bounds__(kThreads) void k_norm_seg2d(const DevTensor* __rest
     // the estimate at both ends of the run, linear in between (a chain holds about 1/8 of it)
     const float e0 = uniform_f32(norm_est_at(t, run0 * kNormSegElems)) * 0.125f;
     const float e1 = uniform_f32(norm_est_at(t, min((run0 + nrun) * kNormSegElems, main))) * 0.125f;
-#pragma unroll 1
-    for (int64_t k = wid; k < nrun; k += 4) {
-      const int64_t seg = run0 + k;
-      const int64_t f0 = seg * kNormSegElems;
+    bool any_two = false, any_tiny = false;
+    for (int64_t k0 = int64_t(wid) * SPW; k0 < nrun; k0 += (kThreads / kWave) * SPW) {
+      const int64_t k = min(k0 + lane / G, nrun - 1);
       int Ea;
       bool two;
       norm_candidates(e0 + (e1 - e0) * (float(k) / float(nrun)), Ea, two);
-      const int ka = 23 - Ea;
-      NormAcc a;
-      a.clear();
-      if (Ea == -126) norm_seg_lds<TG, true, true>(t, cl, f0, ka, lane, a);
-      else if (two) norm_seg_lds<TG, true, false>(t, cl, f0, ka, lane, a);
-      else norm_seg_lds<TG, false, false>(t, cl, f0, ka, lane, a);
-      norm_write_records(t, seg, Ea, two, lane, a);
+      any_two |= two;
+      any_tiny |= Ea == -126;
     }
+    if (__any(any_tiny)) norm_seg2d_wave<TG, G, true, true>(t, cl, run0, nrun, e0, e1, wid, lane);
+    else if (__any(any_two)) norm_seg2d_wave<TG, G, true, false>(t, cl, run0, nrun, e0, e1, wid, lane);
+    else norm_seg2d_wave<TG, G, false, false>(t, cl, run0, nrun, e0, e1, wid, lane);
   }
 }
 
