@@ -80,9 +80,11 @@ float round_to_f16(float f) { return float(_Float16(f)); }
 
 // Kernel-variant keys.
 struct BandKey {
-  int gdt, V, K, TPB, st = 0, ua = 0;  // st: fp32 states (pass 2 only); ua: rows of any length/alignment
+  // st: fp32 states (pass 2 only); ua: rows of any length/alignment; ms: rows wider than a sweep in
+  // column segments (pass 2 only)
+  int gdt, V, K, TPB, st = 0, ua = 0, ms = 0;
   bool operator<(const BandKey& o) const {
-    return std::tie(gdt, V, K, TPB, st, ua) < std::tie(o.gdt, o.V, o.K, o.TPB, o.st, o.ua);
+    return std::tie(gdt, V, K, TPB, st, ua, ms) < std::tie(o.gdt, o.V, o.K, o.TPB, o.st, o.ua, o.ms);
   }
 };
 struct TypeKey {
@@ -173,12 +175,17 @@ BandShapeSel band_variant(const came8_tensor& t, int64_t C, int32_t B, int pass)
     sel.ua = true;
   }
   const int64_t chunks = ceil_div(C, sel.V);
-  (void)pass;  // both passes take the same shapes (wider workgroups cost pass 1 more barrier time)
-  // 256-thread workgroups first: two of them per CU keep one's barriers off the other's loads
+  // 256-thread workgroups first: two of them per CU keep one's barriers off the other's loads.
+  // Pass 2 takes rows wider than one sweep in column segments (its MS variants, (3, 256) and, for
+  // V = 1, (32, 256)), and for 16-bit gradients already rows wider than (3, 256) covers: it reads
+  // each element once either way, and a 512-thread workgroup of its register use (~250) is alone
+  // on its CU (C4's 11008-wide rows: 1.13 -> 0.90 ms).  Pass 1, whose column sums of g^2/R_i need
+  // the whole row first, and the UA variants take the wider sweeps.
   static const int vec_k[][2] = {{1, 256}, {2, 256}, {3, 256}, {2, 512}, {3, 512}, {4, 512}};
   static const int one_k[][2] = {{1, 256}, {2, 256}, {4, 256}, {8, 256}, {16, 256}, {32, 256}};
   const int (*cand)[2] = sel.V > 1 ? vec_k : one_k;
-  const int nc = sel.V > 1 ? 6 : 6;
+  const bool p2seg = pass == 2 && !sel.ua;
+  const int nc = (p2seg && sel.V == 8) ? 3 : 6;
   for (int i = 0; i < nc; ++i) {
     if (int64_t(cand[i][0]) * cand[i][1] >= chunks) {
       sel.K = cand[i][0];
@@ -186,8 +193,8 @@ BandShapeSel band_variant(const came8_tensor& t, int64_t C, int32_t B, int pass)
       return sel;
     }
   }
-  sel.K = cand[nc - 1][0];
-  sel.TPB = cand[nc - 1][1];
+  sel.K = p2seg ? (sel.V > 1 ? 3 : 32) : cand[nc - 1][0];
+  sel.TPB = p2seg ? 256 : cand[nc - 1][1];
   sel.multiseg = true;
   return sel;
 }
@@ -212,7 +219,7 @@ bool norm_est_wide(const came8_tensor& t, const DevTensor& d) {
   return t.factored && !tiny_matrix(t, false) && d.C >= kThreads;
 }
 
-BandFn band_fn(int gdt, bool pass2, int V, int K, int TPB, int st, int ua);
+BandFn band_fn(int gdt, bool pass2, int V, int K, int TPB, int st, int ua, int ms);
 
 // The calling thread's current device, or -1 when no device answers (a host without a GPU).
 int current_device() {
@@ -300,8 +307,9 @@ std::vector<int> band_shrinks(const came8_tensor* ts, int32_t n, int32_t B) {
     const came8_tensor& t0 = ts[kv.second.front()];
     const bool s2d = t0.state_kind == CAME8_STATE_8BIT2D;
     const int st = t0.state_kind == CAME8_STATE_FP32 ? 1 : 0;
-    const int64_t slots1 = resident_slots(reinterpret_cast<const void*>(band_fn(k.gdt, false, k.V, k.K, k.TPB, 0, k.ua)), k.TPB);
-    const int64_t slots2 = s2d ? 0 : resident_slots(reinterpret_cast<const void*>(band_fn(k.gdt, true, k.V, k.K, k.TPB, st, k.ua)), k.TPB);
+    const BandShapeSel s2 = band_variant(t0, t0.cols, B, 2);  // alike over the group
+    const int64_t slots1 = resident_slots(reinterpret_cast<const void*>(band_fn(k.gdt, false, k.V, k.K, k.TPB, 0, k.ua, 0)), k.TPB);
+    const int64_t slots2 = s2d ? 0 : resident_slots(reinterpret_cast<const void*>(band_fn(k.gdt, true, s2.V, s2.K, s2.TPB, st, s2.ua, s2.multiseg)), s2.TPB);
     int best = 0;
     if (slots1 <= 0) {
       for (; best < kMaxShrink; ++best) {
@@ -569,7 +577,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       } else {
         const BandShapeSel sel1 = band_variant(t, d.C, B, 1), sel2 = band_variant(t, d.C, B, 2);
         add_item(plan.band[BandKey{t.grad_dtype, sel1.V, sel1.K, sel1.TPB, 0, sel1.ua}], i, d.P * d.nbands);
-        add_item(plan.band2[BandKey{t.grad_dtype, sel2.V, sel2.K, sel2.TPB, d.fp32st, sel2.ua}], i, d.P * d.nbands);
+        add_item(plan.band2[BandKey{t.grad_dtype, sel2.V, sel2.K, sel2.TPB, d.fp32st, sel2.ua, sel2.multiseg}], i, d.P * d.nbands);
       }
       add_item(plan.factor, i, d.nbr + d.nbc);
       if (fastB) {
@@ -788,11 +796,11 @@ Hp make_hp(const came8_hparams& h) {
 // kernel-variant dispatch
 // ---------------------------------------------------------------------------
 // band-pass kernels are instantiated in came8_band.hip (one translation unit per family)
-BandFn band_fn(int gdt, bool pass2, int V, int K, int TPB, int st, int ua) {
+BandFn band_fn(int gdt, bool pass2, int V, int K, int TPB, int st, int ua, int ms) {
   switch (gdt) {
-    case CAME8_F32: return pass2 ? band_fn_F32_p2(V, K, TPB, st, ua) : band_fn_F32_p1(V, K, TPB, st, ua);
-    case CAME8_BF16: return pass2 ? band_fn_BF16_p2(V, K, TPB, st, ua) : band_fn_BF16_p1(V, K, TPB, st, ua);
-    case CAME8_F16: return pass2 ? band_fn_F16_p2(V, K, TPB, st, ua) : band_fn_F16_p1(V, K, TPB, st, ua);
+    case CAME8_F32: return pass2 ? band_fn_F32_p2(V, K, TPB, st, ua, ms) : band_fn_F32_p1(V, K, TPB, st, ua, 0);
+    case CAME8_BF16: return pass2 ? band_fn_BF16_p2(V, K, TPB, st, ua, ms) : band_fn_BF16_p1(V, K, TPB, st, ua, 0);
+    case CAME8_F16: return pass2 ? band_fn_F16_p2(V, K, TPB, st, ua, ms) : band_fn_F16_p1(V, K, TPB, st, ua, 0);
     default: return nullptr;
   }
 }
@@ -1141,7 +1149,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     const BandKey& k = kv.first;
     const WorkList& wl = kv.second;
     BandFn fn = nullptr;
-    fn = band_fn(k.gdt, false, k.V, k.K, k.TPB, 0, k.ua);
+    fn = band_fn(k.gdt, false, k.V, k.K, k.TPB, 0, k.ua, 0);
     if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
     { PhaseTimer pt(PH_PASS1, alg_bytes(plan, wl, tensors, PH_PASS1), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
@@ -1261,7 +1269,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       const BandKey& k = kv.first;
       const WorkList& wl = kv.second;
       BandFn fn = nullptr;
-      fn = band_fn(k.gdt, true, k.V, k.K, k.TPB, k.st, k.ua);
+      fn = band_fn(k.gdt, true, k.V, k.K, k.TPB, k.st, k.ua, k.ms);
       if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
       { PhaseTimer pt(PH_PASS2, alg_bytes(plan, wl, tensors, PH_PASS2), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);

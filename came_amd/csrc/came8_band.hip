@@ -15,10 +15,10 @@ namespace {
 using TG = CAME8_BAND_TYPE;
 constexpr int kVW = 16 / int(sizeof(TG::storage));  // elements per 16-byte chunk
 
-template <int V, int K, int TPB, bool UA = false>
+template <int V, int K, int TPB, bool UA = false, bool MS = false>
 BandFn pick(int st) {
   if constexpr (CAME8_BAND_PASS == 2)
-    return st ? k_fact_pass2<TG, V, K, TPB, true, UA> : k_fact_pass2<TG, V, K, TPB, false, UA>;
+    return st ? k_fact_pass2<TG, V, K, TPB, true, UA, MS> : k_fact_pass2<TG, V, K, TPB, false, UA, MS>;
   else return (void)st, k_fact_pass1<TG, V, K, TPB, UA>;
 }
 template <int V, int K, int TPB>
@@ -28,8 +28,17 @@ BandFn pick_ua(int st, int ua) {
 }  // namespace
 
 // the (V, K, TPB) variants the host's band_variant() can choose; st selects fp32 states (pass 2), ua the
-// variants for rows of any length and alignment
-BandFn CAME8_BAND_SELECTOR(CAME8_BAND_TYPE, CAME8_BAND_PASS)(int V, int K, int TPB, int st, int ua) {
+// variants for rows of any length and alignment, ms pass 2's variants for rows wider than their sweep
+BandFn CAME8_BAND_SELECTOR(CAME8_BAND_TYPE, CAME8_BAND_PASS)(int V, int K, int TPB, int st, int ua, int ms) {
+  if constexpr (CAME8_BAND_PASS == 2) {
+    if (ms) {
+      if (V == 1 && K == 32 && TPB == 256 && !ua) return pick<1, 32, 256, false, true>(st);
+      if (V == kVW && K == 3 && TPB == 256 && !ua) return pick<kVW, 3, 256, false, true>(st);
+      return nullptr;
+    }
+  } else if (ms) {
+    return nullptr;
+  }
   if (V == 1 && TPB == 256 && !ua) {
     switch (K) {
       case 1: return pick<1, 1, 256>(st);

@@ -722,7 +722,9 @@ __global__ __launch_bounds__(kThreads) void k_tiny_pass2(const DevTensor* __rest
 // rounding of d*d: a few 1e-8 relative even where one element dominates a short column.
 // The 16-bit-gradient UA variants of 256 threads are held to two resident workgroups per CU: left
 // free, the compiler spills a few registers to AGPRs and the total leaves room for one only.
-template <typename TG, int V, int K, int TPB, bool F32ST, bool UA = false>
+// MS: rows wider than one sweep, taken in column segments (a variant of its own: the segment loop
+// costs registers that the single-sweep variants, at the edge of two resident workgroups, lack).
+template <typename TG, int V, int K, int TPB, bool F32ST, bool UA = false, bool MS = false>
 __global__ __launch_bounds__(TPB, (UA && sizeof(typename TG::storage) == 2 && TPB == 256) ? 2 : 1) void k_fact_pass2(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                     const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using GS = typename TG::storage;
@@ -785,10 +787,18 @@ __global__ __launch_bounds__(TPB, (UA && sizeof(typename TG::storage) == 2 && TP
         rowsc[rr] = rfac[row];
         rowold[rr] = f32st ? gbl(t.ra)[row] : deq_u8(rq[PR + row], ra[t.nbr + blk_of(row, hp)]);
       }
+      if constexpr (MS) {  // the per-wave row sums add up over the column segments (the dummy row too)
+        for (int64_t i = tid; i < (r1 - r0) * NW; i += TPB) rowpart[bpar][i / NW][i % NW] = 0.0;
+        if (tid < NW) rowpart[bpar][kMaxBandRows][tid] = 0.0;
+      }
       wait_vm_all();  // on every path: the stage loop's waits then count only its own loads
       __syncthreads();
     };
-    if (nseg == 1) {
+    if (MS || nseg == 1) {  // (the host gives the other variants single-sweep rows only)
+      // The band's columns in segments of one sweep of the workgroup (MS; otherwise the sweep covers a
+      // row), each over all of the band's rows: the column sums of a segment are complete when its
+      // rows are, and the per-wave row sums add up over the segments in LDS.  Every element is read
+      // once.
       // The stage loop is branch-free, so that the compiler can wait for exactly one stage's loads
       // while the next stage's are in flight: a chunk past the row end (cok false) loads the row's
       // first chunk instead, and a row past the band end loads the band's last row; both contribute
@@ -797,34 +807,37 @@ __global__ __launch_bounds__(TPB, (UA && sizeof(typename TG::storage) == 2 && TP
       int32_t coff[K], cskip[K];
       bool cok[K];
       uint32_t cmask[UA ? K : 1][CodeChunk<V>::NWD];
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        const int32_t c = (tid + k * TPB) * V;
-        cok[k] = c < C;  // without UA, C % V == 0: a chunk that starts inside the row ends inside it
-        coff[k] = cok[k] ? c : 0;
-        cskip[k] = 0;
-        if constexpr (UA) {  // the row's partial last chunk reads the row's last V elements
-          if (cok[k] && c + V > C) {
-            coff[k] = int32_t(C) - V;
-            cskip[k] = c - coff[k];
-          }
-#pragma unroll
-          for (int i = 0; i < CodeChunk<V>::NWD; ++i) cmask[k][i] = keep_mask(i, cskip[k], 1);
-        }
-        // a masked leading element has c_j = 0 (so u = 0) and a zeroed code (so m = 0)
-#pragma unroll
-        for (int v = 0; v < V; ++v) cj[k][v] = (cok[k] && v >= cskip[k]) ? cf[coff[k] + v] : 0.0f;
-      }
       Acc colR[K][V];
-#pragma unroll
-      for (int k = 0; k < K; ++k)
-#pragma unroll
-        for (int v = 0; v < V; ++v) colR[k][v] = Acc(0);
-      // When B divides C a row starts a block: the block of chunk k is the row's first block plus
-      // the chunk's (per-thread) block offset cbk[k].
       int32_t cbk[K];
+      int64_t seg = 0;  // the column segment
+      auto setup_segment = [&](int64_t cbase) __attribute__((always_inline)) {
 #pragma unroll
-      for (int k = 0; k < K; ++k) cbk[k] = t.rowal ? int32_t(blk_of(coff[k], hp)) : 0;
+        for (int k = 0; k < K; ++k) {
+          const int32_t c = int32_t(cbase) + (tid + k * TPB) * V;
+          cok[k] = c < C;  // without UA, C % V == 0: a chunk that starts inside the row ends inside it
+          coff[k] = cok[k] ? c : 0;
+          cskip[k] = 0;
+          if constexpr (UA) {  // the row's partial last chunk reads the row's last V elements
+            if (cok[k] && c + V > C) {
+              coff[k] = int32_t(C) - V;
+              cskip[k] = c - coff[k];
+            }
+#pragma unroll
+            for (int i = 0; i < CodeChunk<V>::NWD; ++i) cmask[k][i] = keep_mask(i, cskip[k], 1);
+          }
+          // a masked leading element has c_j = 0 (so u = 0) and a zeroed code (so m = 0)
+#pragma unroll
+          for (int v = 0; v < V; ++v) cj[k][v] = (cok[k] && v >= cskip[k]) ? cf[coff[k] + v] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+#pragma unroll
+          for (int v = 0; v < V; ++v) colR[k][v] = Acc(0);
+        // When B divides C a row starts a block: the block of chunk k is the row's first block plus
+        // the chunk's (per-thread) block offset cbk[k].
+#pragma unroll
+        for (int k = 0; k < K; ++k) cbk[k] = t.rowal ? int32_t(blk_of(coff[k], hp)) : 0;
+      };
       // AL: rows start quantisation blocks; ST: fp32 states
       auto run = [&](auto AL, auto ST) __attribute__((always_inline)) {
         constexpr bool kF32 = decltype(ST)::value;
@@ -908,15 +921,19 @@ __global__ __launch_bounds__(TPB, (UA && sizeof(typename TG::storage) == 2 && TP
           for (int s = 0; s < S; ++s) {
             const double wsum = wave_sum(ps[s]);
             const int64_t slot = (r + s < r1) ? (r + s - r0) : int64_t(kMaxBandRows);
-            if (lane == 0) rowpart[bpar][slot][wid] = wsum;
+            if (lane == 0) {  // MS: the segments add up (stage_rows clears the sums)
+              if constexpr (MS) rowpart[bpar][slot][wid] += wsum;
+              else rowpart[bpar][slot][wid] = wsum;
+            }
           }
         };
         // two register stages in flight; the prefetches are unconditional (rows past the band end
-        // reload its last row, from cache, and count for nothing).  The row staging waits for every
-        // load issued so far, which also retires the previous band's stores.  (Issuing the first
-        // stage before it keeps that stage's registers live across the staging and the barrier,
-        // which costs this kernel more than the overlapped latency gains.)
-        stage_rows();
+        // reload its last row, from cache, and count for nothing).  The row staging (before the
+        // first segment) and the wait after each segment's column partials retire every store
+        // issued so far.  (Issuing the first stage before the staging keeps that stage's registers
+        // live across the staging and the barrier, which costs this kernel more than the
+        // overlapped latency gains.)
+        if (seg == 0) stage_rows();
         load_stage(A, r0);
         for (int64_t r = r0; r < r1; r += 2 * S) {
           load_stage(Bs, r + S);
@@ -925,17 +942,29 @@ __global__ __launch_bounds__(TPB, (UA && sizeof(typename TG::storage) == 2 && TP
           process(Bs, r + S);
         }
       };
-      if constexpr (F32ST) run(std::false_type{}, std::true_type{});
-      else if constexpr (UA) run(std::false_type{}, std::false_type{});
-      else if (t.rowal) run(std::true_type{}, std::false_type{});
-      else run(std::false_type{}, std::false_type{});
+      auto segment = [&]() __attribute__((always_inline)) {
+        if constexpr (F32ST) run(std::false_type{}, std::true_type{});
+        else if constexpr (UA) run(std::false_type{}, std::false_type{});
+        else if (t.rowal) run(std::true_type{}, std::false_type{});
+        else run(std::false_type{}, std::false_type{});
 #pragma unroll
-      for (int k = 0; k < K; ++k) {
-        if (cok[k]) {
+        for (int k = 0; k < K; ++k) {
+          if (cok[k]) {
 #pragma unroll
-          for (int v = 0; v < V; ++v)
-            if (!UA || v >= cskip[k]) pR[coff[k] + v] = float(colR[k][v]) + band_eps;
+            for (int v = 0; v < V; ++v)
+              if (!UA || v >= cskip[k]) pR[coff[k] + v] = float(colR[k][v]) + band_eps;
+          }
         }
+      };
+      if constexpr (MS) {
+        for (seg = 0; seg < nseg; ++seg) {
+          setup_segment(seg * segw);
+          segment();
+          if (seg + 1 < nseg) wait_vm_all();  // the partials' stores: the next stage loop waits for loads only
+        }
+      } else {
+        setup_segment(0);
+        segment();
       }
       __syncthreads();
       // row totals over the waves in a fixed order; the new residual row states go through LDS so
@@ -955,100 +984,6 @@ __global__ __launch_bounds__(TPB, (UA && sizeof(typename TG::storage) == 2 && TP
         if (lane == 0) t.rrsum[b * t.nbands + it.band] = float(sum);
       }
       bpar ^= 1;  // the next band writes the other half (after this band's barriers above)
-    } else if constexpr (!UA) {  // (the host gives UA variants single-sweep rows only)
-      // Rows wider than one sweep of the workgroup: column partials segment by segment, then the row
-      // sums over whole rows (the gradient and momentum are read twice).  A row's K chunks of a
-      // segment are loaded together with their momentum, block scales and column factors, before
-      // any is used; a chunk past the row end loads the row's first chunk and is skipped.  (Without
-      // UA, B is a multiple of V and a chunk starts at a multiple of V: it lies in one block.)
-      stage_rows();
-      using CK = Chunk<TG, V>;
-      using MB = typename std::conditional<F32ST, M32Chunk<V>, CodeChunk<V>>::type;
-      auto seg_col = [&](int64_t seg, int k) { return seg * segw + (int64_t(tid) + int64_t(k) * TPB) * V; };
-      struct SegBuf {
-        CK g[K];
-        MB q[K];
-        float a[K];
-        float c[K][V];
-      };
-      auto load_seg = [&](SegBuf& sb, int64_t r, int64_t seg) __attribute__((always_inline)) {
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          const int64_t c0 = seg_col(seg, k);
-          const int64_t cc = c0 < C ? c0 : 0;
-          const int64_t e = r * C + cc;
-          sb.g[k].load(g + e);
-          if constexpr (F32ST) {
-            sb.q[k].load(m32 + e);
-          } else {
-            sb.q[k].load(mq + e);
-            sb.a[k] = ma[blk_of(ebase + e, hp)];
-          }
-#pragma unroll
-          for (int v = 0; v < V; ++v) sb.c[k][v] = cf[cc + v];
-        }
-      };
-      // d of element v of chunk k, the row factor ri
-      auto d_seg = [&](const SegBuf& sb, int k, int v, float ri) __attribute__((always_inline)) {
-        float mo;
-        if constexpr (F32ST) mo = sb.q[k].m[v];
-        else mo = sb.q[k][v] * scale_s8(sb.a[k]);
-        return d_of(ri, sb.c[k][v], sb.g[k][v], mo);
-      };
-      for (int64_t seg = 0; seg < nseg; ++seg) {
-        Acc colR[K][V];
-#pragma unroll
-        for (int k = 0; k < K; ++k)
-#pragma unroll
-          for (int v = 0; v < V; ++v) colR[k][v] = Acc(0);
-        for (int64_t r = r0; r < r1; ++r) {
-          SegBuf sb;
-          load_seg(sb, r, seg);
-          const float ri = rowsc[r - r0];
-#pragma unroll
-          for (int k = 0; k < K; ++k) {
-            if (seg_col(seg, k) < C) {
-#pragma unroll
-              for (int v = 0; v < V; ++v) {
-                const float e = d_seg(sb, k, v, ri);
-                colR[k][v] = acc_fma(colR[k][v], e, e);
-              }
-            }
-          }
-        }
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          const int64_t c0 = seg_col(seg, k);
-          if (c0 < C) {
-#pragma unroll
-            for (int v = 0; v < V; ++v) pR[c0 + v] = float(colR[k][v]) + band_eps;
-          }
-        }
-      }
-      double bandRR = 0.0;  // sum of the band's new residual row states (thread 0, row order)
-      for (int64_t r = r0; r < r1; ++r) {
-        double ps[1] = {0.0};
-        const float ri = rowsc[r - r0];
-        for (int64_t seg = 0; seg < nseg; ++seg) {
-          SegBuf sb;
-          load_seg(sb, r, seg);
-#pragma unroll
-          for (int k = 0; k < K; ++k) {
-            if (seg_col(seg, k) < C) {
-#pragma unroll
-              for (int v = 0; v < V; ++v) {
-                const float e = d_seg(sb, k, v, ri);
-                ps[0] = acc_fma(ps[0], e, e);
-              }
-            }
-          }
-        }
-        double tot[1];
-        block_row_sums<1, NW>(ps, red, par, tot);
-        par ^= 1;
-        if (tid == 0) bandRR += row_state(r - r0, tot[0]);
-      }
-      if (tid == 0) t.rrsum[b * t.nbands + it.band] = float(bandRR);
     }
     __syncthreads();  // rowsc is rewritten by the next work item
   }

@@ -22,9 +22,10 @@ from tests import parity as P
 pytestmark = pytest.mark.gpu
 
 STATE_KEYS = ("exp_avg", "exp_avg_sq_row", "exp_avg_sq_col", "exp_avg_res_row", "exp_avg_res_col", "exp_avg_sq")
-# (2, 3, 5, 7), (16, 3, 3, 3) and (20, 8, 1, 1) are tensors of tiny matrices (one thread per matrix)
+# (2, 3, 5, 7), (16, 3, 3, 3) and (20, 8, 1, 1) are tensors of tiny matrices (one thread per matrix);
+# (5, 11008) and (2, 20000) have rows wider than one sweep of the residual pass (column segments)
 SHAPES = [(1,), (255,), (4097,), (1000, 3), (3, 5000), (64, 2048), (2, 3, 5, 7), (33, 5461), (130, 1024), (4, 4096),
-          (16, 3, 3, 3), (20, 8, 1, 1)]
+          (16, 3, 3, 3), (20, 8, 1, 1), (5, 11008), (2, 20000)]
 
 
 def _close(g: torch.Tensor, r: torch.Tensor, where: str, tol: float = 1e-5, scale: torch.Tensor | None = None):
