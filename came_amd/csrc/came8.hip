@@ -114,7 +114,7 @@ struct Plan {
   WorkList nest_w;                       // unit estimates, a workgroup per row band (matrices >= 256 wide)
   WorkList nest_n;                       // unit estimates, a thread per unit (per 256 units)
   WorkList nscan;                        // prefix of the estimates (one item per tensor)
-  std::map<int, WorkList> nseg2d;        // segment records of matrices, runs of kNormRunSegs, by grad type
+  std::map<int, WorkList> nseg2d;        // segment records of matrices, runs of kNormRunSegs, by 3 * grad type + form
   std::map<int, WorkList> nseg;          // the other segments' records, by 3 * grad type + chunk form
   WorkList nbsum;                        // the chains' sums per block of segments (one item per block)
   std::map<int, WorkList> nfix;          // records rebuilt under the chains' own estimates, by 3 * grad type + form
@@ -492,8 +492,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     d.ngrp = 1;
     if (!s2d) {
       d.nseg = ceil_div(d.N - (d.N & 7), kNormSegElems);
-      const bool lds = t.factored && d.c8 && d.idx32 && reinterpret_cast<uintptr_t>(t.grad) % 16 == 0 && d.P == 1 &&
-                       !tiny_matrix(t, false) && d.C >= 8 * kNormSegLanes && d.C <= kNormLdsCols;
+      const bool lds = t.factored && d.idx32 && reinterpret_cast<uintptr_t>(t.grad) % 16 == 0 && d.P == 1 &&
+                       !tiny_matrix(t, false) && d.C >= 8 * kNormSegLanes && d.C + (d.c8 ? 0 : 8) <= kNormLdsCols;
       d.nseg0 = lds ? (d.N - (d.N & 7)) / kNormSegElems : 0;
       const int64_t nbase = t.factored ? d.P * d.nbands : d.nclip;
       // the thread-per-unit estimate groups single-band matrices and tiles into at most kNormMaxUnits units
@@ -597,7 +597,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       // (prefix 1) up to kNormLdsCols wide take runs of segments with their column factors in LDS
       const bool vec = t.factored && d.idx32 && reinterpret_cast<uintptr_t>(t.grad) % 16 == 0;
       const int form = vec && d.c8 ? kNormVec : (vec && d.C >= 8 ? kNormRows : kNormAny);
-      if (d.nseg0 > 0) add_item(plan.nseg2d[t.grad_dtype], i, ceil_div(d.nseg0, int64_t(kNormRunSegs)));
+      if (d.nseg0 > 0)
+        add_item(plan.nseg2d[t.grad_dtype * 3 + (d.c8 ? kNormVec : kNormRows)], i, ceil_div(d.nseg0, int64_t(kNormRunSegs)));
       if (d.nseg > d.nseg0) add_item(plan.nseg[t.grad_dtype * 3 + form], i, ceil_div(d.nseg - d.nseg0, int64_t(4)));
       add_item(plan.nbsum, i, d.nblk);
       add_item(plan.nfix[t.grad_dtype * 3 + form], i, ceil_div(d.nseg, int64_t(kNormFixSegs)));
@@ -865,6 +866,18 @@ constexpr GenFn k_fact_pass3b_f32st = k_fact_pass3b<TP, TG, true>;
     }                                                                        \
   }
 CAME8_NORM_FN(norm_seg_fn, k_norm_seg)
+// k_norm_seg2d of a work-list key 3 * grad type + chunk form (kNormVec or kNormRows)
+GenFn norm_seg2d_fn(int key) {
+  switch (key) {
+    case 3 * CAME8_F32 + kNormVec: return k_norm_seg2d<F32, kNormVec>;
+    case 3 * CAME8_F32 + kNormRows: return k_norm_seg2d<F32, kNormRows>;
+    case 3 * CAME8_BF16 + kNormVec: return k_norm_seg2d<BF16, kNormVec>;
+    case 3 * CAME8_BF16 + kNormRows: return k_norm_seg2d<BF16, kNormRows>;
+    case 3 * CAME8_F16 + kNormVec: return k_norm_seg2d<F16, kNormVec>;
+    case 3 * CAME8_F16 + kNormRows: return k_norm_seg2d<F16, kNormRows>;
+    default: return nullptr;
+  }
+}
 CAME8_NORM_FN(norm_fix_fn, k_norm_fix)
 #undef CAME8_NORM_FN
 
@@ -1206,12 +1219,13 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     }
     for (auto& kv : plan.nseg2d) {
       const WorkList& wl = kv.second;
-      GenFn fn;
-      CAME8_TYPE_SWITCH1(k_norm_seg2d, kv.first, fn);
-      int64_t cmax = 0;  // LDS for the widest matrix of the launch
+      const GenFn fn = norm_seg2d_fn(kv.first);
+      if (fn == nullptr) return fail(CAME8_EINVAL, "came8_step: no norm kernel for this variant");
+      int64_t cmax = 0;  // LDS for the widest matrix of the launch (+ 8 factors for the row form)
       for (int32_t ti : wl.tids) cmax = std::max(cmax, plan.dev[ti].C);
+      const int64_t lds = cmax + (kv.first % 3 == kNormRows ? 8 : 0);
       PhaseTimer pt(PH_NORM_SEG, alg_bytes(plan, wl, tensors, PH_NORM_SEG), stream);
-      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, size_t(cmax) * 4, stream, dT, tids(wl), wst(wl),
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, size_t(lds) * 4, stream, dT, tids(wl), wst(wl),
                          int(wl.tids.size()), hp);
       if ((rc = check_launch("norm_seg2d")) != CAME8_OK) return rc;
     }

@@ -523,20 +523,24 @@ __device__ __forceinline__ void norm_candidates(float est, int& Ea, bool& two) {
 }
 
 constexpr int kNormRunSegs = 64;       // segments per work item of k_norm_seg2d
-constexpr int kNormLdsCols = 16384;    // widest rows k_norm_seg2d stages in LDS (64 KB of column factors)
+constexpr int kNormLdsCols = 16384;    // column factors k_norm_seg2d stages in LDS (64 KB; rows of whole chunks
+                                       // up to this wide, other rows 8 less)
 constexpr int kNormSegLanes = 16;      // lanes per segment in k_norm_seg2d (narrowest rows: 8 * this)
 constexpr int kNormSegAhead = 8;       // chunks per lane in flight there
 
 // The per-lane, per-chain sums of one whole segment per group of G lanes (lane i = lane % G of the
 // group takes the 8-element chunks at f0 + 8 * G * q + 8 * i) of a matrix (prefix 1) whose column
-// factors are staged in LDS (cl), rows of whole 8-element chunks at least 8 * G wide, 16-byte aligned,
-// 32-bit flat indices.  A chunk's row and column follow from the previous chunk's by one wrap, as the
-// rows are at least 8 * G wide.  The schedule is fixed by hand, a step per chunk: the column factors
+// factors are staged in LDS (cl), rows at least 8 * G wide, gradient 16-byte aligned, 32-bit flat
+// indices.  A chunk's row and column follow from the previous chunk's by one wrap, as the rows are at
+// least 8 * G wide.  ROWS: rows that are not whole chunks; a chunk may end in the next row, whose
+// column factors continue in cl past C (the staging repeats the first 8 there) and whose row factor
+// the elements from C - col on take (a select per element: a branch around it would double the
+// unrolled loop, which then no longer unrolls).  The schedule is fixed by hand, a step per chunk: the column factors
 // of the next chunk are read from LDS, this chunk is accounted, and the gradient and row factor of
 // the chunk kNormSegAhead on are loaded into the registers this one frees.  Scheduling barriers keep
 // the compiler from hoisting the loads further, and NormAcc::pin keeps each chunk's roundings in its
 // step (either would cost registers, not time).
-template <typename TG, int G, bool TWO, bool TINY>
+template <typename TG, int G, bool TWO, bool TINY, bool ROWS>
 __device__ __forceinline__ void norm_seg_lds(const DevTensor& t, const float* cl, uint32_t f0, int ka, int li,
                                              NormAcc& a) {
   using GS = typename TG::storage;
@@ -544,16 +548,17 @@ __device__ __forceinline__ void norm_seg_lds(const DevTensor& t, const float* cl
   static_assert(Q >= D, "segment chunks");
   const CAME8_GLOBAL GS* __restrict__ g = gbl(static_cast<const GS*>(t.g));
   const CAME8_GLOBAL float* __restrict__ rf = gbl(t.rfac);
-  const uint32_t C = uint32_t(t.C);
+  const uint32_t C = uint32_t(t.C), rlast = uint32_t(t.R) - 1u;
   uint32_t f = f0 + uint32_t(li * 8);
   uint32_t row = udiv_magic(f, t.mC, t.sC);
   uint32_t col = f - row * C;
   uint32_t gw[D][NW];  // 16 or 32 bytes of gradient per chunk
-  float r[D];
+  float r[D], r1[ROWS ? D : 1];
   uint32_t cc[D];
   auto issue = [&](int s) __attribute__((always_inline)) {
     cc[s] = col;
     r[s] = rf[row];
+    if constexpr (ROWS) r1[s] = rf[min(row + 1u, rlast)];  // the next row's, for a chunk that ends there
     if constexpr (sizeof(GS) == 2) {
       const u32x4 v = *(const CAME8_GLOBAL u32x4*)(g + f);
       gw[s][0] = v.x; gw[s][1] = v.y; gw[s][2] = v.z; gw[s][3] = v.w;
@@ -569,22 +574,41 @@ __device__ __forceinline__ void norm_seg_lds(const DevTensor& t, const float* cl
     col = wrap ? col - C : col;
     row += wrap ? 1u : 0u;
   };
+  // the column factors of a chunk at column col (ROWS: 4-byte aligned, read in pairs)
+  auto read_c = [&](uint32_t col, float (&cv)[8]) __attribute__((always_inline)) {
+    if constexpr (ROWS) {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) cv[v] = cl[col + v];
+    } else {
+      const f32x4 c0 = *reinterpret_cast<const f32x4*>(cl + col);
+      const f32x4 c1 = *reinterpret_cast<const f32x4*>(cl + col + 4);
+      cv[0] = c0.x; cv[1] = c0.y; cv[2] = c0.z; cv[3] = c0.w;
+      cv[4] = c1.x; cv[5] = c1.y; cv[6] = c1.z; cv[7] = c1.w;
+    }
+  };
 #pragma unroll
   for (int q = 0; q < D; ++q) issue(q);
-  f32x4 c0 = *reinterpret_cast<const f32x4*>(cl + cc[0]);
-  f32x4 c1 = *reinterpret_cast<const f32x4*>(cl + cc[0] + 4);
+  float cn[8];
+  read_c(cc[0], cn);
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
     __builtin_amdgcn_sched_barrier(0);
     const int s = q % D;
-    const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-    if (q + 1 < Q) {
-      c0 = *reinterpret_cast<const f32x4*>(cl + cc[(q + 1) % D]);
-      c1 = *reinterpret_cast<const f32x4*>(cl + cc[(q + 1) % D] + 4);
-    }
+    float cv[8];
 #pragma unroll
-    for (int v = 0; v < 8; ++v) a.add<TWO, TINY>(v, (r[s] * cv[v]) * TG::elem(gw[s], v), ka);
-    a.template pin<TWO>();
+    for (int v = 0; v < 8; ++v) cv[v] = cn[v];
+    if (q + 1 < Q) read_c(cc[(q + 1) % D], cn);
+    if constexpr (ROWS) {
+      const uint32_t b = C - cc[s];  // the chunk's elements in its first row
+#pragma unroll
+      for (int v = 0; v < 8; ++v)
+        a.add<TWO, TINY>(v, ((uint32_t(v) < b ? r[s] : r1[s]) * cv[v]) * TG::elem(gw[s], v), ka);
+      a.template pin<TWO>();
+    } else {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) a.add<TWO, TINY>(v, (r[s] * cv[v]) * TG::elem(gw[s], v), ka);
+      a.template pin<TWO>();
+    }
     if (q + D < Q) issue(s);
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -649,7 +673,7 @@ __device__ __forceinline__ void norm_write_records_g(const DevTensor& t, int64_t
 
 // The segments of one wavefront in a run of k_norm_seg2d: segments k0 + sub for k0 = wid * SPW,
 // wid * SPW + 4 * SPW, ... below nrun, sub = lane / G.  TWO and TINY hold for all of them.
-template <typename TG, int G, bool TWO, bool TINY>
+template <typename TG, int G, bool TWO, bool TINY, bool ROWS>
 __device__ __forceinline__ void norm_seg2d_wave(const DevTensor& t, const float* cl, int64_t run0, int64_t nrun,
                                                 float e0, float e1, int wid, int lane) {
   constexpr int SPW = kWave / G;
@@ -666,23 +690,26 @@ __device__ __forceinline__ void norm_seg2d_wave(const DevTensor& t, const float*
     NormAcc a;
     a.clear();
     wait_vm_all();  // the previous records' stores: the chunk loads' waits then count only loads
-    norm_seg_lds<TG, G, TWO, TINY>(t, cl, uint32_t(seg * kNormSegElems), 23 - Ea, li, a);
+    norm_seg_lds<TG, G, TWO, TINY, ROWS>(t, cl, uint32_t(seg * kNormSegElems), 23 - Ea, li, a);
     norm_write_records_g<G>(t, seg, Ea, TWO, act, lane, a);
   }
 }
 
-// Records of the whole segments [0, nseg0) of 2-D factored tensors whose rows hold whole 8-element
-// chunks (at least 8 * kNormSegLanes, at most kNormLdsCols), 16-byte aligned, with 32-bit flat indices
-// (the host checks); the last, partial segment is k_norm_seg's.  A work item is a run of kNormRunSegs
+// Records of the whole segments [0, nseg0) of 2-D factored tensors whose rows are at least
+// 8 * kNormSegLanes and at most kNormLdsCols wide, gradient 16-byte aligned, with 32-bit flat indices
+// (the host checks); FORM kNormVec when the rows hold whole 8-element chunks, else kNormRows.  The last,
+// partial segment is k_norm_seg's.  A work item is a run of kNormRunSegs
 // segments: the workgroup stages the matrix's column factors in LDS once, and each wavefront takes
 // kWave / kNormSegLanes consecutive segments at a time, a group of kNormSegLanes lanes per segment.
 // A wavefront forms the sums under Ea + 1 for all its segments of the run when one of them needs them
 // (a record with both sums is never wrong), and the subnormal rule when one of them is in that binade;
 // the choice is made once per run, so that no code is shared between the forms' segment loops (the
 // compiler would hoist a shared start, and the registers it holds, above the branch).
-template <typename TG>
+template <typename TG, int FORM>
 __global__ __launch_bounds__(kThreads) void k_norm_seg2d(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                          const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  static_assert(FORM == kNormVec || FORM == kNormRows, "k_norm_seg2d forms");
+  constexpr bool ROWS = FORM == kNormRows;
   constexpr int G = kNormSegLanes, SPW = kWave / G;  // lanes per segment, segments per wavefront
   extern __shared__ float cl[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -694,8 +721,12 @@ __global__ __launch_bounds__(kThreads) void k_norm_seg2d(const DevTensor* __rest
     const DevTensor& t = T[ti];
     if (ti != staged) {  // uniform over the workgroup
       __syncthreads();
-      for (int64_t j = tid * 4; j < t.C; j += kThreads * 4)
-        *reinterpret_cast<f32x4*>(cl + j) = *reinterpret_cast<const CAME8_GLOBAL f32x4*>(gbl(t.cfac) + j);
+      if constexpr (ROWS) {  // C + 8 factors: the row's, then its first 8 again (for chunks that wrap)
+        for (int64_t j = tid; j < t.C + 8; j += kThreads) cl[j] = gbl(t.cfac)[j < t.C ? j : j - t.C];
+      } else {
+        for (int64_t j = tid * 4; j < t.C; j += kThreads * 4)
+          *reinterpret_cast<f32x4*>(cl + j) = *reinterpret_cast<const CAME8_GLOBAL f32x4*>(gbl(t.cfac) + j);
+      }
       __syncthreads();
       staged = ti;
     }
@@ -714,9 +745,9 @@ __global__ __launch_bounds__(kThreads) void k_norm_seg2d(const DevTensor* __rest
       any_two |= two;
       any_tiny |= Ea == -126;
     }
-    if (__any(any_tiny)) norm_seg2d_wave<TG, G, true, true>(t, cl, run0, nrun, e0, e1, wid, lane);
-    else if (__any(any_two)) norm_seg2d_wave<TG, G, true, false>(t, cl, run0, nrun, e0, e1, wid, lane);
-    else norm_seg2d_wave<TG, G, false, false>(t, cl, run0, nrun, e0, e1, wid, lane);
+    if (__any(any_tiny)) norm_seg2d_wave<TG, G, true, true, ROWS>(t, cl, run0, nrun, e0, e1, wid, lane);
+    else if (__any(any_two)) norm_seg2d_wave<TG, G, true, false, ROWS>(t, cl, run0, nrun, e0, e1, wid, lane);
+    else norm_seg2d_wave<TG, G, false, false, ROWS>(t, cl, run0, nrun, e0, e1, wid, lane);
   }
 }
 
