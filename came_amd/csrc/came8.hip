@@ -1248,8 +1248,12 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       const WorkList& wl = kv.second;
       const GenFn fn = norm_fix_fn(kv.first);
       if (fn == nullptr) return fail(CAME8_EINVAL, "came8_step: no norm kernel for this variant");
+      int64_t lds = 0;  // column factors of the widest tensor that k_norm_seg2d takes (+ 8 for the row form)
+      for (int32_t ti : wl.tids)
+        if (plan.dev[ti].nseg0 > 0) lds = std::max(lds, plan.dev[ti].C + (kv.first % 3 == kNormRows ? 8 : 0));
       PhaseTimer pt(PH_NORM_FIX, 0.0, stream);
-      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, size_t(lds) * 4, stream, dT, tids(wl), wst(wl),
+                         int(wl.tids.size()), hp);
       if ((rc = check_launch("norm_fix")) != CAME8_OK) return rc;
     }
     for (auto& kv : plan.nwalk) {

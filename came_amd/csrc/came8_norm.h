@@ -788,6 +788,45 @@ __global__ __launch_bounds__(kThreads, 4) void k_norm_seg(const DevTensor* __res
   }
 }
 
+// The x of the 8 elements of the chunk at flat index f (a multiple of 8, in a whole segment) of a tensor
+// that k_norm_seg2d takes, with the column factors staged in LDS (cl) as it stages them.  ROWS: the
+// chunk may end in the next row (kNormRows).
+template <typename TG, bool ROWS>
+__device__ __forceinline__ void norm_chunk_lds(const DevTensor& t, const float* cl, uint32_t f, float (&x)[8]) {
+  using GS = typename TG::storage;
+  const uint32_t C = uint32_t(t.C);
+  const uint32_t row = udiv_magic(f, t.mC, t.sC);
+  const uint32_t col = f - row * C;
+  float gv[8];
+  load8<TG>(gbl(static_cast<const GS*>(t.g) + f), gv);
+  const float r0 = gbl(t.rfac)[row];
+  if constexpr (ROWS) {
+    const float r1 = gbl(t.rfac)[min(row + 1u, uint32_t(t.R) - 1u)];
+    const uint32_t b = C - col;  // the chunk's elements in its first row
+#pragma unroll
+    for (int v = 0; v < 8; ++v) x[v] = ((uint32_t(v) < b ? r0 : r1) * cl[col + v]) * gv[v];
+  } else {
+    const f32x4 c0 = *reinterpret_cast<const f32x4*>(cl + col);
+    const f32x4 c1 = *reinterpret_cast<const f32x4*>(cl + col + 4);
+    const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+    for (int v = 0; v < 8; ++v) x[v] = (r0 * cv[v]) * gv[v];
+  }
+}
+
+// Stages the column factors of a tensor that k_norm_seg2d takes in LDS (cl) as k_norm_seg2d does: ROWS,
+// C + 8 factors (the row's, then its first 8 again).  Every thread of the workgroup calls it.
+template <bool ROWS>
+__device__ __forceinline__ void norm_stage_cols(const DevTensor& t, float* cl) {
+  const int tid = threadIdx.x;
+  if constexpr (ROWS) {
+    for (int64_t j = tid; j < t.C + 8; j += kThreads) cl[j] = gbl(t.cfac)[j < t.C ? j : j - t.C];
+  } else {
+    for (int64_t j = tid * 4; j < t.C; j += kThreads * 4)
+      *reinterpret_cast<f32x4*>(cl + j) = *reinterpret_cast<const CAME8_GLOBAL f32x4*>(gbl(t.cfac) + j);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // each chain's own estimate, and records rebuilt under it
 // ---------------------------------------------------------------------------
@@ -900,10 +939,12 @@ __device__ __forceinline__ void norm_write_records_pc(const DevTensor& t, int64_
 // within [-2%, +0.5%] of the chain) are checked against the segment's eight records, and the segments
 // where a record's binades do not cover a chain's are listed in LDS and shared out to the wavefronts,
 // which rebuild them a segment at a time under each chain's own candidates Ea and Ea + 1 (both sums
-// always).  FORM as for k_norm_seg.
+// always).  FORM as for k_norm_seg.  The whole segments of a tensor that k_norm_seg2d takes (nseg0 > 0)
+// read their column factors from LDS, staged once per tensor as k_norm_seg2d stages them.
 template <typename TG, int FORM>
 __global__ __launch_bounds__(kThreads) void k_norm_fix(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                        const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  extern __shared__ float cl[];            // column factors (launches with tensors that k_norm_seg2d takes)
   __shared__ uint32_t list[kNormFixSegs];  // (thread << 8) | mask of the chains to rebuild
   __shared__ int nlist;
   __shared__ float est_l[8][kNormFixSegs];
@@ -911,9 +952,11 @@ __global__ __launch_bounds__(kThreads) void k_norm_fix(const DevTensor* __restri
   __shared__ float base_l[8];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t total = wstart[ntens];
+  int32_t staged = -1;
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
     const int slot = find_slot(wstart, ntens, w);
-    const DevTensor& t = T[tids[slot]];
+    const int32_t ti = tids[slot];
+    const DevTensor& t = T[ti];
     const int64_t nseg = t.nseg;
     const int64_t blk = w - wstart[slot];
     const int64_t base = blk * kNormFixSegs;
@@ -937,6 +980,12 @@ __global__ __launch_bounds__(kThreads) void k_norm_fix(const DevTensor* __restri
     __syncthreads();
     const int n = nlist;
     const int64_t main = t.N - (t.N & 7);
+    constexpr bool kLds = FORM != kNormAny;
+    if (kLds && n > 0 && t.nseg0 > 0 && ti != staged) {  // uniform over the workgroup
+      norm_stage_cols<FORM == kNormRows>(t, cl);
+      __syncthreads();
+      staged = ti;
+    }
     for (int k = wid; k < n; k += kThreads / kWave) {  // uniform over the wavefront
       const uint32_t e = list[k];
       const int64_t sf = base + (e >> 8);
@@ -950,15 +999,29 @@ __global__ __launch_bounds__(kThreads) void k_norm_fix(const DevTensor* __restri
       NormAcc a;
       a.clear();
       const int64_t f0 = sf * kNormSegElems, f1 = min(f0 + kNormSegElems, main);
+      if (kLds && sf < t.nseg0) {  // uniform over the wavefront
 #pragma unroll 1
-      for (int h = 0; h < kNormChunks; h += kNormGroup) {
-        float x[kNormGroup][8];
+        for (int h = 0; h < kNormChunks; h += kNormGroup) {
+          float x[kNormGroup][8];
 #pragma unroll
-        for (int q = 0; q < kNormGroup; ++q) norm_chunk_x<TG, FORM>(t, f0 + (h + q) * 512 + lane * 8, f1, hp, x[q]);
+          for (int q = 0; q < kNormGroup; ++q)
+            norm_chunk_lds<TG, FORM == kNormRows>(t, cl, uint32_t(f0 + (h + q) * 512 + lane * 8), x[q]);
 #pragma unroll
-        for (int q = 0; q < kNormGroup; ++q)
+          for (int q = 0; q < kNormGroup; ++q)
 #pragma unroll
-          for (int v = 0; v < 8; ++v) a.add_both(v, x[q][v], ka[v], Ea[v] == -126);
+            for (int v = 0; v < 8; ++v) a.add_both(v, x[q][v], ka[v], Ea[v] == -126);
+        }
+      } else {
+#pragma unroll 1
+        for (int h = 0; h < kNormChunks; h += kNormGroup) {
+          float x[kNormGroup][8];
+#pragma unroll
+          for (int q = 0; q < kNormGroup; ++q) norm_chunk_x<TG, FORM>(t, f0 + (h + q) * 512 + lane * 8, f1, hp, x[q]);
+#pragma unroll
+          for (int q = 0; q < kNormGroup; ++q)
+#pragma unroll
+            for (int v = 0; v < 8; ++v) a.add_both(v, x[q][v], ka[v], Ea[v] == -126);
+        }
       }
       norm_write_records_pc(t, sf, Ea, e & 255u, lane, a);
     }
