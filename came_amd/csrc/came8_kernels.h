@@ -1464,8 +1464,16 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
         load8<F32>(cfac + bb * C + j, cj);
         load8<F32>(crfac + bb * C + j, crj);
         p3_math8<TP, F32ST>(gv, q, pv, m, amax_old, ri, rri, cj, crj, clip, crcp, clip_fast, hp);
+      } else if (!__any(j + 8 > C)) {
+        // rows of C >= 8 elements that are not a whole number of 8-element groups, where no chunk of
+        // the wavefront reaches the next row (most of them): one row's factors, unaligned loads
+        float cj[8], crj[8];
+        const float ri = rfac[row], rri = rrfac[row];
+        load8u_f32(cfac + bb * C + j, cj);
+        load8u_f32(crfac + bb * C + j, crj);
+        p3_math8<TP, F32ST>(gv, q, pv, m, amax_old, ri, rri, cj, crj, clip, crcp, clip_fast, hp);
       } else {
-        // rows of C >= 8 elements that are not a whole number of 8-element groups: the 8 elements
+        // the same rows where some chunk of the wavefront ends in the next row: the 8 elements
         // lie on at most two rows.  Element v is column j + v of `row`, or, past the row's end,
         // column j + v - C of row + 1 (which may begin the next matrix).  The factors come as two
         // unaligned 8-column loads, C apart, and a select per element; the lanes a select drops
