@@ -88,8 +88,10 @@ __device__ __forceinline__ int norm_est_binade(float v) {
 // The increment of one element whose rounded square is hi under binade E (k = 23 - E) is rint(hi * 2^k),
 // exact for the chain whenever that scaled square dh is not a half-integer and below 2^23 (then
 // half-integers lie on hi's grid, and a true square that is not one rounds like hi).  The segment
-// kernel keeps, per lane and chain, the running sum of rint(dh) and the largest |dh - rint(dh)|; the
-// exceptions are then read off per lane once, not tested per element:
+// kernel keeps, per lane and chain, the running sum of rint(dh) and either the largest |dh - rint(dh)|
+// or (k_norm_seg2d) per chain a wavefront mask of the lanes that met a tie (a compare into a scalar
+// register and a scalar or: one VALU instruction per element instead of two); the exceptions are then
+// read off per lane once:
 //   * a tie (some |dh - rint(dh)| = 0.5): the rounding of that element depends on the chain's parity;
 //   * dh >= 2^23: in a normal binade (m >= 2^23) it takes the chain out of the binade by itself, so
 //     the segment's sum, at least 2^23, already fails the walk's test m + sum < 2^24;
@@ -104,11 +106,23 @@ __device__ __forceinline__ void norm_acc(float hi, int k, float& sum, float& rma
   sum += nf;
   rmax = fmaxf(rmax, fabsf(dh - nf));
 }
+// the same, returning whether the element is a tie
+__device__ __forceinline__ bool norm_acc_tie(float hi, int k, float& sum) {
+  const float dh = ldexpf(hi, k);
+  const float nf = rintf(dh);
+  sum += nf;
+  return fabsf(dh - nf) == 0.5f;
+}
 // the lane's sum for one chain as the record's integer, or kNormFull for an exception
-__device__ __forceinline__ uint32_t norm_lane_value(float sum, float rmax, int E) {
-  const bool bad = !(sum < kNormSpecial) || rmax == 0.5f || (E == -126 && sum != 0.0f);
+__device__ __forceinline__ uint32_t norm_lane_value(float sum, bool tie, int E) {
+  const bool bad = !(sum < kNormSpecial) || tie || (E == -126 && sum != 0.0f);
   return bad ? (1u << 24) : uint32_t(sum);
 }
+__device__ __forceinline__ uint32_t norm_lane_value(float sum, float rmax, int E) {
+  return norm_lane_value(sum, rmax == 0.5f, E);
+}
+// lane `lane`'s bit of a wavefront mask
+__device__ __forceinline__ bool norm_bit(uint64_t mask, int lane) { return ((mask >> lane) & 1u) != 0; }
 
 // Record word 0: Ea + 256 (9 bits) | kRecTwo when word 2 holds the sum under Ea + 1.  Words 1 and 2:
 // the integer sums of the increments under Ea and Ea + 1, at most 2^24 (2^24: the segment leaves
@@ -384,17 +398,6 @@ struct NormAcc {
     if constexpr (TWO) norm_acc(hi, ka - 1, sb[v], rb[v]);
     if constexpr (TINY) ra[v] = fabsf(x) == 0x1p-75f ? 0.5f : ra[v];
   }
-  // An empty asm that reads and writes the sums: in a fully unrolled segment the code generator would
-  // otherwise defer the roundings to the segment's end (their results are read only there) and hold
-  // every square until then.
-  template <bool TWO>
-  __device__ __forceinline__ void pin() {
-#pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      asm volatile("" : "+v"(sa[v]), "+v"(ra[v]), "+v"(hs[v]));
-      if constexpr (TWO) asm volatile("" : "+v"(sb[v]), "+v"(rb[v]));
-    }
-  }
   // both binades, with the TINY rule when tiny (the rebuild of k_norm_fix, a binade per chain)
   __device__ __forceinline__ void add_both(int v, float x, int ka, bool tiny) {
     const float hi = x * x;
@@ -402,6 +405,45 @@ struct NormAcc {
     norm_acc(hi, ka - 1, sb[v], rb[v]);
     ra[v] = tiny && fabsf(x) == 0x1p-75f ? 0.5f : ra[v];
   }
+  __device__ __forceinline__ bool tie_a(int v, int) const { return ra[v] == 0.5f; }
+  __device__ __forceinline__ bool tie_b(int v, int) const { return rb[v] == 0.5f; }
+};
+
+// NormAcc of k_norm_seg2d: the ties as per-chain wavefront masks of the lanes that met one (ta, tb;
+// scalar registers), which takes one VALU instruction per element and binade fewer than the largest
+// rounding distance.  (The other record kernels, whose loops are not unrolled, keep NormAcc: their
+// sixteen masks there spill scalar registers.)  Every lane of the wavefront takes part in add.
+struct NormAccM {
+  float sa[8], sb[8], hs[8];
+  uint64_t ta[8], tb[8];
+  __device__ __forceinline__ void clear() {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      sa[v] = sb[v] = hs[v] = 0.0f;
+      ta[v] = tb[v] = 0;
+    }
+  }
+  template <bool TWO, bool TINY>
+  __device__ __forceinline__ void add(int v, float x, int ka) {
+    const float hi = x * x;
+    hs[v] += hi;
+    ta[v] |= __ballot(norm_acc_tie(hi, ka, sa[v]));
+    if constexpr (TWO) tb[v] |= __ballot(norm_acc_tie(hi, ka - 1, sb[v]));
+    if constexpr (TINY) ta[v] |= __ballot(fabsf(x) == 0x1p-75f);
+  }
+  // An empty asm that reads and writes the sums: in a fully unrolled segment the code generator would
+  // otherwise defer the roundings to the segment's end (their results are read only there) and hold
+  // every square until then.
+  template <bool TWO>
+  __device__ __forceinline__ void pin() {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      asm volatile("" : "+v"(sa[v]), "+v"(hs[v]), "+s"(ta[v]));
+      if constexpr (TWO) asm volatile("" : "+v"(sb[v]), "+s"(tb[v]));
+    }
+  }
+  __device__ __forceinline__ bool tie_a(int v, int lane) const { return norm_bit(ta[v], lane); }
+  __device__ __forceinline__ bool tie_b(int v, int lane) const { return norm_bit(tb[v], lane); }
 };
 
 // The x of the 8 elements at flat index f (a multiple of 8): element v belongs to chain v.  Elements
@@ -483,8 +525,8 @@ __device__ __forceinline__ void norm_write_records(const DevTensor& t, int64_t s
   float hs[8];
 #pragma unroll
   for (int v = 0; v < 8; ++v) {
-    acc[v] = norm_lane_value(a.sa[v], a.ra[v], Ea);
-    acc[8 + v] = two ? norm_lane_value(a.sb[v], a.rb[v], Ea + 1) : 0u;
+    acc[v] = norm_lane_value(a.sa[v], a.tie_a(v, lane), Ea);
+    acc[8 + v] = two ? norm_lane_value(a.sb[v], a.tie_b(v, lane), Ea + 1) : 0u;
     hs[v] = a.hs[v];
   }
   const int64_t nseg = t.nseg;
@@ -542,7 +584,7 @@ constexpr int kNormSegAhead = 8;       // chunks per lane in flight there
 // step (either would cost registers, not time).
 template <typename TG, int G, bool TWO, bool TINY, bool ROWS>
 __device__ __forceinline__ void norm_seg_lds(const DevTensor& t, const float* cl, uint32_t f0, int ka, int li,
-                                             NormAcc& a) {
+                                             NormAccM& a) {
   using GS = typename TG::storage;
   constexpr int Q = kNormSegElems / (8 * G), D = kNormSegAhead, NW = int(sizeof(GS)) * 2;
   static_assert(Q >= D, "segment chunks");
@@ -619,14 +661,14 @@ __device__ __forceinline__ void norm_seg_lds(const DevTensor& t, const float* cl
 // were formed (uniform over the wavefront).
 template <int G>
 __device__ __forceinline__ void norm_write_records_g(const DevTensor& t, int64_t seg, int Ea, bool two, bool act,
-                                                     int lane, const NormAcc& a) {
+                                                     int lane, const NormAccM& a) {
   const int li = lane & (G - 1);
   uint32_t acc[16];
   float hs[8];
 #pragma unroll
   for (int v = 0; v < 8; ++v) {
-    acc[v] = norm_lane_value(a.sa[v], a.ra[v], Ea);
-    acc[8 + v] = two ? norm_lane_value(a.sb[v], a.rb[v], Ea + 1) : 0u;
+    acc[v] = norm_lane_value(a.sa[v], a.tie_a(v, lane), Ea);
+    acc[8 + v] = two ? norm_lane_value(a.sb[v], a.tie_b(v, lane), Ea + 1) : 0u;
     hs[v] = a.hs[v];
   }
   const int64_t nseg = t.nseg;
@@ -687,7 +729,7 @@ __device__ __forceinline__ void norm_seg2d_wave(const DevTensor& t, const float*
     int Ea;
     bool two;
     norm_candidates(e0 + (e1 - e0) * (float(k) / float(nrun)), Ea, two);
-    NormAcc a;
+    NormAccM a;
     a.clear();
     wait_vm_all();  // the previous records' stores: the chunk loads' waits then count only loads
     norm_seg_lds<TG, G, TWO, TINY, ROWS>(t, cl, uint32_t(seg * kNormSegElems), 23 - Ea, li, a);
@@ -914,8 +956,8 @@ __device__ __forceinline__ void norm_write_records_pc(const DevTensor& t, int64_
   uint32_t acc[16];
 #pragma unroll
   for (int v = 0; v < 8; ++v) {
-    acc[v] = norm_lane_value(a.sa[v], a.ra[v], Ea[v]);
-    acc[8 + v] = norm_lane_value(a.sb[v], a.rb[v], Ea[v] + 1);
+    acc[v] = norm_lane_value(a.sa[v], a.tie_a(v, lane), Ea[v]);
+    acc[8 + v] = norm_lane_value(a.sb[v], a.tie_b(v, lane), Ea[v] + 1);
   }
   norm_lane_sums<16>(acc, lane);  // lane 4c: chain c under Ea[c]; lane 32 + 4c: under Ea[c] + 1
   const int c = (lane >> 2) & 7;
