@@ -240,6 +240,63 @@ def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False, tiles=F
     }
 
 
+# ------------------------------------------------------------------------------------------ probes
+def run_probes():
+    """HBM access-mix probes: each pass's bytes per 8-element chunk of a 16-bit gradient streamed with no
+    arithmetic (came8_probe.hip), over 2^27 chunks (2 GiB of "gradient"); then one read of a buffer of
+    64 MiB-1 GiB right after reading it, against one read of it after 4 GiB of other reads (the MALL)."""
+    import ctypes
+    from came_amd import build as B
+    lib = ctypes.CDLL(B.PROBE_OUT)
+    lib.came8_probe.restype = ctypes.c_int
+    lib.came8_probe.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                ctypes.POINTER(ctypes.c_float), ctypes.c_void_p]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    n = 1 << 27
+    a = torch.empty(n * 16, dtype=torch.uint8, device="cuda").random_()
+    b = torch.empty(n * 16, dtype=torch.uint8, device="cuda").random_()
+    c = torch.empty(n * 8, dtype=torch.uint8, device="cuda").random_()
+    flush = torch.empty(4 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+
+    def probe(mode, chunks, nrep, wgs=8, ilp=8, src=None):
+        ms = ctypes.c_float()
+        src = a if src is None else src
+        rc = lib.came8_probe(mode, src.data_ptr(), b.data_ptr(), c.data_ptr(), chunks, nrep, wgs, ilp, sink.data_ptr(),
+                             ctypes.byref(ms), stream)
+        if rc != 0:
+            raise RuntimeError(f"came8_probe mode {mode} failed")
+        return ms.value
+
+    # bytes per chunk read and written
+    mixes = {"read 16B (pass 1)": (0, 16), "read 16B + 8B (pass 2)": (1, 24),
+             "read 16B, read+write 16B, read+write 8B (pass 3)": (2, 64), "read 16B, write 16B (copy)": (3, 32)}
+    out = {"chunks": n, "mixes": {}, "reread": {}}
+    for name, (mode, nbytes) in mixes.items():
+        best, shapes = None, {}
+        for wgs in (4, 8, 16):
+            for ilp in (4, 8):
+                probe(mode, n, 1, wgs, ilp)  # warm-up
+                ms = probe(mode, n, 5, wgs, ilp)
+                shapes[f"{wgs}x{ilp}"] = round(nbytes * n / ms / 1e9, 3)
+                if best is None or ms < best[0]:
+                    best = (ms, wgs, ilp)
+        out["mixes"][name] = {"best_TBps": round(nbytes * n / best[0] / 1e9, 3), "best_ms": round(best[0], 4),
+                              "best_shape": f"{best[1]} workgroups/CU x {best[2]} chunks/thread",
+                              "TBps_by_shape": shapes}
+    for mib in (64, 128, 256, 512, 1024):
+        chunks = (mib << 20) // 16
+        probe(0, flush.numel() // 16, 1, src=flush)  # 4 GiB of other reads: the buffer is no longer cached
+        cold = probe(0, chunks, 1)
+        warm = probe(0, chunks, 1)  # right after reading it
+        out["reread"][f"{mib} MiB"] = {"cold_TBps": round(16 * chunks / cold / 1e9, 3),
+                                       "reread_TBps": round(16 * chunks / warm / 1e9, 3),
+                                       "cold_ms": round(cold, 4), "reread_ms": round(warm, 4)}
+    print(json.dumps(out))
+
+
 # ------------------------------------------------------------------------------------------ main
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -253,6 +310,9 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the step, copy a MIB-sized device buffer --steps times (a plain copy "
                          "kernel of known bytes, to scale the FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--probes", action="store_true",
+                    help="instead of the step, the HBM access-mix probes (came_amd/csrc/came8_probe.hip): the rate "
+                         "of each pass's byte mix alone, and of a re-read of 64 MiB-1 GiB right after reading it")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); across GPUs the "
@@ -275,6 +335,10 @@ def main():
         dt = (time.perf_counter() - t0) / args.steps
         print(json.dumps({"copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n,
                           "ms_per_copy": round(dt * 1e3, 4), "GBps_read_plus_write": round(2 * n / dt / 1e9, 1)}))
+        return
+
+    if args.probes:
+        run_probes()
         return
 
     import came_amd
