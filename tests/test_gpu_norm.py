@@ -151,6 +151,19 @@ def test_norm_matrices():
     _run("CAME8bit", MATRICES, max_ulps=4)
 
 
+# Row widths at the edges of the record kernels' forms: the LDS-staged kernel takes rows of 128 to 16384
+# columns (whole 8-element chunks) or 128 to 16376 (other rows, which read 8 factors past the row);
+# narrower and wider rows take the per-segment kernel.  Latin matrices (widths a multiple of 4) are bit
+# exact; the odd widths within 4 ulps.
+ROW_WIDTHS = [((256, 124), "latin", F32), ((256, 128), "latin", BF16), ((256, 132), "latin", F32),
+              ((64, 16372), "latin", BF16), ((64, 16380), "latin", F32), ((64, 16384), "latin", BF16),
+              ((64, 16388), "latin", F32), ((128, 16375), "normal", F32), ((512, 129), "normal", BF16)]
+
+
+def test_norm_row_widths():
+    _run("CAME8bit", ROW_WIDTHS, max_ulps=4)
+
+
 def test_norm_large_matrices_drift_regime():
     """Chains of millions of elements, where the reference's norm is far from the exact one."""
     _run("CAME8bit", [((8192, 4096), "latin", BF16), ((2048, 11008), "latin", BF16), ((4096, 11008), "normal", BF16)],
