@@ -114,7 +114,7 @@ struct Plan {
   WorkList nest_w;                       // unit estimates, a workgroup per row band (matrices >= 256 wide)
   WorkList nest_n;                       // unit estimates, a thread per unit (per 256 units)
   WorkList nscan;                        // prefix of the estimates (one item per tensor)
-  std::map<int, WorkList> nseg2d;        // segment records of matrices, runs of kNormRunSegs, by 3 * grad type + form
+  std::map<int, WorkList> nseg2d;        // segment records of matrices, runs of nrun segments, by 3 * grad type + form
   std::map<int, WorkList> nseg;          // the other segments' records, by 3 * grad type + chunk form
   WorkList nbsum;                        // the chains' sums per block of segments (one item per block)
   std::map<int, WorkList> nfix;          // records rebuilt under the chains' own estimates, by 3 * grad type + form
@@ -488,6 +488,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     // whose clip is the reference's float sum)
     d.nseg = 0;
     d.nseg0 = 0;
+    d.nrun = kNormRunSegs;
     d.nunit = 0;
     d.ngrp = 1;
     if (!s2d) {
@@ -495,6 +496,9 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       const bool lds = t.factored && d.idx32 && reinterpret_cast<uintptr_t>(t.grad) % 16 == 0 && d.P == 1 &&
                        !tiny_matrix(t, false) && d.C >= 8 * kNormSegLanes && d.C + (d.c8 ? 0 : 8) <= kNormLdsCols;
       d.nseg0 = lds ? (d.N - (d.N & 7)) / kNormSegElems : 0;
+      // runs of 64 segments (the column factors staged once per 256K elements); a tensor of fewer than
+      // 256 such runs takes shorter ones, down to 16, so that it still spreads over the CUs
+      d.nrun = d.nseg0 >= 256 * int64_t(kNormRunSegs) ? kNormRunSegs : (d.nseg0 >= 128 * int64_t(kNormRunSegs) ? 32 : 16);
       const int64_t nbase = t.factored ? d.P * d.nbands : d.nclip;
       // the thread-per-unit estimate groups single-band matrices and tiles into at most kNormMaxUnits units
       if (!norm_est_wide(t, d) && (!t.factored || d.nbands == 1)) d.ngrp = ceil_div(nbase, kNormMaxUnits);
@@ -598,7 +602,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       const bool vec = t.factored && d.idx32 && reinterpret_cast<uintptr_t>(t.grad) % 16 == 0;
       const int form = vec && d.c8 ? kNormVec : (vec && d.C >= 8 ? kNormRows : kNormAny);
       if (d.nseg0 > 0)
-        add_item(plan.nseg2d[t.grad_dtype * 3 + (d.c8 ? kNormVec : kNormRows)], i, ceil_div(d.nseg0, int64_t(kNormRunSegs)));
+        add_item(plan.nseg2d[t.grad_dtype * 3 + (d.c8 ? kNormVec : kNormRows)], i, ceil_div(d.nseg0, d.nrun));
       if (d.nseg > d.nseg0) add_item(plan.nseg[t.grad_dtype * 3 + form], i, ceil_div(d.nseg - d.nseg0, int64_t(4)));
       add_item(plan.nbsum, i, d.nblk);
       add_item(plan.nfix[t.grad_dtype * 3 + form], i, ceil_div(d.nseg, int64_t(kNormFixSegs)));

@@ -67,6 +67,7 @@ struct DevTensor {
   // reference-order norm (the clip's update norm replayed as the reference's eight fp32 chains)
   int64_t nseg;       // chain segments of kNormSegElems flat elements over the first N - N % 8
   int64_t nseg0;      // leading whole segments of the LDS-staged kernel (0: every segment is the other's)
+  int64_t nrun;       // segments per work item of the LDS-staged kernel
   int64_t nunit;      // estimate units: row bands of every matrix (factored), 2048-element tiles (1-D),
   int64_t ngrp;       //   or groups of ngrp single-band matrices / tiles (ngrp > 1 bounds nunit)
   float* nest;        // estimated sum of u^2 per unit, then its exclusive prefix [nunit + 1]

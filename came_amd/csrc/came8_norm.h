@@ -564,7 +564,7 @@ __device__ __forceinline__ void norm_candidates(float est, int& Ea, bool& two) {
   two = norm_est_binade(est * 1.015625f) > Ea;
 }
 
-constexpr int kNormRunSegs = 64;       // segments per work item of k_norm_seg2d
+constexpr int kNormRunSegs = 64;       // segments per work item of k_norm_seg2d (at most; 16 for small tensors)
 constexpr int kNormLdsCols = 16384;    // column factors k_norm_seg2d stages in LDS (64 KB; rows of whole chunks
                                        // up to this wide, other rows 8 less)
 constexpr int kNormSegLanes = 16;      // lanes per segment in k_norm_seg2d (narrowest rows: 8 * this)
@@ -740,7 +740,7 @@ __device__ __forceinline__ void norm_seg2d_wave(const DevTensor& t, const float*
 // Records of the whole segments [0, nseg0) of 2-D factored tensors whose rows are at least
 // 8 * kNormSegLanes and at most kNormLdsCols wide, gradient 16-byte aligned, with 32-bit flat indices
 // (the host checks); FORM kNormVec when the rows hold whole 8-element chunks, else kNormRows.  The last,
-// partial segment is k_norm_seg's.  A work item is a run of kNormRunSegs
+// partial segment is k_norm_seg's.  A work item is a run of nrun (16 to kNormRunSegs)
 // segments: the workgroup stages the matrix's column factors in LDS once, and each wavefront takes
 // kWave / kNormSegLanes consecutive segments at a time, a group of kNormSegLanes lanes per segment.
 // A wavefront forms the sums under Ea + 1 for all its segments of the run when one of them needs them
@@ -772,8 +772,8 @@ __global__ __launch_bounds__(kThreads) void k_norm_seg2d(const DevTensor* __rest
       __syncthreads();
       staged = ti;
     }
-    const int64_t run0 = (w - wstart[slot]) * kNormRunSegs;
-    const int64_t nrun = min(int64_t(kNormRunSegs), t.nseg0 - run0);
+    const int64_t run0 = (w - wstart[slot]) * t.nrun;
+    const int64_t nrun = min(t.nrun, t.nseg0 - run0);
     const int64_t main = t.N - (t.N & 7);
     // the estimate at both ends of the run, linear in between (a chain holds about 1/8 of it)
     const float e0 = uniform_f32(norm_est_at(t, run0 * kNormSegElems)) * 0.125f;
