@@ -65,6 +65,7 @@ constexpr int kNormSegElems = 4096;                    // flat elements per segm
 constexpr int kNormChainSeg = kNormSegElems / 8;       // elements per chain per segment
 constexpr int kNormChunks = kNormSegElems / (8 * 64);  // 8-element chunks per lane of a segment's wavefront
 constexpr int kNormWalkSegs = 16;                      // segments per thread per batch of the walk
+constexpr int kNormPrologue = 64;                      // elements a replay from zero applies one by one
 constexpr int kNormGroup = 2;                          // chunks per lane loaded together
 constexpr int64_t kNormMaxUnits = 4096;                // estimate units per tensor of single-band matrices
                                                        // or tiles (more are grouped)
@@ -1122,15 +1123,15 @@ __device__ float norm_replay(const DevTensor& t, int c, int64_t seg, float s, co
 #pragma unroll
   for (int j = 0; j < 8; ++j) h[j] = x[j] * x[j];
   int pos = 0;  // the elements before pos are applied
-  if (s == 0.0f) {  // a chain's start crosses a binade every few elements: the first 64 one by one
+  if (s == 0.0f) {  // a chain's start crosses a binade every few elements: the first ones one by one
 #pragma unroll
-    for (int k = 0; k < 64; ++k) {
+    for (int k = 0; k < kNormPrologue; ++k) {
       if (k < cnt) {  // uniform
         const float xk = norm_lane(x[k & 7], k >> 3);
         s = fmaf(xk, xk, s);
       }
     }
-    pos = min(cnt, 64);
+    pos = min(cnt, kNormPrologue);
   }
   while (pos < cnt) {  // uniform
     if (!(s <= 0x1.fffffep127f)) {
