@@ -157,8 +157,24 @@ __global__ __launch_bounds__(kThreads) void k_norm_est(const DevTensor* __restri
       const int64_t m = u / t.nbands;
       const float* __restrict__ W = t.partW + u * t.C;
       const float* __restrict__ cf = t.cfac + m * t.C;
+      // kEstBatch columns per thread loaded before the first is added (an estimate: the order is free)
+      constexpr int kEstBatch = 8;
+      float acc[kEstBatch] = {};
+      int64_t j = tid;
+      for (; j + (kEstBatch - 1) * kThreads < t.C; j += kEstBatch * kThreads) {
+        float c[kEstBatch], wv[kEstBatch];
+#pragma unroll
+        for (int q = 0; q < kEstBatch; ++q) {
+          c[q] = cf[j + q * kThreads];
+          wv[q] = W[j + q * kThreads];
+        }
+#pragma unroll
+        for (int q = 0; q < kEstBatch; ++q) acc[q] = fmaf(c[q] * c[q], wv[q], acc[q]);
+      }
+      for (; j < t.C; j += kThreads) acc[0] = fmaf(cf[j] * cf[j], W[j], acc[0]);
       float s = 0.0f;
-      for (int64_t j = tid; j < t.C; j += kThreads) s = fmaf(cf[j] * cf[j], W[j], s);
+#pragma unroll
+      for (int q = 0; q < kEstBatch; ++q) s += acc[q];
       s = wave_sum(s);
       if (lane == 0) ssum[wid] = s;
       __syncthreads();
