@@ -179,7 +179,7 @@ BandShapeSel band_variant(const came8_tensor& t, int64_t C, int32_t B, int pass)
   // Pass 2 takes rows wider than one sweep in column segments (its MS variants, (3, 256) and, for
   // V = 1, (32, 256)), and for 16-bit gradients already rows wider than (3, 256) covers: it reads
   // each element once either way, and a 512-thread workgroup of its register use (~250) is alone
-  // on its CU (C4's 11008-wide rows: 1.13 -> 0.90 ms).  Pass 1, whose column sums of g^2/R_i need
+  // on its CU (C4's 11008-wide rows: 1.13 -> 1.03 ms).  Pass 1, whose column sums of g^2/R_i need
   // the whole row first, and the UA variants take the wider sweeps.
   static const int vec_k[][2] = {{1, 256}, {2, 256}, {3, 256}, {2, 512}, {3, 512}, {4, 512}};
   static const int one_k[][2] = {{1, 256}, {2, 256}, {4, 256}, {8, 256}, {16, 256}, {32, 256}};
