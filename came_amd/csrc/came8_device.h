@@ -304,6 +304,20 @@ __device__ __forceinline__ int8_t quant_s8_inv(float x, float inv) {
   const float q = rintf((x * inv) * kSignedQ);
   return int8_t(fminf(kSignedQ, fmaxf(-kSignedQ, q)));
 }
+// quant_s8_inv of four elements packed into a word (byte v = element v), for a block whose absmax and
+// inv = RN(1/absmax) are finite and every |x| <= absmax: then |RN(x*inv)| <= 1 + 2^-23, so
+// |(x*inv)*Q| < 127.5 and the clamp never acts, and adding 1.5*2^23 rounds that product to an integer
+// k half-to-even (the sum's ulp is 1) leaving k mod 256, the int8 code, in the sum's low byte.
+__device__ __forceinline__ uint32_t quant_s8_inv4(const float* x, float inv) {
+  constexpr float kRound = 12582912.0f;  // 1.5 * 2^23
+  uint32_t b[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) b[v] = __float_as_uint(((x[v] * inv) * kSignedQ) + kRound);
+  // byte selectors: 0-3 pick from the second operand, 4-7 from the first, 0x0c gives 0
+  const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm(b[3], b[2], 0x04000c0cu);
+  return lo | hi;
+}
 __device__ __forceinline__ uint8_t quant_u8_inv(float x, float inv) {
   const float q = rintf((x * inv) * kUnsignedQ);
   return uint8_t(fminf(kUnsignedQ, fmaxf(0.0f, q)));

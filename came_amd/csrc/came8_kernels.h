@@ -1913,7 +1913,7 @@ __global__ __launch_bounds__(kThreads) void k_2d_rows(const DevTensor* __restric
                                                       const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using GS = typename TG::storage;
   __shared__ float xres[4][kWave][kTile2 + 1];  // per wave: 4 tiles x 16 rows x 16 residuals (+1: banks)
-  __shared__ float rpart[kTile2][kTile2];       // [row][tile of the chunk]: each tile row's residual sum
+  __shared__ __align__(16) float rpart[kTile2][kTile2];  // [row][tile of the chunk]: each tile row's residual sum
   __shared__ float racc[kTile2];                // running row sums, tiles in order
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int i = lane & (kTile2 - 1), s = lane >> 4;
@@ -1943,9 +1943,14 @@ __global__ __launch_bounds__(kThreads) void k_2d_rows(const DevTensor* __restric
       const bool tvalid = tx < tc;
       const bool act = tvalid && rvalid;
       const int64_t c0 = tx * kTile2;
-      float m[kTile2], res[kTile2];
-      uint32_t abits = 0;
-      float rsum = 0.0f;
+      // m is set and read only on active lanes, and only active lanes write their residuals to LDS:
+      // the reads below stop at the block's rows and tiles, so an inactive lane's slots are never read
+      float m[kTile2];
+      // the tile's largest |m| as bits, from the largest signed and unsigned raw bits: a max over
+      // the nonnegative elements and one over the negative elements' magnitudes (or both over the
+      // nonnegative ones)
+      int32_t smax = 0;
+      uint32_t umax = 0;
       if (act) {
         Raw8<TG> ga, gb;
         ga.load(grow + c0);
@@ -1980,46 +1985,65 @@ __global__ __launch_bounds__(kThreads) void k_2d_rows(const DevTensor* __restric
         // can differ, which changes no code, sum or parameter)
         // (after the loads: scale_s8's rare branch would make the column-factor loads wait for am_old)
         const float sc_old = am_old > 0.0f ? scale_s8(am_old) : 0.0f;
+        float rsum = 0.0f;
 #pragma unroll
         for (int j = 0; j < kTile2; ++j) {
           const float mold = code_elem(qw, j) * sc_old;
-          m2d_from_u(u[j], mold, hp, m[j], res[j]);
-          abits = max(abits, abs_bits(m[j]));
-          rsum += res[j];
+          float res;
+          m2d_from_u(u[j], mold, hp, m[j], res);
+          smax = max(smax, int32_t(__float_as_uint(m[j])));
+          umax = max(umax, __float_as_uint(m[j]));
+          rsum += res;
+          xres[wid][lane][j] = res;
         }
-      } else {
-#pragma unroll
-        for (int j = 0; j < kTile2; ++j) m[j] = res[j] = 0.0f;
+        rpart[i][wid * 4 + s] = rsum;
       }
-      abits = group_max_bits<kTile2>(abits);  // the tile's 16 rows are 16 consecutive lanes
+      // the tile's 16 rows are 16 consecutive lanes
+      const uint32_t abits = group_max_bits<kTile2>(max(uint32_t(smax), umax & 0x7fffffffu));
       if (act) {
         const float amax = fix_absmax(__uint_as_float(abits));
         const float inv = 1.0f / amax;
         uint32_t ow[4];
+        if (__builtin_expect(abits <= 0x7f7fffffu && inv <= 0x1.fffffep127f, 1)) {
+          // no infinity or NaN in the tile and a finite reciprocal
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          uint32_t wv = 0;
+          for (int k = 0; k < 4; ++k) ow[k] = quant_s8_inv4(m + 4 * k, inv);
+        } else {
 #pragma unroll
-          for (int v = 0; v < 4; ++v) wv |= uint32_t(uint8_t(quant_s8_inv(m[4 * k + v], inv))) << (8 * v);
-          ow[k] = wv;
+          for (int k = 0; k < 4; ++k) {
+            uint32_t wv = 0;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) wv |= uint32_t(uint8_t(quant_s8_inv(m[4 * k + v], inv))) << (8 * v);
+            ow[k] = wv;
+          }
         }
         *(CAME8_GLOBAL u32x4*)(qrow + c0) = u32x4{ow[0], ow[1], ow[2], ow[3]};
         if (i == 0) ma[tx] = amax;
       }
-#pragma unroll
-      for (int j = 0; j < kTile2; ++j) xres[wid][lane][j] = res[j];
-      rpart[i][wid * 4 + s] = rsum;
       __syncthreads();
-      if (tvalid) {  // lane (s, i): column i of its tile, the 16 rows in order
+      if (tvalid) {  // lane (s, i): column i of its tile, the block's rows in order
         float cs = 0.0f;
+        if (nrows == kTile2) {
 #pragma unroll
-        for (int k = 0; k < kTile2; ++k) cs += xres[wid][s * kTile2 + k][i];
+          for (int k = 0; k < kTile2; ++k) cs += xres[wid][s * kTile2 + k][i];
+        } else {
+          for (int k = 0; k < nrows; ++k) cs += xres[wid][s * kTile2 + k][i];
+        }
         t2col[c0 + i] = cs;
       }
-      if (tid < nrows) {
+      if (tid < nrows) {  // row tid's tile sums of the chunk, tiles in order
         float a = racc[tid];
         const int64_t nt = (tc - tx0) < kTile2 ? (tc - tx0) : kTile2;
-        for (int64_t k = 0; k < nt; ++k) a += rpart[tid][k];
+        if (nt == kTile2) {
+          const f32x4* rp = reinterpret_cast<const f32x4*>(&rpart[tid][0]);
+#pragma unroll
+          for (int k = 0; k < kTile2 / 4; ++k) {
+            const f32x4 v = rp[k];
+            a = (((a + v.x) + v.y) + v.z) + v.w;
+          }
+        } else {
+          for (int64_t k = 0; k < nt; ++k) a += rpart[tid][k];
+        }
         racc[tid] = a;
       }
       __syncthreads();

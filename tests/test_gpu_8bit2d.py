@@ -239,25 +239,28 @@ def _misaligned(t: torch.Tensor) -> torch.Tensor:
     return v
 
 
-@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
-def test_8bit2d_vector_and_scalar_forms_agree_bitwise(dtype):
-    """Rows that are a whole number of tiles (C % 16 == 0) with 16-byte aligned buffers take the vector
-    momentum pass and parameter write; a parameter one element off a 16-byte boundary takes the scalar
-    parameter write, and momentum codes 8 bytes off one take the scalar momentum pass too (pass 1,
-    which needs only 8-byte aligned codes, stays the same).  Both forms run the same arithmetic in
-    the same order, so three steps must agree bit for bit."""
+def _bits(t: torch.Tensor) -> torch.Tensor:
+    """The raw bits of a tensor (NaN compares equal to a NaN of the same bits)."""
+    if t.dtype in (torch.float32,):
+        return t.view(torch.int32)
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16)
+    return t
+
+
+def _forms_bitwise(shapes, dtype, grads, wd=1e-2):
+    """Runs the steps of `grads` three ways (aligned: vector momentum pass and parameter write;
+    parameter one element off a 16-byte boundary: scalar parameter write; momentum codes 8 bytes off
+    one: scalar momentum pass too) and checks that parameters and states agree bit for bit."""
     dt = getattr(torch, dtype)
-    shapes = [(64, 2048), (37, 400), (5, 48), (130, 1024), (40, 3072)]
     refs = P.make_params(shapes, dt, seed=81)
-    gen = torch.Generator().manual_seed(82)
-    grads = [[P.heavy_grad(gen, s, dt) for s in shapes] for _ in range(3)]
     runs = {}
     for mode in ("aligned", "param_off", "codes_off"):
         ps = []
         for r in refs:
             d = r.clone().cuda()
             ps.append(torch.nn.Parameter(_misaligned(d) if mode == "param_off" else d))
-        opt = came_amd.CAME8bit2D(ps, lr=1e-3, weight_decay=1e-2)
+        opt = came_amd.CAME8bit2D(ps, lr=1e-3, weight_decay=wd)
         for p, g in zip(ps, grads[0]):
             p.grad = g.cuda()
         opt.prime_for_cuda_graph()  # creates the states
@@ -267,7 +270,7 @@ def test_8bit2d_vector_and_scalar_forms_agree_bitwise(dtype):
                 buf = torch.zeros(q.numel() + 8, dtype=torch.int8, device="cuda")
                 opt.state[p]["exp_avg_q"] = buf[8:].view(q.shape)
                 assert opt.state[p]["exp_avg_q"].data_ptr() % 16 == 8
-        for step in range(3):
+        for step in range(len(grads)):
             for p, g in zip(ps, grads[step]):
                 p.grad = g.cuda()
             opt.step()
@@ -275,6 +278,47 @@ def test_8bit2d_vector_and_scalar_forms_agree_bitwise(dtype):
         runs[mode] = [(p.data.cpu(), {k: opt.state[p][k].cpu() for k in PERSIST}) for p in ps]
     for mode in ("param_off", "codes_off"):
         for i, ((pa, sa), (pb, sb)) in enumerate(zip(runs["aligned"], runs[mode])):
-            assert torch.equal(pa, pb), f"{mode} tensor {i}: parameters differ"
+            assert torch.equal(_bits(pa), _bits(pb)), f"{mode} tensor {i}: parameters differ"
             for k in PERSIST:
-                assert torch.equal(sa[k], sb[k]), f"{mode} tensor {i}: {k} differs"
+                assert torch.equal(_bits(sa[k]), _bits(sb[k])), f"{mode} tensor {i}: {k} differs"
+    return runs
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_8bit2d_vector_and_scalar_forms_agree_bitwise(dtype):
+    """Rows that are a whole number of tiles (C % 16 == 0) with 16-byte aligned buffers take the vector
+    momentum pass and parameter write; a parameter one element off a 16-byte boundary takes the scalar
+    parameter write, and momentum codes 8 bytes off one take the scalar momentum pass too (pass 1,
+    which needs only 8-byte aligned codes, stays the same).  Both forms run the same arithmetic in
+    the same order, so three steps must agree bit for bit."""
+    dt = getattr(torch, dtype)
+    shapes = [(64, 2048), (37, 400), (5, 48), (130, 1024), (40, 3072)]
+    gen = torch.Generator().manual_seed(82)
+    grads = [[P.heavy_grad(gen, s, dt) for s in shapes] for _ in range(3)]
+    _forms_bitwise(shapes, dtype, grads)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_8bit2d_forms_agree_on_special_tiles(dtype):
+    """The vector momentum pass quantises a tile through a rounding constant when the tile holds no
+    infinity or NaN and 1/absmax is finite, and through rint and the clamp otherwise; the scalar pass
+    always takes the second way.  Tiles of zeros, of subnormal gradients (absmax subnormal, so
+    1/absmax overflows, and numerators below the reciprocal division's range), a tensor with a NaN
+    and one with an infinity must give the same bits both ways."""
+    dt = getattr(torch, dtype)
+    shapes = [(64, 2048), (48, 256), (32, 512), (32, 512)]
+    gen = torch.Generator().manual_seed(83)
+    grads = []
+    for _ in range(2):
+        gs = [P.heavy_grad(gen, s, dt) for s in shapes]
+        gs[0][0:16, 0:16] = 0
+        gs[0][16:32, 32:48] = 1e-39
+        gs[0][33, 100] = 1e-39
+        gs[1][16:32, 16:32] = 1e-38
+        gs[2][5, 7] = float("nan")
+        gs[3][9, 300] = float("inf")
+        grads.append(gs)
+    runs = _forms_bitwise(shapes, dtype, grads)
+    p0, s0 = runs["aligned"][0]
+    assert torch.isfinite(p0.float()).all() and (s0["exp_avg_q"][0:16, 0:16] == 0).all()
+    assert (s0["exp_avg_q"][16:32, 32:48] != 0).any()
