@@ -89,6 +89,36 @@ typedef uint32_t u32x4u __attribute__((ext_vector_type(4), aligned(2)));
 typedef uint32_t u32x2u __attribute__((ext_vector_type(2), aligned(1)));
 typedef uint32_t u32u __attribute__((aligned(1)));
 
+// Streamed operands (read or written once per pass, each pass's tensors far larger than the caches)
+// take the nontemporal hint, `global_load ... nt` / `global_store ... nt` (HBM pure-read rate
+// 5.4 -> 6.1 TB/s in a probe), but only where one wavefront instruction covers whole 128-byte lines:
+// 16 bytes or less per lane, the lanes contiguous.  Where a lane's 32 bytes come in two 16-byte
+// instructions, or a wavefront touches half of a line that another one reads, the hint made the
+// kernel slower (fp32 elements 8 to a lane: C5's pass 3 4.53 -> 4.97 ms), and those accesses stay
+// plain, as do operands that other workgroups read again (column factors, scales).
+#ifndef CAME8_NT_LOADS
+#define CAME8_NT_LOADS 1
+#endif
+#ifndef CAME8_NT_STORES
+#define CAME8_NT_STORES 1
+#endif
+template <typename T>
+__device__ __forceinline__ T ld_nt(const CAME8_GLOBAL T* p) {
+#if CAME8_NT_LOADS
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
+template <typename T>
+__device__ __forceinline__ void st_nt(CAME8_GLOBAL T* p, T v) {
+#if CAME8_NT_STORES
+  __builtin_nontemporal_store(v, p);
+#else
+  *p = v;
+#endif
+}
+
 // 8 consecutive floats from a 4-byte aligned address
 __device__ __forceinline__ void load8u_f32(const CAME8_GLOBAL float* __restrict__ p, float (&out)[8]) {
   const f32x4u a = *(const CAME8_GLOBAL f32x4u*)p;
@@ -97,17 +127,20 @@ __device__ __forceinline__ void load8u_f32(const CAME8_GLOBAL float* __restrict_
   out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
 }
 
-// Load / store 8 consecutive elements (16 or 32 bytes, aligned) of any element type.
-template <typename T>
+// Load / store 8 consecutive elements (16 or 32 bytes, aligned) of any element type (NT: a streamed
+// operand; 16-bit elements then load with the nontemporal hint, and 16-bit stores always take it).
+template <typename T, bool NT = false>
 __device__ __forceinline__ void load8(const CAME8_GLOBAL typename T::storage* __restrict__ p, float (&out)[8]) {
+  constexpr bool nt = NT && sizeof(typename T::storage) == 2;  // one 16-byte load per lane
+  auto ld = [](const auto* a) __attribute__((always_inline)) { return nt ? ld_nt(a) : *a; };
   if constexpr (sizeof(typename T::storage) == 4) {
     const CAME8_GLOBAL f32x4* q = (const CAME8_GLOBAL f32x4*)p;
-    const f32x4 a = q[0];
-    const f32x4 b = q[1];
+    const f32x4 a = ld(q);
+    const f32x4 b = ld(q + 1);
     out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
     out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
   } else {
-    const u32x4 raw = *(const CAME8_GLOBAL u32x4*)p;
+    const u32x4 raw = ld((const CAME8_GLOBAL u32x4*)p);
     const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
     for (int v = 0; v < 8; ++v) out[v] = T::elem(w, v);
@@ -125,7 +158,7 @@ __device__ __forceinline__ void store8(CAME8_GLOBAL typename T::storage* __restr
     typename T::storage* s = reinterpret_cast<typename T::storage*>(&raw);
 #pragma unroll
     for (int v = 0; v < 8; ++v) s[v] = T::store(in[v]);
-    *(CAME8_GLOBAL u32x4*)p = raw;
+    st_nt((CAME8_GLOBAL u32x4*)p, raw);
   }
 }
 

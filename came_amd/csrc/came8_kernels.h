@@ -190,7 +190,7 @@ struct Chunk {
     } else {
       static_assert(V * sizeof(typename TG::storage) == 16, "vector chunk must be 16 bytes");
       using VT = typename std::conditional<U, u32x4u, u32x4>::type;
-      const VT r = *(const CAME8_GLOBAL VT*)p;
+      const VT r = ld_nt((const CAME8_GLOBAL VT*)p);
       w[0] = r.x; w[1] = r.y; w[2] = r.z; w[3] = r.w;
     }
   }
@@ -210,11 +210,11 @@ struct CodeChunk {
   __device__ __forceinline__ void load(const CAME8_GLOBAL int8_t* __restrict__ p) {
     if constexpr (V == 8) {
       using VT = typename std::conditional<U, u32x2u, u32x2>::type;
-      const VT r = *(const CAME8_GLOBAL VT*)p;
+      const VT r = ld_nt((const CAME8_GLOBAL VT*)p);
       w[0] = r.x; w[1] = r.y;
     } else if constexpr (V == 4) {
       using WT = typename std::conditional<U, u32u, uint32_t>::type;
-      w[0] = *(const CAME8_GLOBAL WT*)p;
+      w[0] = ld_nt((const CAME8_GLOBAL WT*)p);
     } else {
 #pragma unroll
       for (int i = 0; i < NWD; ++i) w[i] = 0;
@@ -236,7 +236,8 @@ struct M32Chunk {
       using VT = typename std::conditional<U, f32x4u, f32x4>::type;
 #pragma unroll
       for (int i = 0; i < V / 4; ++i) {
-        const VT r = ((const CAME8_GLOBAL VT*)p)[i];
+        const CAME8_GLOBAL VT* q = (const CAME8_GLOBAL VT*)p + i;
+        const VT r = V == 4 ? ld_nt(q) : *q;  // the hint only for one 16-byte load per lane
         m[4 * i] = r.x; m[4 * i + 1] = r.y; m[4 * i + 2] = r.z; m[4 * i + 3] = r.w;
       }
     } else {
@@ -1453,9 +1454,9 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
     if (t.vec_ok && (t.c8 || C >= 8) && base + kTile <= N) {
       // ---- fast tile: vector access to 8 elements of one quantisation block ----
       float gv[8], pv[8], q[8], m[8];
-      load8<TG>(g + e0, gv);
-      load8<TP>(p + e0, pv);
-      if constexpr (F32ST) load8<F32>(gbl(st_m(t)) + e0, q);
+      load8<TG, true>(g + e0, gv);
+      load8<TP, true>(p + e0, pv);
+      if constexpr (F32ST) load8<F32, true>(gbl(st_m(t)) + e0, q);
       else load_codes<8>(mq + e0, q);
       const float amax_old = F32ST ? 0.0f : ma[blk];
       if (t.c8) {
@@ -1509,7 +1510,7 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3(const DevTensor* __rest
       abits = block_max_bits(abits, L, wmax, par);
       const float amax = fix_absmax(__uint_as_float(abits));
       if ((e0 & (hp.B - 1)) == 0) ma[blk] = amax;
-      *(CAME8_GLOBAL u32x2*)(mq + e0) = p3_quant8(m, amax, abits);
+      st_nt((CAME8_GLOBAL u32x2*)(mq + e0), p3_quant8(m, amax, abits));
     } else {
       // ---- general tile: element by element ----
       float m[8], pv[8];
@@ -1586,11 +1587,13 @@ template <typename T>
 struct Raw8 {
   static constexpr int NWD = int(sizeof(typename T::storage)) * 2;
   uint32_t w[NWD];
+  // NT: the nontemporal hint, for a 16-byte load per lane whose wavefront covers whole lines
+  template <bool NT = (NWD == 4)>
   __device__ __forceinline__ void load(const CAME8_GLOBAL typename T::storage* __restrict__ p) {
     const CAME8_GLOBAL u32x4* q = (const CAME8_GLOBAL u32x4*)p;
 #pragma unroll
     for (int i = 0; i < NWD / 4; ++i) {
-      const u32x4 r = q[i];
+      const u32x4 r = NT ? ld_nt(q + i) : q[i];
       w[4 * i] = r.x; w[4 * i + 1] = r.y; w[4 * i + 2] = r.z; w[4 * i + 3] = r.w;
     }
   }
@@ -1685,7 +1688,7 @@ __global__ __launch_bounds__(kThreads) void k_fact_pass3b(const DevTensor* __res
         store8<TP>(p + e, pv);
         const float amax = fix_absmax(__uint_as_float(abits));
         if ((tid & (L - 1)) == 0) ma[row * bpr + cblk] = amax;
-        *(CAME8_GLOBAL u32x2*)(mq + e) = p3_quant8(m, amax, abits);
+        st_nt((CAME8_GLOBAL u32x2*)(mq + e), p3_quant8(m, amax, abits));
       }
     };
     if (active) load_row(r0, gA, pA, qA, aA);
@@ -1953,8 +1956,10 @@ __global__ __launch_bounds__(kThreads) void k_2d_rows(const DevTensor* __restric
       uint32_t umax = 0;
       if (act) {
         Raw8<TG> ga, gb;
-        ga.load(grow + c0);
-        gb.load(grow + c0 + 8);
+        // plain loads and stores: a lane's 32 bytes of gradient come in two instructions, and a
+        // wavefront's codes are 64 bytes of each of 16 rows
+        ga.template load<false>(grow + c0);
+        gb.template load<false>(grow + c0 + 8);
         const u32x4 q = *(const CAME8_GLOBAL u32x4*)(qrow + c0);
         const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
         const float am_old = ma[tx];
@@ -2210,7 +2215,7 @@ __global__ __launch_bounds__(kThreads) void k_2d_param_v(const DevTensor* __rest
       const int64_t row = t.idx32 ? int64_t(udiv_magic(uint32_t(el), t.mC, t.sC)) : el / t.C;
       const int64_t c0 = el - row * t.C;
       praw[gi].load(p + el);
-      q[gi] = *(const CAME8_GLOBAL u32x2*)(mq + el);
+      q[gi] = ld_nt((const CAME8_GLOBAL u32x2*)(mq + el));
       am[gi] = ma[(row >> 4) * t.tc + (c0 >> 4)];
       rr[gi] = rrfac[row];
       load8<F32>(crfac + c0, cr[gi]);
@@ -2262,7 +2267,7 @@ __global__ __launch_bounds__(kThreads) void k_2d_param_b(const DevTensor* __rest
     auto load_row = [&](int64_t r, Raw8<TP>& pr, u32x2& q, float& am, float& rr) {
       const int64_t e = r * C + col;
       pr.load(p + e);
-      q = *(const CAME8_GLOBAL u32x2*)(mq + e);
+      q = ld_nt((const CAME8_GLOBAL u32x2*)(mq + e));
       am = ma[(r >> 4) * tc];
       rr = rrfac[r];
     };

@@ -619,10 +619,10 @@ __device__ __forceinline__ void norm_seg_lds(const DevTensor& t, const float* cl
     r[s] = rf[row];
     if constexpr (ROWS) r1[s] = rf[min(row + 1u, rlast)];  // the next row's, for a chunk that ends there
     if constexpr (sizeof(GS) == 2) {
-      const u32x4 v = *(const CAME8_GLOBAL u32x4*)(g + f);
+      const u32x4 v = ld_nt((const CAME8_GLOBAL u32x4*)(g + f));
       gw[s][0] = v.x; gw[s][1] = v.y; gw[s][2] = v.z; gw[s][3] = v.w;
     } else {
-      const u32x4 b0 = *(const CAME8_GLOBAL u32x4*)(g + f);
+      const u32x4 b0 = *(const CAME8_GLOBAL u32x4*)(g + f);  // two per lane: no hint
       const u32x4 b1 = *(const CAME8_GLOBAL u32x4*)(g + f + 4);
       gw[s][0] = b0.x; gw[s][1] = b0.y; gw[s][2] = b0.z; gw[s][3] = b0.w;
       gw[s][4] = b1.x; gw[s][5] = b1.y; gw[s][6] = b1.z; gw[s][7] = b1.w;
