@@ -243,7 +243,8 @@ def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False, tiles=F
 # ------------------------------------------------------------------------------------------ probes
 def run_probes():
     """HBM access-mix probes: each pass's bytes per 8-element chunk of a 16-bit gradient streamed with no
-    arithmetic (came8_probe.hip), over 2^27 chunks (2 GiB of "gradient"); then one read of a buffer of
+    arithmetic (came8_probe.hip), with plain and with nontemporal loads and stores, over 2^27 chunks
+    (2 GiB of "gradient"); then one read of a buffer of
     64 MiB-1 GiB right after reading it, against one read of it after 4 GiB of other reads (the MALL)."""
     import ctypes
     from came_amd import build as B
@@ -270,9 +271,10 @@ def run_probes():
             raise RuntimeError(f"came8_probe mode {mode} failed")
         return ms.value
 
-    # bytes per chunk read and written
+    # bytes per chunk read and written; modes 4-7: the same with the nontemporal hint
     mixes = {"read 16B (pass 1)": (0, 16), "read 16B + 8B (pass 2)": (1, 24),
              "read 16B, read+write 16B, read+write 8B (pass 3)": (2, 64), "read 16B, write 16B (copy)": (3, 32)}
+    mixes.update({f"{k}, nontemporal": (m + 4, nb) for k, (m, nb) in list(mixes.items())})
     out = {"chunks": n, "mixes": {}, "reread": {}}
     for name, (mode, nbytes) in mixes.items():
         best, shapes = None, {}

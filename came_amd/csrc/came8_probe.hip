@@ -8,6 +8,8 @@
 //   mode 1  read 16 B + 8 B                             (pass 2: gradient and momentum codes)
 //   mode 2  read 16 B, read+write 16 B, read+write 8 B  (pass 3: gradient, parameter, codes)
 //   mode 3  read 16 B, write 16 B                       (a copy)
+// Modes 4-7 are modes 0-3 with the nontemporal hint on every load and store (`global_load ... nt`,
+// `global_store ... nt`); each wavefront instruction covers 1 KiB (or 512 B) of whole lines.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -16,17 +18,26 @@ namespace {
 
 constexpr int kThreads = 256;
 
-struct alignas(16) U4 {
-  uint32_t x, y, z, w;
-};
-struct alignas(8) U2 {
-  uint32_t x, y;
-};
+typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+typedef uint32_t U2 __attribute__((ext_vector_type(2)));
 
-// kIlp: chunks per thread in flight
+template <bool NT, typename T>
+__device__ __forceinline__ T ld(const T* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <bool NT, typename T>
+__device__ __forceinline__ void st(T* p, T v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
+// kIlp: chunks per thread in flight; MODE & 3: the access mix, MODE & 4: the nontemporal hint
 template <int MODE, int kIlp>
 __global__ __launch_bounds__(kThreads) void k_probe(const U4* __restrict__ a, U4* __restrict__ b, U2* __restrict__ c,
                                                     int64_t n, uint32_t* __restrict__ sink) {
+  constexpr int MIX = MODE & 3;
+  constexpr bool NT = (MODE & 4) != 0;
   const int64_t stride = int64_t(gridDim.x) * kThreads;
   uint32_t acc = 0;
   for (int64_t i0 = int64_t(blockIdx.x) * kThreads + threadIdx.x; i0 < n; i0 += stride * kIlp) {
@@ -36,11 +47,11 @@ __global__ __launch_bounds__(kThreads) void k_probe(const U4* __restrict__ a, U4
     for (int u = 0; u < kIlp; ++u) {
       const int64_t i = i0 + u * stride;
       if (i < n) {
-        va[u] = a[i];
-        if constexpr (MODE == 1) vc[u] = c[i];
-        if constexpr (MODE == 2) {
-          vb[u] = b[i];
-          vc[u] = c[i];
+        va[u] = ld<NT>(a + i);
+        if constexpr (MIX == 1) vc[u] = ld<NT>(c + i);
+        if constexpr (MIX == 2) {
+          vb[u] = ld<NT>(b + i);
+          vc[u] = ld<NT>(c + i);
         }
       }
     }
@@ -48,13 +59,13 @@ __global__ __launch_bounds__(kThreads) void k_probe(const U4* __restrict__ a, U4
     for (int u = 0; u < kIlp; ++u) {
       const int64_t i = i0 + u * stride;
       if (i < n) {
-        if constexpr (MODE == 0) acc ^= va[u].x ^ va[u].y ^ va[u].z ^ va[u].w;
-        if constexpr (MODE == 1) acc ^= va[u].x ^ va[u].w ^ vc[u].x ^ vc[u].y;
-        if constexpr (MODE == 2) {
-          b[i] = U4{vb[u].x + va[u].x, vb[u].y + va[u].y, vb[u].z + va[u].z, vb[u].w + va[u].w};
-          c[i] = U2{vc[u].x ^ va[u].y, vc[u].y ^ va[u].z};
+        if constexpr (MIX == 0) acc ^= va[u].x ^ va[u].y ^ va[u].z ^ va[u].w;
+        if constexpr (MIX == 1) acc ^= va[u].x ^ va[u].w ^ vc[u].x ^ vc[u].y;
+        if constexpr (MIX == 2) {
+          st<NT>(b + i, U4{vb[u].x + va[u].x, vb[u].y + va[u].y, vb[u].z + va[u].z, vb[u].w + va[u].w});
+          st<NT>(c + i, U2{vc[u].x ^ va[u].y, vc[u].y ^ va[u].z});
         }
-        if constexpr (MODE == 3) b[i] = va[u];
+        if constexpr (MIX == 3) st<NT>(b + i, va[u]);
       }
     }
   }
@@ -65,9 +76,9 @@ __global__ __launch_bounds__(kThreads) void k_probe(const U4* __restrict__ a, U4
 
 extern "C" {
 
-// Runs mode `mode` over n chunks nrep times on `stream` and writes the average duration of one run
-// (HIP events on that stream) to *ms.  a: n * 16 bytes; b: n * 16 bytes (modes 2, 3); c: n * 8 bytes
-// (modes 1, 2); sink: 4 bytes.  Launch shape: wgs_per_cu workgroups of 256 threads per CU, ilp (4 or
+// Runs mode `mode` (0-7) over n chunks nrep times on `stream` and writes the average duration of one run
+// (HIP events on that stream) to *ms.  a: n * 16 bytes; b: n * 16 bytes (modes 2, 3, 6, 7);
+// c: n * 8 bytes (modes 1, 2, 5, 6); sink: 4 bytes.  Launch shape: wgs_per_cu workgroups of 256 threads per CU, ilp (4 or
 // 8) chunks per thread in flight.  Returns 0, or -1 for a bad argument or a HIP error.
 int came8_probe(int mode, const void* a, void* b, void* c, int64_t n, int nrep, int wgs_per_cu, int ilp, void* sink,
                 float* ms, void* stream) {
@@ -89,10 +100,14 @@ int came8_probe(int mode, const void* a, void* b, void* c, int64_t n, int nrep, 
       case 1: i8 ? go(k_probe<1, 8>) : go(k_probe<1, 4>); break;
       case 2: i8 ? go(k_probe<2, 8>) : go(k_probe<2, 4>); break;
       case 3: i8 ? go(k_probe<3, 8>) : go(k_probe<3, 4>); break;
+      case 4: i8 ? go(k_probe<4, 8>) : go(k_probe<4, 4>); break;
+      case 5: i8 ? go(k_probe<5, 8>) : go(k_probe<5, 4>); break;
+      case 6: i8 ? go(k_probe<6, 8>) : go(k_probe<6, 4>); break;
+      case 7: i8 ? go(k_probe<7, 8>) : go(k_probe<7, 4>); break;
       default: break;
     }
   };
-  if (mode < 0 || mode > 3 || nrep < 1) return -1;
+  if (mode < 0 || mode > 7 || nrep < 1) return -1;
   hipEvent_t e0, e1;
   if (hipEventCreate(&e0) != hipSuccess) return -1;
   if (hipEventCreate(&e1) != hipSuccess) {
