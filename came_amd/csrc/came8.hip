@@ -963,6 +963,74 @@ struct PhaseTimer {
   }
 };
 
+// A second queue for the launches of one pass.  The launches of a pass (its kernel variants, the tiny
+// and 1-D kernels) work on disjoint tensors; spread over the caller's stream and a side stream they
+// may overlap, so that a variant whose workgroups leave CU slots free (the 512-thread pass 1 over
+// 11008-wide rows: one workgroup per CU) shares the device with the next one instead of queueing
+// before it.  One side stream per (device, caller stream), created on first use and kept; not used
+// while the caller's stream is capturing, nor by came8_step_static (which allocates nothing).
+struct SideQueue {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex g_side_mu;
+std::map<std::pair<int, hipStream_t>, SideQueue> g_side;
+
+int side_queue(hipStream_t caller, SideQueue* out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(CAME8_EHIP, "came8_step: no current HIP device");
+  std::lock_guard<std::mutex> lk(g_side_mu);
+  auto it = g_side.find(std::make_pair(dev, caller));
+  if (it == g_side.end()) {
+    SideQueue q;
+    if (hipStreamCreateWithFlags(&q.s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&q.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&q.join, hipEventDisableTiming) != hipSuccess)
+      return fail(CAME8_EHIP, std::string("came8_step: creating the side stream failed: ") +
+                                  hipGetErrorString(hipGetLastError()));
+    it = g_side.emplace(std::make_pair(dev, caller), q).first;
+  }
+  *out = it->second;
+  return CAME8_OK;
+}
+
+// The queue of each launch of a pass: with at least kSideMinLaunches launches in the pass, the first
+// on the caller's stream and each later one on whichever of the two has fewer algorithmic bytes
+// queued in this pass; else all on the caller's stream.  (Two or three launches gained nothing: the
+// first fills the device and the next one's workgroups only start in its tail, while the fork and
+// join cost 20-50 us on the small C1 and C2 steps; C5's 13-14 launches per pass gained 0.47 ms.)
+// The side stream first waits for everything before the pass on the caller's stream (fork);
+// finish() makes the caller's stream wait for the side stream's launches (join).
+constexpr size_t kSideMinLaunches = 4;
+struct PassQueues {
+  hipStream_t main;
+  SideQueue side;
+  bool can_side, use_side = false;
+  double load[2] = {0.0, 0.0};
+  bool forked = false;
+  PassQueues(hipStream_t m, const SideQueue& s, bool on) : main(m), side(s), can_side(on) {}
+  void begin(size_t launches) { use_side = can_side && launches >= kSideMinLaunches; }
+  int pick(double bytes, hipStream_t* out) {
+    const int k = (use_side && load[1] < load[0]) ? 1 : 0;
+    load[k] += bytes;
+    if (k == 1 && !forked) {
+      if (hipEventRecord(side.fork, main) != hipSuccess || hipStreamWaitEvent(side.s, side.fork, 0) != hipSuccess)
+        return fail(CAME8_EHIP, "came8_step: fork to the side stream failed");
+      forked = true;
+    }
+    *out = k ? side.s : main;
+    return CAME8_OK;
+  }
+  int finish() {
+    load[0] = load[1] = 0.0;
+    if (!forked) return CAME8_OK;
+    forked = false;
+    if (hipEventRecord(side.join, side.s) != hipSuccess || hipStreamWaitEvent(main, side.join, 0) != hipSuccess)
+      return fail(CAME8_EHIP, "came8_step: join of the side stream failed");
+    return CAME8_OK;
+  }
+};
+
 double elem_bytes(int dt) { return dt == CAME8_F32 ? 4.0 : 2.0; }
 
 // Algorithmic bytes of one launch: every operand the kernel must touch, counted once.
@@ -1151,6 +1219,20 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     }
   }
   if (h.flags & CAME8_FLAG_PLAN_ONLY) return CAME8_OK;
+  // the side stream: neither under capture (a captured step keeps one queue) nor for the static entry
+  SideQueue side;
+  bool use_side = workspace_tag != kStaticScratchTag;
+  if (use_side) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess) {
+      (void)hipGetLastError();
+      cap = hipStreamCaptureStatusActive;  // unknown: stay on one queue
+    }
+    use_side = cap == hipStreamCaptureStatusNone;
+  }
+  if (use_side && (rc = side_queue(stream, &side)) != CAME8_OK) return rc;
+  PassQueues pq(stream, side, use_side);
+  hipStream_t ls = stream;  // the queue of the next launch
   Hp hp = make_hp(h);
   const char* base = static_cast<const char*>(workspace);
   hp.zeros = base + plan.zero_off;
@@ -1162,32 +1244,40 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
   const bool fastB = fast_block(h.block_size);
 
   // ---- P1 and 1-D pass A ----
+  pq.begin(plan.band.size() + plan.tiny1.size() + plan.vecA.size());
   for (auto& kv : plan.band) {
     const BandKey& k = kv.first;
     const WorkList& wl = kv.second;
     BandFn fn = nullptr;
     fn = band_fn(k.gdt, false, k.V, k.K, k.TPB, 0, k.ua, 0);
     if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
-    { PhaseTimer pt(PH_PASS1, alg_bytes(plan, wl, tensors, PH_PASS1), stream);
-    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+    const double ab = alg_bytes(plan, wl, tensors, PH_PASS1);
+    if ((rc = pq.pick(ab, &ls)) != CAME8_OK) return rc;
+    { PhaseTimer pt(PH_PASS1, ab, ls);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, ls, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
     if ((rc = check_launch("pass1")) != CAME8_OK) return rc; }
   }
   for (auto& kv : plan.tiny1) {
     const WorkList& wl = kv.second;
     GenFn fn;
     CAME8_TYPE_SWITCH1(k_tiny_pass1, kv.first, fn);
-    { PhaseTimer pt(PH_PASS1, alg_bytes(plan, wl, tensors, PH_PASS1), stream);
-    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+    const double ab = alg_bytes(plan, wl, tensors, PH_PASS1);
+    if ((rc = pq.pick(ab, &ls)) != CAME8_OK) return rc;
+    { PhaseTimer pt(PH_PASS1, ab, ls);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, ls, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
     if ((rc = check_launch("tiny_pass1")) != CAME8_OK) return rc; }
   }
   for (auto& kv : plan.vecA) {
     const WorkList& wl = kv.second;
     GenFn fn;
     CAME8_TYPE_SWITCH1(k_vec_passA, kv.first, fn);
-    { PhaseTimer pt(PH_VECA, alg_bytes(plan, wl, tensors, PH_VECA), stream);
-    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+    const double ab = alg_bytes(plan, wl, tensors, PH_VECA);
+    if ((rc = pq.pick(ab, &ls)) != CAME8_OK) return rc;
+    { PhaseTimer pt(PH_VECA, ab, ls);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, ls, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
     if ((rc = check_launch("vec_passA")) != CAME8_OK) return rc; }
   }
+  if ((rc = pq.finish()) != CAME8_OK) return rc;
   const bool any_fact = !plan.factor.tids.empty();
   if (any_fact) {
     const WorkList& fb = plan.factor;
@@ -1287,22 +1377,27 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
   }
   // ---- P2, residual factors ----
   if (any_fact) {
+    pq.begin(plan.band2.size() + plan.tiny2.size());
     for (auto& kv : plan.band2) {
       const BandKey& k = kv.first;
       const WorkList& wl = kv.second;
       BandFn fn = nullptr;
       fn = band_fn(k.gdt, true, k.V, k.K, k.TPB, k.st, k.ua, k.ms);
       if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
-      { PhaseTimer pt(PH_PASS2, alg_bytes(plan, wl, tensors, PH_PASS2), stream);
-    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      const double ab = alg_bytes(plan, wl, tensors, PH_PASS2);
+      if ((rc = pq.pick(ab, &ls)) != CAME8_OK) return rc;
+      { PhaseTimer pt(PH_PASS2, ab, ls);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, ls, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("pass2")) != CAME8_OK) return rc; }
     }
     for (auto& kv : plan.tiny2) {
       const WorkList& wl = kv.second;
       GenFn fn;
       CAME8_TYPE_SWITCH1(k_tiny_pass2, kv.first, fn);
-      { PhaseTimer pt(PH_PASS2, alg_bytes(plan, wl, tensors, PH_PASS2), stream);
-      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      const double ab = alg_bytes(plan, wl, tensors, PH_PASS2);
+      if ((rc = pq.pick(ab, &ls)) != CAME8_OK) return rc;
+      { PhaseTimer pt(PH_PASS2, ab, ls);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, ls, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("tiny_pass2")) != CAME8_OK) return rc; }
     }
     for (auto& kv : plan.tiles2d_v) {
@@ -1328,6 +1423,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
                          int(wl.tids.size()), hp);
       if ((rc = check_launch("res_rows2d")) != CAME8_OK) return rc;
     }
+    if ((rc = pq.finish()) != CAME8_OK) return rc;
     const WorkList& fb = plan.factor;
     { PhaseTimer pt(PH_FACTOR_RES, alg_bytes(plan, fb, tensors, PH_FACTOR_RES), stream);
     hipLaunchKernelGGL(k_factor_blocks<true>, dim3(grid_for(fb.total())), blk, 0, stream, dT, tids(fb), wst(fb),
@@ -1360,30 +1456,38 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     if ((rc = check_launch("param2d")) != CAME8_OK) return rc; }
   }
   if (fastB) {
+    pq.begin(plan.upd.size() + plan.updb.size() + plan.vecB.size());
     for (auto& kv : plan.upd) {
       const WorkList& wl = kv.second;
       GenFn fn;
       CAME8_TYPE_SWITCH3(k_fact_pass3, kv.first.pdt, kv.first.gdt, kv.first.st, fn);
-      { PhaseTimer pt(PH_PASS3, alg_bytes(plan, wl, tensors, PH_PASS3), stream);
-    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      const double ab = alg_bytes(plan, wl, tensors, PH_PASS3);
+      if ((rc = pq.pick(ab, &ls)) != CAME8_OK) return rc;
+      { PhaseTimer pt(PH_PASS3, ab, ls);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, ls, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("pass3")) != CAME8_OK) return rc; }
     }
     for (auto& kv : plan.updb) {
       const WorkList& wl = kv.second;
       GenFn fn;
       CAME8_TYPE_SWITCH3(k_fact_pass3b, kv.first.pdt, kv.first.gdt, kv.first.st, fn);
-      { PhaseTimer pt(PH_PASS3, alg_bytes(plan, wl, tensors, PH_PASS3), stream);
-    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      const double ab = alg_bytes(plan, wl, tensors, PH_PASS3);
+      if ((rc = pq.pick(ab, &ls)) != CAME8_OK) return rc;
+      { PhaseTimer pt(PH_PASS3, ab, ls);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, ls, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("pass3")) != CAME8_OK) return rc; }
     }
     for (auto& kv : plan.vecB) {
       const WorkList& wl = kv.second;
       GenFn fn;
       CAME8_TYPE_SWITCH2(k_vec_passB, kv.first.pdt, kv.first.gdt, fn);
-      { PhaseTimer pt(PH_VECB, alg_bytes(plan, wl, tensors, PH_VECB), stream);
-    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      const double ab = alg_bytes(plan, wl, tensors, PH_VECB);
+      if ((rc = pq.pick(ab, &ls)) != CAME8_OK) return rc;
+      { PhaseTimer pt(PH_VECB, ab, ls);
+    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, ls, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("vec_passB")) != CAME8_OK) return rc; }
     }
+    if ((rc = pq.finish()) != CAME8_OK) return rc;
   } else {
     for (auto& kv : plan.generic) {
       const WorkList& wl = kv.second;

@@ -736,13 +736,12 @@ __global__ __launch_bounds__(TPB, (UA && sizeof(typename TG::storage) == 2 && TP
   // workgroups per CU instead of two); the stage loop has no barrier (C3 pass 2: 1.00 -> 0.89 ms)
   constexpr int S = (V > 1 && K == 1) ? 2 : Stage<TG, V, K>::S;
   constexpr int64_t segw = int64_t(TPB) * V * K;
-  __shared__ double red[2][16][NW];
   __shared__ double rowpart[2][kMaxBandRows + 1][NW];  // per-wave row sums of a band (+1: a dummy row)
   __shared__ float rowval[kMaxBandRows];           // the band's new residual row states
   __shared__ float rowsc[kMaxBandRows];            // the band's row factors r_i
   __shared__ float rowold[kMaxBandRows];           // the band's old residual row states
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  int par = 0, bpar = 0;
+  int bpar = 0;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
     const BandItem it = band_item(T, tids, wstart, ntens, w);
