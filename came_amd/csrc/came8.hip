@@ -1009,6 +1009,9 @@ struct PassQueues {
   double load[2] = {0.0, 0.0};
   bool forked = false;
   PassQueues(hipStream_t m, const SideQueue& s, bool on) : main(m), side(s), can_side(on) {}
+  ~PassQueues() { (void)finish(); }  // an early return still leaves the caller's stream after the side's work
+  PassQueues(const PassQueues&) = delete;
+  PassQueues& operator=(const PassQueues&) = delete;
   void begin(size_t launches) { use_side = can_side && launches >= kSideMinLaunches; }
   int pick(double bytes, hipStream_t* out) {
     const int k = (use_side && load[1] < load[0]) ? 1 : 0;

@@ -1,0 +1,62 @@
+"""The side stream of a pass with many kernel launches: came8_step spreads a pass of four or more launches
+(band variants of several row widths, the tiny-matrix and 1-D kernels) over the caller's stream and a side
+stream, while came8_step_static keeps every launch on the caller's stream.  Both must step the same
+tensors to the same bits, on two steps in a row and on a second, different tensor list."""
+import ctypes
+
+import pytest
+import torch
+
+import came_amd
+from came_amd import _lib
+from tests import parity as P
+
+pytestmark = pytest.mark.gpu
+
+# row widths that take different pass-1/pass-2 variants (4096-, 11008-, 5461-wide, ragged, one chunk),
+# plus a tiny N-D tensor and 1-D tensors: at least four launches in passes 1 and 2
+SHAPES = [(48, 4096), (20, 11008), (33, 5461), (40, 100), (64, 64), (3, 5, 7), (2048,), (17,)]
+SHAPES_2 = [(16, 11008), (30, 2000), (5, 3, 3), (64, 128), (1000,)]
+
+
+def _static_step(opt, params):
+    group = opt.param_groups[0]
+    items = []
+    for p in params:
+        state, grad = opt._prepare_param(p, opt._group_block_size(group))
+        opt._count_step(state)
+        items.append((p, state, grad))
+    descs, keep, copyback = opt._descriptors(items)
+    hp = opt._group_hparams(group)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.came8_step_static(descs, len(items), ctypes.byref(hp), stream), "came8_step_static")
+    assert not copyback
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_side_stream_step_matches_one_stream(dtype):
+    gen = torch.Generator().manual_seed(5)
+    for call, shapes in enumerate((SHAPES, SHAPES_2)):
+        params0 = P.make_params(shapes, dtype, seed=30 + call)
+        pa = [torch.nn.Parameter(p.clone().cuda()) for p in params0]
+        pb = [torch.nn.Parameter(p.clone().cuda()) for p in params0]
+        oa = came_amd.CAME8bit(pa, lr=2e-4, weight_decay=1e-2)
+        ob = came_amd.CAME8bit(pb, lr=2e-4, weight_decay=1e-2)
+        for step in range(2):
+            grads = [P.heavy_grad(gen, s, dtype).cuda() for s in shapes]
+            for p, q, g in zip(pa, pb, grads):
+                p.grad = g
+                q.grad = g.clone()
+            if step == 0:
+                oa.prime_for_cuda_graph()
+                ob.prime_for_cuda_graph()
+            oa.step()
+            _static_step(ob, pb)
+            torch.cuda.synchronize()
+            for i, (a, b) in enumerate(zip(pa, pb)):
+                where = f"call {call} step {step + 1} tensor {i} {tuple(a.shape)}"
+                assert torch.equal(a.data, b.data), f"{where}: parameters differ"
+                for k, v in oa.state[a].items():
+                    if torch.is_tensor(v):
+                        assert torch.equal(v, ob.state[b][k]), f"{where}: state {k} differs"
