@@ -1002,6 +1002,7 @@ int side_queue(hipStream_t caller, SideQueue* out) {
 // The side stream first waits for everything before the pass on the caller's stream (fork);
 // finish() makes the caller's stream wait for the side stream's launches (join).
 constexpr size_t kSideMinLaunches = 4;
+constexpr size_t kSideMinNormLaunches = 3;  // the clip-norm record and rebuild kernels: C5 11.25 -> 10.87 ms
 struct PassQueues {
   hipStream_t main;
   SideQueue side;
@@ -1012,7 +1013,9 @@ struct PassQueues {
   ~PassQueues() { (void)finish(); }  // an early return still leaves the caller's stream after the side's work
   PassQueues(const PassQueues&) = delete;
   PassQueues& operator=(const PassQueues&) = delete;
-  void begin(size_t launches) { use_side = can_side && launches >= kSideMinLaunches; }
+  void begin(size_t launches, size_t min_launches = kSideMinLaunches) {
+    use_side = can_side && launches >= min_launches;
+  }
   int pick(double bytes, hipStream_t* out) {
     const int k = (use_side && load[1] < load[0]) ? 1 : 0;
     load[k] += bytes;
@@ -1314,6 +1317,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
                          int(wl.tids.size()));
       if ((rc = check_launch("norm_scan")) != CAME8_OK) return rc;
     }
+    pq.begin(plan.nseg2d.size() + plan.nseg.size(), kSideMinNormLaunches);
     for (auto& kv : plan.nseg2d) {
       const WorkList& wl = kv.second;
       const GenFn fn = norm_seg2d_fn(kv.first);
@@ -1321,8 +1325,10 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       int64_t cmax = 0;  // LDS for the widest matrix of the launch (+ 8 factors for the row form)
       for (int32_t ti : wl.tids) cmax = std::max(cmax, plan.dev[ti].C);
       const int64_t lds = cmax + (kv.first % 3 == kNormRows ? 8 : 0);
-      PhaseTimer pt(PH_NORM_SEG, alg_bytes(plan, wl, tensors, PH_NORM_SEG), stream);
-      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, size_t(lds) * 4, stream, dT, tids(wl), wst(wl),
+      const double ab = alg_bytes(plan, wl, tensors, PH_NORM_SEG);
+      if ((rc = pq.pick(ab, &ls)) != CAME8_OK) return rc;
+      PhaseTimer pt(PH_NORM_SEG, ab, ls);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, size_t(lds) * 4, ls, dT, tids(wl), wst(wl),
                          int(wl.tids.size()), hp);
       if ((rc = check_launch("norm_seg2d")) != CAME8_OK) return rc;
     }
@@ -1330,10 +1336,13 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       const WorkList& wl = kv.second;
       const GenFn fn = norm_seg_fn(kv.first);
       if (fn == nullptr) return fail(CAME8_EINVAL, "came8_step: no norm kernel for this variant");
-      PhaseTimer pt(PH_NORM_SEG, alg_bytes(plan, wl, tensors, PH_NORM_SEG), stream);
-      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      const double ab = alg_bytes(plan, wl, tensors, PH_NORM_SEG);
+      if ((rc = pq.pick(ab, &ls)) != CAME8_OK) return rc;
+      PhaseTimer pt(PH_NORM_SEG, ab, ls);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, ls, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("norm_seg")) != CAME8_OK) return rc;
     }
+    if ((rc = pq.finish()) != CAME8_OK) return rc;
     if (!plan.nbsum.tids.empty()) {
       const WorkList& wl = plan.nbsum;
       PhaseTimer pt(PH_NORM_SCAN, 0.0, stream);
@@ -1341,6 +1350,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
                          int(wl.tids.size()));
       if ((rc = check_launch("norm_bsum")) != CAME8_OK) return rc;
     }
+    pq.begin(plan.nfix.size(), kSideMinNormLaunches);
     for (auto& kv : plan.nfix) {
       const WorkList& wl = kv.second;
       const GenFn fn = norm_fix_fn(kv.first);
@@ -1348,11 +1358,14 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       int64_t lds = 0;  // column factors of the widest tensor that k_norm_seg2d takes (+ 8 for the row form)
       for (int32_t ti : wl.tids)
         if (plan.dev[ti].nseg0 > 0) lds = std::max(lds, plan.dev[ti].C + (kv.first % 3 == kNormRows ? 8 : 0));
-      PhaseTimer pt(PH_NORM_FIX, 0.0, stream);
-      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, size_t(lds) * 4, stream, dT, tids(wl), wst(wl),
+      // (no algorithmic bytes: balanced by work items)
+      if ((rc = pq.pick(double(wl.total()), &ls)) != CAME8_OK) return rc;
+      PhaseTimer pt(PH_NORM_FIX, 0.0, ls);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, size_t(lds) * 4, ls, dT, tids(wl), wst(wl),
                          int(wl.tids.size()), hp);
       if ((rc = check_launch("norm_fix")) != CAME8_OK) return rc;
     }
+    if ((rc = pq.finish()) != CAME8_OK) return rc;
     for (auto& kv : plan.nwalk) {
       const WorkList& wl = kv.second;
       GenFn fn;
