@@ -141,7 +141,7 @@ void add_item(WorkList& wl, int32_t tid, int64_t count) {
 
 bool fast_block(int B) { return B >= 8 && B <= kTile && (B & (B - 1)) == 0; }
 
-constexpr int kP3BandRows = 32;       // rows per work item of the band form of P3 (at most)
+constexpr int kP3BandRows = 16;       // rows per work item of the band form of P3 (at most; 32 ran C2 2% slower)
 constexpr int64_t kP3MinItems = 1024;  // band-form P3 work items wanted per launch (4 per CU)
 constexpr int64_t kP3BandMinCols = 1024;  // narrower rows leave too many of a workgroup's lanes idle
 
