@@ -3,8 +3,9 @@
 // The reference clips the update by its RMS, u.norm(2) / sqrt(N) (came_pytorch/CAME8bitFull.py:121-122,
 // 1032).  On CPU, torch sums a contiguous fp32 tensor's squares for norm(2) in one thread as eight
 // interleaved accumulators, acc[i % 8] = fma(u_i, u_i, acc[i % 8]) over the first N - N % 8 elements,
-// then acc[0] + acc[1] + ... + acc[7] left to right, then the remaining elements as separately
-// rounded square-and-add, then a correctly rounded sqrt.  Each accumulator is a serial chain of up to
+// then acc[0] + acc[1] + ... + acc[7] left to right, then the N % 8 remaining elements: when four or
+// more remain, the next four as rounded squares added one at a time, b = (b + RN(u*u)), then the last
+// N % 4 as fused multiply-adds, b = fma(u, u, b); then a correctly rounded sqrt.  Each accumulator is a serial chain of up to
 // N / 8 dependent fused multiply-adds (16.4 M for a 32000 x 4096 matrix); its rounding errors are
 // part of the result (about 1.5% of the norm at that size), so the exact chain has to be replayed.
 //
@@ -1324,8 +1325,9 @@ __global__ __launch_bounds__(kNormWalkThreads) void k_norm_walk(const DevTensor*
   }
 }
 
-// The eight accumulators added left to right, the tail elements as rounded square-and-add, sqrt, and
-// the clip divisor.  A thread per tensor.
+// The eight accumulators added left to right, then the N % 8 tail elements in torch's order (a block
+// of four rounded squares added one at a time when four or more remain, then the rest as fused
+// multiply-adds), sqrt, and the clip divisor.  A thread per tensor.
 template <typename TG>
 __global__ __launch_bounds__(kThreads) void k_norm_final(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                          int ntens, Hp hp) {
@@ -1334,10 +1336,17 @@ __global__ __launch_bounds__(kThreads) void k_norm_final(const DevTensor* __rest
   const DevTensor& t = T[tids[k]];
   float b = t.nchain[0];
   for (int j = 1; j < 8; ++j) b = b + t.nchain[j];
-  for (int64_t d = t.N - (t.N & 7); d < t.N; ++d) {
+  int64_t d = t.N - (t.N & 7);
+  if (t.N - d >= 4) {
+    for (const int64_t e = d + 4; d < e; ++d) {
+      const float u = u_at<TG>(t, d, hp);
+      const float uu = u * u;  // rounded on its own (the build does not contract)
+      b = b + uu;
+    }
+  }
+  for (; d < t.N; ++d) {
     const float u = u_at<TG>(t, d, hp);
-    const float uu = u * u;
-    b = b + uu;
+    b = fmaf(u, u, b);
   }
   const float c = clip_from_norm(sqrtf(b), t.N, hp);
   t.clip[0] = c;

@@ -76,9 +76,9 @@ def _ulps(a: float, b: float) -> int:
     return abs(ia - ib)
 
 
-def _run(cls_name, cases, steps=2, max_ulps=0, check_exact_gap=False, **hp_kw):
+def _run(cls_name, cases, steps=2, max_ulps=0, check_exact_gap=False, seed=1234, **hp_kw):
     import came_amd
-    gen = torch.Generator().manual_seed(1234)
+    gen = torch.Generator().manual_seed(seed)
     shapes = [c[0] for c in cases]
     dts = [c[2] for c in cases]
     params = [(torch.randn(s, generator=gen) * 0.02).to(dt) for s, dt in zip(shapes, dts)]
@@ -138,6 +138,18 @@ ONE_D = [((n,), "normal", F32) for n in (1, 7, 8, 9, 63, 4095, 4096, 4097, 8193,
 
 def test_norm_one_d():
     _run("CAME8bit", ONE_D)
+
+
+# Every tail length N % 8 = 1..7, short and long: torch adds the tail after the eight chains as a block of
+# four separately rounded squares (when four or more remain) and then fused multiply-adds; each rule
+# decides the last bit in a few percent of draws, so several seeds are needed to see a wrong rule.
+TAILS = [((n,), "normal", F32) for n in (2, 3, 4, 5, 6, 7, 12, 13, 14, 15, 17, 4097, 4098, 4099, 4100, 4101,
+                                         4102, 4103)]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_norm_one_d_tails(seed):
+    _run("CAME8bit", TAILS, seed=seed)
 
 
 MATRICES = [((2048, 2048), "latin", F32), ((256, 4096), "latin", BF16), ((64, 1000), "latin", F32),
