@@ -95,14 +95,28 @@ def heavy_grad(shape, gen, dtype, device="cuda"):
     return g.reshape(shape).to(dtype)
 
 
+def grad_stds(gspec, n, seed=1):
+    """Per-tensor gradient standard deviations for a config's gradient spec: a float (the same for every
+    tensor), None (heavy_grad, no std), or ("loguniform", base, lo, hi): base * 10^U(lo, hi) per tensor,
+    drawn from a CPU generator of its own (N(0, 1e-3^2) times a per-tensor scale
+    log-uniform in [1e-5, 1e-2])."""
+    if gspec is None or isinstance(gspec, float):
+        return [gspec] * n
+    kind, base, lo, hi = gspec
+    assert kind == "loguniform", gspec
+    gen = torch.Generator().manual_seed(seed)
+    u = torch.rand(n, generator=gen, dtype=torch.float64)
+    return [base * 10.0 ** (lo + (hi - lo) * float(x)) for x in u]
+
+
 CONFIGS = {
-    # name: (workload label, shapes, param dtype, grad dtype, grad std (None: heavy_grad), optimizer, hparams)
+    # name: (workload label, shapes, param dtype, grad dtype, grad spec (grad_stds), optimizer, hparams)
     "c4": ("llama7b-shape/CAME8bit/bf16", lambda: llama_shapes(32, 4096, 11008, 32000), torch.bfloat16,
            torch.bfloat16, 2e-4, "CAME8bit", dict(lr=2e-4, weight_decay=1e-2, betas=(0.9, 0.999, 0.9999))),
     "c3": ("llama1b-style/CAME8bitMemory/bf16", lambda: llama_shapes(24, 2048, 5461, 32000), torch.bfloat16,
            torch.bfloat16, 5e-4, "CAME8bitMemory", dict(lr=2e-4, weight_decay=1e-2, betas=(0.9, 0.95, 0.995))),
-    "c2": ("gpt2-medium/CAME8bit/fp32", gpt2_medium_shapes, torch.float32, torch.float32, 1e-3, "CAME8bit",
-           dict(lr=2e-4, weight_decay=1e-2)),
+    "c2": ("gpt2-medium/CAME8bit/fp32", gpt2_medium_shapes, torch.float32, torch.float32, ("loguniform", 1e-3, -5, -2),
+           "CAME8bit", dict(lr=2e-4, weight_decay=1e-2)),
     "c1": ("2048x2048+2048/CAME8bit/fp32", lambda: [(2048, 2048), (2048,)], torch.float32, torch.float32, 1e-3,
            "CAME8bit", dict(lr=2e-4, weight_decay=1e-2)),
     # the Llama-7B matrices stepped by CAME8bit2D (8bit2d layout: momentum in 16x16 tiles; 2-D only)
@@ -154,18 +168,30 @@ def compulsory_bytes(shapes, pdt, gdt, block=256, fp32_state=False, tiles=False)
 CPU_SAMPLE_MAX = 400_000_000  # elements the CPU baseline steps (about 10-20 s of CPU work in all)
 
 
+def sample_index(cfg_name, shapes):
+    """Indices of the tensors the CPU baseline steps (cpu_sample)."""
+    idx = list(range(len(shapes)))
+    if sum(math.prod(s) for s in shapes) <= CPU_SAMPLE_MAX:
+        return idx
+    if cfg_name in ("c3", "c4", "c4fp"):
+        return idx[:10] + idx[-2:]
+    k = 1
+    while sum(math.prod(shapes[i]) for i in idx[::k]) > CPU_SAMPLE_MAX:
+        k += 1
+    return idx[::k]
+
+
 def cpu_sample(cfg_name, shapes):
     """The tensors the CPU baseline steps: the whole workload when it is small enough; for the
     Llama-shaped sets the embedding, the first decoder layer, the final norm and the lm_head (the
     other layers repeat the first); otherwise every k-th tensor."""
-    if sum(math.prod(s) for s in shapes) <= CPU_SAMPLE_MAX:
-        return list(shapes), "the whole workload"
+    idx = sample_index(cfg_name, shapes)
+    sample = [shapes[i] for i in idx]
+    if len(idx) == len(shapes):
+        return sample, "the whole workload"
     if cfg_name in ("c3", "c4", "c4fp"):
-        return shapes[:10] + shapes[-2:], "embedding + decoder layer 0 + final norm + lm_head"
-    k = 1
-    while sum(math.prod(s) for s in shapes[::k]) > CPU_SAMPLE_MAX:
-        k += 1
-    return shapes[::k], f"every {k}-th tensor"
+        return sample, "embedding + decoder layer 0 + final norm + lm_head"
+    return sample, f"every {idx[1] - idx[0]}-th tensor"
 
 
 def cpu_model_name() -> str:
@@ -193,7 +219,9 @@ def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False, tiles=F
     sample, how = cpu_sample(cfg_name, shapes)
     gen = torch.Generator().manual_seed(123)
     params = [(torch.randn(s, generator=gen) * 0.02).to(pdt) for s in sample]
-    grads = [(torch.randn(s, generator=gen) * (gstd or 1e-3)).to(gdt) for s in sample]
+    stds = dict(zip(range(len(shapes)), grad_stds(gstd, len(shapes))))
+    pick = sample_index(cfg_name, shapes)
+    grads = [(torch.randn(s, generator=gen) * (stds[i] or 1e-3)).to(gdt) for s, i in zip(sample, pick)]
     b1, b2, b3 = hp.get("betas", (0.9, 0.999, 0.9999))
     ohp = dict(beta1=b1, beta2=b2, beta3=b3, eps0=1e-30, eps1=1e-16, lr=hp["lr"], clip_threshold=1.0,
                weight_decay=hp.get("weight_decay", 0.0), block_size=256)
@@ -240,65 +268,6 @@ def cpu_baseline(cfg_name, shapes, pdt, gdt, gstd, hp, fp32_state=False, tiles=F
     }
 
 
-# ------------------------------------------------------------------------------------------ probes
-def run_probes():
-    """HBM access-mix probes: each pass's bytes per 8-element chunk of a 16-bit gradient streamed with no
-    arithmetic (came8_probe.hip), with plain and with nontemporal loads and stores, over 2^27 chunks
-    (2 GiB of "gradient"); then one read of a buffer of
-    64 MiB-1 GiB right after reading it, against one read of it after 4 GiB of other reads (the MALL)."""
-    import ctypes
-    from came_amd import build as B
-    lib = ctypes.CDLL(B.PROBE_OUT)
-    lib.came8_probe.restype = ctypes.c_int
-    lib.came8_probe.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
-                                ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
-                                ctypes.POINTER(ctypes.c_float), ctypes.c_void_p]
-    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    n = 1 << 27
-    a = torch.empty(n * 16, dtype=torch.uint8, device="cuda").random_()
-    b = torch.empty(n * 16, dtype=torch.uint8, device="cuda").random_()
-    c = torch.empty(n * 8, dtype=torch.uint8, device="cuda").random_()
-    flush = torch.empty(4 << 30, dtype=torch.uint8, device="cuda").fill_(1)
-    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
-    torch.cuda.synchronize()
-
-    def probe(mode, chunks, nrep, wgs=8, ilp=8, src=None):
-        ms = ctypes.c_float()
-        src = a if src is None else src
-        rc = lib.came8_probe(mode, src.data_ptr(), b.data_ptr(), c.data_ptr(), chunks, nrep, wgs, ilp, sink.data_ptr(),
-                             ctypes.byref(ms), stream)
-        if rc != 0:
-            raise RuntimeError(f"came8_probe mode {mode} failed")
-        return ms.value
-
-    # bytes per chunk read and written; modes 4-7: the same with the nontemporal hint
-    mixes = {"read 16B (pass 1)": (0, 16), "read 16B + 8B (pass 2)": (1, 24),
-             "read 16B, read+write 16B, read+write 8B (pass 3)": (2, 64), "read 16B, write 16B (copy)": (3, 32)}
-    mixes.update({f"{k}, nontemporal": (m + 4, nb) for k, (m, nb) in list(mixes.items())})
-    out = {"chunks": n, "mixes": {}, "reread": {}}
-    for name, (mode, nbytes) in mixes.items():
-        best, shapes = None, {}
-        for wgs in (4, 8, 16):
-            for ilp in (4, 8):
-                probe(mode, n, 1, wgs, ilp)  # warm-up
-                ms = probe(mode, n, 5, wgs, ilp)
-                shapes[f"{wgs}x{ilp}"] = round(nbytes * n / ms / 1e9, 3)
-                if best is None or ms < best[0]:
-                    best = (ms, wgs, ilp)
-        out["mixes"][name] = {"best_TBps": round(nbytes * n / best[0] / 1e9, 3), "best_ms": round(best[0], 4),
-                              "best_shape": f"{best[1]} workgroups/CU x {best[2]} chunks/thread",
-                              "TBps_by_shape": shapes}
-    for mib in (64, 128, 256, 512, 1024):
-        chunks = (mib << 20) // 16
-        probe(0, flush.numel() // 16, 1, src=flush)  # 4 GiB of other reads: the buffer is no longer cached
-        cold = probe(0, chunks, 1)
-        warm = probe(0, chunks, 1)  # right after reading it
-        out["reread"][f"{mib} MiB"] = {"cold_TBps": round(16 * chunks / cold / 1e9, 3),
-                                       "reread_TBps": round(16 * chunks / warm / 1e9, 3),
-                                       "cold_ms": round(cold, 4), "reread_ms": round(warm, 4)}
-    print(json.dumps(out))
-
-
 # ------------------------------------------------------------------------------------------ main
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -312,9 +281,6 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the step, copy a MIB-sized device buffer --steps times (a plain copy "
                          "kernel of known bytes, to scale the FETCH_SIZE / WRITE_SIZE counters)")
-    ap.add_argument("--probes", action="store_true",
-                    help="instead of the step, the HBM access-mix probes (came_amd/csrc/came8_probe.hip): the rate "
-                         "of each pass's byte mix alone, and of a re-read of 64 MiB-1 GiB right after reading it")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); across GPUs the "
@@ -339,10 +305,6 @@ def main():
                           "ms_per_copy": round(dt * 1e3, 4), "GBps_read_plus_write": round(2 * n / dt / 1e9, 1)}))
         return
 
-    if args.probes:
-        run_probes()
-        return
-
     import came_amd
     from came_amd import _lib
 
@@ -352,12 +314,12 @@ def main():
     torch.cuda.set_device(dev)
     gen = torch.Generator(device=dev).manual_seed(0)
     params, grads = [], []
-    for s in shapes:
+    for s, std in zip(shapes, grad_stds(gstd, len(shapes))):
         p = torch.randn(s, device=dev, dtype=torch.float32, generator=gen).mul_(0.02).to(pdt)
-        if gstd is None:
+        if std is None:
             g = heavy_grad(s, gen, gdt, device=dev)
         else:
-            g = torch.randn(s, device=dev, dtype=torch.float32, generator=gen).mul_(gstd).to(gdt)
+            g = torch.randn(s, device=dev, dtype=torch.float32, generator=gen).mul_(std).to(gdt)
         params.append(torch.nn.Parameter(p))
         params[-1].grad = g
         grads.append(g)
@@ -423,7 +385,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded N(0,0.02^2) params, " + ("N(0,std^2)" if gstd else "heavy-tailed Student-t(2)")
+        "data": "synthetic (seeded N(0,0.02^2) params, "
+                + ("heavy-tailed Student-t(2)" if gstd is None else f"N(0,{gstd:g}^2)" if isinstance(gstd, float)
+                   else f"N(0,{gstd[1]:g}^2) x per-tensor 10^U({gstd[2]},{gstd[3]})")
                 + " grads, resident in HBM)",
         "config": {
             "workload": label,

@@ -22,7 +22,6 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "lib")
 OUT = os.path.join(OUT_DIR, "libcame8.so")
-PROBE_OUT = os.path.join(OUT_DIR, "libcame8probe.so")  # bench.py --probes only (HBM access-mix probes)
 ARCH = os.environ.get("CAME8_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -88,12 +87,6 @@ def build(verbose: bool = True, jobs: int | None = None) -> str:
     for o in objs:
         os.remove(o)
     os.replace(tmp, OUT)
-    # the access-mix probes of bench.py --probes: a library of their own, not part of libcame8.so
-    ptmp = PROBE_OUT + ".tmp"
-    rc, errs = _run([cc, *HIPCC_FLAGS, "-shared", "-o", ptmp, os.path.join(CSRC, "came8_probe.hip")])
-    if rc != 0:
-        raise RuntimeError(f"hipcc failed on came8_probe.hip ({rc}):\n{errs}")
-    os.replace(ptmp, PROBE_OUT)
     return OUT
 
 

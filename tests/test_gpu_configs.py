@@ -76,6 +76,7 @@ def test_baseline_config_full_size_vs_oracle(name):
     _lib.load()
     label, shapes_fn, pdt, gdt, gstd, cls_name, hp = bench.CONFIGS[name]
     shapes = shapes_fn()
+    stds = bench.grad_stds(gstd, len(shapes))  # c2: a per-tensor scale, log-uniform in [1e-5, 1e-2]
     dev = torch.device("cuda", 0)
     gen = torch.Generator(device=dev).manual_seed(17)
     ps = [torch.nn.Parameter(torch.randn(s, device=dev, generator=gen).mul_(0.02).to(pdt)) for s in shapes]
@@ -90,7 +91,7 @@ def test_baseline_config_full_size_vs_oracle(name):
     n_el = sum(math.prod(s) for s in shapes)
     print(f"[{name}] {label}: {len(shapes)} tensors, {n_el} elements; checked {[shapes[i] for i in chk]}", flush=True)
     for step in range(2):
-        grads = [torch.randn(s, device=dev, generator=gen).mul_(gstd).to(gdt) for s in shapes]
+        grads = [torch.randn(s, device=dev, generator=gen).mul_(std).to(gdt) for s, std in zip(shapes, stds)]
         with torch.no_grad():
             for i in chk:
                 ps[i].data.copy_(refs[i].to(dev))
