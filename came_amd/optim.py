@@ -44,6 +44,27 @@ _VIEW_KEYS = (
 )
 
 
+# The reference's per-parameter routing flags.  Its CPU path writes every one as False
+# (CAME8bitFull.py:783-787, 921; CAME8bitMemory.py:431-447; CAMECUDA.py:117-118); so does this build,
+# whose kernels read none of the per-tensor scratch buffers a True flag promises the reference.
+_FACTORED_FLAGS = ("_cuda_factored_fastpath", "_cuda_factored_nd_ext_path", "_cuda_factored_nd_chunked_ext_path",
+                   "_cuda_factored_ext_path")
+_NONFACTORED_FLAGS = ("_cuda_nonfactored_fastpath",)
+_FP32_FLAGS = ("_cuda_fp_factored_fastpath", "_cuda_fp_nonfactored_fastpath")
+# Per-tensor scratch the reference's CUDA paths keep in the state (CAME8bitFull.py:790-937,
+# CAMECUDA.py:120-140; 12-16 bytes per element).  A state loaded from such a run drops them (the
+# library's workspace replaces them) and its flags are set False, so the state saved back loads in the
+# reference, which then takes its generic path.
+_REFERENCE_SCRATCH_KEYS = (
+    "exp_avg_fp32", "scratch_fp32", "grad_fp32", "update_fp32", "_cuda_nonfactored_update_fp16",
+    "row_factor_fp32", "col_factor_fp32", "row_mean_fp32", "factored_row_fp32", "factored_col_fp32",
+    "row_absmax_scratch", "reduce_partial", "sum_row_state", "sum_update", "sum_update_partial",
+    "sum_update_slice", "sum_update_chunk", "sum_update_equiv", "row_workspace", "col_workspace",
+    "param_workspace", "matrix_rows", "matrix_cols", "prefix_batch", "nd_chunk_size",
+    "_cuda_factored_nd_chunked_direct_row_sum",
+)
+
+
 def _release_workspace(ptr: int) -> None:
     try:
         _lib.load().came8_release_workspace(ptr)
@@ -56,6 +77,7 @@ class _Came8Base(torch.optim.Optimizer):
 
     _MODE = "full8bit"                 # state["_mode"] of this optimizer's layout
     _STATE_KIND = _lib.CAME8_STATE_Q8  # how the library reads the state pointers
+    _VIEWS_BEFORE_FLAGS = False        # the reference's key order (CAME8bitMemory: views first)
 
     def _validate_and_defaults(self, lr, eps, clip_threshold, betas, weight_decay, block_size):
         # came_pytorch/CAME8bitFull.py:73-91
@@ -107,10 +129,16 @@ class _Came8Base(torch.optim.Optimizer):
                 row_shape, batch_size=2, device=grad.device, signed=False, block_size=block_size)
             state["factored_col_q"], state["factored_col_absmax"] = init_batched_qstate(
                 col_shape, batch_size=2, device=grad.device, signed=False, block_size=block_size)
+            if self._VIEWS_BEFORE_FLAGS:
+                self._bind_factored_views(state)
+            for k in _FACTORED_FLAGS:
+                state[k] = False
             self._bind_factored_views(state)
         else:
             state["exp_avg_sq_q"], state["exp_avg_sq_absmax"] = init_qstate(
                 grad.shape, device=grad.device, signed=False, block_size=block_size)
+            for k in _NONFACTORED_FLAGS:
+                state[k] = False
 
     def _check_state(self, p: torch.Tensor, state: dict, block_size: int) -> None:
         if tuple(state["exp_avg_q"].shape) != tuple(p.shape):
@@ -176,6 +204,15 @@ class _Came8Base(torch.optim.Optimizer):
         src = state_layout.layout_of(state)
         if not src or src == self._MODE or (self._MODE == "8bit2d" and p.dim() != 2):
             return
+        if src == "8bit1d" and self._MODE == "full8bit" and p.dim() == 1:
+            # the reference CAME8bit's 1-D batched-path states (CAME8bit.py:252-262) keep full8bit's
+            # 1-D tensors under another _mode: relabelled, codes untouched
+            state["_mode"] = "full8bit"
+            for k in ("_cuda_nonfactored_batched_fastpath", "_cuda_nonfactored_multitensor_fastpath",
+                      "_cuda_batched_update_fp16"):
+                state.pop(k, None)
+            self._after_load(state)
+            return
         block_size = int(self._group_of(p).get("block_size", 256))
         new = state_layout.convert_state(state, tuple(p.shape), self._MODE, block_size)
         state.clear()
@@ -189,8 +226,20 @@ class _Came8Base(torch.optim.Optimizer):
         self._after_load(state)
 
     def _after_load(self, state: dict) -> None:
+        self._drop_reference_scratch(state)
         if state.get("factored") and "factored_row_q" in state:
             self._bind_factored_views(state)
+
+    def _drop_reference_scratch(self, state: dict) -> None:
+        # a state already in this optimizer's own layout (not the reference's per-matrix N-D blocks,
+        # which load_state_dict converts next, and not 8bit2d, whose state keeps its partial buffers)
+        if self._MODE != "8bit2d" and state_layout.layout_of(state) == self._MODE:
+            for k in _REFERENCE_SCRATCH_KEYS:
+                state.pop(k, None)
+            flags = _FP32_FLAGS if self._MODE == "cudafp" else (
+                _FACTORED_FLAGS if state.get("factored") else _NONFACTORED_FLAGS)
+            for k in flags:
+                state[k] = False
 
     # ------------------------------------------------------------------- step
     def _group_hparams(self, group: dict) -> _lib.Came8HParams:
@@ -464,6 +513,8 @@ class CAME8bitMemory(CAME8bitFull):
                          weight_decay=weight_decay, block_size=block_size,
                          prefer_factored_cuda_ext_path=False, cuda_nonfactored_use_fp16_update=False)
 
+    _VIEWS_BEFORE_FLAGS = True  # CAME8bitMemory.py:423-436
+
 
 class CAME8bit(CAME8bitFull):
     """Single-entry 8-bit CAME (reference came_pytorch/CAME8bit.py:24).
@@ -711,6 +762,8 @@ class CAMECUDA(_Came8Base):
                 state[k] = torch.zeros(sh, device=grad.device, dtype=torch.float32)
         else:
             state["exp_avg_sq"] = torch.zeros(shape, device=grad.device, dtype=torch.float32)
+        for k in _FP32_FLAGS:
+            state[k] = False
 
     def _check_state(self, p: torch.Tensor, state: dict, block_size: int) -> None:
         if tuple(state["exp_avg"].shape) != tuple(p.shape):
@@ -738,7 +791,7 @@ class CAMECUDA(_Came8Base):
             d.row_absmax = None
 
     def _after_load(self, state: dict) -> None:
-        pass
+        self._drop_reference_scratch(state)
 
 
 _TILE_2D = 16

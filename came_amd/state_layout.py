@@ -144,7 +144,7 @@ def state_values(state: dict, shape, block_size: int = 256) -> dict:
             out[k] = _deq_blocks(state[f"exp_avg_{k}_q"], state[f"exp_avg_{k}_absmax"], signed=False,
                                  block_size=256)
         return out
-    if mode in ("full8bit", "full8bit-nd"):
+    if mode in ("full8bit", "full8bit-nd", "8bit1d"):  # 8bit1d: CAME8bit's 1-D states, full8bit's keys
         nd = mode == "full8bit-nd"
         prefix = math.prod(shape[:-2]) if factored else 1
         items = prefix if nd else 1

@@ -98,9 +98,14 @@ def init_full8bit_state(shape, block_size: int = 256) -> Dict[str, object]:
         st["factored_row_absmax"] = torch.ones((2, num_blocks(math.prod(row_shape), block_size)), dtype=torch.float32)
         st["factored_col_q"] = torch.zeros((2,) + col_shape, dtype=torch.uint8)
         st["factored_col_absmax"] = torch.ones((2, num_blocks(math.prod(col_shape), block_size)), dtype=torch.float32)
+        # the CUDA routing flags, all False on CPU (CAME8bitFull.py:783-787)
+        for k in ("_cuda_factored_fastpath", "_cuda_factored_nd_ext_path", "_cuda_factored_nd_chunked_ext_path",
+                  "_cuda_factored_ext_path"):
+            st[k] = False
     else:
         st["exp_avg_sq_q"] = torch.zeros(shape, dtype=torch.uint8)
         st["exp_avg_sq_absmax"] = torch.ones(num_blocks(numel, block_size), dtype=torch.float32)
+        st["_cuda_nonfactored_fastpath"] = False  # CAME8bitFull.py:921
     return st
 
 
@@ -240,6 +245,8 @@ def init_fp32_state(shape) -> Dict[str, object]:
         st["exp_avg_res_col"] = torch.zeros(shape[:-2] + shape[-1:], dtype=torch.float32)
     else:
         st["exp_avg_sq"] = torch.zeros(shape, dtype=torch.float32)
+    st["_cuda_fp_factored_fastpath"] = False  # CAMECUDA.py:117-118, False on CPU
+    st["_cuda_fp_nonfactored_fastpath"] = False
     return st
 
 

@@ -2,10 +2,12 @@
 include/came8.h declares, argument validation returns the documented error codes before any device
 work, and the optimizer classes keep the reference's constructor validation and state layout."""
 import ctypes
+import json
 import os
 import re
 import warnings
 
+import numpy as np
 import pytest
 import torch
 
@@ -149,6 +151,82 @@ def test_state_layout_matches_reference(shape, block):
             assert st[k] == v, k
     if len(shape) >= 2:
         assert st["exp_avg_res_col_q"].data_ptr() == st["factored_col_q"][1].data_ptr()
+
+
+_VIEWS = {"exp_avg_sq_row_q", "exp_avg_res_row_q", "exp_avg_sq_col_q", "exp_avg_res_col_q",
+          "exp_avg_sq_row_absmax", "exp_avg_res_row_absmax", "exp_avg_sq_col_absmax", "exp_avg_res_col_absmax"}
+
+
+def _golden_key_sets(path, case):
+    """{tensor index: {key: value or None}} of the reference's states after step 1, as the golden file
+    recorded them: every key but the views of the stacked row/column states and the _mode string."""
+    z = np.load(path)
+    out = {}
+    pre = f"{case}/s1/"
+    for k in z.keys():
+        if k.startswith(pre):
+            i, key = k[len(pre):].split("/", 1)
+            v = z[k]
+            out.setdefault(int(i), {})[key] = v.item() if v.ndim == 0 and v.dtype == np.bool_ else None
+    return out
+
+
+@pytest.mark.parametrize("case", ["full_ragged_fp32", "came8bit_heavy_fp32", "memory_bf16", "came8bit_bs64_clip"])
+def test_state_key_set_matches_reference(golden_dir, case):
+    """Each state holds exactly the reference's keys (golden_small.npz, written by the reference's own CPU
+    path), its CUDA routing flags included with the reference's CPU values (all False), plus _mode and,
+    for factored tensors, the eight views."""
+    meta = json.loads(str(np.load(os.path.join(golden_dir, "golden_small.npz"))["meta_json"]))[case]
+    ref = _golden_key_sets(os.path.join(golden_dir, "golden_small.npz"), case)
+    cls = getattr(came_amd, meta["cls"])
+    block = meta["hp"].get("block_size", 256)
+    for i, shape in enumerate(meta["shapes"]):
+        p = torch.nn.Parameter(torch.zeros(shape))
+        opt = cls([p], lr=1e-3, block_size=block) if meta["cls"] != "CAME8bitMemory" else cls([p], lr=1e-3)
+        st = {}
+        opt._init_state(st, torch.zeros(shape), block)
+        want = set(ref[i]) | {"_mode"} | (_VIEWS if len(shape) >= 2 else set())
+        assert set(st) == want, (case, shape, sorted(set(st) ^ want))
+        for k, v in ref[i].items():
+            if v is not None:  # the boolean flags
+                assert st[k] is v, (case, shape, k, st[k], v)
+
+
+def test_camecuda_state_key_set_matches_reference(golden_dir):
+    path = os.path.join(golden_dir, "golden_camecuda.npz")
+    meta = json.loads(str(np.load(path)["meta_json"]))
+    for case, m in meta.items():
+        if not isinstance(m, dict) or "shapes" not in m:
+            continue
+        ref = _golden_key_sets(path, case)
+        for i, shape in enumerate(m["shapes"]):
+            opt = came_amd.CAMECUDA([torch.nn.Parameter(torch.zeros(shape))], lr=1e-3)
+            st = {}
+            opt._init_state(st, torch.zeros(shape), 256)
+            assert set(st) == set(ref[i]) | {"_mode"}, (case, shape, sorted(set(st) ^ (set(ref[i]) | {"_mode"})))
+            for k, v in ref[i].items():
+                if v is not None:
+                    assert st[k] is v, (case, shape, k)
+
+
+def test_loaded_reference_cuda_state_drops_its_scratch():
+    """A state saved by the reference's CUDA path (flags True, per-tensor fp32 scratch) loads with the flags
+    False and the scratch dropped (the library's workspace replaces it)."""
+    p = torch.nn.Parameter(torch.zeros(40, 60))
+    opt = came_amd.CAME8bitFull([p], lr=1e-3)
+    st = {}
+    opt._init_state(st, torch.zeros(40, 60), 256)
+    saved = {k: v for k, v in st.items() if k not in _VIEWS}
+    saved["_cuda_factored_fastpath"] = saved["_cuda_factored_ext_path"] = True
+    saved["exp_avg_fp32"] = torch.zeros(40, 60)
+    saved["scratch_fp32"] = torch.zeros(40, 60)
+    saved["sum_update"] = torch.zeros(1)
+    sd = {"state": {0: saved}, "param_groups": [dict(opt.state_dict()["param_groups"][0])]}
+    opt2 = came_amd.CAME8bitFull([p], lr=1e-3)
+    opt2.load_state_dict(sd)
+    live = opt2.state[p]
+    assert set(live) == set(st), sorted(set(live) ^ set(st))
+    assert live["_cuda_factored_fastpath"] is False and live["_cuda_factored_ext_path"] is False
 
 
 def test_load_state_dict_keeps_dtypes_mode_and_copies():
