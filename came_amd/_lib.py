@@ -15,11 +15,12 @@ LIB_PATH = os.path.join(HERE, "lib", "libcame8.so")
 
 CAME8_F32, CAME8_BF16, CAME8_F16 = 0, 1, 2
 CAME8_OK, CAME8_EINVAL, CAME8_ESPACE, CAME8_EHIP = 0, -1, -2, -3
-ABI_VERSION = 4  # include/came8.h: CAME8_ABI_VERSION
+ABI_VERSION = 5  # include/came8.h: CAME8_ABI_VERSION
 CAME8_FLAG_REFERENCE_NORM = 1  # the default (accepted for callers of ABI 3)
 CAME8_FLAG_EXACT_NORM = 2
 CAME8_FLAG_PLAN_ONLY = 4
 CAME8_FLAG_FP16_UPDATE = 8
+CAME8_TENSOR_FP16_UPDATE = 1  # came8_tensor.tensor_flags
 CAME8_STATE_Q8 = 0
 CAME8_STATE_FP32 = 1
 CAME8_STATE_8BIT2D = 2
@@ -66,6 +67,8 @@ class Came8Tensor(ctypes.Structure):
         ("res_col_absmax", ctypes.c_void_p),
         ("res_row_partial", ctypes.c_void_p),
         ("res_col_partial", ctypes.c_void_p),
+        ("tensor_flags", ctypes.c_uint32),
+        ("reserved", ctypes.c_int32),
     ]
 
 

@@ -391,6 +391,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       if (dt != CAME8_F32 && dt != CAME8_BF16 && dt != CAME8_F16) return fail(CAME8_EINVAL, who + "unsupported dtype");
     if (t.prefix < 1 || t.rows < 1 || t.cols < 1) return fail(CAME8_EINVAL, who + "empty or negative shape");
     if (!t.factored && (t.prefix != 1 || t.rows != 1)) return fail(CAME8_EINVAL, who + "1-D tensors take prefix = rows = 1");
+    if ((t.tensor_flags & ~CAME8_TENSOR_FP16_UPDATE) != 0 || t.reserved != 0)
+      return fail(CAME8_EINVAL, who + "unknown tensor_flags bits or nonzero reserved field");
     if (t.factored && (!t.col_q || !t.col_absmax)) return fail(CAME8_EINVAL, who + "null column state");
     if ((B & (B - 1)) != 0 && t.prefix * t.rows * t.cols >= (int64_t(1) << 31))
       return fail(CAME8_EINVAL, who + "block sizes that are not powers of two need fewer than 2^31 elements");
@@ -410,6 +412,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     d.nbm = std::max<int64_t>(1, ceil_div(d.N, B));
     d.factored = t.factored ? 1 : 0;
     d.fp32st = f32st ? 1 : 0;
+    d.fp16u = (!t.factored && !f32st && !s2d && (t.tensor_flags & CAME8_TENSOR_FP16_UPDATE)) ? 1 : 0;
     d.mode2d = s2d ? 1 : 0;
     bool v2d = false, v2dp = false;  // vector forms of the 8bit2d momentum pass / parameter write
     if (s2d) {

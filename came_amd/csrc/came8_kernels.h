@@ -101,6 +101,7 @@ struct DevTensor {
   float* t2row;
   float* t2col;
   int32_t v2d, v2dp;  // vector forms of the momentum pass / parameter write apply
+  int32_t fp16u;      // this unfactored tensor takes the fp16-rounded update (CAME8_TENSOR_FP16_UPDATE)
 };
 
 // fp32-state views of the state pointers
@@ -1732,7 +1733,7 @@ __global__ __launch_bounds__(kThreads) void k_vec_passB(const DevTensor* __restr
         const float gv = TG::load(g[e]);
         vv[v] = vec_v_new<TG>(t, e, gv, hp);
         float uu = rsqrt_ref(vv[v]) * gv;
-        if (hp.fp16u && !t.fp32st) uu = round_f16(uu);
+        if ((hp.fp16u || t.fp16u) && !t.fp32st) uu = round_f16(uu);
         const float u = uu / clip;
         const float mold = t.fp32st ? st_m(t)[e] : deq_s8(t.mq[e], t.ma[blk_of(e, hp)]);
         m[v] = fmaf(u, hp.a1, mold * hp.b1);
@@ -1808,7 +1809,7 @@ __global__ __launch_bounds__(kThreads) void k_vec_passB(const DevTensor* __restr
 template <typename TG>
 __device__ __forceinline__ float m_new_fact(const DevTensor& t, int64_t e, float clip, const Hp& hp) {
   float uu = u_at<TG>(t, e, hp);
-  if (hp.fp16u && !t.factored) uu = round_f16(uu);
+  if ((hp.fp16u || t.fp16u) && !t.factored) uu = round_f16(uu);
   const float u = uu / clip;
   return fmaf(u, hp.a1, deq_s8(t.mq[e], t.ma[blk_of(e, hp)]) * hp.b1);
 }

@@ -26,7 +26,7 @@ import math
 import time
 import warnings
 import weakref
-from collections import defaultdict
+from collections import Counter, defaultdict
 from itertools import chain
 
 import torch
@@ -246,12 +246,6 @@ class _Came8Base(torch.optim.Optimizer):
         b1, b2, b3 = group["betas"]
         e0, e1 = group["eps"]
         flags = _lib.CAME8_FLAG_EXACT_NORM if getattr(self, "exact_norm", False) else 0
-        # the reference's fp16-update kernels for unfactored tensors (CAME8bitFull.py:488-509; CAME8bit
-        # selects them with cuda_1d_batched_use_fp16_update or the repeated_fp16_pairmin runtime mode,
-        # CAME8bit.py:142-156); one launch steps every 1-D tensor here, so the flag covers all of them
-        if getattr(self, "cuda_nonfactored_use_fp16_update", False) or getattr(self, "cuda_1d_batched_use_fp16_update",
-                                                                               False):
-            flags |= _lib.CAME8_FLAG_FP16_UPDATE
         return _lib.Came8HParams(float(group["lr"]), float(b1), float(b2), float(b3), float(e0), float(e1),
                                  float(group["clip_threshold"]), float(group["weight_decay"]),
                                  int(group["block_size"]), flags)
@@ -353,7 +347,7 @@ class _Came8Base(torch.optim.Optimizer):
             if not items:
                 continue
             n = len(items)
-            descs, keep, copyback = self._descriptors(items)
+            descs, keep, copyback = self._descriptors(items, block_size)
             ws, tag = self._workspace(group, device, descs, n, block_size)
             with torch.cuda.device(device):
                 stream = torch.cuda.current_stream(device).cuda_stream
@@ -365,11 +359,20 @@ class _Came8Base(torch.optim.Optimizer):
             for p, pd in copyback:
                 p.data.copy_(pd)
 
-    def _descriptors(self, items: list):
+    def _fp16_update_tensors(self, items: list, block_size: int) -> list:
+        """Which of the (param, state, grad) items take the reference's fp16-update rounding of the 1-D update
+        (CAME8_TENSOR_FP16_UPDATE): with cuda_nonfactored_use_fp16_update every unfactored tensor, as the
+        reference's CAME8bitFull nonfactored CUDA step selects its fp16-update kernel for all of them
+        (CAME8bitFull.py:485-490)."""
+        on = bool(getattr(self, "cuda_nonfactored_use_fp16_update", False)) and self._STATE_KIND == _lib.CAME8_STATE_Q8
+        return [on and not self._is_factored(st) for _, st, _ in items]
+
+    def _descriptors(self, items: list, block_size: int = 256):
         """came8_tensor descriptors of (param, state, grad) triples (include/came8.h), the contiguous
         gradient copies they point to, and (param, contiguous copy) pairs to write back after the step."""
         descs = (_lib.Came8Tensor * len(items))()
         keep, copyback = [], []
+        fp16u = self._fp16_update_tensors(items, block_size)
         for i, (p, state, grad) in enumerate(items):
             pd = p.data
             if not pd.is_contiguous():
@@ -391,6 +394,7 @@ class _Came8Base(torch.optim.Optimizer):
             else:
                 d.prefix, d.rows, d.cols = 1, 1, p.numel()
                 d.factored = 0
+            d.tensor_flags = _lib.CAME8_TENSOR_FP16_UPDATE if fp16u[i] else 0
             self._fill_desc(d, p, state)
         return descs, keep, copyback
 
@@ -658,6 +662,40 @@ class CAME8bit(CAME8bitFull):
         return tuple(k for k, default in cls.EXPERIMENTAL_CUDA_TUNING_DEFAULTS.items() if kwargs[k] != default)
 
     @torch.no_grad()
+    def _fp16_update_tensors(self, items: list, block_size: int) -> list:
+        """The reference's per-tensor choice of the fp16-update kernels (CAME8bit.py:224-245 predicates,
+        :712-861 per-parameter routing, :862-891 bucket flush, :441-529 multi-tensor step).  A contiguous
+        1-D CUDA tensor:
+
+        - with prefer_cuda_1d_fast_path, in the batched size range [cuda_1d_batched_min_numel,
+          cuda_1d_batched_max_numel] under prefer_cuda_1d_batched_fast_path, and in a bucket of at least
+          cuda_1d_batched_min_bucket_size tensors of its device, dtype and length: the multi-tensor kernels
+          when prefer_cuda_1d_multitensor_fast_path is set, fp16 update iff cuda_1d_batched_use_fp16_update;
+          else the batched kernel, whose update is always fp32;
+        - otherwise (the single-tensor 1-D path or the full8bit direct path): fp16 update iff
+          cuda_nonfactored_use_fp16_update.
+
+        Other tensors (factored, or not contiguous: the reference's generic path) keep the fp32 update."""
+        def fast_1d(p, g):
+            return p.is_cuda and p.dim() == 1 and p.is_contiguous() and g.is_contiguous()
+
+        def batched(p, g):
+            return (self.prefer_cuda_1d_fast_path and self.prefer_cuda_1d_batched_fast_path and fast_1d(p, g)
+                    and self.cuda_1d_batched_min_numel <= p.numel() <= self.cuda_1d_batched_max_numel
+                    and block_size > 0)
+
+        buckets = Counter((p.device, p.dtype, p.numel()) for p, st, g in items
+                          if not self._is_factored(st) and batched(p, g))
+        out = []
+        for p, st, g in items:
+            if self._is_factored(st) or not fast_1d(p, g):
+                out.append(False)
+            elif batched(p, g) and buckets[(p.device, p.dtype, p.numel())] >= self.cuda_1d_batched_min_bucket_size:
+                out.append(self.prefer_cuda_1d_multitensor_fast_path and self.cuda_1d_batched_use_fp16_update)
+            else:
+                out.append(bool(self.cuda_nonfactored_use_fp16_update))
+        return out
+
     def prime_for_cuda_graph(self) -> None:
         """Create every state, the workspace and its uploaded launch plan before capture
         (CAME8bit.py:672-693), so that a captured step only enqueues kernel launches."""

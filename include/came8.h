@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define CAME8_ABI_VERSION 4
+#define CAME8_ABI_VERSION 5
 
 /* element types of parameters and gradients */
 #define CAME8_F32 0
@@ -79,6 +79,12 @@ extern "C" {
                                         1546-1601; selected by CAME8bitFull.py:488-509, and always by
                                         CAME8bitMemory.py:524-557).  The clip's norm stays that of the fp32
                                         update.  Lossy: the update moves by up to 2^-11 relative. */
+
+/* flags for came8_tensor.tensor_flags */
+#define CAME8_TENSOR_FP16_UPDATE 1u  /* this unfactored tensor takes the fp16-update rounding of
+                                        CAME8_FLAG_FP16_UPDATE on its own: the reference selects those kernels
+                                        per tensor (CAME8bit routes a 1-D tensor to them only on some of its
+                                        paths, came_pytorch/CAME8bit.py:224-245,441-529,712-861) */
 
 /*
  * One parameter tensor and its full8bit state, laid out exactly as the
@@ -155,6 +161,8 @@ typedef struct came8_tensor {
   float* res_col_absmax;
   float* res_row_partial;  /* CAME8_STATE_8BIT2D only, optional (NULL: workspace) */
   float* res_col_partial;
+  uint32_t tensor_flags;   /* CAME8_TENSOR_* (ABI 5) */
+  int32_t reserved;        /* 0 */
 } came8_tensor;
 
 /* Hyper-parameters of one param group (the reference's group keys, as Python floats). */

@@ -11,6 +11,8 @@ by the reference's CUDA CAME8bitMemory for 1-D tensors, CAME8bitMemory.py:524-55
     of the two variants part by at most lr * (1 - beta1) * |u / clip| * 2^-11 (half an fp16 ulp,
     relative) plus the usual 1e-5 relative.
   * Matrices are unaffected: with the flag set they step bit for bit as without it.
+  * CAME8bit chooses per tensor, as the reference routes each 1-D tensor (CAME8_TENSOR_FP16_UPDATE):
+    seven kwarg combinations over one tensor set that exercises every route.
 """
 import pytest
 import torch
@@ -106,3 +108,63 @@ def test_fp16_update_leaves_matrices_alone():
     for a, b in zip(out[False][0] + out[False][1], out[True][0] + out[True][1]):
         assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
                            b.view(torch.int16) if b.dtype == torch.bfloat16 else b)
+
+
+# ------------------------------------------------------------------ CAME8bit's per-tensor selection
+# The reference's CAME8bit takes the fp16-update kernels for a 1-D tensor only on some of its routes
+# (CAME8bit.py:224-245, 441-529, 712-891); which ones depends on the kwargs and on the tensor's bucket
+# (device, dtype, length) within the group.  Tensors: a bucket of five 2048-long vectors (batched range
+# [1024, 65536], bucket >= 4), a bucket of two 4096-long ones (below the minimum bucket), lengths outside the
+# range (512, 100003), a non-contiguous gradient (the reference's generic path) and a matrix.
+SEL_SHAPES = [(2048,)] * 5 + [(4096,)] * 2 + [(512,), (100003,), (3000,), (64, 96)]
+NONCONTIG = 9  # index of the tensor whose gradient is a strided view
+SEL_CASES = {
+    "default": ({}, [False] * 11),
+    "batched_fp16_alone": ({"cuda_1d_batched_use_fp16_update": True}, [False] * 11),
+    "batched_no_multitensor": ({"prefer_cuda_1d_batched_fast_path": True, "cuda_1d_batched_use_fp16_update": True},
+                               [False] * 11),
+    "multitensor_fp16": ({"prefer_cuda_1d_batched_fast_path": True, "prefer_cuda_1d_multitensor_fast_path": True,
+                          "cuda_1d_batched_use_fp16_update": True}, [True] * 5 + [False] * 6),
+    "nonfactored_fp16": ({"cuda_nonfactored_use_fp16_update": True}, [True] * 9 + [False, False]),
+    "multitensor_fp32_rest_fp16": ({"prefer_cuda_1d_batched_fast_path": True,
+                                    "prefer_cuda_1d_multitensor_fast_path": True,
+                                    "cuda_nonfactored_use_fp16_update": True}, [False] * 5 + [True] * 4 + [False] * 2),
+    "repeated_fp16_pairmin": ({"cuda_1d_runtime_mode": "repeated_fp16_pairmin"}, [True] * 9 + [False, False]),
+}
+
+
+@pytest.mark.filterwarnings("ignore::RuntimeWarning")
+@pytest.mark.parametrize("case", sorted(SEL_CASES))
+def test_came8bit_fp16_update_selection_per_tensor(case):
+    kw, want = SEL_CASES[case]
+    params = P.make_params(SEL_SHAPES, torch.float32, seed=101)
+    gen = torch.Generator().manual_seed(103)
+    grads = [P.heavy_grad(gen, s, torch.float32) for s in SEL_SHAPES]
+    hp = dict(lr=1e-3, weight_decay=1e-2)
+    ohp = P.oracle_hp(hp)
+    ps = [torch.nn.Parameter(p.clone().cuda()) for p in params]
+    opt = came_amd.CAME8bit(ps, **hp, **kw)
+    for i, (p, g) in enumerate(zip(ps, grads)):
+        if i == NONCONTIG:
+            wide = torch.zeros(2 * g.numel(), device="cuda")
+            wide[::2] = g.cuda()
+            p.grad = wide[::2]
+            assert not p.grad.is_contiguous()
+        else:
+            p.grad = g.cuda()
+    opt.step()
+    torch.cuda.synchronize()
+    check = _tight_step_check(f"CAME8bit {case}")
+    for i, (p0, g) in enumerate(zip(params, grads)):
+        outs = {}
+        for fp16 in (False, True):
+            r, st, cap = p0.clone(), orc.init_full8bit_state(p0.shape), {}
+            orc.full8bit_step(r, g, st, capture=cap, fp16_update=fp16, **ohp)
+            outs[fp16] = (r, st, cap)
+        r, st, cap = outs[want[i]]
+        check(1, i, ps[i].data, r, opt.state[ps[i]], st, (r.double() - p0.double()).abs(), cap)
+        if p0.dim() == 1 and p0.numel() >= 2048:  # the choice is visible: nearer the expected variant
+            gp = ps[i].data.cpu().double()
+            d_want = (gp - outs[want[i]][0].double()).abs().max().item()
+            d_other = (gp - outs[not want[i]][0].double()).abs().max().item()
+            assert d_want < d_other, f"{case} tensor {i} {SEL_SHAPES[i]}: fp16 update {not want[i]} fits better"

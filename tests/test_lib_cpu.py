@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     assert set(declared) == set(L.EXPORTED_SYMBOLS), declared
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.came8_abi_version() == L.ABI_VERSION == 4
+    assert lib.came8_abi_version() == L.ABI_VERSION == 5
     assert b"gfx950" in lib.came8_version()
 
 
