@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "came8_profile_enable",
     "came8_profile_read",
     "came8_read_clip",
+    "came8_side_stream_count",
     "came8_quantize_blockwise",
     "came8_dequantize_blockwise",
 )
@@ -148,6 +149,8 @@ def load(path: str | None = None) -> ctypes.CDLL:
         lib.came8_step_static.restype = ctypes.c_int
         lib.came8_step_static.argtypes = [ctypes.POINTER(Came8Tensor), i32, ctypes.POINTER(Came8HParams), vp]
         lib.came8_profile_enable.restype = ctypes.c_int
+        lib.came8_side_stream_count.restype = ctypes.c_int
+        lib.came8_side_stream_count.argtypes = []
         lib.came8_profile_enable.argtypes = [i32]
         lib.came8_profile_read.restype = ctypes.c_int
         lib.came8_profile_read.argtypes = [ctypes.POINTER(Came8PhaseStat), i32, ctypes.POINTER(i32), i32]

@@ -976,25 +976,84 @@ struct SideQueue {
   hipStream_t s = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
 };
+// One side stream and two events per (device, caller stream).  Those not in use by a step are idle; at
+// most kMaxIdleSideQueues idle ones are kept: when a new one is needed beyond that, the least recently
+// used idle one is released once its work has completed.
+constexpr size_t kMaxIdleSideQueues = 16;
+struct SideEntry {
+  SideQueue q;
+  uint64_t last = 0;  // the step that last took it
+  int users = 0;      // steps holding it now
+};
 std::mutex g_side_mu;
-std::map<std::pair<int, hipStream_t>, SideQueue> g_side;
+std::map<std::pair<int, hipStream_t>, SideEntry> g_side;
+uint64_t g_side_tick = 0;
 
-int side_queue(hipStream_t caller, SideQueue* out) {
+void destroy_side(SideQueue& q) {
+  if (q.s) {
+    (void)hipStreamSynchronize(q.s);
+    (void)hipStreamDestroy(q.s);
+  }
+  if (q.fork) (void)hipEventDestroy(q.fork);
+  if (q.join) (void)hipEventDestroy(q.join);
+  q = SideQueue{};
+}
+
+// A step's hold on its side stream (released when the step's launches are queued).
+struct SideLease {
+  std::pair<int, hipStream_t> key{-1, nullptr};
+  bool held = false;
+  SideLease() = default;
+  SideLease(const SideLease&) = delete;
+  SideLease& operator=(const SideLease&) = delete;
+  ~SideLease() {
+    if (!held) return;
+    std::lock_guard<std::mutex> lk(g_side_mu);
+    auto it = g_side.find(key);
+    if (it != g_side.end()) --it->second.users;
+  }
+};
+
+int side_queue(hipStream_t caller, SideQueue* out, SideLease* lease) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess) return fail(CAME8_EHIP, "came8_step: no current HIP device");
+  const auto key = std::make_pair(dev, caller);
   std::lock_guard<std::mutex> lk(g_side_mu);
-  auto it = g_side.find(std::make_pair(dev, caller));
+  auto it = g_side.find(key);
   if (it == g_side.end()) {
-    SideQueue q;
-    if (hipStreamCreateWithFlags(&q.s, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&q.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&q.join, hipEventDisableTiming) != hipSuccess)
-      return fail(CAME8_EHIP, std::string("came8_step: creating the side stream failed: ") +
-                                  hipGetErrorString(hipGetLastError()));
-    it = g_side.emplace(std::make_pair(dev, caller), q).first;
+    size_t idle = 0;
+    auto lru = g_side.end();
+    for (auto e = g_side.begin(); e != g_side.end(); ++e) {
+      if (e->second.users) continue;
+      ++idle;
+      if (lru == g_side.end() || e->second.last < lru->second.last) lru = e;
+    }
+    if (idle >= kMaxIdleSideQueues) {
+      destroy_side(lru->second.q);
+      g_side.erase(lru);
+    }
+    SideEntry ent;
+    if (hipStreamCreateWithFlags(&ent.q.s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&ent.q.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&ent.q.join, hipEventDisableTiming) != hipSuccess) {
+      const hipError_t e = hipGetLastError();
+      destroy_side(ent.q);
+      return fail(CAME8_EHIP, std::string("came8_step: creating the side stream failed: ") + hipGetErrorString(e));
+    }
+    it = g_side.emplace(key, ent).first;
   }
-  *out = it->second;
+  ++it->second.users;
+  it->second.last = ++g_side_tick;
+  lease->key = key;
+  lease->held = true;
+  *out = it->second.q;
   return CAME8_OK;
+}
+
+// Side streams kept now (idle and in use), for tests.
+size_t side_queue_count() {
+  std::lock_guard<std::mutex> lk(g_side_mu);
+  return g_side.size();
 }
 
 // The queue of each launch of a pass: with at least kSideMinLaunches launches in the pass, the first
@@ -1002,7 +1061,8 @@ int side_queue(hipStream_t caller, SideQueue* out) {
 // queued in this pass; else all on the caller's stream.  (Two or three launches gained nothing: the
 // first fills the device and the next one's workgroups only start in its tail, while the fork and
 // join cost 20-50 us on the small C1 and C2 steps; C5's 13-14 launches per pass gained 0.47 ms.)
-// The side stream first waits for everything before the pass on the caller's stream (fork);
+// The side stream first waits for everything before the pass on the caller's stream (fork, recorded
+// when the pass begins, so that the side's first launch can start with the pass's first one);
 // finish() makes the caller's stream wait for the side stream's launches (join).
 constexpr size_t kSideMinLaunches = 4;
 constexpr size_t kSideMinNormLaunches = 3;  // the clip-norm record and rebuild kernels: C5 11.25 -> 10.87 ms
@@ -1018,12 +1078,17 @@ struct PassQueues {
   PassQueues& operator=(const PassQueues&) = delete;
   void begin(size_t launches, size_t min_launches = kSideMinLaunches) {
     use_side = can_side && launches >= min_launches;
+    // a failed record leaves the pass on the caller's stream alone
+    if (use_side && hipEventRecord(side.fork, main) != hipSuccess) {
+      (void)hipGetLastError();
+      use_side = false;
+    }
   }
   int pick(double bytes, hipStream_t* out) {
     const int k = (use_side && load[1] < load[0]) ? 1 : 0;
     load[k] += bytes;
     if (k == 1 && !forked) {
-      if (hipEventRecord(side.fork, main) != hipSuccess || hipStreamWaitEvent(side.s, side.fork, 0) != hipSuccess)
+      if (hipStreamWaitEvent(side.s, side.fork, 0) != hipSuccess)
         return fail(CAME8_EHIP, "came8_step: fork to the side stream failed");
       forked = true;
     }
@@ -1122,6 +1187,7 @@ extern "C" {
 
 const char* came8_version(void) { return "came8-mi355x 0.1 (gfx950)"; }
 int came8_abi_version(void) { return CAME8_ABI_VERSION; }
+int came8_side_stream_count(void) { return int(side_queue_count()); }
 const char* came8_last_error(void) { return g_last_error.c_str(); }
 
 int came8_workspace_size(const came8_tensor* tensors, int32_t n_tensors, int32_t block_size, size_t* bytes) {
@@ -1230,6 +1296,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
   if (h.flags & CAME8_FLAG_PLAN_ONLY) return CAME8_OK;
   // the side stream: neither under capture (a captured step keeps one queue) nor for the static entry
   SideQueue side;
+  SideLease lease;  // outlives pq, whose destructor may still join the side stream
   bool use_side = workspace_tag != kStaticScratchTag;
   if (use_side) {
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
@@ -1239,7 +1306,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     }
     use_side = cap == hipStreamCaptureStatusNone;
   }
-  if (use_side && (rc = side_queue(stream, &side)) != CAME8_OK) return rc;
+  if (use_side && (rc = side_queue(stream, &side, &lease)) != CAME8_OK) return rc;
   PassQueues pq(stream, side, use_side);
   hipStream_t ls = stream;  // the queue of the next launch
   Hp hp = make_hp(h);

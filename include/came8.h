@@ -260,6 +260,16 @@ int came8_profile_read(came8_phase_stat* out, int32_t max_phases, int32_t* n_pha
 int came8_read_clip(const void* workspace, uint64_t workspace_tag, int32_t n_tensors, float* out, void* stream);
 
 /*
+ * Per-stream resources: came8_step keeps one side stream and two events per (device, caller stream)
+ * it has stepped on (launches of a pass with many kernel variants are spread over the caller's
+ * stream and that side stream).  A side stream not in use by a step is idle; at most 16 idle ones
+ * are kept, the least recently used released (after its work completes) when another is needed.
+ * came8_side_stream_count returns how many are kept now.  No reference counterpart (the reference
+ * launches on the caller's stream only).
+ */
+int came8_side_stream_count(void);
+
+/*
  * Blockwise absmax quantisation of n fp32 values into int8 (is_signed, Q = 127)
  * or uint8 (Q = 255) codes with one fp32 absmax per block of block_size
  * (came_pytorch/blockwise_quantization.py:66-82).

@@ -60,3 +60,33 @@ def test_side_stream_step_matches_one_stream(dtype):
                 for k, v in oa.state[a].items():
                     if torch.is_tensor(v):
                         assert torch.equal(v, ob.state[b][k]), f"{where}: state {k} differs"
+
+
+def test_side_streams_are_bounded_across_caller_streams():
+    """A caller stepping on many streams in turn: at most 16 idle side streams are kept (the least recently
+    used released after its work completes), and every step still matches the one-stream static entry."""
+    lib = _lib.load()
+    params0 = P.make_params(SHAPES, torch.float32, seed=77)
+    pa = [torch.nn.Parameter(p.clone().cuda()) for p in params0]
+    pb = [torch.nn.Parameter(p.clone().cuda()) for p in params0]
+    oa = came_amd.CAME8bit(pa, lr=2e-4, weight_decay=1e-2)
+    ob = came_amd.CAME8bit(pb, lr=2e-4, weight_decay=1e-2)
+    gen = torch.Generator().manual_seed(79)
+    streams = [torch.cuda.Stream() for _ in range(40)]  # default priority
+    most = 0
+    for k, s in enumerate(streams):
+        grads = [P.heavy_grad(gen, sh, torch.float32).cuda() for sh in SHAPES]
+        for p, q, g in zip(pa, pb, grads):
+            p.grad = g
+            q.grad = g.clone()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            oa.step()
+        s.synchronize()
+        _static_step(ob, pb)
+        torch.cuda.synchronize()
+        most = max(most, lib.came8_side_stream_count())
+        for i, (a, b) in enumerate(zip(pa, pb)):
+            assert torch.equal(a.data, b.data), f"stream {k} tensor {i}: parameters differ"
+    assert lib.came8_side_stream_count() <= 16, lib.came8_side_stream_count()
+    assert most <= 17, most  # the 16 idle ones and at most the one a step was using
