@@ -24,6 +24,7 @@ CAME8_TENSOR_FP16_UPDATE = 1  # came8_tensor.tensor_flags
 CAME8_STATE_Q8 = 0
 CAME8_STATE_FP32 = 1
 CAME8_STATE_8BIT2D = 2
+CAME8_STATE_Q8_MATRIX = 3  # the reference CUDA N-D path's per-matrix blocks
 
 # every symbol include/came8.h declares
 EXPORTED_SYMBOLS = (

@@ -162,9 +162,11 @@ struct BandShapeSel {
   bool ua;  // vector chunks over rows that are not whole chunks or not aligned (V > 1, one sweep)
 };
 
-BandShapeSel band_variant(const came8_tensor& t, int64_t C, int32_t B, int pass) {
+BandShapeSel band_variant(const came8_tensor& t, int64_t C, int32_t B, int pass, bool pm_m = false) {
   const int vw = t.grad_dtype == CAME8_F32 ? 4 : 8;
-  const bool aligned = (C % vw == 0) && (B % vw == 0) && (reinterpret_cast<uintptr_t>(t.grad) % 16 == 0) &&
+  // pm_m (pass 2): per-matrix momentum blocks that are not flat ones take the unaligned variant or V = 1,
+  // whose block lookups handle them
+  const bool aligned = !pm_m && (C % vw == 0) && (B % vw == 0) && (reinterpret_cast<uintptr_t>(t.grad) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(t.exp_avg_q) % vw == 0);
   BandShapeSel sel{aligned ? vw : 1, 0, 256, false, false};
   // other rows of at least vw elements take vector chunks with unaligned loads (a partial last chunk
@@ -370,8 +372,13 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
   for (int i = 0; i < n; ++i) {
     const came8_tensor& t = ts[i];
     const std::string who = "came8: tensor " + std::to_string(i) + ": ";
-    if (t.state_kind != CAME8_STATE_Q8 && t.state_kind != CAME8_STATE_FP32 && t.state_kind != CAME8_STATE_8BIT2D)
+    if (t.state_kind != CAME8_STATE_Q8 && t.state_kind != CAME8_STATE_FP32 && t.state_kind != CAME8_STATE_8BIT2D &&
+        t.state_kind != CAME8_STATE_Q8_MATRIX)
       return fail(CAME8_EINVAL, who + "unknown state_kind " + std::to_string(t.state_kind));
+    if (t.state_kind == CAME8_STATE_Q8_MATRIX && !t.factored)
+      return fail(CAME8_EINVAL, who + "per-matrix blocks need a factored tensor");
+    if (t.state_kind == CAME8_STATE_Q8_MATRIX && t.prefix > 1 && t.prefix * t.rows * t.cols >= (int64_t(1) << 31))
+      return fail(CAME8_EINVAL, who + "per-matrix blocks need fewer than 2^31 elements");
     const bool f32st = t.state_kind == CAME8_STATE_FP32;
     const bool s2d = t.state_kind == CAME8_STATE_8BIT2D;
     if (s2d) {
@@ -409,7 +416,13 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     d.R = t.rows;
     d.C = t.cols;
     d.N = t.prefix * t.rows * t.cols;
-    d.nbm = std::max<int64_t>(1, ceil_div(d.N, B));
+    // per-matrix blocks: only where they differ from flat ones (P > 1); blocks per matrix of the
+    // momentum, a row state and a column state
+    d.pm = (t.state_kind == CAME8_STATE_Q8_MATRIX && t.prefix > 1) ? 1 : 0;
+    d.pmb_m = ceil_div(t.rows * t.cols, int64_t(B));
+    d.pmb_r = ceil_div(t.rows, int64_t(B));
+    d.pmb_c = ceil_div(t.cols, int64_t(B));
+    d.nbm = d.pm ? t.prefix * d.pmb_m : std::max<int64_t>(1, ceil_div(d.N, B));
     d.factored = t.factored ? 1 : 0;
     d.fp32st = f32st ? 1 : 0;
     d.fp16u = (!t.factored && !f32st && !s2d && (t.tensor_flags & CAME8_TENSOR_FP16_UPDATE)) ? 1 : 0;
@@ -458,8 +471,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     if (t.factored) {
       d.rb = tiny_matrix(t, s2d) ? d.R : band_rows(d.R, d.C, shrink[i]);
       d.nbands = ceil_div(d.R, d.rb);
-      d.nbr = std::max<int64_t>(1, ceil_div(d.P * d.R, B));
-      d.nbc = std::max<int64_t>(1, ceil_div(d.P * d.C, B));
+      d.nbr = d.pm ? d.P * d.pmb_r : std::max<int64_t>(1, ceil_div(d.P * d.R, B));
+      d.nbc = d.pm ? d.P * d.pmb_c : std::max<int64_t>(1, ceil_div(d.P * d.C, B));
       d.nclip = d.nbc;
       const size_t pr = size_t(d.P * d.R) * 4, pc = size_t(d.P * d.C) * 4;
       const size_t part = size_t(d.P * d.nbands * d.C) * 4;
@@ -582,14 +595,20 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
         add_item(plan.tiny1[t.grad_dtype], i, ceil_div(d.P, int64_t(kThreads)));
         add_item(plan.tiny2[t.grad_dtype], i, ceil_div(d.P, int64_t(kThreads)));
       } else {
-        const BandShapeSel sel1 = band_variant(t, d.C, B, 1), sel2 = band_variant(t, d.C, B, 2);
+        const bool pm_m = d.pm && (d.R * d.C) % B != 0;
+        const BandShapeSel sel1 = band_variant(t, d.C, B, 1), sel2 = band_variant(t, d.C, B, 2, pm_m);
         add_item(plan.band[BandKey{t.grad_dtype, sel1.V, sel1.K, sel1.TPB, 0, sel1.ua}], i, d.P * d.nbands);
         add_item(plan.band2[BandKey{t.grad_dtype, sel2.V, sel2.K, sel2.TPB, d.fp32st, sel2.ua, sel2.multiseg}], i, d.P * d.nbands);
       }
       add_item(plan.factor, i, d.nbr + d.nbc);
-      if (fastB) {
+      // per-matrix momentum blocks that end inside a matrix (B does not divide R*C) are not the flat
+      // passes' blocks: such tensors take the per-block kernel
+      const bool pm_odd = d.pm && (d.R * d.C) % B != 0;
+      if (fastB && !pm_odd) {
         if (d.p3_nbands > 0) add_item(plan.updb[tk], i, d.P * d.p3_nbands * d.p3_nseg);
         else add_item(plan.upd[tk], i, ceil_div(d.N, kTile));
+      } else if (fastB) {
+        add_item(plan.generic[tk], i, d.nbm);
       }
     } else {
       add_item(plan.vecA[t.grad_dtype], i, d.nclip);
@@ -1574,15 +1593,16 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       if ((rc = check_launch("vec_passB")) != CAME8_OK) return rc; }
     }
     if ((rc = pq.finish()) != CAME8_OK) return rc;
-  } else {
-    for (auto& kv : plan.generic) {
-      const WorkList& wl = kv.second;
-      GenFn fn;
-      CAME8_TYPE_SWITCH2(k_generic_update, kv.first.pdt, kv.first.gdt, fn);
-      { PhaseTimer pt(PH_GENERIC, alg_bytes(plan, wl, tensors, PH_GENERIC), stream);
+  }
+  // every tensor when the block size is not a power of two in [8, 2048]; otherwise only those whose
+  // per-matrix momentum blocks end inside a matrix
+  for (auto& kv : plan.generic) {
+    const WorkList& wl = kv.second;
+    GenFn fn;
+    CAME8_TYPE_SWITCH2(k_generic_update, kv.first.pdt, kv.first.gdt, fn);
+    { PhaseTimer pt(PH_GENERIC, alg_bytes(plan, wl, tensors, PH_GENERIC), stream);
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
-      if ((rc = check_launch("generic_update")) != CAME8_OK) return rc; }
-    }
+    if ((rc = check_launch("generic_update")) != CAME8_OK) return rc; }
   }
   return CAME8_OK;
 }

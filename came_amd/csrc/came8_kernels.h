@@ -34,7 +34,7 @@
 namespace came8 {
 
 // Per-tensor descriptor in device memory (built by the host plan).
-struct DevTensor {
+struct alignas(128) DevTensor {  // each descriptor on whole cache lines
   void* p;
   const void* g;
   int8_t* mq;     // exp_avg codes [N]
@@ -102,6 +102,11 @@ struct DevTensor {
   float* t2col;
   int32_t v2d, v2dp;  // vector forms of the momentum pass / parameter write apply
   int32_t fp16u;      // this unfactored tensor takes the fp16-rounded update (CAME8_TENSOR_FP16_UPDATE)
+  // CAME8_STATE_Q8_MATRIX with P > 1: quantisation blocks restart at every matrix (the reference's CUDA
+  // N-D layout); blocks per matrix of the momentum (R*C elements), of a row state (R) and of a column
+  // state (C).  nbm, nbr, nbc are then P times these.
+  int32_t pm;
+  int64_t pmb_m, pmb_r, pmb_c;
 };
 
 // fp32-state views of the state pointers
@@ -139,6 +144,29 @@ __device__ __forceinline__ int64_t blk_of_nb(int64_t e, const Hp& hp) {
   return int64_t((uint64_t(e) * hp.mB) >> hp.sB);
 }
 
+// Block of row state `row` (0 <= row < P*R), of column state i (0 <= i < P*C) and of momentum element e:
+// flat blocks, or per-matrix blocks (t.pm) that restart at every matrix's first row / column / element.
+// Per-matrix tensors hold fewer than 2^31 elements (the host checks), so the matrix of an index comes from
+// the 32-bit magic divisions by R and C.
+__device__ __forceinline__ int64_t rblk(const DevTensor& t, int64_t row, const Hp& hp) {
+  if (!t.pm) return blk_of(row, hp);
+  const int64_t b = udiv_magic(uint32_t(row), t.mR, t.sR);
+  return b * t.pmb_r + blk_of(row - b * t.R, hp);
+}
+__device__ __forceinline__ int64_t cblk(const DevTensor& t, int64_t i, const Hp& hp) {
+  if (!t.pm) return blk_of(i, hp);
+  const int64_t b = udiv_magic(uint32_t(i), t.mC, t.sC);
+  return b * t.pmb_c + blk_of(i - b * t.C, hp);
+}
+// matrix of momentum element e (per-matrix tensors): floor(floor(e / C) / R)
+__device__ __forceinline__ int64_t pm_matrix(const DevTensor& t, int64_t e) {
+  return udiv_magic(udiv_magic(uint32_t(e), t.mC, t.sC), t.mR, t.sR);
+}
+__device__ __forceinline__ int64_t mblk(const DevTensor& t, int64_t e, const Hp& hp) {
+  if (!t.pm) return blk_of(e, hp);
+  const int64_t b = pm_matrix(t, e);
+  return b * t.pmb_m + blk_of(e - b * (t.R * t.C), hp);
+}
 // wstart has n+1 entries, wstart[0] = 0; returns k with wstart[k] <= w < wstart[k+1]
 __device__ __forceinline__ int find_slot(const int64_t* __restrict__ wstart, int n, int64_t w) {
   int lo = 0, hi = n;
@@ -365,6 +393,9 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
     const CAME8_GLOBAL GS* __restrict__ g = gbl(static_cast<const GS*>(t.g) + (b * R) * C);
     const CAME8_GLOBAL uint8_t* __restrict__ rq = gbl(t.rq);
     const CAME8_GLOBAL float* __restrict__ ra = gbl(t.ra);
+    // the row state block of band row rr is rbb + blk_of(roff + r0 + rr): flat blocks over the tensor's
+    // rows, or per-matrix blocks from the band's matrix b's first row (uniform per band)
+    const int64_t rbb = t.pm ? b * t.pmb_r : 0, roff = t.pm ? 0 : b * R;
     CAME8_GLOBAL float* __restrict__ Rn = gbl(t.Rn);
     const float fC = float(C);
     const int64_t nseg = (C + segw - 1) / segw;
@@ -378,7 +409,7 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
     auto stage_rows = [&]() __attribute__((always_inline)) {
       for (int64_t rr = tid; rr < r1 - r0; rr += TPB) {
         const int64_t row = b * R + r0 + rr;
-        rowold[rr] = t.fp32st ? gbl(st_sq_row(t))[row] : deq_u8(rq[row], ra[blk_of(row, hp)]);
+        rowold[rr] = t.fp32st ? gbl(st_sq_row(t))[row] : deq_u8(rq[row], ra[rbb + blk_of(roff + r0 + rr, hp)]);
       }
       wait_vm_all();  // on every path: the stage loop's waits then count only its own loads
       __syncthreads();
@@ -639,7 +670,7 @@ __global__ __launch_bounds__(kThreads) void k_tiny_pass1(const DevTensor* __rest
         s = fma(x, x, s);
       }
       const int64_t row = b * R + i;
-      const float Rold = t.fp32st ? st_sq_row(t)[row] : deq_u8(t.rq[row], t.ra[blk_of(row, hp)]);
+      const float Rold = t.fp32st ? st_sq_row(t)[row] : deq_u8(t.rq[row], t.ra[rblk(t, row, hp)]);
       const float mean = float(s + double(C) * double(hp.eps0)) * invC;
       const float Rnew = fmaf(mean, hp.a2, Rold * hp.b2);
       Rn[i] = Rnew;
@@ -682,7 +713,7 @@ __global__ __launch_bounds__(kThreads) void k_tiny_pass2(const DevTensor* __rest
     auto d_at = [&](int64_t i, int64_t j) {
       const int64_t e = e0 + i * C + j;
       const float mo = t.fp32st ? st_m(t)[e]
-                                : float(t.mq[e]) * div_fast(t.ma[blk_of_nb(e, hp)], kSignedQ, kRcpSignedQ);
+                                : float(t.mq[e]) * div_fast(t.ma[t.pm ? mblk(t, e, hp) : blk_of_nb(e, hp)], kSignedQ, kRcpSignedQ);
       const float u = div_fast((rf[i] * cf[j]) * TG::load(g[i * C + j]), clip, crcp);
       const float m = fmaf(u, hp.a1, mo * hp.b1);
       return u - m;
@@ -696,7 +727,7 @@ __global__ __launch_bounds__(kThreads) void k_tiny_pass2(const DevTensor* __rest
       }
       const int64_t row = b * R + i;
       const float tot = float(s + double(C) * double(hp.eps1));
-      const float RRold = t.fp32st ? t.ra[row] : deq_u8(t.rq[PR + row], t.ra[t.nbr + blk_of(row, hp)]);
+      const float RRold = t.fp32st ? t.ra[row] : deq_u8(t.rq[PR + row], t.ra[t.nbr + rblk(t, row, hp)]);
       const float RRnew = fmaf(tot / float(C), hp.a3, RRold * hp.b3);
       gbl(t.RRn)[row] = RRnew;
       bandRR += RRnew;
@@ -757,6 +788,7 @@ __global__ __launch_bounds__(TPB, (UA && sizeof(typename TG::storage) == 2 && TP
     const CAME8_GLOBAL float* __restrict__ rfac = gbl(t.rfac);
     const CAME8_GLOBAL uint8_t* __restrict__ rq = gbl(t.rq);
     const CAME8_GLOBAL float* __restrict__ ra = gbl(t.ra);
+    const int64_t rbb = t.pm ? b * t.pmb_r : 0, roff = t.pm ? 0 : b * R;  // row state blocks, as in pass 1
     CAME8_GLOBAL float* __restrict__ RRn = gbl(t.RRn);
     const float clip = uniform_f32(t.clip[0]);
     const float crcp = 1.0f / clip;  // the clip divisor is >= 1, so division through it is exact or 1 ulp off
@@ -787,7 +819,7 @@ __global__ __launch_bounds__(TPB, (UA && sizeof(typename TG::storage) == 2 && TP
       for (int64_t rr = tid; rr < r1 - r0; rr += TPB) {
         const int64_t row = b * R + r0 + rr;
         rowsc[rr] = rfac[row];
-        rowold[rr] = f32st ? gbl(t.ra)[row] : deq_u8(rq[PR + row], ra[t.nbr + blk_of(row, hp)]);
+        rowold[rr] = f32st ? gbl(t.ra)[row] : deq_u8(rq[PR + row], ra[t.nbr + rbb + blk_of(roff + r0 + rr, hp)]);
       }
       if constexpr (MS) {  // the per-wave row sums add up over the column segments (the dummy row too)
         for (int64_t i = tid; i < (r1 - r0) * NW; i += TPB) rowpart[bpar][i / NW][i % NW] = 0.0;
@@ -870,14 +902,21 @@ __global__ __launch_bounds__(TPB, (UA && sizeof(typename TG::storage) == 2 && TP
                 sb.q[s][k].load(m32 + rs * C + coff[k]);
               } else if constexpr (UA) {
                 sb.q[s][k].load(mq + rs * C + coff[k]);
-                const int64_t e0 = erow + coff[k];
+                // per-matrix blocks (t.pm; the host sends such tensors to this variant or to V = 1): block
+                // numbers from the band's matrix's first element, after that matrix's first block
+                const int64_t e0 = (t.pm ? rs * C : erow) + coff[k];
+                const CAME8_GLOBAL float* __restrict__ mab = t.pm ? ma + b * t.pmb_m : ma;
                 const int64_t b0 = blk_of_nb(e0, hp), b1 = blk_of_nb(e0 + V - 1, hp);
-                sb.a[s][k] = ma[b0];
-                sb.a2[s][k] = ma[b1];
+                sb.a[s][k] = mab[b0];
+                sb.a2[s][k] = mab[b1];
                 sb.split[s][k] = int32_t((b0 + 1) * int64_t(hp.B) - e0);
               } else {
                 sb.q[s][k].load(mq + rs * C + coff[k]);
-                sb.a[s][k] = kAligned ? marow[cbk[k]] : ma[blk_of_nb(erow + coff[k], hp)];
+                if constexpr (V == 1) {  // one element: its own block, per matrix when t.pm
+                  sb.a[s][k] = t.pm ? ma[b * t.pmb_m + blk_of_nb(rs * C + coff[k], hp)] : ma[blk_of_nb(erow + coff[k], hp)];
+                } else {  // flat momentum blocks (the host routes per-matrix ones elsewhere)
+                  sb.a[s][k] = kAligned ? marow[cbk[k]] : ma[blk_of_nb(erow + coff[k], hp)];
+                }
               }
             }
           }
@@ -1081,9 +1120,17 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
     const int64_t local = w - wstart[slot];
     const bool is_row = local < t.nbr;
     const int64_t blk = is_row ? local : local - t.nbr;
-    const int64_t len = is_row ? t.P * t.R : t.P * t.C;
-    const int64_t i0 = blk * hp.B;
-    const int64_t i1 = (i0 + hp.B < len) ? (i0 + hp.B) : len;
+    int64_t i0, i1;
+    if (t.pm) {  // blocks restart at every matrix: block blk is block jb of matrix mb's R (or C) states
+      const int64_t per = is_row ? t.pmb_r : t.pmb_c, n = is_row ? t.R : t.C;
+      const int64_t mb = blk / per, jb = blk - mb * per;
+      i0 = mb * n + jb * hp.B;
+      i1 = (jb * hp.B + hp.B < n) ? (i0 + hp.B) : (mb * n + n);
+    } else {
+      const int64_t len = is_row ? t.P * t.R : t.P * t.C;
+      i0 = blk * hp.B;
+      i1 = (i0 + hp.B < len) ? (i0 + hp.B) : len;
+    }
     const bool partial = (i1 - i0) < hp.B;  // zero padding joins the max
     float vmax = partial ? 0.0f : -__builtin_inff();
     double csum = 0.0;
@@ -1144,7 +1191,7 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
           else band_column_sums<2>(pp, t.partW + (b * t.nbands) * t.C + j, t.nbands, t.C, sw);
           const double s = sw[0];
           W = sw[1];
-          Cold = t.fp32st ? cst[i] : deq_u8(t.cq[off + i], t.ca[aoff + blk_of(i, hp)]);
+          Cold = t.fp32st ? cst[i] : deq_u8(t.cq[off + i], t.ca[aoff + cblk(t, i, hp)]);
           Cv = clamp_min_tiny(fmaf(float(s) / fR, alpha, Cold * beta));
         }
         const float c = rsqrt_ref(Cv);
@@ -1811,7 +1858,7 @@ __device__ __forceinline__ float m_new_fact(const DevTensor& t, int64_t e, float
   float uu = u_at<TG>(t, e, hp);
   if ((hp.fp16u || t.fp16u) && !t.factored) uu = round_f16(uu);
   const float u = uu / clip;
-  return fmaf(u, hp.a1, deq_s8(t.mq[e], t.ma[blk_of(e, hp)]) * hp.b1);
+  return fmaf(u, hp.a1, deq_s8(t.mq[e], t.ma[mblk(t, e, hp)]) * hp.b1);
 }
 
 template <typename TP, typename TG>
@@ -1825,8 +1872,15 @@ __global__ __launch_bounds__(kThreads) void k_generic_update(const DevTensor* __
     const int slot = find_slot(wstart, ntens, w);
     const DevTensor& t = T[tids[slot]];
     const int64_t blk = w - wstart[slot];
-    const int64_t i0 = blk * hp.B;
-    const int64_t i1 = (i0 + hp.B < t.N) ? (i0 + hp.B) : t.N;
+    int64_t i0, i1;
+    if (t.pm) {  // block jb of matrix mb
+      const int64_t rc = t.R * t.C, mb = blk / t.pmb_m, jb = blk - mb * t.pmb_m;
+      i0 = mb * rc + jb * hp.B;
+      i1 = (jb * hp.B + hp.B < rc) ? (i0 + hp.B) : (mb * rc + rc);
+    } else {
+      i0 = blk * hp.B;
+      i1 = (i0 + hp.B < t.N) ? (i0 + hp.B) : t.N;
+    }
     const float clip = t.clip[0];
     const typename TG::storage* __restrict__ g = static_cast<const typename TG::storage*>(t.g);
     PS* __restrict__ p = static_cast<PS*>(t.p);

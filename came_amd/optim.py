@@ -76,6 +76,9 @@ class _Came8Base(torch.optim.Optimizer):
     """Shared step machinery: state layout, descriptor table, workspace, one library call per group."""
 
     _MODE = "full8bit"                 # state["_mode"] of this optimizer's layout
+    # layouts the library steps in place (state_layout.layout_of): this optimizer's own, and for full8bit
+    # the reference CUDA N-D path's per-matrix blocks (CAME8_STATE_Q8_MATRIX)
+    _IN_PLACE = ("full8bit", "full8bit-nd")
     _STATE_KIND = _lib.CAME8_STATE_Q8  # how the library reads the state pointers
     _VIEWS_BEFORE_FLAGS = False        # the reference's key order (CAME8bitMemory: views first)
 
@@ -103,7 +106,22 @@ class _Came8Base(torch.optim.Optimizer):
     # ------------------------------------------------------------------ state
     @staticmethod
     def _bind_factored_views(state: dict) -> None:
-        """Views of the stacked row/col states (CAME8bitFull.py:214-223)."""
+        """Views of the stacked row/col states (CAME8bitFull.py:214-223; per-matrix layout :188-210)."""
+        if state_layout.layout_of(state) == "full8bit-nd":
+            P, R, C = state["prefix_batch"], state["matrix_rows"], state["matrix_cols"]
+            rq = state["factored_row_q"].view(2, P, R)
+            cq = state["factored_col_q"].view(2, P, C)
+            ra = state["factored_row_absmax"].view(2, P, -1)
+            ca = state["factored_col_absmax"].view(2, P, -1)
+            state["exp_avg_sq_row_q"], state["exp_avg_res_row_q"] = rq[0], rq[1]
+            state["exp_avg_sq_col_q"], state["exp_avg_res_col_q"] = cq[0], cq[1]
+            state["exp_avg_sq_row_absmax"], state["exp_avg_res_row_absmax"] = ra[0], ra[1]
+            state["exp_avg_sq_col_absmax"], state["exp_avg_res_col_absmax"] = ca[0], ca[1]
+            state["exp_avg_q_batched"] = state["exp_avg_q"].view(P, R, C)
+            for k, n in (("row", R), ("col", C)):
+                if f"{k}_factor_fp32" in state:  # the reference's scratch, kept for its round trip
+                    state[f"{k}_factor_batched"] = state[f"{k}_factor_fp32"].view(P, n)
+            return
         state["exp_avg_sq_row_q"] = state["factored_row_q"][0]
         state["exp_avg_res_row_q"] = state["factored_row_q"][1]
         state["exp_avg_sq_col_q"] = state["factored_col_q"][0]
@@ -143,15 +161,30 @@ class _Came8Base(torch.optim.Optimizer):
     def _check_state(self, p: torch.Tensor, state: dict, block_size: int) -> None:
         if tuple(state["exp_avg_q"].shape) != tuple(p.shape):
             raise RuntimeError("Parameter shape changed; this optimizer does not support resizing 8-bit state.")
-        if state["exp_avg_absmax"].numel() != num_blocks(p.numel(), block_size):
+        if (state["exp_avg_absmax"].numel() != num_blocks(p.numel(), block_size)
+                and state_layout.layout_of(state) != "full8bit-nd"):
             raise RuntimeError("block_size changed after the 8-bit state was created; the state layout is fixed.")
         if state["exp_avg_q"].device != p.device:
             raise RuntimeError("optimizer state lives on a different device than its parameter")
         if state.get("factored") and "factored_row_absmax" in state:
-            # the flat layout: [2][blocks of the P*R row states] and [2][blocks of the P*C column states]
-            # (a per-matrix layout with as many codes has [2*P][blocks per matrix] scales instead)
             rows = math.prod(p.shape[:-1])
             cols = math.prod(p.shape[:-2]) * p.shape[-1]
+            if state_layout.layout_of(state) == "full8bit-nd":
+                # per-matrix blocks: [2*P][blocks of R] and [2*P][blocks of C] scales, [P][blocks of R*C]
+                P, R, C = math.prod(p.shape[:-2]), p.shape[-2], p.shape[-1]
+                if (p.dim() < 3 or (state.get("prefix_batch"), state.get("matrix_rows"), state.get("matrix_cols"))
+                        != (P, R, C)):
+                    raise RuntimeError("per-matrix state does not match this parameter's matrices")
+                want = {"exp_avg_absmax": P * num_blocks(R * C, block_size),
+                        "factored_row_absmax": 2 * P * num_blocks(R, block_size),
+                        "factored_col_absmax": 2 * P * num_blocks(C, block_size),
+                        "factored_row_q": 2 * rows, "factored_col_q": 2 * cols}
+                for key, n in want.items():
+                    if state[key].numel() != n:
+                        raise RuntimeError(f"{key} does not have the per-matrix layout of this parameter "
+                                           f"(block size {block_size})")
+                return
+            # the flat layout: [2][blocks of the P*R row states] and [2][blocks of the P*C column states]
             for key, n in (("factored_row", rows), ("factored_col", cols)):
                 if (state[f"{key}_q"].numel() != 2 * n
                         or state[f"{key}_absmax"].numel() != 2 * num_blocks(n, block_size)):
@@ -202,7 +235,7 @@ class _Came8Base(torch.optim.Optimizer):
     def _adopt_layout(self, p: torch.Tensor, state: dict) -> None:
         """Convert a loaded state of another layout into this optimizer's (see load_state_dict)."""
         src = state_layout.layout_of(state)
-        if not src or src == self._MODE or (self._MODE == "8bit2d" and p.dim() != 2):
+        if not src or src in self._IN_PLACE or (self._MODE == "8bit2d" and p.dim() != 2):
             return
         if src == "8bit1d" and self._MODE == "full8bit" and p.dim() == 1:
             # the reference CAME8bit's 1-D batched-path states (CAME8bit.py:252-262) keep full8bit's
@@ -293,7 +326,7 @@ class _Came8Base(torch.optim.Optimizer):
         state = self.state[p]
         # another layout (a different _mode, or the reference CUDA N-D path's per-matrix blocks under
         # _mode "full8bit") starts over, as the reference does (CAME8bit.py:757-759)
-        if len(state) == 0 or state_layout.layout_of(state) != self._MODE:
+        if len(state) == 0 or state_layout.layout_of(state) not in self._IN_PLACE:
             state.clear()
             self._init_state(state, grad, block_size)
         self._check_state(p, state, block_size)
@@ -385,7 +418,8 @@ class _Came8Base(torch.optim.Optimizer):
             d.grad = g.data_ptr()
             d.param_dtype = _DTYPE_CODE[p.dtype]
             d.grad_dtype = _DTYPE_CODE[g.dtype]
-            d.state_kind = self._STATE_KIND
+            d.state_kind = (_lib.CAME8_STATE_Q8_MATRIX if self._STATE_KIND == _lib.CAME8_STATE_Q8
+                            and state_layout.layout_of(state) == "full8bit-nd" else self._STATE_KIND)
             if self._is_factored(state):
                 shape = tuple(p.shape)
                 d.prefix = math.prod(shape[:-2])
@@ -732,6 +766,7 @@ class CAMECUDA(_Came8Base):
     """
 
     _MODE = "cudafp"
+    _IN_PLACE = ("cudafp",)
     _STATE_KIND = _lib.CAME8_STATE_FP32
     _WORK_BLOCK = 256  # shapes the library's work decomposition only; fp32 states have no blocks
 
@@ -882,6 +917,7 @@ class CAME8bit2D(_Came8Base):
     """
 
     _MODE = "8bit2d"
+    _IN_PLACE = ("8bit2d",)
     _STATE_KIND = _lib.CAME8_STATE_8BIT2D
 
     def __init__(

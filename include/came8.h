@@ -62,6 +62,11 @@ extern "C" {
 #define CAME8_STATE_Q8 0   /* 8-bit states, full8bit layout (CAME8bit, CAME8bitFull, CAME8bitMemory) */
 #define CAME8_STATE_FP32 1 /* fp32 states, CAMECUDA layout */
 #define CAME8_STATE_8BIT2D 2 /* 8-bit states, 8bit2d layout (CAME8bit2D): momentum in 16x16 tiles */
+#define CAME8_STATE_Q8_MATRIX 3 /* 8-bit states of an N-D tensor (ndim >= 3) blocked per matrix, as the
+                                   reference's CUDA N-D path keeps them (came_pytorch/CAME8bitFull.py:
+                                   790-842, views :188-223): the codes as in CAME8_STATE_Q8, but every one of
+                                   the P matrices has blocks of its own -- exp_avg_absmax [P][ceil(R*C/B)],
+                                   row_absmax [2][P][ceil(R/B)], col_absmax [2][P][ceil(C/B)] (ABI 5) */
 
 /* flags for came8_hparams.flags.  By default the clip's update norm is the reference's own: torch's
  * CPU norm(2) order (eight fp32 fused-multiply-add chains, came_pytorch/CAME8bitFull.py:121-122,1032),

@@ -79,12 +79,69 @@ def dequantize_blockwise(q: torch.Tensor, absmax: torch.Tensor, *, signed: bool,
     return (qf * step).view_as(q)
 
 
+def quantize_items(x: torch.Tensor, items: int, *, signed: bool, block_size: int):
+    """quantize_blockwise restarted at each of ``items`` equal consecutive parts of ``x`` (the per-matrix
+    blocks of the reference's CUDA N-D layout, CAME8bitFull.py:790-829, which quantises with
+    init_batched_qstate's (batch, n) shapes, blockwise_quantization.py:30-42): every part zero padded to
+    whole blocks of its own.  Returns the codes (shape of x) and the scales [items][blocks per part]."""
+    parts = x.detach().reshape(items, -1).to(torch.float32)
+    n = parts.shape[1]
+    nb = num_blocks(n, block_size)
+    buf = torch.zeros(items, nb * block_size, dtype=torch.float32)
+    buf[:, :n] = parts
+    blocks = buf.view(items, nb, block_size)
+    if signed:
+        amax = blocks.abs().amax(dim=2)
+        qmax, lo, qdtype = SIGNED_QMAX, -SIGNED_QMAX, torch.int8
+    else:
+        amax = blocks.amax(dim=2)
+        qmax, lo, qdtype = UNSIGNED_QMAX, 0.0, torch.uint8
+    amax = torch.where(amax > 0, amax, torch.ones_like(amax))
+    scaled = (blocks / amax.unsqueeze(2)) * qmax
+    q = torch.round(scaled).clamp(lo, qmax).to(qdtype)
+    return q.reshape(items, -1)[:, :n].reshape(x.shape), amax
+
+
+def dequantize_items(q: torch.Tensor, absmax: torch.Tensor, items: int, *, signed: bool,
+                     block_size: int) -> torch.Tensor:
+    """dequantize_blockwise of each of ``items`` consecutive parts with its own scales [items][blocks]."""
+    parts = q.reshape(items, -1).to(torch.float32)
+    n = parts.shape[1]
+    step = absmax.reshape(items, -1).repeat_interleave(block_size, dim=1)[:, :n] / (
+        SIGNED_QMAX if signed else UNSIGNED_QMAX)
+    return (parts * step).reshape(q.shape)
+
+
+def is_per_matrix(st: Dict[str, object]) -> bool:
+    """The reference CUDA N-D path's per-matrix layout (flags of CAME8bitFull.py:783-785)."""
+    return bool(st.get("_cuda_factored_nd_ext_path", False) or st.get("_cuda_factored_nd_chunked_ext_path", False))
+
+
 # --------------------------------------------------------------------------
 # state layout (reference CAME8bitFull._init_state, CPU branch)
 # --------------------------------------------------------------------------
-def init_full8bit_state(shape, block_size: int = 256) -> Dict[str, object]:
-    """Reference CAME8bitFull.py:748-788,919-923 (CPU branch) and blockwise_quantization.py:17-42."""
+def init_full8bit_state(shape, block_size: int = 256, per_matrix: bool = False) -> Dict[str, object]:
+    """Reference CAME8bitFull.py:748-788,919-923 (CPU branch) and blockwise_quantization.py:17-42.
+
+    ``per_matrix`` (N-D shapes, ndim >= 3): the reference CUDA N-D path's layout instead
+    (CAME8bitFull.py:790-829): scales per matrix, ``exp_avg_absmax`` [P][ceil(R*C/B)], row codes
+    [2P][R] with scales [2P][ceil(R/B)], column codes [2P][C] with scales [2P][ceil(C/B)], its
+    routing flags and shape keys (its fp32 scratch buffers are left out)."""
     shape = tuple(int(s) for s in shape)
+    if per_matrix and len(shape) >= 3:
+        P, R, C = math.prod(shape[:-2]), shape[-2], shape[-1]
+        st = {"step": 0, "_mode": "full8bit", "RMS": 0}
+        st["exp_avg_q"] = torch.zeros(shape, dtype=torch.int8)
+        st["exp_avg_absmax"] = torch.ones((P, num_blocks(R * C, block_size)), dtype=torch.float32)
+        st["factored"] = True
+        st["factored_row_q"] = torch.zeros((2 * P, R), dtype=torch.uint8)
+        st["factored_row_absmax"] = torch.ones((2 * P, num_blocks(R, block_size)), dtype=torch.float32)
+        st["factored_col_q"] = torch.zeros((2 * P, C), dtype=torch.uint8)
+        st["factored_col_absmax"] = torch.ones((2 * P, num_blocks(C, block_size)), dtype=torch.float32)
+        st.update(_cuda_factored_fastpath=True, _cuda_factored_nd_ext_path=True,
+                  _cuda_factored_nd_chunked_ext_path=False, _cuda_factored_ext_path=True,
+                  prefix_batch=P, matrix_rows=R, matrix_cols=C)
+        return st
     numel = math.prod(shape)
     st: Dict[str, object] = {"step": 0, "_mode": "full8bit", "RMS": 0}
     st["exp_avg_q"] = torch.zeros(shape, dtype=torch.int8)
@@ -159,14 +216,31 @@ def full8bit_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *,
     if grad.dtype in (torch.float16, torch.bfloat16):
         grad = grad.float()
     bs = block_size
-    m = dequantize_blockwise(st["exp_avg_q"], st["exp_avg_absmax"], signed=True, block_size=bs)
-    upd = (grad ** 2) + eps0
     factored = st["factored"]
+    # the reference CUDA N-D path's per-matrix blocks (is_per_matrix): the same arithmetic, each of the P
+    # matrices quantised in blocks of its own (items); one item is the flat layout
+    pm = factored and is_per_matrix(st) and p.dim() >= 3
+    P = math.prod(p.shape[:-2]) if pm else 1
+
+    def deq(q, a, signed, items):
+        if pm:
+            return dequantize_items(q, a, items, signed=signed, block_size=bs)
+        return dequantize_blockwise(q, a, signed=signed, block_size=bs)
+
+    def quant(x, signed, items):
+        if pm:
+            return quantize_items(x, items, signed=signed, block_size=bs)
+        return quantize_blockwise(x, signed=signed, block_size=bs)
+
+    m = deq(st["exp_avg_q"], st["exp_avg_absmax"], True, P)
+    upd = (grad ** 2) + eps0
     if factored:
-        rq, ra = st["factored_row_q"], st["factored_row_absmax"]
-        cq, ca = st["factored_col_q"], st["factored_col_absmax"]
-        sq_row = dequantize_blockwise(rq[0], ra[0], signed=False, block_size=bs)
-        sq_col = dequantize_blockwise(cq[0], ca[0], signed=False, block_size=bs)
+        # [0]: the second moment, [1]: the residual (per-matrix: [2P][n] stored, the same element order)
+        rq, ra = st["factored_row_q"].view(2, -1), st["factored_row_absmax"].view(2, -1)
+        cq, ca = st["factored_col_q"].view(2, -1), st["factored_col_absmax"].view(2, -1)
+        row_shape, col_shape = p.shape[:-1], p.shape[:-2] + p.shape[-1:]
+        sq_row = deq(rq[0], ra[0], False, P).view(row_shape)
+        sq_col = deq(cq[0], ca[0], False, P).view(col_shape)
         sq_row.mul_(beta2).add_(upd.mean(dim=-1), alpha=1.0 - beta2)
         sq_col.mul_(beta2).add_(upd.mean(dim=-2), alpha=1.0 - beta2)
         upd = _approx_sq_grad(sq_row, sq_col)
@@ -190,8 +264,8 @@ def full8bit_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *,
     m.mul_(beta1).add_(upd, alpha=1.0 - beta1)
     res = (upd - m) ** 2 + eps1
     if factored:
-        res_row = dequantize_blockwise(rq[1], ra[1], signed=False, block_size=bs)
-        res_col = dequantize_blockwise(cq[1], ca[1], signed=False, block_size=bs)
+        res_row = deq(rq[1], ra[1], False, P).view(row_shape)
+        res_col = deq(cq[1], ca[1], False, P).view(col_shape)
         res_row.mul_(beta3).add_(res.mean(dim=-1), alpha=1.0 - beta3)
         res_col.mul_(beta3).add_(res.mean(dim=-2), alpha=1.0 - beta3)
         step_dir = _approx_sq_grad(res_row, res_col)
@@ -213,17 +287,17 @@ def full8bit_step(p: torch.Tensor, grad: torch.Tensor, st: Dict[str, object], *,
                            res_col=res_col.clone())
         else:
             capture["sq"] = sq.clone()
-    q, a = quantize_blockwise(m, signed=True, block_size=bs)
+    q, a = quant(m, True, P)
     st["exp_avg_q"].copy_(q)
-    st["exp_avg_absmax"].copy_(a)
+    st["exp_avg_absmax"].copy_(a.view_as(st["exp_avg_absmax"]))
     if factored:
         for k, (row, col) in enumerate(((sq_row, sq_col), (res_row, res_col))):
-            q, a = quantize_blockwise(row, signed=False, block_size=bs)
-            rq[k].copy_(q)
-            ra[k].copy_(a)
-            q, a = quantize_blockwise(col, signed=False, block_size=bs)
-            cq[k].copy_(q)
-            ca[k].copy_(a)
+            q, a = quant(row, False, P)
+            rq[k].copy_(q.reshape(-1))
+            ra[k].copy_(a.reshape(-1))
+            q, a = quant(col, False, P)
+            cq[k].copy_(q.reshape(-1))
+            ca[k].copy_(a.reshape(-1))
     else:
         q, a = quantize_blockwise(sq, signed=False, block_size=bs)
         st["exp_avg_sq_q"].copy_(q)

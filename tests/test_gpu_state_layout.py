@@ -162,49 +162,70 @@ def _nd_checkpoint(shape, B, seed):
     return {"state": {0: st}, "param_groups": [group]}
 
 
-@pytest.mark.parametrize("shape,B", [((3, 40, 24), 64), ((2, 5, 33, 7), 16)])
-def test_nd_per_matrix_checkpoint_loads_into_came8bitfull(shape, B):
+# Shapes over every route the per-matrix blocks take: rows and columns in partial blocks per matrix (the
+# factor kernel's per-matrix block ranges), rows that straddle blocks (pass 2's unaligned variant), momentum
+# blocks ending inside a matrix (the per-block parameter pass), tiny matrices (one thread per matrix),
+# blocks that coincide with flat ones (the band passes, where the layouts agree), a block size that is not
+# a power of two (every tensor on the per-block pass), fp32 and bf16.
+ND_CASES = [((3, 40, 24), 64, "float32"), ((2, 5, 33, 7), 16, "float32"), ((4, 100, 100), 256, "bfloat16"),
+            ((3, 64, 4096), 256, "bfloat16"), ((2, 3, 5), 4, "float32"), ((3, 40, 24), 100, "float32"),
+            ((5, 300, 520), 256, "float32"), ((3, 129, 1001), 256, "bfloat16")]
+
+
+@pytest.mark.parametrize("convert", [True, False])
+@pytest.mark.parametrize("shape,B,dtype", ND_CASES)
+def test_nd_per_matrix_checkpoint_steps_in_place(shape, B, dtype, convert):
+    """A state dict of the reference's CUDA N-D path (per-matrix blocks, CAME8bitFull.py:790-842) loads into
+    CAME8bitFull and is stepped in place (CAME8_STATE_Q8_MATRIX), whether or not layouts are converted: three
+    steps, each teacher-forced against the oracle's per-matrix step, under the parity tolerances; the state
+    keeps the reference's shapes, keys and views."""
+    dt = getattr(torch, dtype)
+    P_, R, C = math.prod(shape[:-2]), shape[-2], shape[-1]
     sd = _nd_checkpoint(shape, B, seed=4)
-    p = torch.nn.Parameter(P.make_params([shape], torch.float32, seed=5)[0].cuda())
+    p = torch.nn.Parameter(P.make_params([shape], dt, seed=5)[0].cuda())
     opt = came_amd.CAME8bitFull([p], lr=1e-3, weight_decay=1e-2, block_size=B)
+    opt.load_state_dict(sd, convert_layouts=convert)
+    ref_state = _cpu_state(opt.state[p])
+    r = p.data.detach().cpu().clone()
+    ohp = P.oracle_hp(dict(lr=1e-3, weight_decay=1e-2, block_size=B))
+    check = T2_tight(f"nd per-matrix {shape} B={B} {dtype} convert={convert}", B)
+    for step in range(3):
+        with torch.no_grad():  # teacher forcing
+            p.data.copy_(r.to(dt).cuda() if r.dtype != dt else r.cuda())
+            for k in Q8_KEYS:
+                opt.state[p][k].copy_(ref_state[k].cuda())
+        g = _grads([shape], dt, 60 + step)
+        _run(opt, [p], g)
+        cap = {}
+        before = r.double()
+        orc.full8bit_step(r, g[0], ref_state, capture=cap, **ohp)
+        check(step + 1, 0, p.data, r, opt.state[p], ref_state, (r.double() - before).abs(), cap)
+    st = opt.state[p]
+    assert SL.layout_of(st) == "full8bit-nd" and st["step"] == 8
+    assert st["exp_avg_absmax"].shape == (P_, math.ceil(R * C / B))
+    assert st["factored_row_absmax"].shape == (2 * P_, math.ceil(R / B))
+    assert st["factored_col_absmax"].shape == (2 * P_, math.ceil(C / B))
+    assert st["exp_avg_res_row_q"].shape == (P_, R)
+    assert st["exp_avg_res_row_q"].data_ptr() == st["factored_row_q"].data_ptr() + P_ * R
+
+
+def T2_tight(tag, B):
+    from tests.test_gpu_parity import _tight_step_check
+    return _tight_step_check(tag, block=B)
+
+
+def test_nd_per_matrix_checkpoint_converts_for_camecuda():
+    """CAMECUDA keeps fp32 states: a per-matrix checkpoint converts to them, each value the per-matrix
+    dequantisation of its code (done by torch on the GPU here, on the CPU in the expectation: within
+    1e-6 relative; the conversion's formula is pinned on the CPU in tests/test_state_layout.py)."""
+    shape, B = (3, 40, 24), 64
+    sd = _nd_checkpoint(shape, B, seed=8)
+    ex = SL.state_values(sd["state"][0], shape, B)
+    p = torch.nn.Parameter(P.make_params([shape], torch.float32, seed=9)[0].cuda())
+    opt = came_amd.CAMECUDA([p], lr=1e-3, weight_decay=1e-2)
     opt.load_state_dict(sd)
     st = opt.state[p]
-    assert SL.layout_of(st) == "full8bit" and st["step"] == 5
-    assert st["exp_avg_absmax"].numel() == math.ceil(math.prod(shape) / B)
-    assert st["factored_row_absmax"].shape == (2, math.ceil(math.prod(shape[:-1]) / B))
-    ref_state = _cpu_state(st)
-    r = p.data.detach().cpu().clone()
-    g = _grads([shape], torch.float32, 60)
-    _run(opt, [p], g)
-    cap = {}
-    before = r.double()
-    orc.full8bit_step(r, g[0], ref_state, capture=cap, **P.oracle_hp(dict(lr=1e-3, weight_decay=1e-2, block_size=B)))
-    where = f"nd per-matrix -> flat {shape} B={B}"
-    P.compare_states(opt.state[p], ref_state, code_frac=1.5e-2, abs_rel=1e-6, where=where, ref_fp32=cap, tie_tol=2e-4,
-                     block=B)
-    tainted = opt.state[p]["exp_avg_q"].cpu() != ref_state["exp_avg_q"]
-    P.check_untainted_params(p.data, r, tainted, where, (r.double() - before).abs())
-    assert opt.state[p]["step"] == 6
-
-
-@pytest.mark.parametrize("shape,B", [((4, 16, 256), 256), ((3, 40, 24), 64)])
-def test_nd_per_matrix_checkpoint_without_conversion_resets(shape, B):
-    """convert_layouts=False with the reference CUDA N-D path's per-matrix state (_mode "full8bit" plus
-    _cuda_factored_nd_ext_path): the next step starts the state over, as the reference does for a
-    layout it does not step (CAME8bit.py:757-759), rather than reading the per-matrix scales as flat
-    ones.  (4, 16, 256) at block 256 is a shape whose per-matrix codes have the flat layout's element
-    count, so only the layout check tells the two apart."""
-    sd = _nd_checkpoint(shape, B, seed=6)
-    p = torch.nn.Parameter(P.make_params([shape], torch.float32, seed=7)[0].cuda())
-    q = torch.nn.Parameter(p.detach().clone())
-    opt = came_amd.CAME8bitFull([p], lr=1e-3, weight_decay=1e-2, block_size=B)
-    opt.load_state_dict(sd, convert_layouts=False)
-    assert SL.layout_of(opt.state[p]) == "full8bit-nd"
-    fresh = came_amd.CAME8bitFull([q], lr=1e-3, weight_decay=1e-2, block_size=B)
-    g = _grads([shape], torch.float32, 61)
-    _run(opt, [p], g)
-    _run(fresh, [q], g)
-    assert opt.state[p]["step"] == 1 and SL.layout_of(opt.state[p]) == "full8bit"
-    assert torch.equal(p.data, q.data)
-    for k in Q8_KEYS:
-        assert torch.equal(opt.state[p][k], fresh.state[q][k]), k
+    assert st["_mode"] == "cudafp"
+    torch.testing.assert_close(st["exp_avg"].cpu(), ex["exp_avg"], rtol=1e-6, atol=0)
+    for k in ("sq_row", "res_row", "sq_col", "res_col"):
+        torch.testing.assert_close(st[f"exp_avg_{k}"].cpu(), ex[k], rtol=1e-6, atol=0, msg=k)
