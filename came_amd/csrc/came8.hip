@@ -120,6 +120,13 @@ struct Plan {
   std::map<int, WorkList> nfix;          // records rebuilt under the chains' own estimates, by 3 * grad type + form
   std::map<int, WorkList> nwalk;         // chain walks (8 items per tensor), by grad type
   std::map<int, WorkList> nfinal;        // accumulators + tail + clip (one item per tensor), by grad type
+  // The long-chain group (walk_split): factored tensors whose clip-norm chains are much longer than the
+  // others'.  In the default norm mode their walk, clip and pass 2 run on the side stream, so that the
+  // other tensors' pass 2 does not wait for the longest chain; band2 / tiny2 / nwalk / nfinal then hold
+  // the other tensors only.
+  bool walk_split = false;
+  std::map<BandKey, WorkList> band2L;
+  std::map<int, WorkList> tiny2L, nwalkL, nfinalL;
   WorkList factor;                       // F1b / F2b (per state block)
   std::map<int, WorkList> tiles2d_v;     // 8bit2d momentum pass, vector form (per tile row), by grad type
   std::map<int, WorkList> tiles2d;       // 8bit2d momentum pass, scalar form (per 16 rows x 256 columns)
@@ -144,6 +151,9 @@ bool fast_block(int B) { return B >= 8 && B <= kTile && (B & (B - 1)) == 0; }
 constexpr int kP3BandRows = 16;       // rows per work item of the band form of P3 (at most; 32 ran C2 2% slower)
 constexpr int64_t kP3MinItems = 1024;  // band-form P3 work items wanted per launch (4 per CU)
 constexpr int64_t kP3BandMinCols = 1024;  // narrower rows leave too many of a workgroup's lanes idle
+// The clip-norm walk takes 12-17 ns per segment of a tensor's chain and runs serially along it; below
+// this longest chain, the long-chain group's gain is less than its fork and join cost (20-50 us).
+constexpr int64_t kWalkSplitMinSegs = 8192;
 
 int log2_or_minus1(int B) {
   if (B <= 0 || (B & (B - 1)) != 0) return -1;
@@ -569,6 +579,29 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
 
   // --- work lists ---
   const bool fastB = fast_block(B);
+  // The long-chain group: factored tensors with more than half the longest chain's segments, when the
+  // longest chain is long (kWalkSplitMinSegs) and the group holds at most 60% of the factored elements.
+  std::vector<char> longc(size_t(n), 0);
+  {
+    int64_t maxseg = 0;
+    for (int i = 0; i < n; ++i)
+      if (!plan.dev[i].mode2d) maxseg = std::max(maxseg, plan.dev[i].nseg);
+    double nall = 0.0, nlong = 0.0;
+    bool any_short = false;
+    for (int i = 0; i < n; ++i) {
+      const DevTensor& d = plan.dev[i];
+      if (d.mode2d || !ts[i].factored) continue;
+      nall += double(d.N);
+      if (2 * d.nseg > maxseg) {
+        longc[i] = 1;
+        nlong += double(d.N);
+      } else {
+        any_short = true;
+      }
+    }
+    plan.walk_split = maxseg >= kWalkSplitMinSegs && any_short && nlong <= 0.6 * nall;
+    if (!plan.walk_split) longc.assign(size_t(n), 0);
+  }
   for (int i = 0; i < n; ++i) {
     const came8_tensor& t = ts[i];
     const DevTensor& d = plan.dev[i];
@@ -593,12 +626,13 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     if (t.factored) {
       if (tiny_matrix(t, false)) {
         add_item(plan.tiny1[t.grad_dtype], i, ceil_div(d.P, int64_t(kThreads)));
-        add_item(plan.tiny2[t.grad_dtype], i, ceil_div(d.P, int64_t(kThreads)));
+        add_item((longc[i] ? plan.tiny2L : plan.tiny2)[t.grad_dtype], i, ceil_div(d.P, int64_t(kThreads)));
       } else {
         const bool pm_m = d.pm && (d.R * d.C) % B != 0;
         const BandShapeSel sel1 = band_variant(t, d.C, B, 1), sel2 = band_variant(t, d.C, B, 2, pm_m);
         add_item(plan.band[BandKey{t.grad_dtype, sel1.V, sel1.K, sel1.TPB, 0, sel1.ua}], i, d.P * d.nbands);
-        add_item(plan.band2[BandKey{t.grad_dtype, sel2.V, sel2.K, sel2.TPB, d.fp32st, sel2.ua, sel2.multiseg}], i, d.P * d.nbands);
+        add_item((longc[i] ? plan.band2L : plan.band2)[BandKey{t.grad_dtype, sel2.V, sel2.K, sel2.TPB, d.fp32st, sel2.ua,
+                                                              sel2.multiseg}], i, d.P * d.nbands);
       }
       add_item(plan.factor, i, d.nbr + d.nbc);
       // per-matrix momentum blocks that end inside a matrix (B does not divide R*C) are not the flat
@@ -629,8 +663,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       add_item(plan.nbsum, i, d.nblk);
       add_item(plan.nfix[t.grad_dtype * 3 + form], i, ceil_div(d.nseg, int64_t(kNormFixSegs)));
     }
-    add_item(plan.nwalk[t.grad_dtype], i, 8);
-    add_item(plan.nfinal[t.grad_dtype], i, 1);
+    add_item((longc[i] ? plan.nwalkL : plan.nwalk)[t.grad_dtype], i, 8);
+    add_item((longc[i] ? plan.nfinalL : plan.nfinal)[t.grad_dtype], i, 1);
   }
 
   // --- blob: DevTensor[n] then every work list (tids, wstart) ---
@@ -665,6 +699,10 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
   for (auto& kv : plan.nfix) place(kv.second);
   for (auto& kv : plan.nwalk) place(kv.second);
   for (auto& kv : plan.nfinal) place(kv.second);
+  for (auto& kv : plan.band2L) place(kv.second);
+  for (auto& kv : plan.tiny2L) place(kv.second);
+  for (auto& kv : plan.nwalkL) place(kv.second);
+  for (auto& kv : plan.nfinalL) place(kv.second);
   place(plan.factor);
   plan.zero_off = align_up(off);
   off = plan.zero_off + kZeroBytes;
@@ -733,6 +771,10 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     for (auto& kv : plan.nfix) put(kv.second);
     for (auto& kv : plan.nwalk) put(kv.second);
     for (auto& kv : plan.nfinal) put(kv.second);
+    for (auto& kv : plan.band2L) put(kv.second);
+    for (auto& kv : plan.tiny2L) put(kv.second);
+    for (auto& kv : plan.nwalkL) put(kv.second);
+    for (auto& kv : plan.nfinalL) put(kv.second);
     put(plan.factor);
   }
   return CAME8_OK;
@@ -1091,6 +1133,7 @@ struct PassQueues {
   bool can_side, use_side = false;
   double load[2] = {0.0, 0.0};
   bool forked = false;
+  bool pending = false;  // the side stream holds work queued outside a pass (the long-chain group)
   PassQueues(hipStream_t m, const SideQueue& s, bool on) : main(m), side(s), can_side(on) {}
   ~PassQueues() { (void)finish(); }  // an early return still leaves the caller's stream after the side's work
   PassQueues(const PassQueues&) = delete;
@@ -1114,10 +1157,17 @@ struct PassQueues {
     *out = k ? side.s : main;
     return CAME8_OK;
   }
+  // Fork the side stream now, for work queued on it outside a pass; the next finish() joins it.
+  int fork_now() {
+    if (hipEventRecord(side.fork, main) != hipSuccess || hipStreamWaitEvent(side.s, side.fork, 0) != hipSuccess)
+      return fail(CAME8_EHIP, "came8_step: fork to the side stream failed");
+    pending = true;
+    return CAME8_OK;
+  }
   int finish() {
     load[0] = load[1] = 0.0;
-    if (!forked) return CAME8_OK;
-    forked = false;
+    if (!forked && !pending) return CAME8_OK;
+    forked = pending = false;
     if (hipEventRecord(side.join, side.s) != hipSuccess || hipStreamWaitEvent(main, side.join, 0) != hipSuccess)
       return fail(CAME8_EHIP, "came8_step: join of the side stream failed");
     return CAME8_OK;
@@ -1338,6 +1388,63 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
   const bool exact_norm = (h.flags & CAME8_FLAG_EXACT_NORM) != 0;
   const bool fastB = fast_block(h.block_size);
 
+  // the chain walks and per-tensor clips of one group of tensors, on queue q
+  auto launch_walk = [&](const std::map<int, WorkList>& walks, const std::map<int, WorkList>& finals,
+                         hipStream_t q) -> int {
+    using FinFn = void (*)(const DevTensor*, const int32_t*, int, Hp);
+    int r;
+    for (auto& kv : walks) {
+      const WorkList& wl = kv.second;
+      GenFn fn;
+      CAME8_TYPE_SWITCH1(k_norm_walk, kv.first, fn);
+      PhaseTimer pt(PH_NORM_WALK, 0.0, q);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(kNormWalkThreads), 0, q, dT, tids(wl), wst(wl),
+                         int(wl.tids.size()), hp);
+      if ((r = check_launch("norm_walk")) != CAME8_OK) return r;
+    }
+    for (auto& kv : finals) {
+      const WorkList& wl = kv.second;
+      FinFn fn;
+      CAME8_TYPE_SWITCH1(k_norm_final, kv.first, fn);
+      PhaseTimer pt(PH_NORM_FINAL, 0.0, q);
+      hipLaunchKernelGGL(fn, dim3(grid_for(int64_t(wl.tids.size()), kThreads)), blk, 0, q, dT, tids(wl),
+                         int(wl.tids.size()), hp);
+      if ((r = check_launch("norm_final")) != CAME8_OK) return r;
+    }
+    return CAME8_OK;
+  };
+  // P2 of one group of factored tensors: through the pass's queues, or all on queue q
+  auto launch_pass2 = [&](const std::map<BandKey, WorkList>& bands, const std::map<int, WorkList>& tinies,
+                          bool via_pq, hipStream_t q) -> int {
+    int r;
+    for (auto& kv : bands) {
+      const BandKey& k = kv.first;
+      const WorkList& wl = kv.second;
+      const BandFn fn = band_fn(k.gdt, true, k.V, k.K, k.TPB, k.st, k.ua, k.ms);
+      if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
+      const double ab = alg_bytes(plan, wl, tensors, PH_PASS2);
+      if (!via_pq) ls = q;
+      else if ((r = pq.pick(ab, &ls)) != CAME8_OK) return r;
+      PhaseTimer pt(PH_PASS2, ab, ls);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, ls, dT, tids(wl), wst(wl),
+                         int(wl.tids.size()), hp);
+      if ((r = check_launch("pass2")) != CAME8_OK) return r;
+    }
+    for (auto& kv : tinies) {
+      const WorkList& wl = kv.second;
+      GenFn fn;
+      CAME8_TYPE_SWITCH1(k_tiny_pass2, kv.first, fn);
+      const double ab = alg_bytes(plan, wl, tensors, PH_PASS2);
+      if (!via_pq) ls = q;
+      else if ((r = pq.pick(ab, &ls)) != CAME8_OK) return r;
+      PhaseTimer pt(PH_PASS2, ab, ls);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, ls, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
+      if ((r = check_launch("tiny_pass2")) != CAME8_OK) return r;
+    }
+    return CAME8_OK;
+  };
+  bool split = false;  // the long-chain group runs on the side stream (set by the clip-norm section)
+
   // ---- P1 and 1-D pass A ----
   pq.begin(plan.band.size() + plan.tiny1.size() + plan.vecA.size());
   for (auto& kv : plan.band) {
@@ -1384,7 +1491,6 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
   // ---- clip divisor ----
   if (!exact_norm) {  // the update norm in the reference's order (came8_norm.h)
     using EstFn = void (*)(const DevTensor*, const int32_t*, const int64_t*, int, Hp);
-    using FinFn = void (*)(const DevTensor*, const int32_t*, int, Hp);
     if (!plan.nest_w.tids.empty()) {
       const WorkList& wl = plan.nest_w;
       PhaseTimer pt(PH_NORM_EST, 0.0, stream);
@@ -1455,24 +1561,17 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       if ((rc = check_launch("norm_fix")) != CAME8_OK) return rc;
     }
     if ((rc = pq.finish()) != CAME8_OK) return rc;
-    for (auto& kv : plan.nwalk) {
-      const WorkList& wl = kv.second;
-      GenFn fn;
-      CAME8_TYPE_SWITCH1(k_norm_walk, kv.first, fn);
-      PhaseTimer pt(PH_NORM_WALK, 0.0, stream);
-      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(kNormWalkThreads), 0, stream, dT, tids(wl), wst(wl),
-                         int(wl.tids.size()), hp);
-      if ((rc = check_launch("norm_walk")) != CAME8_OK) return rc;
+    // the long-chain group walks on the side stream, then takes its clip and its pass 2 there, while the
+    // other tensors do the same on the caller's stream; the join comes before the residual factors
+    split = plan.walk_split && use_side;
+    if (split) {
+      if ((rc = pq.fork_now()) != CAME8_OK) return rc;
+      if ((rc = launch_walk(plan.nwalkL, plan.nfinalL, side.s)) != CAME8_OK) return rc;
+      if ((rc = launch_pass2(plan.band2L, plan.tiny2L, false, side.s)) != CAME8_OK) return rc;
+    } else if ((rc = launch_walk(plan.nwalkL, plan.nfinalL, stream)) != CAME8_OK) {
+      return rc;
     }
-    for (auto& kv : plan.nfinal) {
-      const WorkList& wl = kv.second;
-      FinFn fn;
-      CAME8_TYPE_SWITCH1(k_norm_final, kv.first, fn);
-      PhaseTimer pt(PH_NORM_FINAL, 0.0, stream);
-      hipLaunchKernelGGL(fn, dim3(grid_for(int64_t(wl.tids.size()), kThreads)), blk, 0, stream, dT, tids(wl),
-                         int(wl.tids.size()), hp);
-      if ((rc = check_launch("norm_final")) != CAME8_OK) return rc;
-    }
+    if ((rc = launch_walk(plan.nwalk, plan.nfinal, stream)) != CAME8_OK) return rc;
   }
   const bool any2d = !plan.tiles2d.empty() || !plan.tiles2d_v.empty();
   if (exact_norm || any2d) {  // reference order: only the 8bit2d tensors take this divisor
@@ -1482,29 +1581,12 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
   }
   // ---- P2, residual factors ----
   if (any_fact) {
-    pq.begin(plan.band2.size() + plan.tiny2.size());
-    for (auto& kv : plan.band2) {
-      const BandKey& k = kv.first;
-      const WorkList& wl = kv.second;
-      BandFn fn = nullptr;
-      fn = band_fn(k.gdt, true, k.V, k.K, k.TPB, k.st, k.ua, k.ms);
-      if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
-      const double ab = alg_bytes(plan, wl, tensors, PH_PASS2);
-      if ((rc = pq.pick(ab, &ls)) != CAME8_OK) return rc;
-      { PhaseTimer pt(PH_PASS2, ab, ls);
-    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, ls, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
-      if ((rc = check_launch("pass2")) != CAME8_OK) return rc; }
-    }
-    for (auto& kv : plan.tiny2) {
-      const WorkList& wl = kv.second;
-      GenFn fn;
-      CAME8_TYPE_SWITCH1(k_tiny_pass2, kv.first, fn);
-      const double ab = alg_bytes(plan, wl, tensors, PH_PASS2);
-      if ((rc = pq.pick(ab, &ls)) != CAME8_OK) return rc;
-      { PhaseTimer pt(PH_PASS2, ab, ls);
-      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, ls, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
-      if ((rc = check_launch("tiny_pass2")) != CAME8_OK) return rc; }
-    }
+    const bool withL = !split;  // else the long-chain group's pass 2 is queued on the side stream already
+    pq.begin(plan.band2.size() + plan.tiny2.size() + (withL ? plan.band2L.size() + plan.tiny2L.size() : 0));
+    if (split)
+      for (auto& kv : plan.band2L) pq.load[1] += alg_bytes(plan, kv.second, tensors, PH_PASS2);
+    if ((rc = launch_pass2(plan.band2, plan.tiny2, true, stream)) != CAME8_OK) return rc;
+    if (withL && (rc = launch_pass2(plan.band2L, plan.tiny2L, true, stream)) != CAME8_OK) return rc;
     for (auto& kv : plan.tiles2d_v) {
       const WorkList& wl = kv.second;
       GenFn fn;

@@ -267,7 +267,8 @@ int came8_read_clip(const void* workspace, uint64_t workspace_tag, int32_t n_ten
 /*
  * Per-stream resources: came8_step keeps one side stream and two events per (device, caller stream)
  * it has stepped on (launches of a pass with many kernel variants are spread over the caller's
- * stream and that side stream).  A side stream not in use by a step is idle; at most 16 idle ones
+ * stream and that side stream, and the tensors with the longest clip-norm chains take their walk,
+ * clip and pass 2 there).  A side stream not in use by a step is idle; at most 16 idle ones
  * are kept, the least recently used released (after its work completes) when another is needed.
  * came8_side_stream_count returns how many are kept now.  No reference counterpart (the reference
  * launches on the caller's stream only).

@@ -90,3 +90,43 @@ def test_side_streams_are_bounded_across_caller_streams():
             assert torch.equal(a.data, b.data), f"stream {k} tensor {i}: parameters differ"
     assert lib.came8_side_stream_count() <= 16, lib.came8_side_stream_count()
     assert most <= 17, most  # the 16 idle ones and at most the one a step was using
+
+
+# The long-chain group: a matrix whose clip-norm chain is at least 8192 segments of 4096 elements and
+# more than twice as long as the others', holding at most 60% of the factored elements.  An eager
+# came8_step walks it, takes its clip and runs its pass 2 on the side stream while the other tensors do
+# the same on the caller's stream; under graph capture everything stays on one stream in pass order.
+LONG_SHAPES = [(8200, 4096), (2048, 4096), (1000, 11008), (2048, 4096), (4096,), (3, 5, 7)]
+
+
+def test_long_chain_group_matches_one_stream():
+    dtype = torch.bfloat16
+    params0 = P.make_params(LONG_SHAPES, dtype, seed=41)
+    gen = torch.Generator(device="cuda").manual_seed(43)
+    hp = dict(lr=2e-4, weight_decay=1e-2)
+    pe = [torch.nn.Parameter(p.clone().cuda()) for p in params0]
+    pg = [torch.nn.Parameter(p.clone().cuda()) for p in params0]
+    oe = came_amd.CAME8bit(pe, **hp)
+    og = came_amd.CAME8bit(pg, **hp)
+    static = [torch.zeros_like(p) for p in pg]
+    for p, g in zip(pg, static):
+        p.grad = g
+    og.prime_for_cuda_graph()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        og.step()
+    torch.cuda.synchronize()
+    for step in range(3):
+        grads = [(torch.randn(s, generator=gen, device="cuda") * 1e-3).to(dtype) for s in LONG_SHAPES]
+        for p, sg, g in zip(pe, static, grads):
+            p.grad = g
+            sg.copy_(g)
+        oe.step()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(pe, pg)):
+            where = f"step {step + 1} tensor {i} {tuple(a.shape)}"
+            assert torch.equal(a.data, b.data), f"{where}: parameters differ"
+            for k, v in oe.state[a].items():
+                if torch.is_tensor(v):
+                    assert torch.equal(v, og.state[b][k]), f"{where}: state {k} differs"
