@@ -136,8 +136,9 @@ float chain_serial(const float* x, int64_t n) {
   return s;
 }
 
-/* est[g]: estimated chain value at the start of segment g; returns the chain, *replays the count */
-float chain_replay(const float* x, int64_t n, const double* est, int64_t* replays) {
+/* est[g]: estimated chain value at the start of segment g; returns the chain, *replays the count of
+   replayed segments and *rounds the wavefront rounds they took */
+float chain_replay_stats(const float* x, int64_t n, const double* est, int64_t* replays, int64_t* rounds) {
   const int L = 512;
   int64_t nseg = (n + L - 1) / L;
   int* Ea = malloc(sizeof(int) * (nseg ? nseg : 1));
@@ -153,6 +154,7 @@ float chain_replay(const float* x, int64_t n, const double* est, int64_t* replay
   }
   float s = 0.0f;
   *replays = 0;
+  *rounds = 0;
   for (int64_t g = 0; g < nseg && s == s; ++g) {
     int64_t k0 = g * L, cnt = n - k0 < L ? n - k0 : L;
     int ok = 0;
@@ -171,9 +173,8 @@ float chain_replay(const float* x, int64_t n, const double* est, int64_t* replay
       ok = 1; /* s = +inf and no element of the segment can be NaN */
     }
     if (!ok) {
-      int64_t rounds = 0;
       ++*replays;
-      s = segment_replay(x + k0, (int)cnt, s, &rounds);
+      s = segment_replay(x + k0, (int)cnt, s, rounds);
     }
   }
   free(Ea);
@@ -181,4 +182,9 @@ float chain_replay(const float* x, int64_t n, const double* est, int64_t* replay
   free(wa);
   free(wb);
   return s;
+}
+
+float chain_replay(const float* x, int64_t n, const double* est, int64_t* replays) {
+  int64_t rounds = 0;
+  return chain_replay_stats(x, n, est, replays, &rounds);
 }

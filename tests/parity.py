@@ -168,6 +168,39 @@ def make_params(shapes, dtype, seed, device="cpu"):
     return [(torch.randn(s, generator=gen) * 0.02).to(dtype) for s in shapes]
 
 
+# Tie-dense clip-norm chains: bf16 gradients m * 2^(k - 20), m an integer in [64, 127] (7 significant bits),
+# k uniform in [-8, 0], random signs.  Under a power-of-two factor the update u keeps those bits, so each
+# u^2 has at most 14 significant bits and its lowest set bit lies at one of nine exponents: wherever the
+# running sum's unit is twice that bit, the fused multiply-add lands exactly half-way (a rounding tie).
+# TIE_DENSE_STATE makes the factors powers of two in the first step with betas[1] = 0.5: row states 255
+# (every row alike: r_i = 1) and column states 128 (c_j = rsqrt(0.5 * 128) = 1/8), which g^2 <= 2^-26
+# does not move.
+TIE_DENSE_BETAS = (0.9, 0.5, 0.9999)
+
+
+def tie_dense_grad(gen, shape):
+    n = math.prod(shape)
+    m = torch.randint(64, 128, (n,), generator=gen).double()
+    k = torch.randint(-8, 1, (n,), generator=gen).double()
+    sign = torch.where(torch.rand(n, generator=gen) < 0.5, -1.0, 1.0).double()
+    return (sign * m * torch.exp2(k - 20)).reshape(shape).to(torch.bfloat16)
+
+
+# The tie-dense case of the GPU walk test and its counts under the replay rules (the C model of
+# tests/native/norm_replay_model.c with exact estimates, pinned by tests/test_norm_replay_model.py): the
+# most segments one of the eight chains replays (of 2048) and the most wavefront rounds those replays take.
+TIE_SHAPE, TIE_SEED = (2048, 4096), 11
+TIE_REPLAYS_MAX, TIE_ROUNDS_MAX = 1058, 14886
+
+
+def tie_dense_state(state: dict) -> None:
+    """Second-moment codes of a factored full8bit state (flat or GPU tensors) set to the power-of-two
+    factor state described at TIE_DENSE_BETAS: rows 255, columns 128, absmax 255."""
+    for key, code in (("factored_row", 255), ("factored_col", 128)):
+        state[key + "_q"].view(2, -1)[0].fill_(code)
+        state[key + "_absmax"].view(2, -1)[0].fill_(255.0)
+
+
 def heavy_grad(gen, shape, dtype):
     """Student-t(2) * 1e-3 with 10% exact zeros and ~1 outlier of +-1e3 per 256 elements."""
     z = torch.randn(shape, generator=gen)

@@ -187,3 +187,52 @@ def test_norm_memory_and_camecuda():
          max_ulps=4, betas=(0.9, 0.95, 0.995))
     _run("CAMECUDA", [((256, 5460), "latin", BF16), ((300, 5461), "normal", BF16), ((2048,), "normal", F32),
                       ((33, 4, 4), "heavy", F32)], max_ulps=4)
+
+
+# Time bound of the walk on tie-dense chains: every replayed segment costs a load of its elements and
+# factors (at most 6 us, under contention) and every wavefront round at most 0.8 us (a round's scan,
+# ballot and lane reads are one dependent chain of about 2000 cycles: 14.5 ms measured for this input,
+# 18.7 ms allowed); the counts are the replay rules' on this input (tests.parity.TIE_REPLAYS_MAX /
+# TIE_ROUNDS_MAX, pinned on the CPU).
+WALK_US_PER_REPLAY, WALK_US_PER_ROUND, WALK_MS_FIXED = 6.0, 0.8, 0.5
+
+
+def test_norm_walk_on_tie_dense_chains_is_bounded():
+    """A 2048 x 4096 bf16 matrix whose update under power-of-two factors puts a rounding tie in about
+    half of every chain's segments (1058 of 2048 replayed, against ~16 for Gaussian data): the divisor is
+    the reference's bit for bit, and the walk's time stays within the bound its replay and round counts
+    give.  A Gaussian matrix of the same shape from the zero state (factors that are not powers of two,
+    so an update of 24 significant bits) is timed beside it."""
+    import came_amd
+    from came_amd import _lib
+    gen = torch.Generator().manual_seed(P.TIE_SEED)
+    g = P.tie_dense_grad(gen, P.TIE_SHAPE)
+    p0 = (torch.randn(P.TIE_SHAPE, generator=gen) * 0.02).to(torch.bfloat16)
+    hp = dict(lr=2e-4, weight_decay=0.0, betas=P.TIE_DENSE_BETAS, clip_threshold=1e-6)
+    walk = {}
+    for kind in ("normal", "tie-dense"):
+        grad = g if kind == "tie-dense" else (torch.randn(P.TIE_SHAPE, generator=gen) * 1e-5).to(torch.bfloat16)
+        ps = [torch.nn.Parameter(p0.clone().to(DEV))]
+        opt = came_amd.CAME8bit(ps, **hp)
+        ps[0].grad = grad.to(DEV)
+        opt.prime_for_cuda_graph()  # creates the state
+        st = orc.init_full8bit_state(P.TIE_SHAPE)
+        if kind == "tie-dense":
+            P.tie_dense_state(opt.state[ps[0]])
+            P.tie_dense_state(st)
+        torch.cuda.synchronize()
+        _lib.profile_enable(True)
+        _lib.profile_read(reset=True)
+        opt.step()
+        torch.cuda.synchronize()
+        phases = _lib.profile_read(reset=True)
+        _lib.profile_enable(False)
+        walk[kind] = phases["norm_walk"][1]
+        cap = {}
+        orc.full8bit_step(p0.clone(), grad, st, capture=cap, **P.oracle_hp(hp))
+        have, want = opt.last_clip_divisors()[ps[0]], float(cap["clip"])
+        print(f"[walk] {kind}: {walk[kind]:.3f} ms; clip {have!r} vs {want!r}", flush=True)
+        # exact factors make u the reference's bit for bit; the Gaussian case's factors may differ by an ulp
+        assert _ulps(have, want) <= (0 if kind == "tie-dense" else 4), f"{kind}: clip {have!r} != reference {want!r}"
+    bound = (P.TIE_REPLAYS_MAX * WALK_US_PER_REPLAY + P.TIE_ROUNDS_MAX * WALK_US_PER_ROUND) / 1e3 + WALK_MS_FIXED
+    assert walk["tie-dense"] <= bound, f"tie-dense walk {walk['tie-dense']:.3f} ms > bound {bound:.3f} ms"

@@ -29,6 +29,9 @@ def lib(tmp_path_factory):
     so.chain_serial.argtypes = [ctypes.c_void_p, ctypes.c_int64]
     so.chain_replay.restype = ctypes.c_float
     so.chain_replay.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64)]
+    so.chain_replay_stats.restype = ctypes.c_float
+    so.chain_replay_stats.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                      ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]
     so.chain_serial_from.restype = ctypes.c_float
     so.chain_serial_from.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_float]
     so.segment_replay.restype = ctypes.c_float
@@ -102,6 +105,39 @@ def test_replays_are_few_on_realistic_chains(lib):
     b = lib.chain_replay(x.ctypes.data, n, est.ctypes.data, ctypes.byref(rep))
     assert np.float32(a).tobytes() == np.float32(b).tobytes()
     assert rep.value < 60, rep.value
+
+
+def test_replays_on_tie_dense_chains(lib):
+    """The tie-dense matrix of the GPU walk test (tests.parity.tie_dense_grad under power-of-two factors):
+    the oracle's first step with that state has factors r_i = 1 and c_j = 1/8 exactly, so u = g / 8; each
+    of its eight chains (1 M elements, 2048 segments) replays about half of its segments, against 16 for
+    a Gaussian chain of the same length, and the counts are the ones the GPU test bounds its time by."""
+    import torch
+    from oracle import came8_oracle as orc
+    from tests import parity as P
+    gen = torch.Generator().manual_seed(P.TIE_SEED)
+    g = P.tie_dense_grad(gen, P.TIE_SHAPE)
+    st = orc.init_full8bit_state(P.TIE_SHAPE)
+    P.tie_dense_state(st)
+    cap = {}
+    hp = P.oracle_hp(dict(lr=2e-4, weight_decay=0.0, betas=P.TIE_DENSE_BETAS, clip_threshold=1e-6))
+    orc.full8bit_step(torch.zeros(P.TIE_SHAPE, dtype=torch.bfloat16), g, st, capture=cap, **hp)
+    assert bool((cap["sq_row"] == 127.5).all()) and bool((cap["sq_col"] == 64.0).all())
+    u = (g.float() * 0.125).reshape(-1).numpy()
+    reps, rounds = [], []
+    for c in range(8):
+        x = np.ascontiguousarray(u[c::8])
+        n = x.size
+        nseg = (n + 511) // 512
+        est = np.ascontiguousarray(np.concatenate([[0.0], np.cumsum(x.astype(np.float64) ** 2)])[::512][:nseg])
+        rep, rnd = ctypes.c_int64(0), ctypes.c_int64(0)
+        a = lib.chain_serial(x.ctypes.data, n)
+        b = lib.chain_replay_stats(x.ctypes.data, n, est.ctypes.data, ctypes.byref(rep), ctypes.byref(rnd))
+        assert np.float32(a).tobytes() == np.float32(b).tobytes()
+        assert rep.value >= 0.4 * nseg, f"chain {c}: {rep.value} of {nseg} segments replayed: not tie-dense"
+        reps.append(rep.value)
+        rounds.append(rnd.value)
+    assert (max(reps), max(rounds)) == (P.TIE_REPLAYS_MAX, P.TIE_ROUNDS_MAX), (reps, rounds)
 
 
 def _starts(rng):
