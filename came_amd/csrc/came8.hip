@@ -80,8 +80,8 @@ float round_to_f16(float f) { return float(_Float16(f)); }
 
 // Kernel-variant keys.
 struct BandKey {
-  // st: fp32 states (pass 2 only); ua: rows of any length/alignment; ms: rows wider than a sweep in
-  // column segments (pass 2 only)
+  // st: fp32 states (pass 2), no column sums of g^2/R_i (pass 1: k_fact_pass1n); ua: rows of any
+  // length/alignment; ms: rows wider than a sweep in column segments (pass 2, k_fact_pass1n)
   int gdt, V, K, TPB, st = 0, ua = 0, ms = 0;
   bool operator<(const BandKey& o) const {
     return std::tie(gdt, V, K, TPB, st, ua, ms) < std::tie(o.gdt, o.V, o.K, o.TPB, o.st, o.ua, o.ms);
@@ -101,7 +101,9 @@ struct WorkList {
 
 struct Plan {
   std::vector<DevTensor> dev;
-  std::map<BandKey, WorkList> band;      // P1 (every factored tensor)
+  std::map<BandKey, WorkList> band;      // P1 of the exact clip mode (factored tensors of the full8bit / fp32 layouts)
+  std::map<BandKey, WorkList> bandN;     // P1 of the default clip mode, the same tensors (k_fact_pass1n; st = 1)
+  std::map<BandKey, WorkList> band2dw;   // P1 of the 8bit2d tensors (both modes: their clip takes W)
   std::map<BandKey, WorkList> band2;     // P2 (factored tensors of the full8bit / fp32 layouts)
   std::map<int, WorkList> tiny1;         // P1 of tensors of tiny matrices (per 256 matrices), by grad type
   std::map<int, WorkList> tiny2;         // P2 of tensors of tiny matrices, by grad type
@@ -460,8 +462,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       return o;
     };
     struct Offs {
-      size_t Rn, rfac, RRn, rrfac, Cn, cfac, CRn, crfac, pU, pW, pR, rm, rmr, clipp, clip, t2r, t2c, nest, nrec, nsum,
-          nbsum, nch;
+      size_t Rn, rfac, RRn, rrfac, Cn, cfac, CRn, crfac, pU, pW, pR, rm, rmr, esm, clipp, clip, t2r, t2c, nest, nrec,
+          nsum, nbsum, nch;
     } o{};
     d.idx32 = d.N < (int64_t(1) << 31) ? 1 : 0;
     d.rowal = (d.C % B) == 0 ? 1 : 0;
@@ -498,6 +500,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
         o.pR = take(part);
       }
       o.rm = take(size_t(d.P * d.nbands) * 4);
+      o.esm = take(size_t(d.P * d.nbands) * 4);
       o.rmr = take(size_t(d.P * (s2d ? std::max<int64_t>(d.nbands, d.tr) : d.nbands)) * 4);
       o.clipp = take(size_t(d.nclip) * 8);
       o.clip = take(8);
@@ -551,7 +554,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       } else {
         d.partRes = at(o.pR);
       }
-      d.rsum = at(o.rm); d.rrsum = at(o.rmr);
+      d.rsum = at(o.rm); d.rrsum = at(o.rmr); d.esum = at(o.esm);
     }
     d.clip_part = reinterpret_cast<double*>(scr + o.clipp);
     d.clip = at(o.clip);
@@ -608,7 +611,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     const TypeKey tk{t.param_dtype, t.grad_dtype, d.fp32st};
     if (d.mode2d) {
       const BandShapeSel sel = band_variant(t, d.C, B, 1);
-      add_item(plan.band[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB, 0, sel.ua}], i, d.nbands);
+      add_item(plan.band2dw[BandKey{t.grad_dtype, sel.V, sel.K, sel.TPB, 0, sel.ua}], i, d.nbands);
       add_item(plan.factor, i, d.nbr + d.nbc);
       if (d.v2d) {
         add_item(plan.tiles2d_v[t.grad_dtype], i, d.tr);
@@ -630,7 +633,11 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       } else {
         const bool pm_m = d.pm && (d.R * d.C) % B != 0;
         const BandShapeSel sel1 = band_variant(t, d.C, B, 1), sel2 = band_variant(t, d.C, B, 2, pm_m);
+        // the default mode's pass 1 takes pass 2's row shapes (column segments for wide rows)
+        const BandShapeSel sel1n = band_variant(t, d.C, B, 2);
         add_item(plan.band[BandKey{t.grad_dtype, sel1.V, sel1.K, sel1.TPB, 0, sel1.ua}], i, d.P * d.nbands);
+        add_item(plan.bandN[BandKey{t.grad_dtype, sel1n.V, sel1n.K, sel1n.TPB, 1, sel1n.ua, sel1n.multiseg}], i,
+                 d.P * d.nbands);
         add_item((longc[i] ? plan.band2L : plan.band2)[BandKey{t.grad_dtype, sel2.V, sel2.K, sel2.TPB, d.fp32st, sel2.ua,
                                                               sel2.multiseg}], i, d.P * d.nbands);
       }
@@ -676,6 +683,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     off = align_up(off + wl.wstart.size() * 8, 16);
   };
   for (auto& kv : plan.band) place(kv.second);
+  for (auto& kv : plan.bandN) place(kv.second);
+  for (auto& kv : plan.band2dw) place(kv.second);
   for (auto& kv : plan.band2) place(kv.second);
   for (auto& kv : plan.tiny1) place(kv.second);
   for (auto& kv : plan.tiny2) place(kv.second);
@@ -729,7 +738,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
         } else {
           rebase(d.partRes);
         }
-        rebase(d.rsum); rebase(d.rrsum);
+        rebase(d.rsum); rebase(d.rrsum); rebase(d.esum);
       }
       rebase(d.clip_part);
       rebase(d.clip);
@@ -748,6 +757,8 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       std::memcpy(plan.blob.data() + wl.wstart_off, wl.wstart.data(), wl.wstart.size() * 8);
     };
     for (auto& kv : plan.band) put(kv.second);
+    for (auto& kv : plan.bandN) put(kv.second);
+    for (auto& kv : plan.band2dw) put(kv.second);
     for (auto& kv : plan.band2) put(kv.second);
     for (auto& kv : plan.tiny1) put(kv.second);
     for (auto& kv : plan.tiny2) put(kv.second);
@@ -850,6 +861,7 @@ Hp make_hp(const came8_hparams& h) {
   const float lr_wd = float(h.lr) * float(h.weight_decay);
   hp.wdfac = 1.0f - lr_wd;
   hp.fp16u = (h.flags & CAME8_FLAG_FP16_UPDATE) ? 1 : 0;
+  hp.noW = (h.flags & CAME8_FLAG_EXACT_NORM) ? 0 : 1;
   hp.B = h.block_size;
   hp.log2B = log2_or_minus1(h.block_size);
   if (hp.log2B >= 0) {
@@ -867,9 +879,9 @@ Hp make_hp(const came8_hparams& h) {
 // band-pass kernels are instantiated in came8_band.hip (one translation unit per family)
 BandFn band_fn(int gdt, bool pass2, int V, int K, int TPB, int st, int ua, int ms) {
   switch (gdt) {
-    case CAME8_F32: return pass2 ? band_fn_F32_p2(V, K, TPB, st, ua, ms) : band_fn_F32_p1(V, K, TPB, st, ua, 0);
-    case CAME8_BF16: return pass2 ? band_fn_BF16_p2(V, K, TPB, st, ua, ms) : band_fn_BF16_p1(V, K, TPB, st, ua, 0);
-    case CAME8_F16: return pass2 ? band_fn_F16_p2(V, K, TPB, st, ua, ms) : band_fn_F16_p1(V, K, TPB, st, ua, 0);
+    case CAME8_F32: return pass2 ? band_fn_F32_p2(V, K, TPB, st, ua, ms) : band_fn_F32_p1(V, K, TPB, st, ua, ms);
+    case CAME8_BF16: return pass2 ? band_fn_BF16_p2(V, K, TPB, st, ua, ms) : band_fn_BF16_p1(V, K, TPB, st, ua, ms);
+    case CAME8_F16: return pass2 ? band_fn_F16_p2(V, K, TPB, st, ua, ms) : band_fn_F16_p1(V, K, TPB, st, ua, ms);
     default: return nullptr;
   }
 }
@@ -1446,18 +1458,23 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
   bool split = false;  // the long-chain group runs on the side stream (set by the clip-norm section)
 
   // ---- P1 and 1-D pass A ----
-  pq.begin(plan.band.size() + plan.tiny1.size() + plan.vecA.size());
-  for (auto& kv : plan.band) {
-    const BandKey& k = kv.first;
-    const WorkList& wl = kv.second;
-    BandFn fn = nullptr;
-    fn = band_fn(k.gdt, false, k.V, k.K, k.TPB, 0, k.ua, 0);
-    if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
-    const double ab = alg_bytes(plan, wl, tensors, PH_PASS1);
-    if ((rc = pq.pick(ab, &ls)) != CAME8_OK) return rc;
-    { PhaseTimer pt(PH_PASS1, ab, ls);
-    hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, ls, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
-    if ((rc = check_launch("pass1")) != CAME8_OK) return rc; }
+  // the default clip mode's pass 1 keeps no column sums of g^2/R_i (k_fact_pass1n), except for the
+  // 8bit2d tensors, whose clip is formed from them
+  const std::map<BandKey, WorkList>& band1 = exact_norm ? plan.band : plan.bandN;
+  pq.begin(band1.size() + plan.band2dw.size() + plan.tiny1.size() + plan.vecA.size());
+  for (const auto* lists : {&band1, &plan.band2dw}) {
+    for (auto& kv : *lists) {
+      const BandKey& k = kv.first;
+      const WorkList& wl = kv.second;
+      const BandFn fn = band_fn(k.gdt, false, k.V, k.K, k.TPB, k.st, k.ua, k.ms);
+      if (!fn) return fail(CAME8_EINVAL, "came8_step: no band kernel for this variant");
+      const double ab = alg_bytes(plan, wl, tensors, PH_PASS1);
+      if ((rc = pq.pick(ab, &ls)) != CAME8_OK) return rc;
+      PhaseTimer pt(PH_PASS1, ab, ls);
+      hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), dim3(k.TPB), 0, ls, dT, tids(wl), wst(wl),
+                         int(wl.tids.size()), hp);
+      if ((rc = check_launch("pass1")) != CAME8_OK) return rc;
+    }
   }
   for (auto& kv : plan.tiny1) {
     const WorkList& wl = kv.second;

@@ -15,11 +15,14 @@ namespace {
 using TG = CAME8_BAND_TYPE;
 constexpr int kVW = 16 / int(sizeof(TG::storage));  // elements per 16-byte chunk
 
+// st: pass 2 with fp32 states; pass 1 without the column sums of g^2/R_i (k_fact_pass1n, which also
+// has the MS variants)
 template <int V, int K, int TPB, bool UA = false, bool MS = false>
 BandFn pick(int st) {
   if constexpr (CAME8_BAND_PASS == 2)
     return st ? k_fact_pass2<TG, V, K, TPB, true, UA, MS> : k_fact_pass2<TG, V, K, TPB, false, UA, MS>;
-  else return (void)st, k_fact_pass1<TG, V, K, TPB, UA>;
+  else if constexpr (MS) return st ? k_fact_pass1n<TG, V, K, TPB, UA, true> : nullptr;
+  else return st ? k_fact_pass1n<TG, V, K, TPB, UA> : k_fact_pass1<TG, V, K, TPB, UA>;
 }
 template <int V, int K, int TPB>
 BandFn pick_ua(int st, int ua) {
@@ -27,16 +30,13 @@ BandFn pick_ua(int st, int ua) {
 }
 }  // namespace
 
-// the (V, K, TPB) variants the host's band_variant() can choose; st selects fp32 states (pass 2), ua the
-// variants for rows of any length and alignment, ms pass 2's variants for rows wider than their sweep
+// the (V, K, TPB) variants the host's band_variant() can choose; st selects fp32 states (pass 2) or the
+// default clip mode's pass 1, ua the variants for rows of any length and alignment, ms the variants for
+// rows wider than their sweep (pass 2, and pass 1 with st)
 BandFn CAME8_BAND_SELECTOR(CAME8_BAND_TYPE, CAME8_BAND_PASS)(int V, int K, int TPB, int st, int ua, int ms) {
-  if constexpr (CAME8_BAND_PASS == 2) {
-    if (ms) {
-      if (V == 1 && K == 32 && TPB == 256 && !ua) return pick<1, 32, 256, false, true>(st);
-      if (V == kVW && K == 3 && TPB == 256 && !ua) return pick<kVW, 3, 256, false, true>(st);
-      return nullptr;
-    }
-  } else if (ms) {
+  if (ms) {
+    if (V == 1 && K == 32 && TPB == 256 && !ua) return pick<1, 32, 256, false, true>(st);
+    if (V == kVW && K == 3 && TPB == 256 && !ua) return pick<kVW, 3, 256, false, true>(st);
     return nullptr;
   }
   if (V == 1 && TPB == 256 && !ua) {

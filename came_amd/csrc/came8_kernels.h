@@ -107,6 +107,9 @@ struct alignas(128) DevTensor {  // each descriptor on whole cache lines
   // state (C).  nbm, nbr, nbc are then P times these.
   int32_t pm;
   int64_t pmb_m, pmb_r, pmb_c;
+  // default clip mode: per row band the sum of e_i / R_i (e_i the row's sum of g^2), which the
+  // clip-norm estimates weigh with the band's column partials of g^2 [P*nbands]
+  float* esum;
 };
 
 // fp32-state views of the state pointers
@@ -132,6 +135,7 @@ struct Hp {
   float wdfac;          // 8bit2d: multiplicative weight decay 1 - lr * wd, computed in float
   const void* zeros;    // kZeroBytes of zeros in the workspace (reads that must count for nothing)
   int32_t fp16u;        // 1-D tensors: the momentum takes the update rounded to fp16 (CAME8_FLAG_FP16_UPDATE)
+  int32_t noW;          // default clip mode: the band passes wrote no column sums of g^2/R_i (partW)
 };
 constexpr int kZeroBytes = 32768;  // >= TPB*V*K elements of any band-pass shape
 
@@ -636,6 +640,187 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1(const DevTensor* __restrict_
       __syncthreads();  // rowR is reused by the next work item
     }
     if (tid == 0) t.rsum[b * t.nbands + it.band] = float(bandR);
+    __syncthreads();  // rowold is rewritten by the next work item
+  }
+}
+
+// ---------------- P1, default clip mode ----------------
+// Pass 1 without the column sums of g^2/R_i.  Only the exactly rounded clip and the clip-norm
+// estimates use them; in the default mode the estimates take instead each band's sum of e_i/R_i
+// (e_i the row's sum of g^2; esum) with the band's column profile of g^2 (the partials of U), and the
+// exact clip is not formed.  No column sum then needs a row's R_i, so:
+//   * the stage loop has no barrier: each wave's share of a row sum goes to LDS (rows past the band
+//     end to a dummy row), and the band's rows are combined once, after its last stage;
+//   * rows wider than one sweep of the workgroup are taken in column segments (MS), each over all of
+//     the band's rows, the per-wave row sums adding up over the segments; every element is read once.
+// The row sums, new row states and column partials are those of k_fact_pass1 (the same fp64 sums;
+// a row's waves combined in the same order for single-sweep rows).
+template <typename TG, int V, int K, int TPB, bool UA = false, bool MS = false>
+__global__ __launch_bounds__(TPB) void k_fact_pass1n(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
+                                                     const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  using GS = typename TG::storage;
+  using Acc = ColAcc<V, K>;
+  using CK = Chunk<TG, V, UA>;
+  constexpr int NW = TPB / kWave;
+  constexpr int S = (V > 1 && K == 1) ? 2 : Stage<TG, V, K>::S;
+  constexpr int64_t segw = int64_t(TPB) * V * K;
+  __shared__ double rowpart[2][kMaxBandRows + 1][NW];  // per-wave row sums of a band (+1: a dummy row)
+  __shared__ float rowval[kMaxBandRows];  // the band's new row states
+  __shared__ float rowe[kMaxBandRows];    // e_i / R_i
+  __shared__ float rowold[kMaxBandRows];  // the band's old row states
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  int bpar = 0;
+  const int64_t total = wstart[ntens];
+  for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const BandItem it = band_item(T, tids, wstart, ntens, w);
+    const DevTensor& t = *it.t;
+    const int64_t R = t.R, C = t.C, b = it.b, r0 = it.r0, r1 = it.r1;
+    const CAME8_GLOBAL GS* __restrict__ g = gbl(static_cast<const GS*>(t.g) + (b * R) * C);
+    const CAME8_GLOBAL uint8_t* __restrict__ rq = gbl(t.rq);
+    const CAME8_GLOBAL float* __restrict__ ra = gbl(t.ra);
+    const int64_t rbb = t.pm ? b * t.pmb_r : 0, roff = t.pm ? 0 : b * R;  // row state blocks, as in k_fact_pass1
+    CAME8_GLOBAL float* __restrict__ Rn = gbl(t.Rn);
+    const int64_t nseg = (C + segw - 1) / segw;
+    CAME8_GLOBAL float* __restrict__ pU = gbl(t.partU + (b * t.nbands + it.band) * C);
+    const float band_eps = float(r1 - r0) * hp.eps0;  // eps0 of each element of a column partial
+    const float invC = 1.0f / float(C);
+    // The old row states go through LDS (a per-row global load at the band's end would wait for the
+    // stage loop's loads as well); MS clears the per-wave row sums, which add up over the segments.
+    auto stage_rows = [&]() __attribute__((always_inline)) {
+      for (int64_t rr = tid; rr < r1 - r0; rr += TPB) {
+        const int64_t row = b * R + r0 + rr;
+        rowold[rr] = t.fp32st ? gbl(st_sq_row(t))[row] : deq_u8(rq[row], ra[rbb + blk_of(roff + r0 + rr, hp)]);
+      }
+      if constexpr (MS) {
+        for (int64_t i = tid; i < (r1 - r0) * NW; i += TPB) rowpart[bpar][i / NW][i % NW] = 0.0;
+        if (tid < NW) rowpart[bpar][kMaxBandRows][tid] = 0.0;
+      }
+      wait_vm_all();  // on every path: the stage loop's waits then count only its own loads
+      __syncthreads();
+    };
+    int32_t coff[K], cskip[K];
+    bool cok[K];
+    uint32_t gmask[UA ? K : 1][CK::NWD];
+    Acc colU[K][V];
+    auto setup_segment = [&](int64_t cbase) __attribute__((always_inline)) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int32_t c = int32_t(cbase) + (tid + k * TPB) * V;
+        cok[k] = c < C;  // without UA, C % V == 0: a chunk that starts inside the row ends inside it
+        coff[k] = cok[k] ? c : 0;
+        cskip[k] = 0;
+        if constexpr (UA) {  // the row's partial last chunk reads the row's last V elements
+          if (cok[k] && c + V > C) {
+            coff[k] = int32_t(C) - V;
+            cskip[k] = c - coff[k];
+          }
+#pragma unroll
+          for (int i = 0; i < CK::NWD; ++i) gmask[k][i] = keep_mask(i, cskip[k], int(sizeof(GS)));
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) colU[k][v] = Acc(0);
+      }
+    };
+    // The stage loop issues loads only, unconditionally: a chunk past the row end (cok false) loads the
+    // row's first chunk and is skipped, and a row past the band end loads the band's last row and adds
+    // nothing (its row sum goes to the dummy row).
+    auto load_stage = [&](CK (&buf)[S][K], int64_t r) __attribute__((always_inline)) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const CAME8_GLOBAL GS* __restrict__ grow = g + ((r + s < r1) ? (r + s) : (r1 - 1)) * C;
+#pragma unroll
+        for (int k = 0; k < K; ++k) buf[s][k].load(grow + coff[k]);
+      }
+    };
+    auto process = [&](CK (&buf)[S][K], int64_t r) __attribute__((always_inline)) {
+      if constexpr (UA) {  // the masked leading elements of a partial last chunk read as zero
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+          for (int k = 0; k < K; ++k) buf[s][k].mask(gmask[k]);
+      }
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const bool rok = r + s < r1;  // uniform
+        double ps = 0.0;
+        if (rok) {
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            if (cok[k]) {
+#pragma unroll
+              for (int v = 0; v < V; ++v) {
+                const double x = double(buf[s][k][v]);
+                ps = fma(x, x, ps);
+                colU[k][v] = fma(x, x, colU[k][v]);
+              }
+            }
+          }
+        }
+        const double wsum = wave_sum(ps);
+        const int64_t slot = rok ? (r + s - r0) : int64_t(kMaxBandRows);
+        if (lane == 0) {
+          if constexpr (MS) rowpart[bpar][slot][wid] += wsum;
+          else rowpart[bpar][slot][wid] = wsum;
+        }
+      }
+    };
+    auto segment = [&](int64_t cbase) __attribute__((always_inline)) {
+      setup_segment(cbase);
+      CK A[S][K], Bf[S][K];
+      load_stage(A, r0);
+      for (int64_t r = r0; r < r1; r += 2 * S) {
+        load_stage(Bf, r + S);
+        process(A, r);
+        load_stage(A, r + 2 * S);
+        process(Bf, r + S);
+      }
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        if (cok[k]) {
+#pragma unroll
+          for (int v = 0; v < V; ++v)
+            if (!UA || v >= cskip[k]) pU[coff[k] + v] = float(colU[k][v]) + band_eps;
+        }
+      }
+    };
+    stage_rows();
+    if constexpr (MS) {
+      for (int64_t seg = 0; seg < nseg; ++seg) {
+        segment(seg * segw);
+        if (seg + 1 < nseg) wait_vm_all();  // the partials' stores: the next stage loop waits for loads only
+      }
+    } else {
+      segment(0);  // (the host gives the other variants single-sweep rows only)
+    }
+    __syncthreads();
+    // row totals over the waves in a fixed order, the new row states, and e_i / R_i; the first wave
+    // adds up the band's (lane l over rows l, l+64, ..., then the lanes in the wave sum's order)
+    for (int64_t rr = tid; rr < r1 - r0; rr += TPB) {
+      double tot = rowpart[bpar][rr][0];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) tot += rowpart[bpar][rr][w2];
+      const float Rold = rowold[rr];
+      const float mean = float(tot + double(C) * double(hp.eps0)) * invC;
+      const float Rnew = t.mode2d ? (Rold * hp.b2) + (hp.a2f * mean) : fmaf(mean, hp.a2, Rold * hp.b2);
+      Rn[b * R + r0 + rr] = Rnew;
+      rowval[rr] = Rnew;
+      rowe[rr] = Rnew > 0.0f ? float(tot) / Rnew : 0.0f;
+    }
+    __syncthreads();
+    if (wid == 0) {
+      double sr = 0.0, se = 0.0;
+      for (int64_t rr = lane; rr < r1 - r0; rr += kWave) {
+        sr += rowval[rr];
+        se += rowe[rr];
+      }
+      sr = wave_sum(sr);
+      se = wave_sum(se);
+      if (lane == 0) {
+        t.rsum[b * t.nbands + it.band] = float(sr);
+        t.esum[b * t.nbands + it.band] = float(se);
+      }
+    }
+    bpar ^= 1;  // the next band writes the other half (after this band's barriers above)
     __syncthreads();  // rowold is rewritten by the next work item
   }
 }
@@ -1187,7 +1372,8 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
         } else {
           const float* __restrict__ pp = part + (b * t.nbands) * t.C + j;
           double sw[2] = {0.0, 0.0};  // column sums of the partials, and for !RES of the clip weights
-          if (RES) band_column_sums<1>(pp, nullptr, t.nbands, t.C, sw);
+          // (in the default clip mode the band passes wrote no partW: the clip partial is not used)
+          if (RES || hp.noW) band_column_sums<1>(pp, nullptr, t.nbands, t.C, sw);
           else band_column_sums<2>(pp, t.partW + (b * t.nbands) * t.C + j, t.nbands, t.C, sw);
           const double s = sw[0];
           W = sw[1];

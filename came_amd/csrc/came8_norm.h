@@ -136,9 +136,14 @@ constexpr uint32_t kNormFull = 1u << 24;
 // estimates
 // ---------------------------------------------------------------------------
 // Units: row band b of matrix m (unit m * nbands + b; for matrices of the thread-per-matrix passes the
-// matrix is its band) or 2048-element tile u of a 1-D tensor.  The estimate of a band is
-// rm * sum_j c_j^2 * W_j with W_j = sum over the band's rows of g_ij^2 / R_i (pass 1's column
-// partials): the sum of u_ij^2 = (rm / R_i) * c_j^2 * g_ij^2 without the roundings.
+// matrix is its band) or 2048-element tile u of a 1-D tensor.  The sum of u_ij^2 over a band is
+// rm * sum_i (1 / R_i) * sum_j c_j^2 * g_ij^2 without the roundings.  A matrix of the thread-per-matrix
+// passes has it from W_j = sum_i g_ij^2 / R_i (their column partials): rm * sum_j c_j^2 * W_j.  The band
+// passes of the default clip mode keep no W (k_fact_pass1n); their estimate gives every row of the band
+// the band's column profile of g^2 (the partials U_j):
+//   rm * (sum_i e_i / R_i) * (sum_j c_j^2 U_j) / (sum_j U_j),   e_i = sum_j g_ij^2,
+// exact when the rows' profiles agree (Gaussian rows: ~1e-5 relative per band) and a few percent off
+// on heavy-tailed rows; k_norm_fix rebuilds the records of a chain that the estimate misleads.
 __device__ __forceinline__ float norm_unit_rm(const DevTensor& t, int64_t u) {
   return matrix_row_mean(t, t.rsum, u / t.nbands, t.nbands);
 }
@@ -147,39 +152,56 @@ __device__ __forceinline__ float norm_unit_rm(const DevTensor& t, int64_t u) {
 template <bool WIDE>
 __global__ __launch_bounds__(kThreads) void k_norm_est(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                        const int64_t* __restrict__ wstart, int ntens, Hp hp) {
-  __shared__ float ssum[4];
+  __shared__ float ssum[4], usum[4];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
     const int slot = find_slot(wstart, ntens, w);
     const DevTensor& t = T[tids[slot]];
-    if constexpr (WIDE) {
+    if constexpr (WIDE) {  // band passes (never the thread-per-matrix ones)
       const int64_t u = w - wstart[slot];
       const int64_t m = u / t.nbands;
-      const float* __restrict__ W = t.partW + u * t.C;
+      const float* __restrict__ Up = t.partU + u * t.C;
       const float* __restrict__ cf = t.cfac + m * t.C;
       // kEstBatch columns per thread loaded before the first is added (an estimate: the order is free)
       constexpr int kEstBatch = 8;
-      float acc[kEstBatch] = {};
+      float acc[kEstBatch] = {}, accu[kEstBatch] = {};
       int64_t j = tid;
       for (; j + (kEstBatch - 1) * kThreads < t.C; j += kEstBatch * kThreads) {
-        float c[kEstBatch], wv[kEstBatch];
+        float c[kEstBatch], uv[kEstBatch];
 #pragma unroll
         for (int q = 0; q < kEstBatch; ++q) {
           c[q] = cf[j + q * kThreads];
-          wv[q] = W[j + q * kThreads];
+          uv[q] = Up[j + q * kThreads];
         }
 #pragma unroll
-        for (int q = 0; q < kEstBatch; ++q) acc[q] = fmaf(c[q] * c[q], wv[q], acc[q]);
+        for (int q = 0; q < kEstBatch; ++q) {
+          acc[q] = fmaf(c[q] * c[q], uv[q], acc[q]);
+          accu[q] += uv[q];
+        }
       }
-      for (; j < t.C; j += kThreads) acc[0] = fmaf(cf[j] * cf[j], W[j], acc[0]);
-      float s = 0.0f;
+      for (; j < t.C; j += kThreads) {
+        acc[0] = fmaf(cf[j] * cf[j], Up[j], acc[0]);
+        accu[0] += Up[j];
+      }
+      float s = 0.0f, su = 0.0f;
 #pragma unroll
-      for (int q = 0; q < kEstBatch; ++q) s += acc[q];
+      for (int q = 0; q < kEstBatch; ++q) {
+        s += acc[q];
+        su += accu[q];
+      }
       s = wave_sum(s);
-      if (lane == 0) ssum[wid] = s;
+      su = wave_sum(su);
+      if (lane == 0) {
+        ssum[wid] = s;
+        usum[wid] = su;
+      }
       __syncthreads();
-      if (tid == 0) t.nest[u] = norm_unit_rm(t, u) * (((ssum[0] + ssum[1]) + ssum[2]) + ssum[3]);
+      if (tid == 0) {
+        const float cs = ((ssum[0] + ssum[1]) + ssum[2]) + ssum[3];
+        const float us = ((usum[0] + usum[1]) + usum[2]) + usum[3];
+        t.nest[u] = us > 0.0f ? norm_unit_rm(t, u) * t.esum[u] * (cs / us) : 0.0f;
+      }
       __syncthreads();
     } else {
       const int64_t u = (w - wstart[slot]) * kThreads + tid;
@@ -189,13 +211,23 @@ __global__ __launch_bounds__(kThreads) void k_norm_est(const DevTensor* __restri
       const int64_t b0 = u * t.ngrp, b1 = min(nbase, b0 + t.ngrp);
       float e = 0.0f;
       for (int64_t b = b0; b < b1; ++b) {
-        if (t.factored) {
+        if (t.factored && t.R * t.C <= kTinyElems) {  // the thread-per-matrix passes wrote W
           const int64_t m = b / t.nbands;
           const float* __restrict__ W = t.partW + b * t.C;
           const float* __restrict__ cf = t.cfac + m * t.C;
           float s = 0.0f;
           for (int64_t j = 0; j < t.C; ++j) s = fmaf(cf[j] * cf[j], W[j], s);
           e += norm_unit_rm(t, b) * s;
+        } else if (t.factored) {  // a band pass of the default mode: the band's profile of g^2
+          const int64_t m = b / t.nbands;
+          const float* __restrict__ Up = t.partU + b * t.C;
+          const float* __restrict__ cf = t.cfac + m * t.C;
+          float s = 0.0f, su = 0.0f;
+          for (int64_t j = 0; j < t.C; ++j) {
+            s = fmaf(cf[j] * cf[j], Up[j], s);
+            su += Up[j];
+          }
+          e += su > 0.0f ? norm_unit_rm(t, b) * t.esum[b] * (s / su) : 0.0f;
         } else {
           e += float(t.clip_part[b]);
         }
