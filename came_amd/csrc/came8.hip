@@ -150,7 +150,9 @@ void add_item(WorkList& wl, int32_t tid, int64_t count) {
 
 bool fast_block(int B) { return B >= 8 && B <= kTile && (B & (B - 1)) == 0; }
 
-constexpr int kP3BandRows = 16;       // rows per work item of the band form of P3 (at most; 32 ran C2 2% slower)
+// rows per work item of the band form of P3 (at most).  Measured on C4 / C2 pass 3: 4 rows 10.69 / 0.948 ms,
+// 8 rows 10.37 / 0.923, 16 rows 10.48 / 0.948, 32 rows 10.55 (C4), 64 rows 10.90 (C4)
+constexpr int kP3BandRows = 8;
 constexpr int64_t kP3MinItems = 1024;  // band-form P3 work items wanted per launch (4 per CU)
 constexpr int64_t kP3BandMinCols = 1024;  // narrower rows leave too many of a workgroup's lanes idle
 // The clip-norm walk takes 12-17 ns per segment of a tensor's chain and runs serially along it; below
