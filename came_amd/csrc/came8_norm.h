@@ -65,7 +65,10 @@ namespace came8 {
 constexpr int kNormSegElems = 4096;                    // flat elements per segment (a multiple of 8)
 constexpr int kNormChainSeg = kNormSegElems / 8;       // elements per chain per segment
 constexpr int kNormChunks = kNormSegElems / (8 * 64);  // 8-element chunks per lane of a segment's wavefront
-constexpr int kNormWalkSegs = 16;                      // segments per thread per batch of the walk
+// segments per thread per batch of the walk: after each replay the walk scans its lanes' records again,
+// so a batch of fewer records per lane makes each scan shorter, at one batch load more per 512 segments
+// (C1 0.264 / 0.247 / 0.243 ms with 16 / 8 / 4; C4 the same within 0.03 ms; 32 slower everywhere)
+constexpr int kNormWalkSegs = 8;
 constexpr int kNormPrologue = 64;                      // elements a replay from zero applies one by one
 constexpr int kNormGroup = 2;                          // chunks per lane loaded together
 constexpr int64_t kNormMaxUnits = 4096;                // estimate units per tensor of single-band matrices
@@ -1291,7 +1294,7 @@ __global__ __launch_bounds__(kNormWalkThreads) void k_norm_walk(const DevTensor*
       const int64_t base = bstart + int64_t(lane) * kNormWalkSegs;
       const int64_t bend = min(nseg, bstart + int64_t(kWave) * kNormWalkSegs);
       uint32_t r0[kNormWalkSegs], ra[kNormWalkSegs], rb[kNormWalkSegs];
-      if (base + kNormWalkSegs <= nseg) {  // 16 consecutive records of each array: 4-dword loads
+      if (base + kNormWalkSegs <= nseg) {  // consecutive records of each array: 4-dword loads
 #pragma unroll
         for (int q = 0; q < kNormWalkSegs / 4; ++q) {
           const u32x4u a0 = *reinterpret_cast<const CAME8_GLOBAL u32x4u*>(W0 + base + 4 * q);
