@@ -13,6 +13,7 @@ namespace came8 {
 
 constexpr int kThreads = 256;  // four 64-lane wavefronts per workgroup
 constexpr int kWave = 64;
+constexpr int kXcds = 8;  // MI355X: eight XCDs, each with its own L2
 
 // Global-memory view of a pointer taken from a descriptor (loads and stores through it are
 // global_* instructions instead of flat_* ones, which also wait on the LDS counter).

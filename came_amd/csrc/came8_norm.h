@@ -1278,10 +1278,16 @@ __global__ __launch_bounds__(kNormWalkThreads) void k_norm_walk(const DevTensor*
                                                                 const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   const int lane = threadIdx.x;
   const int64_t total = wstart[ntens];
+  // Workgroup w runs on XCD w % 8 (the dispatcher deals a launch's workgroups to the eight XCDs in
+  // turn).  The items, eight per tensor (its chains), go to the XCDs in eight contiguous ranges, so
+  // that a tensor's chains share one XCD's L2: they mostly replay the same segments at about the same
+  // time, and each replay reads the cache lines that hold all eight chains' elements.
+  const int64_t per = total % kXcds == 0 ? total / kXcds : 0;
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
-    const int slot = find_slot(wstart, ntens, w);
+    const int64_t item = per > 0 ? (w % kXcds) * per + w / kXcds : w;
+    const int slot = find_slot(wstart, ntens, item);
     const DevTensor& t = T[tids[slot]];
-    const int c = int(w - wstart[slot]);
+    const int c = int(item - wstart[slot]);
     const int64_t nseg = t.nseg;
     const CAME8_GLOBAL uint32_t* __restrict__ W0 = gbl(t.nrec + c * nseg);
     const CAME8_GLOBAL uint32_t* __restrict__ WA = gbl(t.nrec + (8 + c) * nseg);
