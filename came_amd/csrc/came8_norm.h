@@ -1165,12 +1165,36 @@ __device__ float norm_replay(const DevTensor& t, int c, int64_t seg, float s, co
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t main = t.N - (t.N & 7);
   const int64_t f0 = seg * kNormSegElems;
-  const int cnt = int(min(int64_t(kNormChainSeg), (main - f0) / 8));
+  const int cnt = int(min(int64_t(kNormChainSeg), (main - f0) / 8));  // at least 1
   float x[8], h[8];
+  if (t.factored && t.idx32) {  // uniform
+    // Every operand of the lane's 8 elements is loaded before the first is waited for (a per-element
+    // branch would wait out each element's loads in turn).  An element past the segment's end reads
+    // the segment's first element of the chain and counts for nothing.
+    using GS = typename TG::storage;
+    const CAME8_GLOBAL GS* __restrict__ gp = gbl(static_cast<const GS*>(t.g));
+    const CAME8_GLOBAL float* __restrict__ rf = gbl(t.rfac);
+    const CAME8_GLOBAL float* __restrict__ cf = gbl(t.cfac);
+    float gv[8], rv[8], cv[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int k = lane * 8 + j;
-    x[j] = k < cnt ? norm_x_at<TG>(t, f0 + 8 * int64_t(k) + c, hp) : 0.0f;
+    for (int j = 0; j < 8; ++j) {
+      const int k = lane * 8 + j;
+      const uint32_t e = uint32_t(f0 + 8 * int64_t(k < cnt ? k : 0) + c);
+      const uint32_t row = udiv_magic(e, t.mC, t.sC);
+      const uint32_t col = e - row * uint32_t(t.C);
+      const uint32_t m = udiv_magic(row, t.mR, t.sR);
+      gv[j] = TG::load(gp[e]);
+      rv[j] = rf[row];
+      cv[j] = cf[int64_t(m) * t.C + col];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = lane * 8 + j < cnt ? (rv[j] * cv[j]) * gv[j] : 0.0f;  // as norm_x_at
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int k = lane * 8 + j;
+      x[j] = k < cnt ? norm_x_at<TG>(t, f0 + 8 * int64_t(k) + c, hp) : 0.0f;
+    }
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) h[j] = x[j] * x[j];
