@@ -1437,10 +1437,14 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
 // ===========================================================================
 // 1-D tensors, pass A: sum of u^2 per tile, u = rsqrt(clamp(v)) * g
 // ===========================================================================
+// the new second moment of a 1-D element from its gradient and its old (dequantised) second moment
+__device__ __forceinline__ float vec_v_from(float gv, float vold, const Hp& hp) {
+  return clamp_min_tiny(fmaf(gv * gv + hp.eps0, hp.a2, vold * hp.b2));
+}
 template <typename TG>
 __device__ __forceinline__ float vec_v_new(const DevTensor& t, int64_t e, float gv, const Hp& hp) {
   const float vold = t.fp32st ? st_sq_row(t)[e] : deq_u8(t.rq[e], t.ra[blk_of(e, hp)]);
-  return clamp_min_tiny(fmaf(gv * gv + hp.eps0, hp.a2, vold * hp.b2));
+  return vec_v_from(gv, vold, hp);
 }
 
 template <typename TG>

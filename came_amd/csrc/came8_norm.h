@@ -373,17 +373,50 @@ __device__ __forceinline__ void norm_lane_sums(T (&v)[L], int lane) {
   norm_group_sums<kWave, NV>(v, lane);
 }
 
-// u at flat index e (u_at), with 32-bit index arithmetic where the flat indices fit.
+// u_at of the 8 elements e[v] (in bounds) of any tensor, every operand loaded before the first is
+// used: the tensor's kind is tested once for the 8, so that no branch between the elements makes the
+// wavefront wait out each element's loads in turn.
 template <typename TG>
-__device__ __forceinline__ float norm_x_at(const DevTensor& t, int64_t e, const Hp& hp) {
-  if (t.factored && t.idx32) {
-    const uint32_t row = udiv_magic(uint32_t(e), t.mC, t.sC);
-    const uint32_t j = uint32_t(e) - row * uint32_t(t.C);
-    const uint32_t m = udiv_magic(row, t.mR, t.sR);
-    const float gv = TG::load(gbl(static_cast<const typename TG::storage*>(t.g))[e]);
-    return (gbl(t.rfac)[row] * gbl(t.cfac)[int64_t(m) * t.C + j]) * gv;
+__device__ __forceinline__ void norm_x_any8(const DevTensor& t, const int64_t (&e)[8], const Hp& hp, float (&x)[8]) {
+  using GS = typename TG::storage;
+  const CAME8_GLOBAL GS* __restrict__ gp = gbl(static_cast<const GS*>(t.g));
+  float gv[8], a[8], b[8];
+#pragma unroll
+  for (int v = 0; v < 8; ++v) gv[v] = TG::load(gp[e[v]]);
+  if (t.factored) {
+    const CAME8_GLOBAL float* __restrict__ rf = gbl(t.rfac);
+    const CAME8_GLOBAL float* __restrict__ cf = gbl(t.cfac);
+    if (t.idx32) {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const uint32_t row = udiv_magic(uint32_t(e[v]), t.mC, t.sC);
+        const uint32_t j = uint32_t(e[v]) - row * uint32_t(t.C);
+        const uint32_t m = udiv_magic(row, t.mR, t.sR);
+        a[v] = rf[row];
+        b[v] = cf[int64_t(m) * t.C + j];
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const int64_t row = e[v] / t.C;
+        const int64_t j = e[v] - row * t.C;
+        a[v] = rf[row];
+        b[v] = cf[(row / t.R) * t.C + j];
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 8; ++v) x[v] = (a[v] * b[v]) * gv[v];
+  } else {
+    if (t.fp32st) {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) a[v] = gbl(st_sq_row(t))[e[v]];
+    } else {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) a[v] = deq_u8(gbl(t.rq)[e[v]], gbl(t.ra)[blk_of(e[v], hp)]);
+    }
+#pragma unroll
+    for (int v = 0; v < 8; ++v) x[v] = rsqrt_ref(vec_v_from(gv[v], a[v], hp)) * gv[v];
   }
-  return u_at<TG>(t, e, hp);
 }
 
 // The x = u of the 8 elements at flat index f (a multiple of 8) of a factored tensor whose rows hold
@@ -429,7 +462,7 @@ __device__ __forceinline__ void norm_chunk_rows(const DevTensor& t, uint32_t f, 
 
 // How a norm kernel loads the x of a tensor's 8-element chunks: kNormVec for factored tensors whose rows
 // hold whole chunks, kNormRows for other factored tensors of at least 8 columns (both: gradient 16-byte
-// aligned, N < 2^31; the host checks), kNormAny (u_at per element) for the rest.
+// aligned, N < 2^31; the host checks), kNormAny (u_at of each element) for the rest.
 constexpr int kNormAny = 0, kNormRows = 1, kNormVec = 2;
 
 // Per-lane, per-chain accumulators of one segment: the integer sums of the increments under the
@@ -514,9 +547,13 @@ __device__ __forceinline__ void norm_chunk_x(const DevTensor& t, int64_t f, int6
     norm_chunk_rows<TG>(t, uint32_t(in ? f : f1 - 8), x);
 #pragma unroll
     for (int v = 0; v < 8; ++v) x[v] = in ? x[v] : 0.0f;
-  } else {
+  } else {  // a chunk past f1 reads the last chunk before it (f1 >= 8)
+    int64_t e[8];
 #pragma unroll
-    for (int v = 0; v < 8; ++v) x[v] = in ? norm_x_at<TG>(t, f + v, hp) : 0.0f;
+    for (int v = 0; v < 8; ++v) e[v] = (in ? f : f1 - 8) + v;
+    norm_x_any8<TG>(t, e, hp, x);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) x[v] = in ? x[v] : 0.0f;
   }
 }
 
@@ -559,14 +596,15 @@ __device__ __forceinline__ void norm_seg_sums(const DevTensor& t, int64_t f0, in
         account(x);
       }
     }
-  } else {
-    for (int q = 0; q < kNormChunks; ++q) {
-      const int64_t f = f0 + q * 512 + lane * 8;
-      if (f >= f1) break;
-      float x[8];
+  } else {  // chunks past the segment's end count for nothing
+#pragma unroll 1
+    for (int h = 0; h < kNormChunks; h += kNormGroup) {
+      float x[kNormGroup][8];
 #pragma unroll
-      for (int v = 0; v < 8; ++v) x[v] = norm_x_at<TG>(t, f + v, hp);
-      account(x);
+      for (int q = 0; q < kNormGroup; ++q)
+        norm_chunk_x<TG, kNormAny>(t, f0 + (h + q) * 512 + lane * 8, FULL ? f0 + kNormSegElems : f1, hp, x[q]);
+#pragma unroll
+      for (int q = 0; q < kNormGroup; ++q) account(x[q]);
     }
   }
 }
@@ -1167,34 +1205,15 @@ __device__ float norm_replay(const DevTensor& t, int c, int64_t seg, float s, co
   const int64_t f0 = seg * kNormSegElems;
   const int cnt = int(min(int64_t(kNormChainSeg), (main - f0) / 8));  // at least 1
   float x[8], h[8];
-  if (t.factored && t.idx32) {  // uniform
-    // Every operand of the lane's 8 elements is loaded before the first is waited for (a per-element
-    // branch would wait out each element's loads in turn).  An element past the segment's end reads
-    // the segment's first element of the chain and counts for nothing.
-    using GS = typename TG::storage;
-    const CAME8_GLOBAL GS* __restrict__ gp = gbl(static_cast<const GS*>(t.g));
-    const CAME8_GLOBAL float* __restrict__ rf = gbl(t.rfac);
-    const CAME8_GLOBAL float* __restrict__ cf = gbl(t.cfac);
-    float gv[8], rv[8], cv[8];
+  {
+    // an element past the segment's end reads the segment's first element of the chain and counts
+    // for nothing
+    int64_t e[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int k = lane * 8 + j;
-      const uint32_t e = uint32_t(f0 + 8 * int64_t(k < cnt ? k : 0) + c);
-      const uint32_t row = udiv_magic(e, t.mC, t.sC);
-      const uint32_t col = e - row * uint32_t(t.C);
-      const uint32_t m = udiv_magic(row, t.mR, t.sR);
-      gv[j] = TG::load(gp[e]);
-      rv[j] = rf[row];
-      cv[j] = cf[int64_t(m) * t.C + col];
-    }
+    for (int j = 0; j < 8; ++j) e[j] = f0 + 8 * int64_t(lane * 8 + j < cnt ? lane * 8 + j : 0) + c;
+    norm_x_any8<TG>(t, e, hp, x);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = lane * 8 + j < cnt ? (rv[j] * cv[j]) * gv[j] : 0.0f;  // as norm_x_at
-  } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int k = lane * 8 + j;
-      x[j] = k < cnt ? norm_x_at<TG>(t, f0 + 8 * int64_t(k) + c, hp) : 0.0f;
-    }
+    for (int j = 0; j < 8; ++j) x[j] = lane * 8 + j < cnt ? x[j] : 0.0f;
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) h[j] = x[j] * x[j];
