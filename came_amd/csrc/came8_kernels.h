@@ -1329,6 +1329,7 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
       // the 8bit2d momentum pass sums its residual row states per tile row
       const int64_t nsum = (RES && t.mode2d) ? int64_t(t.tr) : t.nbands;
       int64_t mb = i0 / t.R;  // matrix of the block's first row; blocks may span matrices
+      const float vfirst = i0 + tid < i1 ? Rsrc[i0 + tid] : 0.0f;  // loaded before the mean's sums
       float mean = matrix_row_mean(t, bsum, mb, nsum);
       for (int64_t i = i0 + tid; i < i1; i += kThreads) {
         const int64_t bi = i / t.R;
@@ -1336,7 +1337,7 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
           mb = bi;
           mean = matrix_row_mean(t, bsum, mb, nsum);
         }
-        const float v = Rsrc[i];
+        const float v = i == i0 + tid ? vfirst : Rsrc[i];
         fac[i] = rsqrt_ref(v / mean);
         vmax = nan_max(vmax, v);
         if (t.fp32st) (RES ? t.ra : st_sq_row(t))[i] = v;  // the fp32 row state itself
@@ -1371,13 +1372,14 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
           Cv = (Cold * beta) + (alpha_f * (s2 / fR));
         } else {
           const float* __restrict__ pp = part + (b * t.nbands) * t.C + j;
+          // the old state's loads go out before the partial sums' (their latencies overlap)
+          Cold = t.fp32st ? cst[i] : deq_u8(t.cq[off + i], t.ca[aoff + cblk(t, i, hp)]);
           double sw[2] = {0.0, 0.0};  // column sums of the partials, and for !RES of the clip weights
           // (in the default clip mode the band passes wrote no partW: the clip partial is not used)
           if (RES || hp.noW) band_column_sums<1>(pp, nullptr, t.nbands, t.C, sw);
           else band_column_sums<2>(pp, t.partW + (b * t.nbands) * t.C + j, t.nbands, t.C, sw);
           const double s = sw[0];
           W = sw[1];
-          Cold = t.fp32st ? cst[i] : deq_u8(t.cq[off + i], t.ca[aoff + cblk(t, i, hp)]);
           Cv = clamp_min_tiny(fmaf(float(s) / fR, alpha, Cold * beta));
         }
         const float c = rsqrt_ref(Cv);
@@ -1385,7 +1387,7 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
         fac[i] = c;
         if (t.fp32st) cst[i] = Cv;
         vmax = nan_max(vmax, Cv);
-        if (!RES) {
+        if (!RES && (t.mode2d || !hp.noW)) {  // the clip partial (k_clip: exact mode, and 8bit2d tensors always)
           if (b != cmb) {
             cmb = b;
             crm = matrix_row_mean(t, t.rsum, b, t.nbands);
