@@ -1255,15 +1255,18 @@ __device__ __forceinline__ float ordered_sum_f32(const float* __restrict__ p, in
   return acc;
 }
 
+// A matrix's mean row state from the sum of its row states.
+__device__ __forceinline__ float row_mean_of_sum(const DevTensor& t, double s) {
+  const float m = float(s) / float(t.R);
+  if (t.mode2d) return m > 0.0f ? m : 1.0f;  // 8bit2d: a mean that is not positive counts as 1
+  return clamp_min_tiny(m);
+}
 // Mean row state of matrix b, max(mean, 1e-30): the per-band sums the band pass wrote (each an fp64
 // sum rounded once), added in band order in fp64 (the reference: R.mean(dim=-1,
 // keepdim=True).clamp_min(1e-30), CAME8bitFull.py:1021,1044).
 __device__ __forceinline__ float matrix_row_mean(const DevTensor& t, const float* __restrict__ bandsum, int64_t b,
                                                  int64_t nb) {
-  const double s = ordered_sum_f64(bandsum + b * nb, nb, 1);
-  const float m = float(s) / float(t.R);
-  if (t.mode2d) return m > 0.0f ? m : 1.0f;  // 8bit2d: a mean that is not positive counts as 1
-  return clamp_min_tiny(m);
+  return row_mean_of_sum(t, ordered_sum_f64(bandsum + b * nb, nb, 1));
 }
 
 // Sums over the nbands band partials of one column (stride C) of one or two partial arrays: four
@@ -1296,7 +1299,7 @@ template <bool RES>
 __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                             const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   __shared__ float smax[4];
-  __shared__ double ssum[4];
+  __shared__ double ssum[4], msum[4];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
@@ -1330,7 +1333,20 @@ __global__ __launch_bounds__(kThreads) void k_factor_blocks(const DevTensor* __r
       const int64_t nsum = (RES && t.mode2d) ? int64_t(t.tr) : t.nbands;
       int64_t mb = i0 / t.R;  // matrix of the block's first row; blocks may span matrices
       const float vfirst = i0 + tid < i1 ? Rsrc[i0 + tid] : 0.0f;  // loaded before the mean's sums
-      float mean = matrix_row_mean(t, bsum, mb, nsum);
+      float mean;
+      if ((i1 - 1) / t.R == mb) {
+        // the block's rows are one matrix's (uniform): the workgroup sums the matrix's band sums together,
+        // thread k over sums k, k + 256, ..., then in a fixed order (one round of loads instead of one
+        // thread's chain over all of them)
+        double ms = 0.0;
+        for (int64_t k = tid; k < nsum; k += kThreads) ms += double(bsum[mb * nsum + k]);
+        ms = wave_sum(ms);
+        if (lane == 0) msum[wid] = ms;
+        __syncthreads();  // (msum is written again only after the block maximum's barrier below)
+        mean = row_mean_of_sum(t, ((msum[0] + msum[1]) + msum[2]) + msum[3]);
+      } else {
+        mean = matrix_row_mean(t, bsum, mb, nsum);
+      }
       for (int64_t i = i0 + tid; i < i1; i += kThreads) {
         const int64_t bi = i / t.R;
         if (bi != mb) {
