@@ -63,8 +63,6 @@ int64_t band_rows(int64_t R, int64_t C, int shrink = 0) {
 }
 
 
-int elem_size(int dt) { return dt == CAME8_F32 ? 4 : 2; }
-
 float round_to_bf16(float f) {
   uint32_t u;
   std::memcpy(&u, &f, 4);

@@ -1464,11 +1464,31 @@ __device__ __forceinline__ float vec_v_new(const DevTensor& t, int64_t e, float 
   const float vold = t.fp32st ? st_sq_row(t)[e] : deq_u8(t.rq[e], t.ra[blk_of(e, hp)]);
   return vec_v_from(gv, vold, hp);
 }
+// The clamped indices of a thread's 8 elements e0 .. e0 + 7 of a 1-D tensor (an element at or past N
+// reads element N - 1 and counts for nothing), and their gradients and old second moments, every
+// load issued before the first is used: a branch per element would wait out each element's loads in
+// turn.
+template <typename TG>
+__device__ __forceinline__ void vec_load8(const DevTensor& t, int64_t e0, const Hp& hp, int64_t (&ec)[8],
+                                          float (&gv)[8], float (&vo)[8]) {
+  using GS = typename TG::storage;
+  const GS* __restrict__ g = static_cast<const GS*>(t.g);
+#pragma unroll
+  for (int v = 0; v < 8; ++v) ec[v] = min(e0 + v, t.N - 1);
+#pragma unroll
+  for (int v = 0; v < 8; ++v) gv[v] = TG::load(g[ec[v]]);
+  if (t.fp32st) {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) vo[v] = st_sq_row(t)[ec[v]];
+  } else {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) vo[v] = deq_u8(t.rq[ec[v]], t.ra[blk_of(ec[v], hp)]);
+  }
+}
 
 template <typename TG>
 __global__ __launch_bounds__(kThreads) void k_vec_passA(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                         const int64_t* __restrict__ wstart, int ntens, Hp hp) {
-  using GS = typename TG::storage;
   __shared__ double ssum[4];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t total = wstart[ntens];
@@ -1477,14 +1497,14 @@ __global__ __launch_bounds__(kThreads) void k_vec_passA(const DevTensor* __restr
     const DevTensor& t = T[tids[slot]];
     const int64_t tile = w - wstart[slot];
     const int64_t e0 = tile * kTile + int64_t(tid) * 8;
-    const GS* __restrict__ g = static_cast<const GS*>(t.g);
+    int64_t ec[8];
+    float gv[8], vo[8];
+    vec_load8<TG>(t, e0, hp, ec, gv, vo);
     double s = 0.0;
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
-      const int64_t e = e0 + v;
-      if (e < t.N) {
-        const float gv = TG::load(g[e]);
-        const float u = rsqrt_ref(vec_v_new<TG>(t, e, gv, hp)) * gv;
+      if (e0 + v < t.N) {
+        const float u = rsqrt_ref(vec_v_from(gv[v], vo[v], hp)) * gv[v];
         s += double(u) * double(u);
       }
     }
@@ -1965,7 +1985,6 @@ template <typename TP, typename TG>
 __global__ __launch_bounds__(kThreads) void k_vec_passB(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                         const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   using PS = typename TP::storage;
-  using GS = typename TG::storage;
   __shared__ float wmax[2][2][4];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int L = hp.B >> 3;
@@ -1978,24 +1997,34 @@ __global__ __launch_bounds__(kThreads) void k_vec_passB(const DevTensor* __restr
     const int64_t e0 = tile * kTile + int64_t(tid) * 8;
     const int64_t N = t.N;
     PS* __restrict__ p = static_cast<PS*>(t.p);
-    const GS* __restrict__ g = static_cast<const GS*>(t.g);
     const float clip = t.clip[0];
     float m[8], vv[8], pv[8];
+    {
+      int64_t ec[8];
+      float gv[8], vo[8], mo[8], po[8];
+      vec_load8<TG>(t, e0, hp, ec, gv, vo);
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const int64_t e = e0 + v;
-      if (e < N) {
-        const float gv = TG::load(g[e]);
-        vv[v] = vec_v_new<TG>(t, e, gv, hp);
-        float uu = rsqrt_ref(vv[v]) * gv;
-        if ((hp.fp16u || t.fp16u) && !t.fp32st) uu = round_f16(uu);
-        const float u = uu / clip;
-        const float mold = t.fp32st ? st_m(t)[e] : deq_s8(t.mq[e], t.ma[blk_of(e, hp)]);
-        m[v] = fmaf(u, hp.a1, mold * hp.b1);
-        pv[v] = param_update<TP>(TP::load(p[e]), m[v], hp);
+      for (int v = 0; v < 8; ++v) po[v] = TP::load(p[ec[v]]);
+      if (t.fp32st) {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) mo[v] = st_m(t)[ec[v]];
       } else {
-        m[v] = 0.0f;
-        vv[v] = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) mo[v] = deq_s8(t.mq[ec[v]], t.ma[blk_of(ec[v], hp)]);
+      }
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        if (e0 + v < N) {
+          vv[v] = vec_v_from(gv[v], vo[v], hp);
+          float uu = rsqrt_ref(vv[v]) * gv[v];
+          if ((hp.fp16u || t.fp16u) && !t.fp32st) uu = round_f16(uu);
+          const float u = uu / clip;
+          m[v] = fmaf(u, hp.a1, mo[v] * hp.b1);
+          pv[v] = param_update<TP>(po[v], m[v], hp);
+        } else {
+          m[v] = 0.0f;
+          vv[v] = 0.0f;
+        }
       }
     }
     if (t.fp32st) {  // fp32 states: store the values (uniform per work item)
