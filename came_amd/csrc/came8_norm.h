@@ -156,6 +156,7 @@ template <bool WIDE>
 __global__ __launch_bounds__(kThreads) void k_norm_est(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                        const int64_t* __restrict__ wstart, int ntens, Hp hp) {
   __shared__ float ssum[4], usum[4];
+  __shared__ double rsm[4];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
@@ -187,6 +188,10 @@ __global__ __launch_bounds__(kThreads) void k_norm_est(const DevTensor* __restri
         acc[0] = fmaf(cf[j] * cf[j], Up[j], acc[0]);
         accu[0] += Up[j];
       }
+      // the matrix's mean row state (norm_unit_rm's): the workgroup sums the band sums, thread k over
+      // sums k, k + 256, ... (one round of loads, not one thread's chain after the reductions)
+      double rp = 0.0;
+      for (int64_t k = tid; k < t.nbands; k += kThreads) rp += double(t.rsum[m * t.nbands + k]);
       float s = 0.0f, su = 0.0f;
 #pragma unroll
       for (int q = 0; q < kEstBatch; ++q) {
@@ -195,15 +200,18 @@ __global__ __launch_bounds__(kThreads) void k_norm_est(const DevTensor* __restri
       }
       s = wave_sum(s);
       su = wave_sum(su);
+      rp = wave_sum(rp);
       if (lane == 0) {
         ssum[wid] = s;
         usum[wid] = su;
+        rsm[wid] = rp;
       }
       __syncthreads();
       if (tid == 0) {
         const float cs = ((ssum[0] + ssum[1]) + ssum[2]) + ssum[3];
         const float us = ((usum[0] + usum[1]) + usum[2]) + usum[3];
-        t.nest[u] = us > 0.0f ? norm_unit_rm(t, u) * t.esum[u] * (cs / us) : 0.0f;
+        const float rm = row_mean_of_sum(t, ((rsm[0] + rsm[1]) + rsm[2]) + rsm[3]);
+        t.nest[u] = us > 0.0f ? rm * t.esum[u] * (cs / us) : 0.0f;
       }
       __syncthreads();
     } else {
