@@ -1603,11 +1603,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
   // ---- P2, residual factors ----
   if (any_fact) {
     const bool withL = !split;  // else the long-chain group's pass 2 is queued on the side stream already
-    // With the long-chain group on the side stream the join after this pass is needed anyway, so two
-    // launches already share the streams: C4's 11008-wide pass 2 (occupancy-bound at 4.3 TB/s alone)
-    // then runs beside the 4096-wide one instead of after it.
-    pq.begin(plan.band2.size() + plan.tiny2.size() + (withL ? plan.band2L.size() + plan.tiny2L.size() : 0),
-             split ? 2 : kSideMinLaunches);
+    pq.begin(plan.band2.size() + plan.tiny2.size() + (withL ? plan.band2L.size() + plan.tiny2L.size() : 0));
     if (split)
       for (auto& kv : plan.band2L) pq.load[1] += alg_bytes(plan, kv.second, tensors, PH_PASS2);
     if ((rc = launch_pass2(plan.band2, plan.tiny2, true, stream)) != CAME8_OK) return rc;
