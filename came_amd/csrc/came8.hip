@@ -189,17 +189,19 @@ BandShapeSel band_variant(const came8_tensor& t, int64_t C, int32_t B, int pass,
     sel.ua = true;
   }
   const int64_t chunks = ceil_div(C, sel.V);
-  // 256-thread workgroups first: two of them per CU keep one's barriers off the other's loads.
-  // Pass 2 takes rows wider than one sweep in column segments (its MS variants, (3, 256) and, for
+  // Rows of at most 256 vector chunks take 128-thread workgroups, two chunks a thread: a thread's
+  // share of each row's sums then covers twice the elements, and a CU holds more workgroups (C2's
+  // 1024-wide fp32 rows: pass 2 0.45 -> 0.40 ms).  Wider rows take 256-thread workgroups first: two of
+  // them per CU keep one's barriers off the other's loads.  Pass 2 takes rows wider than one sweep in column segments (its MS variants, (3, 256) and, for
   // V = 1, (32, 256)), and for 16-bit gradients already rows wider than (3, 256) covers: it reads
   // each element once either way, and a 512-thread workgroup of its register use (~250) is alone
   // on its CU (C4's 11008-wide rows: 1.13 -> 1.03 ms).  Pass 1, whose column sums of g^2/R_i need
   // the whole row first, and the UA variants take the wider sweeps.
-  static const int vec_k[][2] = {{1, 256}, {2, 256}, {3, 256}, {2, 512}, {3, 512}, {4, 512}};
+  static const int vec_k[][2] = {{1, 128}, {2, 128}, {2, 256}, {3, 256}, {2, 512}, {3, 512}, {4, 512}};
   static const int one_k[][2] = {{1, 256}, {2, 256}, {4, 256}, {8, 256}, {16, 256}, {32, 256}};
   const int (*cand)[2] = sel.V > 1 ? vec_k : one_k;
   const bool p2seg = pass == 2 && !sel.ua;
-  const int nc = (p2seg && sel.V == 8) ? 3 : 6;
+  const int nc = sel.V > 1 ? ((p2seg && sel.V == 8) ? 4 : 7) : 6;
   for (int i = 0; i < nc; ++i) {
     if (int64_t(cand[i][0]) * cand[i][1] >= chunks) {
       sel.K = cand[i][0];

@@ -51,6 +51,8 @@ BandFn CAME8_BAND_SELECTOR(CAME8_BAND_TYPE, CAME8_BAND_PASS)(int V, int K, int T
     }
   }
   if (V == kVW) {
+    if (TPB == 128 && K == 1) return pick_ua<kVW, 1, 128>(st, ua);
+    if (TPB == 128 && K == 2) return pick_ua<kVW, 2, 128>(st, ua);
     if (TPB == 256 && K == 1) return pick_ua<kVW, 1, 256>(st, ua);
     if (TPB == 256 && K == 2) return pick_ua<kVW, 2, 256>(st, ua);
     if (TPB == 256 && K == 3) return pick_ua<kVW, 3, 256>(st, ua);
