@@ -570,14 +570,14 @@ __device__ __forceinline__ void norm_chunk_x(const DevTensor& t, int64_t f, int6
 // FULL: the segment holds all kNormSegElems elements.
 template <typename TG, int FORM, bool TWO, bool TINY, bool FULL>
 __device__ __forceinline__ void norm_seg_sums(const DevTensor& t, int64_t f0, int64_t f1, int ka, int lane,
-                                              const Hp& hp, NormAcc& a) {
+                                              const Hp& hp, NormAcc& a, int h0 = 0, int h1 = kNormChunks) {
   auto account = [&](const float (&x)[8]) {
 #pragma unroll
     for (int v = 0; v < 8; ++v) a.add<TWO, TINY>(v, x[v], ka);
   };
   if constexpr (FORM == kNormRows) {
 #pragma unroll 1
-    for (int h = 0; h < kNormChunks; h += kNormGroup) {
+    for (int h = h0; h < h1; h += kNormGroup) {
       float x[kNormGroup][8];
 #pragma unroll
       for (int q = 0; q < kNormGroup; ++q)
@@ -588,7 +588,7 @@ __device__ __forceinline__ void norm_seg_sums(const DevTensor& t, int64_t f0, in
   } else if constexpr (FORM == kNormVec) {
     // in a partial segment, chunks past its end load its last chunk and count for nothing
 #pragma unroll 1
-    for (int h = 0; h < kNormChunks; h += kNormGroup) {
+    for (int h = h0; h < h1; h += kNormGroup) {
       NormChunk<TG> ch[kNormGroup];
 #pragma unroll
       for (int q = 0; q < kNormGroup; ++q) {
@@ -606,7 +606,7 @@ __device__ __forceinline__ void norm_seg_sums(const DevTensor& t, int64_t f0, in
     }
   } else {  // chunks past the segment's end count for nothing
 #pragma unroll 1
-    for (int h = 0; h < kNormChunks; h += kNormGroup) {
+    for (int h = h0; h < h1; h += kNormGroup) {
       float x[kNormGroup][8];
 #pragma unroll
       for (int q = 0; q < kNormGroup; ++q)
@@ -617,9 +617,13 @@ __device__ __forceinline__ void norm_seg_sums(const DevTensor& t, int64_t f0, in
   }
 }
 
-// Writes the records of one segment from the lanes' per-chain sums, and the chains' sums of squares.
+// Writes the records of one segment from the per-lane, per-chain sums of the workgroup's wavefronts
+// (each took a part of the segment's chunks), and the chains' sums of squares.  Each wavefront sums its
+// lanes' integer records (a lane's sum is an exact integer below 2^24, or 2^24 when it holds a tie or
+// leaves the binade) and caps the total at 2^24; wavefront 0 adds the four totals in order, caps again
+// and writes the records.  xacc and xhs are LDS of the workgroup; every thread of it calls this.
 __device__ __forceinline__ void norm_write_records(const DevTensor& t, int64_t seg, int Ea, bool two, int lane,
-                                                   const NormAcc& a) {
+                                                   int wid, const NormAcc& a, uint32_t (*xacc)[16], float (*xhs)[8]) {
   uint32_t acc[16];
   float hs[8];
 #pragma unroll
@@ -628,33 +632,34 @@ __device__ __forceinline__ void norm_write_records(const DevTensor& t, int64_t s
     acc[8 + v] = two ? norm_lane_value(a.sb[v], a.tie_b(v, lane), Ea + 1) : 0u;
     hs[v] = a.hs[v];
   }
-  const int64_t nseg = t.nseg;
-  uint32_t* __restrict__ W0 = t.nrec;
-  uint32_t* __restrict__ WA = t.nrec + 8 * nseg;
-  uint32_t* __restrict__ WB = t.nrec + 16 * nseg;
-  norm_lane_sums<8>(hs, lane);  // lane 8c: chain c
-  if ((lane & 7) == 0) t.nsum[(lane >> 3) * nseg + seg] = hs[0];
-  if (two) {
-    norm_lane_sums<16>(acc, lane);  // lane 4c: chain c under Ea; lane 32 + 4c: under Ea + 1
-    const int c = (lane >> 2) & 7;
-    if ((lane & 3) == 0) {
-      const uint32_t sum = min(acc[0], kNormFull);
-      if (lane < 32) {
-        W0[c * nseg + seg] = uint32_t(Ea + 256) | kRecTwo;
-        WA[c * nseg + seg] = sum;
+  norm_lane_sums<8>(hs, lane);    // lane 8c: chain c
+  norm_lane_sums<16>(acc, lane);  // lane 4c: chain c under Ea; lane 32 + 4c: under Ea + 1
+  if ((lane & 7) == 0) xhs[wid][lane >> 3] = hs[0];
+  if ((lane & 3) == 0) xacc[wid][lane >> 2] = min(acc[0], kNormFull);
+  __syncthreads();
+  if (wid == 0) {
+    const int64_t nseg = t.nseg;
+    const int c = lane & 7;
+    if (lane < 16) {
+      uint32_t sum = 0;
+#pragma unroll
+      for (int k = 0; k < kThreads / kWave; ++k) sum += xacc[k][lane];
+      sum = min(sum, kNormFull);
+      if (lane < 8) {
+        t.nrec[c * nseg + seg] = uint32_t(Ea + 256) | (two ? kRecTwo : 0u);
+        t.nrec[(8 + c) * nseg + seg] = sum;
       } else {
-        WB[c * nseg + seg] = sum;
+        t.nrec[(16 + c) * nseg + seg] = two ? sum : kNormFull;
       }
     }
-  } else {
-    norm_lane_sums<8>(acc, lane);  // lane 8c: chain c under Ea
-    const int c = lane >> 3;
-    if ((lane & 7) == 0) {
-      W0[c * nseg + seg] = uint32_t(Ea + 256);
-      WA[c * nseg + seg] = min(acc[0], kNormFull);
-      WB[c * nseg + seg] = kNormFull;
+    if (lane < 8) {
+      float h = xhs[0][lane];
+#pragma unroll
+      for (int k = 1; k < kThreads / kWave; ++k) h += xhs[k][lane];
+      t.nsum[lane * nseg + seg] = h;
     }
   }
+  __syncthreads();  // xacc and xhs are written again by the next segment
 }
 
 // Candidate binades of a chain whose estimated value is est: Ea, and whether Ea + 1 is one too.
@@ -898,13 +903,17 @@ __global__ __launch_bounds__(kThreads) void k_norm_seg2d(const DevTensor* __rest
 template <typename TG, int FORM>
 __global__ __launch_bounds__(kThreads, 4) void k_norm_seg(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                           const int64_t* __restrict__ wstart, int ntens, Hp hp) {
+  static_assert(kNormChunks == (kThreads / kWave) * kNormGroup, "a wavefront per kNormGroup chunk steps");
+  __shared__ uint32_t xacc[kThreads / kWave][16];
+  __shared__ float xhs[kThreads / kWave][8];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t total = wstart[ntens];
   for (int64_t w = blockIdx.x; w < total; w += gridDim.x) {
     const int slot = find_slot(wstart, ntens, w);
     const DevTensor& t = T[tids[slot]];
-    const int64_t seg = t.nseg0 + (w - wstart[slot]) * 4 + wid;
-    if (seg >= t.nseg) continue;  // uniform over the wavefront
+    // one segment per work item; wavefront wid takes its chunk steps [wid, wid + 1) * kNormGroup
+    const int64_t seg = t.nseg0 + (w - wstart[slot]);
+    const int h0 = wid * kNormGroup, h1 = h0 + kNormGroup;
     const int64_t main = t.N - (t.N & 7);
     const int64_t f0 = seg * kNormSegElems;
     const int64_t f1 = min(f0 + kNormSegElems, main);
@@ -917,15 +926,15 @@ __global__ __launch_bounds__(kThreads, 4) void k_norm_seg(const DevTensor* __res
     a.clear();
     const bool full = f1 - f0 == kNormSegElems;
     if (Ea == -126) {
-      norm_seg_sums<TG, FORM, true, true, false>(t, f0, f1, ka, lane, hp, a);
+      norm_seg_sums<TG, FORM, true, true, false>(t, f0, f1, ka, lane, hp, a, h0, h1);
     } else if (two) {
-      if (full) norm_seg_sums<TG, FORM, true, false, true>(t, f0, f1, ka, lane, hp, a);
-      else norm_seg_sums<TG, FORM, true, false, false>(t, f0, f1, ka, lane, hp, a);
+      if (full) norm_seg_sums<TG, FORM, true, false, true>(t, f0, f1, ka, lane, hp, a, h0, h1);
+      else norm_seg_sums<TG, FORM, true, false, false>(t, f0, f1, ka, lane, hp, a, h0, h1);
     } else {
-      if (full) norm_seg_sums<TG, FORM, false, false, true>(t, f0, f1, ka, lane, hp, a);
-      else norm_seg_sums<TG, FORM, false, false, false>(t, f0, f1, ka, lane, hp, a);
+      if (full) norm_seg_sums<TG, FORM, false, false, true>(t, f0, f1, ka, lane, hp, a, h0, h1);
+      else norm_seg_sums<TG, FORM, false, false, false>(t, f0, f1, ka, lane, hp, a, h0, h1);
     }
-    norm_write_records(t, seg, Ea, two, lane, a);
+    norm_write_records(t, seg, Ea, two, lane, wid, a, xacc, xhs);
   }
 }
 
