@@ -25,7 +25,7 @@
 //   k_norm_est, k_norm_scan  an estimate of each chain's value along the tensor, from sums the step
 //                            has already formed (per row band: rm * sum_j c_j^2 * sum_i g_ij^2 / R_i;
 //                            per 1-D tile: the tile's sum of u^2), as an exclusive prefix per tensor.
-//   k_norm_seg               one wavefront per segment of kNormSegElems elements (512 per chain):
+//   k_norm_seg               one workgroup per segment of kNormSegElems elements (512 per chain):
 //                            per chain, the candidate binade Ea of the estimate (and Ea + 1 near a
 //                            binade edge), the integer sums of the increments under each, whether
 //                            the segment holds special elements, and whether it holds a NaN; and
@@ -897,9 +897,10 @@ __global__ __launch_bounds__(kThreads) void k_norm_seg2d(const DevTensor* __rest
   }
 }
 
-// Records of the segments [nseg0, nseg).  One wavefront per segment (four per workgroup).  Lane l
-// takes the 8-element chunks at 512q + 8l (q < kNormChunks) of the segment: element v of a chunk
-// belongs to chain v.  FORM: how the chunks are loaded (norm_chunk_x).
+// Records of the segments [nseg0, nseg).  One workgroup per segment: lane l of wavefront w takes the
+// 8-element chunks at 512q + 8l of the segment for q in [w, w + 1) * kNormGroup (element v of a chunk
+// belongs to chain v), and norm_write_records adds the wavefronts' sums.  FORM: how the chunks are
+// loaded (norm_chunk_x).
 template <typename TG, int FORM>
 __global__ __launch_bounds__(kThreads, 4) void k_norm_seg(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
                                                           const int64_t* __restrict__ wstart, int ntens, Hp hp) {
