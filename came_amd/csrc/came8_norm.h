@@ -1010,15 +1010,26 @@ __global__ __launch_bounds__(kThreads) void k_norm_bsum(const DevTensor* __restr
 
 // The chains' estimates at the segments of one work item of k_norm_fix, into est[c][thread]: the sums of
 // the blocks before it (k_norm_bsum) plus an exclusive scan of the item's own segment sums.
-__device__ __forceinline__ void norm_item_estimates(const DevTensor& t, int64_t blk, float (&est)[8][kNormFixSegs],
-                                                    float (&part)[kThreads / kWave][8], float (&base)[8]) {
+__device__ __forceinline__ void norm_item_estimates(const DevTensor& t, int64_t blk, const float (&v)[8],
+                                                    float (&est)[8][kNormFixSegs], float (&part)[kThreads / kWave][8],
+                                                    float (&base)[8]) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int64_t nseg = t.nseg;
-  // the blocks before this one: thread i adds chain i % 8's blocks i / 8, i / 8 + 32, ...
+  // the blocks before this one: thread i adds chain i % 8's blocks i / 8, i / 8 + 32, ... in that order,
+  // four loads in flight at a time
   {
     float acc = 0.0f;
     const int c = tid & 7;
-    for (int64_t b = tid >> 3; b < blk; b += kThreads / 8) acc += t.nbsum[c * t.nblk + b];
+    constexpr int kStep = kThreads / 8;
+    const float* __restrict__ nb = t.nbsum + c * t.nblk;
+    int64_t b = tid >> 3;
+    for (; b + 3 * kStep < blk; b += 4 * kStep) {
+      float y[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) y[u] = nb[b + u * kStep];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc += y[u];
+    }
+    for (; b < blk; b += kStep) acc += nb[b];
     est[c][tid >> 3] = acc;  // scratch: 32 partials per chain
   }
   __syncthreads();
@@ -1028,14 +1039,11 @@ __device__ __forceinline__ void norm_item_estimates(const DevTensor& t, int64_t 
     base[tid] = acc;
   }
   __syncthreads();
-  // this item's segments: an exclusive scan over the threads, per chain
-  const int64_t seg = blk * kNormFixSegs + tid;
-  float v[8], incl[8];
+  // this item's segments (v: this thread's segment's sums of squares, 0 past the tensor's segments):
+  // an exclusive scan over the threads, per chain
+  float incl[8];
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    v[c] = seg < nseg ? t.nsum[c * nseg + seg] : 0.0f;
-    incl[c] = v[c];
-  }
+  for (int c = 0; c < 8; ++c) incl[c] = v[c];
 #pragma unroll
   for (int o = 1; o < kWave; o <<= 1) {
 #pragma unroll
@@ -1113,13 +1121,26 @@ __global__ __launch_bounds__(kThreads) void k_norm_fix(const DevTensor* __restri
     const int64_t base = blk * kNormFixSegs;
     const int64_t seg = base + tid;
     if (tid == 0) nlist = 0;
-    norm_item_estimates(t, blk, est_l, part, base_l);  // synchronises the workgroup
+    // this thread's segment's sums of squares and record words, loaded before the estimates' sums
+    float v[8];
+    uint32_t w0s[8];
+    {
+      const int64_t sc = seg < nseg ? seg : nseg - 1;  // nseg >= 1 for a tensor in the list
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        v[c] = t.nsum[c * nseg + sc];
+        w0s[c] = t.nrec[c * nseg + sc];
+      }
+#pragma unroll
+      for (int c = 0; c < 8; ++c) v[c] = seg < nseg ? v[c] : 0.0f;
+    }
+    norm_item_estimates(t, blk, v, est_l, part, base_l);  // synchronises the workgroup
     uint32_t need = 0;
     if (seg < nseg) {
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
         const float est = est_l[c][tid];
-        const uint32_t w0 = t.nrec[c * nseg + seg];
+        const uint32_t w0 = w0s[c];
         const int Ea = int(w0 & 511u) - 256;
         const bool two = (w0 & kRecTwo) != 0;
         const int lo = norm_est_binade(est * 0.98f), hi = norm_est_binade(est * 1.005f);
