@@ -66,9 +66,10 @@ constexpr int kNormSegElems = 4096;                    // flat elements per segm
 constexpr int kNormChainSeg = kNormSegElems / 8;       // elements per chain per segment
 constexpr int kNormChunks = kNormSegElems / (8 * 64);  // 8-element chunks per lane of a segment's wavefront
 // segments per thread per batch of the walk: after each replay the walk scans its lanes' records again,
-// so a batch of fewer records per lane makes each scan shorter, at one batch load more per 512 segments
-// (C1 0.264 / 0.247 / 0.243 ms with 16 / 8 / 4; C4 the same within 0.03 ms; 32 slower everywhere)
-constexpr int kNormWalkSegs = 8;
+// so a batch of fewer records per lane makes each scan shorter, at one batch load more per 64 * this
+// many segments (with the replays' loads issued together: C1 0.2058 / 0.1997 ms and C2 2.131 / 2.115
+// ms with 8 / 4, C4 the same; 16 and 32 slower)
+constexpr int kNormWalkSegs = 4;
 constexpr int kNormPrologue = 64;                      // elements a replay from zero applies one by one
 constexpr int kNormGroup = 2;                          // chunks per lane loaded together
 constexpr int64_t kNormMaxUnits = 4096;                // estimate units per tensor of single-band matrices
