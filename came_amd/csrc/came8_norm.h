@@ -70,6 +70,7 @@ constexpr int kNormChunks = kNormSegElems / (8 * 64);  // 8-element chunks per l
 // many segments (with the replays' loads issued together: C1 0.2058 / 0.1997 ms and C2 2.131 / 2.115
 // ms with 8 / 4, C4 the same; 16 and 32 slower)
 constexpr int kNormWalkSegs = 4;
+static_assert(kNormWalkSegs % 4 == 0, "the walk loads each lane's records four at a time");
 constexpr int kNormPrologue = 64;                      // elements a replay from zero applies one by one
 constexpr int kNormGroup = 2;                          // chunks per lane loaded together
 constexpr int64_t kNormMaxUnits = 4096;                // estimate units per tensor of single-band matrices
