@@ -662,7 +662,9 @@ __global__ __launch_bounds__(TPB) void k_fact_pass1n(const DevTensor* __restrict
   using Acc = ColAcc<V, K>;
   using CK = Chunk<TG, V, UA>;
   constexpr int NW = TPB / kWave;
-  constexpr int S = (V > 1 && K == 1) ? 2 : Stage<TG, V, K>::S;
+  // aligned 128-thread workgroups of fp32 gradients (narrow rows) take twice the rows per stage: more
+  // bytes in flight per wave (as pass 2's)
+  constexpr int S = ((V > 1 && K == 1) ? 2 : Stage<TG, V, K>::S) * ((TPB == 128 && sizeof(GS) == 4 && !UA) ? 2 : 1);
   constexpr int64_t segw = int64_t(TPB) * V * K;
   __shared__ double rowpart[2][kMaxBandRows + 1][NW];  // per-wave row sums of a band (+1: a dummy row)
   __shared__ float rowval[kMaxBandRows];  // the band's new row states
@@ -951,7 +953,11 @@ __global__ __launch_bounds__(TPB, (UA && sizeof(typename TG::storage) == 2 && TP
   constexpr int NW = TPB / kWave;
   // one-chunk vector rows take two-row stages instead of four: 157 VGPRs instead of 227 (three
   // workgroups per CU instead of two); the stage loop has no barrier (C3 pass 2: 1.00 -> 0.89 ms)
-  constexpr int S = (V > 1 && K == 1) ? 2 : Stage<TG, V, K>::S;
+  // Aligned 128-thread workgroups of fp32 gradients take twice the rows per stage, as pass 1's do (C2's
+  // 1024-wide rows: the step 2.053 -> 2.029 ms).  Not the others: for 16-bit gradients it took C3's
+  // 2048-wide rows from 4.35 to 4.66 ms, and C5's unaligned fp32 rows slowed down too (their registers
+  // then leave fewer waves per SIMD).
+  constexpr int S = ((V > 1 && K == 1) ? 2 : Stage<TG, V, K>::S) * ((TPB == 128 && sizeof(GS) == 4 && !UA) ? 2 : 1);
   constexpr int64_t segw = int64_t(TPB) * V * K;
   __shared__ double rowpart[2][kMaxBandRows + 1][NW];  // per-wave row sums of a band (+1: a dummy row)
   __shared__ float rowval[kMaxBandRows];           // the band's new residual row states
