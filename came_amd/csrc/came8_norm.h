@@ -71,7 +71,6 @@ constexpr int kNormChunks = kNormSegElems / (8 * 64);  // 8-element chunks per l
 // ms with 8 / 4, C4 the same; 16 and 32 slower)
 constexpr int kNormWalkSegs = 4;
 static_assert(kNormWalkSegs % 4 == 0, "the walk loads each lane's records four at a time");
-constexpr int kNormPrologue = 64;                      // elements a replay from zero applies one by one
 constexpr int kNormGroup = 2;                          // chunks per lane loaded together
 constexpr int64_t kNormMaxUnits = 4096;                // estimate units per tensor of single-band matrices
                                                        // or tiles (more are grouped)
@@ -1258,17 +1257,19 @@ __device__ float norm_replay(const DevTensor& t, int c, int64_t seg, float s, co
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) h[j] = x[j] * x[j];
-  int pos = 0;  // the elements before pos are applied
-  if (s == 0.0f) {  // a chain's start crosses a binade every few elements: the first ones one by one
+  if (s == 0.0f) {
+    // A chain's first segment crosses a binade every few elements, and its early increments keep many
+    // fractional bits, so ties are common too: instead of a round per crossing or tie, its elements are
+    // applied one by one (the reference's own loop), each broadcast from its lane.  Elements past the
+    // segment's end are 0, and fmaf(0, 0, s) is s, so the loop needs no branch.
 #pragma unroll
-    for (int k = 0; k < kNormPrologue; ++k) {
-      if (k < cnt) {  // uniform
-        const float xk = norm_lane(x[k & 7], k >> 3);
-        s = fmaf(xk, xk, s);
-      }
+    for (int k = 0; k < kNormChainSeg; ++k) {
+      const float xk = norm_lane(x[k & 7], k >> 3);
+      s = fmaf(xk, xk, s);
     }
-    pos = min(cnt, kNormPrologue);
+    return s;
   }
+  int pos = 0;  // the elements before pos are applied
   while (pos < cnt) {  // uniform
     if (!(s <= 0x1.fffffep127f)) {
       if (s != s) break;
