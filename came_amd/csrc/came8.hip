@@ -109,6 +109,7 @@ struct Plan {
   std::map<TypeKey, WorkList> updb;      // P3, band form
   std::map<TypeKey, WorkList> vecB;      // 1-D pass B (fast block sizes)
   std::map<int, WorkList> vecA;          // 1-D pass A, by grad type
+  std::map<int, WorkList> vecAn;         // the same for the default clip mode: tensors of several segments
   std::map<TypeKey, WorkList> generic;   // P3 / B for other block sizes (per quantisation block)
   // the clip's norm in the reference's order (came8_norm.h)
   WorkList nest_w;                       // unit estimates, a workgroup per row band (matrices >= 256 wide)
@@ -655,13 +656,17 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       }
     } else {
       add_item(plan.vecA[t.grad_dtype], i, d.nclip);
+      // in the default clip mode pass A's tile sums only feed the norm's estimates
+      if (d.nseg > 1) add_item(plan.vecAn[t.grad_dtype], i, d.nclip);
       if (fastB) add_item(plan.vecB[tk], i, ceil_div(d.N, kTile));
     }
     if (!fastB) add_item(plan.generic[tk], i, d.nbm);
-    if (norm_est_wide(t, d)) add_item(plan.nest_w, i, d.nunit);
-    else add_item(plan.nest_n, i, ceil_div(d.nunit, int64_t(kThreads)));
-    add_item(plan.nscan, i, 1);
-    if (d.nseg > 0) {
+    // The walk replays every chain's first segment from zero without reading its record, so a tensor of
+    // one segment needs no estimates, records or rebuild.
+    if (d.nseg > 1) {
+      if (norm_est_wide(t, d)) add_item(plan.nest_w, i, d.nunit);
+      else add_item(plan.nest_n, i, ceil_div(d.nunit, int64_t(kThreads)));
+      add_item(plan.nscan, i, 1);
       // the vector forms need rows of whole aligned 8-element chunks and 32-bit flat indices; matrices
       // (prefix 1) up to kNormLdsCols wide take runs of segments with their column factors in LDS
       const bool vec = t.factored && d.idx32 && reinterpret_cast<uintptr_t>(t.grad) % 16 == 0;
@@ -700,6 +705,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
   for (auto& kv : plan.updb) place(kv.second);
   for (auto& kv : plan.vecB) place(kv.second);
   for (auto& kv : plan.vecA) place(kv.second);
+  for (auto& kv : plan.vecAn) place(kv.second);
   for (auto& kv : plan.generic) place(kv.second);
   place(plan.nest_w);
   place(plan.nest_n);
@@ -774,6 +780,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     for (auto& kv : plan.updb) put(kv.second);
     for (auto& kv : plan.vecB) put(kv.second);
     for (auto& kv : plan.vecA) put(kv.second);
+    for (auto& kv : plan.vecAn) put(kv.second);
     for (auto& kv : plan.generic) put(kv.second);
     put(plan.nest_w);
     put(plan.nest_n);
@@ -1467,7 +1474,8 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
   // the default clip mode's pass 1 keeps no column sums of g^2/R_i (k_fact_pass1n), except for the
   // 8bit2d tensors, whose clip is formed from them
   const std::map<BandKey, WorkList>& band1 = exact_norm ? plan.band : plan.bandN;
-  pq.begin(band1.size() + plan.band2dw.size() + plan.tiny1.size() + plan.vecA.size());
+  const std::map<int, WorkList>& vecA = exact_norm ? plan.vecA : plan.vecAn;
+  pq.begin(band1.size() + plan.band2dw.size() + plan.tiny1.size() + vecA.size());
   for (const auto* lists : {&band1, &plan.band2dw}) {
     for (auto& kv : *lists) {
       const BandKey& k = kv.first;
@@ -1492,7 +1500,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, ls, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
     if ((rc = check_launch("tiny_pass1")) != CAME8_OK) return rc; }
   }
-  for (auto& kv : plan.vecA) {
+  for (auto& kv : vecA) {
     const WorkList& wl = kv.second;
     GenFn fn;
     CAME8_TYPE_SWITCH1(k_vec_passA, kv.first, fn);

@@ -1377,8 +1377,10 @@ __global__ __launch_bounds__(kNormWalkThreads) void k_norm_walk(const DevTensor*
     const CAME8_GLOBAL uint32_t* __restrict__ W0 = gbl(t.nrec + c * nseg);
     const CAME8_GLOBAL uint32_t* __restrict__ WA = gbl(t.nrec + (8 + c) * nseg);
     const CAME8_GLOBAL uint32_t* __restrict__ WB = gbl(t.nrec + (16 + c) * nseg);
-    float s = 0.0f;
-    int64_t seg = 0;
+    // the first segment is replayed from zero without reading its record (a tensor of one segment forms
+    // none)
+    float s = nseg > 0 ? norm_replay<TG>(t, c, 0, 0.0f, hp) : 0.0f;
+    int64_t seg = 1;
     while (seg < nseg && s == s) {  // a NaN chain stays NaN
       // the batch starts at a multiple of kNormWalkSegs; its segments before seg count for nothing
       const int64_t bstart = seg & ~int64_t(kNormWalkSegs - 1);
