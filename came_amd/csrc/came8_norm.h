@@ -35,15 +35,16 @@
 //                            (an eighth of the prefix) named others.  The chains of heavy-tailed
 //                            updates drift far apart; without the rebuild most of their segments
 //                            would miss and be replayed.
-//   k_norm_walk              one wavefront per chain: from s = 0, skips every run of segments whose
-//                            record covers the chain's current binade without specials and without
-//                            leaving the binade (a wavefront scan of the integer sums), and replays
-//                            the segment where that fails: the chain's start, binade crossings,
-//                            specials, and estimates that missed.  A replay holds the segment's 512
-//                            elements in the wavefront and applies the increments of the chain's
-//                            binade with a saturating prefix sum up to the first element that leaves
-//                            the binade or is special, that element with fmaf, and so on: one round
-//                            per crossing or special element.
+//   k_norm_walk              one wavefront per chain: applies the first segment from s = 0 element by
+//                            element (no record of it is read: a tensor of one segment forms none),
+//                            then skips every run of segments whose record covers the chain's current
+//                            binade without specials and without leaving the binade (a wavefront scan
+//                            of the integer sums), and replays the segment where that fails: binade
+//                            crossings, specials, and estimates that missed.  A replay holds the
+//                            segment's 512 elements in the wavefront and applies the increments of the
+//                            chain's binade with a saturating prefix sum up to the first element that
+//                            leaves the binade or is special, that element with fmaf, and so on: one
+//                            round per crossing or special element.
 //   k_norm_final             the eight accumulators and the tail in the reference's order, sqrt,
 //                            and the clip divisor.
 //
