@@ -114,7 +114,6 @@ struct Plan {
   // the clip's norm in the reference's order (came8_norm.h)
   WorkList nest_w;                       // unit estimates, a workgroup per row band (matrices >= 256 wide)
   WorkList nest_n;                       // unit estimates, a thread per unit (per 256 units)
-  WorkList nscan;                        // prefix of the estimates (one item per tensor)
   std::map<int, WorkList> nseg2d;        // segment records of matrices, runs of nrun segments, by 3 * grad type + form
   std::map<int, WorkList> nseg;          // the other segments' records, by 3 * grad type + chunk form
   WorkList nbsum;                        // the chains' sums per block of segments (one item per block)
@@ -666,7 +665,6 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     if (d.nseg > 1) {
       if (norm_est_wide(t, d)) add_item(plan.nest_w, i, d.nunit);
       else add_item(plan.nest_n, i, ceil_div(d.nunit, int64_t(kThreads)));
-      add_item(plan.nscan, i, 1);
       // the vector forms need rows of whole aligned 8-element chunks and 32-bit flat indices; matrices
       // (prefix 1) up to kNormLdsCols wide take runs of segments with their column factors in LDS
       const bool vec = t.factored && d.idx32 && reinterpret_cast<uintptr_t>(t.grad) % 16 == 0;
@@ -709,7 +707,6 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
   for (auto& kv : plan.generic) place(kv.second);
   place(plan.nest_w);
   place(plan.nest_n);
-  place(plan.nscan);
   for (auto& kv : plan.nseg2d) place(kv.second);
   for (auto& kv : plan.nseg) place(kv.second);
   place(plan.nbsum);
@@ -784,7 +781,6 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
     for (auto& kv : plan.generic) put(kv.second);
     put(plan.nest_w);
     put(plan.nest_n);
-    put(plan.nscan);
     for (auto& kv : plan.nseg2d) put(kv.second);
     for (auto& kv : plan.nseg) put(kv.second);
     put(plan.nbsum);
@@ -1535,13 +1531,6 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
       EstFn fn = k_norm_est<false>;
       hipLaunchKernelGGL(fn, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl), int(wl.tids.size()), hp);
       if ((rc = check_launch("norm_est")) != CAME8_OK) return rc;
-    }
-    if (!plan.nscan.tids.empty()) {
-      const WorkList& wl = plan.nscan;
-      PhaseTimer pt(PH_NORM_SCAN, 0.0, stream);
-      hipLaunchKernelGGL(k_norm_scan<>, dim3(grid_for(int64_t(wl.tids.size()))), blk, 0, stream, dT, tids(wl),
-                         int(wl.tids.size()));
-      if ((rc = check_launch("norm_scan")) != CAME8_OK) return rc;
     }
     pq.begin(plan.nseg2d.size() + plan.nseg.size(), kSideMinNormLaunches);
     for (auto& kv : plan.nseg2d) {

@@ -22,9 +22,10 @@
 // half an ulp of hi, less than the distance from hi to any half-integer, for every binade above the
 // subnormal one, whose half-integers lie on hi's grid.)
 //
-//   k_norm_est, k_norm_scan  an estimate of each chain's value along the tensor, from sums the step
+//   k_norm_est               an estimate of each chain's value along the tensor, from sums the step
 //                            has already formed (per row band: rm * sum_j c_j^2 * sum_i g_ij^2 / R_i;
-//                            per 1-D tile: the tile's sum of u^2), as an exclusive prefix per tensor.
+//                            per 1-D tile: the tile's sum of u^2); the records kernels add the units
+//                            before a segment themselves (norm_unit_prefix).
 //   k_norm_seg               one workgroup per segment of kNormSegElems elements (512 per chain):
 //                            per chain, the candidate binade Ea of the estimate (and Ea + 1 near a
 //                            binade edge), the integer sums of the increments under each, whether
@@ -250,64 +251,24 @@ __global__ __launch_bounds__(kThreads) void k_norm_est(const DevTensor* __restri
   }
 }
 
-constexpr int kScanBatch = 16;  // loads per thread in flight in block_excl_scan
-
-// In-place exclusive prefix sum of a[0, n) by one workgroup of NT threads; returns the total to every
-// thread.  Thread i takes the i-th run of ceil(n / NT) consecutive values.  part: NT / kWave floats of
-// LDS.
-template <int NT>
-__device__ float block_excl_scan(float* a, int64_t n, float* part) {
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int64_t per = (n + NT - 1) / NT;
-  const int64_t u0 = min(n, int64_t(tid) * per), u1 = min(n, u0 + per);
+// The estimated sum of u^2 over the units before unit u (0 <= u <= nunit), from the units' own
+// estimates: the wavefront adds them, lane l over units l, l + 64, ..., eight loads in flight.  Every
+// lane of the wavefront calls it with the same u and gets the same value.  (The order of the sum is
+// free: an estimate decides only which segments are replayed, never the result.)
+__device__ __forceinline__ float norm_unit_prefix(const DevTensor& t, int64_t u) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const CAME8_GLOBAL float* __restrict__ e = gbl(t.nest);
   float s = 0.0f;
-  for (int64_t u = u0; u < u1; u += kScanBatch) {
-    float v[kScanBatch];
+  int64_t k = lane;
+  for (; k + 7 * kWave < u; k += 8 * kWave) {
+    float v[8];
 #pragma unroll
-    for (int q = 0; q < kScanBatch; ++q) v[q] = u + q < u1 ? a[u + q] : 0.0f;
+    for (int q = 0; q < 8; ++q) v[q] = e[k + q * kWave];
 #pragma unroll
-    for (int q = 0; q < kScanBatch; ++q) s += v[q];
+    for (int q = 0; q < 8; ++q) s += v[q];
   }
-  float incl = s;  // inclusive scan of the runs' sums over the wavefront, then over the wavefronts
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const float y = __shfl_up(incl, o, kWave);
-    if (lane >= o) incl += y;
-  }
-  if (lane == kWave - 1) part[wid] = incl;
-  __syncthreads();
-  float off = 0.0f, tot = 0.0f;
-#pragma unroll
-  for (int k = 0; k < NT / kWave; ++k) {
-    off += k < wid ? part[k] : 0.0f;
-    tot += part[k];
-  }
-  float run = off + (incl - s);
-  for (int64_t u = u0; u < u1; u += kScanBatch) {
-    float v[kScanBatch];
-#pragma unroll
-    for (int q = 0; q < kScanBatch; ++q) v[q] = u + q < u1 ? a[u + q] : 0.0f;
-#pragma unroll
-    for (int q = 0; q < kScanBatch; ++q) {
-      if (u + q < u1) a[u + q] = run;
-      run += v[q];
-    }
-  }
-  __syncthreads();  // part is reused by the next call
-  return tot;
-}
-
-// In place: the unit estimates of one tensor per work item become their exclusive prefix; nest[nunit]
-// = total (block_excl_scan).
-template <int = 0>
-__global__ __launch_bounds__(kThreads) void k_norm_scan(const DevTensor* __restrict__ T, const int32_t* __restrict__ tids,
-                                                        int ntens) {
-  __shared__ float part[kThreads / kWave];
-  for (int k = blockIdx.x; k < ntens; k += gridDim.x) {
-    const DevTensor& t = T[tids[k]];
-    const float tot = block_excl_scan<kThreads>(t.nest, t.nunit, part);
-    if (threadIdx.x == 0) t.nest[t.nunit] = tot;
-  }
+  for (; k < u; k += kWave) s += e[k];
+  return wave_sum(s);
 }
 
 // Estimated sum of u^2 over the flat elements before f (0 <= f <= N), linear inside a unit.
@@ -316,7 +277,7 @@ __device__ __forceinline__ float norm_est_at(const DevTensor& t, int64_t f) {
   if (t.factored) {
     const int64_t row = t.idx32 ? int64_t(udiv_magic(uint32_t(f), t.mC, t.sC)) : f / t.C;
     const int64_t m = t.idx32 ? int64_t(udiv_magic(uint32_t(row), t.mR, t.sR)) : row / t.R;
-    if (m >= t.P) return t.nest[t.nunit];
+    if (m >= t.P) return norm_unit_prefix(t, t.nunit);
     const int64_t i = row - m * t.R;
     if (t.ngrp > 1) {  // groups of ngrp single-band matrices
       u = m / t.ngrp;
@@ -330,12 +291,11 @@ __device__ __forceinline__ float norm_est_at(const DevTensor& t, int64_t f) {
     }
   } else {
     u = f / (kTile * t.ngrp);
-    if (u >= t.nunit) return t.nest[t.nunit];
+    if (u >= t.nunit) return norm_unit_prefix(t, t.nunit);
     us = u * kTile * t.ngrp;
     ue = min(us + kTile * t.ngrp, t.N);
   }
-  const float p0 = t.nest[u], p1 = t.nest[u + 1];
-  return p0 + (p1 - p0) * (float(f - us) / float(ue - us));
+  return norm_unit_prefix(t, u) + gbl(t.nest)[u] * (float(f - us) / float(ue - us));
 }
 
 // ---------------------------------------------------------------------------
