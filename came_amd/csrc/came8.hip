@@ -988,11 +988,11 @@ int check_launch(const char* what) {
 // ---------------------------------------------------------------------------
 const char* const kPhaseNames[] = {"pass1", "vec_passA", "row_mean", "factor_blocks", "clip", "norm_est",
                                    "pass2", "row_mean_res", "factor_blocks_res", "pass3", "vec_passB",
-                                   "generic_update", "tiles2d", "res_rows2d", "param2d", "norm_scan",
+                                   "generic_update", "tiles2d", "res_rows2d", "param2d", "norm_bsum",
                                    "norm_seg", "norm_walk", "norm_final", "norm_fix"};
 constexpr int kNumPhases = sizeof(kPhaseNames) / sizeof(kPhaseNames[0]);
 enum Phase { PH_PASS1, PH_VECA, PH_ROWMEAN, PH_FACTOR, PH_CLIP, PH_NORM_EST, PH_PASS2, PH_ROWMEAN_RES,
-             PH_FACTOR_RES, PH_PASS3, PH_VECB, PH_GENERIC, PH_TILES2D, PH_RES2D, PH_PARAM2D, PH_NORM_SCAN,
+             PH_FACTOR_RES, PH_PASS3, PH_VECB, PH_GENERIC, PH_TILES2D, PH_RES2D, PH_PARAM2D, PH_NORM_BSUM,
              PH_NORM_SEG, PH_NORM_WALK, PH_NORM_FINAL, PH_NORM_FIX };
 
 struct Pending {
@@ -1560,7 +1560,7 @@ int came8_step(const came8_tensor* tensors, int32_t n_tensors, const came8_hpara
     if ((rc = pq.finish()) != CAME8_OK) return rc;
     if (!plan.nbsum.tids.empty()) {
       const WorkList& wl = plan.nbsum;
-      PhaseTimer pt(PH_NORM_SCAN, 0.0, stream);
+      PhaseTimer pt(PH_NORM_BSUM, 0.0, stream);
       hipLaunchKernelGGL(k_norm_bsum<>, dim3(grid_for(wl.total())), blk, 0, stream, dT, tids(wl), wst(wl),
                          int(wl.tids.size()));
       if ((rc = check_launch("norm_bsum")) != CAME8_OK) return rc;
