@@ -672,7 +672,7 @@ int build_plan(const came8_tensor* ts, int32_t n, int32_t B, char* ws_base, Plan
       if (d.nseg0 > 0)
         add_item(plan.nseg2d[t.grad_dtype * 3 + (d.c8 ? kNormVec : kNormRows)], i, ceil_div(d.nseg0, d.nrun));
       if (d.nseg > d.nseg0) add_item(plan.nseg[t.grad_dtype * 3 + form], i, d.nseg - d.nseg0);
-      add_item(plan.nbsum, i, d.nblk);
+      if (d.nblk > kNormFixDirect) add_item(plan.nbsum, i, d.nblk);
       add_item(plan.nfix[t.grad_dtype * 3 + form], i, ceil_div(d.nseg, int64_t(kNormFixSegs)));
     }
     add_item((longc[i] ? plan.nwalkL : plan.nwalk)[t.grad_dtype], i, 8);

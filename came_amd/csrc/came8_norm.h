@@ -944,6 +944,7 @@ __device__ __forceinline__ void norm_stage_cols(const DevTensor& t, float* cl) {
 // each chain's own estimate, and records rebuilt under it
 // ---------------------------------------------------------------------------
 constexpr int kNormFixSegs = kThreads;  // segments per block of the chains' estimates and per work item of k_norm_fix
+constexpr int64_t kNormFixDirect = 4;   // tensors of at most this many blocks: k_norm_fix adds the segments' sums itself
 
 // Each chain's sum of squares over a block of kNormFixSegs segments (nbsum[c][block]), for the prefix
 // k_norm_fix forms.  One work item per block; thread i takes segment i of the block.
@@ -977,21 +978,24 @@ __device__ __forceinline__ void norm_item_estimates(const DevTensor& t, int64_t 
                                                     float (&base)[8]) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   // the blocks before this one: thread i adds chain i % 8's blocks i / 8, i / 8 + 32, ... in that order,
-  // four loads in flight at a time
+  // four loads in flight at a time.  A tensor of at most kNormFixDirect blocks has no block sums
+  // (k_norm_bsum skips it): its threads add the segments' sums themselves.
   {
     float acc = 0.0f;
     const int c = tid & 7;
     constexpr int kStep = kThreads / 8;
-    const float* __restrict__ nb = t.nbsum + c * t.nblk;
+    const bool direct = t.nblk <= kNormFixDirect;  // uniform
+    const float* __restrict__ nb = direct ? t.nsum + c * t.nseg : t.nbsum + c * t.nblk;
+    const int64_t nend = direct ? blk * kNormFixSegs : blk;
     int64_t b = tid >> 3;
-    for (; b + 3 * kStep < blk; b += 4 * kStep) {
+    for (; b + 3 * kStep < nend; b += 4 * kStep) {
       float y[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) y[u] = nb[b + u * kStep];
 #pragma unroll
       for (int u = 0; u < 4; ++u) acc += y[u];
     }
-    for (; b < blk; b += kStep) acc += nb[b];
+    for (; b < nend; b += kStep) acc += nb[b];
     est[c][tid >> 3] = acc;  // scratch: 32 partials per chain
   }
   __syncthreads();
